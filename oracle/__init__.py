@@ -1,0 +1,257 @@
+"""Oracle for the KMeans Lloyd path -- TEST INFRASTRUCTURE ONLY.
+
+CPU restatement of scikit-learn 1.7.2's dense Lloyd k-means (the CPU path
+skmetal dispatches ``KMeans`` to), used exclusively as the checker by
+``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py``.  Nothing in the product package imports this module.
+
+Two independent restatements live here:
+
+* ``lloyd_oracle.c`` (compiled to ``liboracle.so`` by ``make -C oracle``),
+  fp64 arithmetic on fp32 data, OpenMP-parallel so it handles the 500k x 100
+  workload in seconds; every function cites the sklearn file:line it follows.
+* ``numpy_lloyd`` below, a vectorised numpy restatement of the same steps for
+  small inputs, used to cross-check the C one.
+
+Parity status per function (what pins it, see tests/test_oracle.py):
+
+* ``assign``      -- skmetal's known-answer vector (tests/test_kernels.py:93-99),
+                     brute force over all k on random inputs, permutation and
+                     duplicate-centre invariants, sklearn golden labels.
+* ``mstep``       -- closed forms (k=1 mean, init=X rows), sklearn's
+                     _relocate_empty_clusters_dense vector
+                     (sklearn/cluster/tests/test_k_means.py:115-153),
+                     sklearn golden centres.
+* ``lloyd``       -- sklearn golden trajectories (tests/golden/*.npz written by
+                     tests/golden/make_fixtures.py), the unit-weight toy case,
+                     strict-convergence n_iter, monotone inertia.
+* ``inertia``     -- closed form (sum of squares about the mean for k=1),
+                     sklearn golden inertia.
+* ``mean_f32``    -- bit-exact against numpy's float32 X.mean(axis=0).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "liboracle.so"
+_lib = None
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_f64p = ctypes.POINTER(ctypes.c_double)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_i64 = ctypes.c_int64
+
+
+def build(force: bool = False) -> Path:
+    """Compile liboracle.so with gcc (make -C oracle)."""
+    if force or not _LIB_PATH.exists():
+        subprocess.run(["make", "-s", "-B", "-C", str(_HERE)], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not _LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(_LIB_PATH))
+        L.oracle_mean_f32.argtypes = [_f32p, _i64, _i64, _f32p]
+        L.oracle_mean_f32.restype = None
+        L.oracle_assign.argtypes = [_f32p, _i64, _i64, _f32p, _i64, _i32p, _f64p, _f64p]
+        L.oracle_assign.restype = None
+        L.oracle_sums.argtypes = [_f32p, _i64, _i64, _i32p, _i64, _f64p, _i64p]
+        L.oracle_sums.restype = None
+        L.oracle_mindists.argtypes = [_f32p, _i64, _i64, _f32p, _i32p, _f64p]
+        L.oracle_mindists.restype = None
+        L.oracle_inertia.argtypes = [_f32p, _i64, _i64, _f32p, _i32p]
+        L.oracle_inertia.restype = ctypes.c_double
+        L.oracle_mstep.argtypes = [_f32p, _i64, _i64, _i32p, _f32p, _i64, _f32p, _f64p]
+        L.oracle_mstep.restype = ctypes.c_int
+        L.oracle_lloyd.argtypes = [_f32p, _i64, _i64, _f32p, _i64, ctypes.c_int, ctypes.c_double,
+                                   _f32p, _i32p, _f64p, _f32p]
+        L.oracle_lloyd.restype = ctypes.c_int
+        L.oracle_num_threads.argtypes = []
+        L.oracle_num_threads.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _p(a, t):
+    return a.ctypes.data_as(t)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def num_threads() -> int:
+    return int(lib().oracle_num_threads())
+
+
+def mean_f32(X):
+    X = _f32(X)
+    n, d = X.shape
+    out = np.empty(d, np.float32)
+    lib().oracle_mean_f32(_p(X, _f32p), n, d, _p(out, _f32p))
+    return out
+
+
+def assign(X, C, return_gap: bool = False):
+    """Labels (int32) by strict-'<' argmin of ||c||^2 - 2 x.c (fp64).
+
+    With return_gap, also returns (best, second) true squared distances.
+    """
+    X = _f32(X)
+    C = _f32(C)
+    n, d = X.shape
+    k = C.shape[0]
+    labels = np.empty(n, np.int32)
+    if return_gap:
+        best = np.empty(n, np.float64)
+        second = np.empty(n, np.float64)
+        lib().oracle_assign(_p(X, _f32p), n, d, _p(C, _f32p), k, _p(labels, _i32p),
+                            _p(best, _f64p), _p(second, _f64p))
+        return labels, best, second
+    lib().oracle_assign(_p(X, _f32p), n, d, _p(C, _f32p), k, _p(labels, _i32p), None, None)
+    return labels
+
+
+def sums(X, labels, k):
+    X = _f32(X)
+    labels = np.ascontiguousarray(labels, dtype=np.int32)
+    n, d = X.shape
+    s = np.empty((k, d), np.float64)
+    c = np.empty(k, np.int64)
+    lib().oracle_sums(_p(X, _f32p), n, d, _p(labels, _i32p), k, _p(s, _f64p), _p(c, _i64p))
+    return s, c
+
+
+def mindists(X, C, labels):
+    X = _f32(X)
+    C = _f32(C)
+    labels = np.ascontiguousarray(labels, dtype=np.int32)
+    n, d = X.shape
+    out = np.empty(n, np.float64)
+    lib().oracle_mindists(_p(X, _f32p), n, d, _p(C, _f32p), _p(labels, _i32p), _p(out, _f64p))
+    return out
+
+
+def inertia(X, C, labels) -> float:
+    X = _f32(X)
+    C = _f32(C)
+    labels = np.ascontiguousarray(labels, dtype=np.int32)
+    n, d = X.shape
+    return float(lib().oracle_inertia(_p(X, _f32p), n, d, _p(C, _f32p), _p(labels, _i32p)))
+
+
+def mstep(X, labels, C_old):
+    """One M-step (sums, relocation, averaging, shift). Returns (C_new, shift, n_empty)."""
+    X = _f32(X)
+    C_old = _f32(C_old)
+    labels = np.ascontiguousarray(labels, dtype=np.int32)
+    n, d = X.shape
+    k = C_old.shape[0]
+    C_new = np.empty_like(C_old)
+    shift = np.empty(k, np.float64)
+    ne = lib().oracle_mstep(_p(X, _f32p), n, d, _p(labels, _i32p), _p(C_old, _f32p), k,
+                            _p(C_new, _f32p), _p(shift, _f64p))
+    return C_new, shift, int(ne)
+
+
+def lloyd(X, C_init, max_iter: int, tol_abs: float = 0.0, trace: bool = False):
+    """sklearn KMeans(init=C_init, n_init=1, algorithm='lloyd').fit(X), unit weights.
+
+    Returns dict(centers, labels, inertia, n_iter[, trace]).
+    """
+    X = _f32(X)
+    C_init = _f32(C_init)
+    n, d = X.shape
+    k = C_init.shape[0]
+    C_out = np.empty((k, d), np.float32)
+    labels = np.empty(n, np.int32)
+    inert = ctypes.c_double(0.0)
+    tr = np.empty((max_iter, k, d), np.float32) if trace else None
+    n_iter = lib().oracle_lloyd(_p(X, _f32p), n, d, _p(C_init, _f32p), k, int(max_iter),
+                                float(tol_abs), _p(C_out, _f32p), _p(labels, _i32p),
+                                ctypes.byref(inert), _p(tr, _f32p) if trace else None)
+    if n_iter < 0:
+        raise MemoryError("oracle_lloyd allocation failed")
+    out = dict(centers=C_out, labels=labels, inertia=inert.value, n_iter=int(n_iter))
+    if trace:
+        out["trace"] = tr[:n_iter]
+    return out
+
+
+def sklearn_tolerance(X, tol: float) -> float:
+    """sklearn's _tolerance (sklearn/cluster/_kmeans.py:279-287) for dense X."""
+    if tol == 0:
+        return 0.0
+    return float(np.mean(np.var(np.asarray(X, dtype=np.float32), axis=0)) * tol)
+
+
+# ---------------------------------------------------------------------------
+# Independent numpy restatement (small inputs only), used to cross-check C.
+# ---------------------------------------------------------------------------
+
+def numpy_lloyd(X, C_init, max_iter: int, tol_abs: float = 0.0):
+    """Vectorised restatement of the same sklearn steps, fp64 arithmetic."""
+    X = _f32(X)
+    mean = X.mean(axis=0)  # numpy float32 mean, as sklearn
+    Xc = X - mean
+    C = _f32(C_init) - mean
+    Xd = Xc.astype(np.float64)
+    n, d = X.shape
+    k = C.shape[0]
+    old = np.full(n, -1, np.int32)
+    strict = False
+    it = 0
+    for it in range(max_iter):
+        Cd = C.astype(np.float64)
+        D = (Cd * Cd).sum(1)[None, :] - 2.0 * Xd @ Cd.T
+        labels = np.argmin(D, axis=1).astype(np.int32)  # first minimum, as strict '<'
+        counts = np.bincount(labels, minlength=k).astype(np.int64)
+        S = np.zeros((k, d), np.float64)
+        np.add.at(S, labels, Xd)
+        empty = np.flatnonzero(counts == 0)
+        if empty.size:
+            dist = ((Xd - Cd[labels]) ** 2).sum(1)
+            if dist.max() > 0:
+                order = np.lexsort((np.arange(n), -dist))
+                for e, j in enumerate(empty):
+                    far = order[e]
+                    o = labels[far]
+                    S[o] -= Xd[far]
+                    S[j] = Xd[far]
+                    counts[j] = 1
+                    counts[o] -= 1
+        amax = int(np.argmax(counts))
+        cur = S.copy()
+        for j in range(k):
+            if counts[j] > 0:
+                cur[j] = cur[j] / counts[j]
+            else:
+                cur[j] = cur[amax]
+        C_new = cur.astype(np.float32)
+        shift = np.sqrt(((C_new.astype(np.float64) - C.astype(np.float64)) ** 2).sum(1))
+        C = C_new
+        if np.array_equal(labels, old):
+            strict = True
+            break
+        if (shift ** 2).sum() <= tol_abs:
+            break
+        old = labels
+    n_iter = it + 1
+    Cd = C.astype(np.float64)
+    if not strict:
+        D = (Cd * Cd).sum(1)[None, :] - 2.0 * Xd @ Cd.T
+        labels = np.argmin(D, axis=1).astype(np.int32)
+    inert = float(((Xd - Cd[labels]) ** 2).sum())
+    return dict(centers=(C + mean).astype(np.float32), labels=labels, inertia=inert, n_iter=n_iter)

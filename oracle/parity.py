@@ -1,0 +1,109 @@
+"""Parity rules for the KMeans Lloyd path -- TEST INFRASTRUCTURE ONLY.
+
+The acceptance rule compared against the oracle (and against sklearn's own
+outputs in the golden fixtures):
+
+* labels  -- identical, except rows whose oracle best-vs-second squared
+             distance gap is below ``LABEL_GAP_REL * ||x||^2`` (x in the
+             coordinates the distances were evaluated in);
+* centres -- per centre row j: max_c |a_jc - b_jc| <= CENTER_RTOL * max_c |b_jc|
+             (relative to the row's own magnitude, so coordinates that happen
+             to sit near zero do not make the test ill-conditioned);
+* inertia -- |a - b| <= INERTIA_RTOL * |b| against an fp64 recomputation.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+LABEL_GAP_REL = 1e-5
+CENTER_RTOL = 1e-4
+INERTIA_RTOL = 1e-5
+
+
+def label_mismatches(labels, ref_labels, best, second, X, gap_rel=LABEL_GAP_REL):
+    """Return (n_mismatch, n_unexcused, idx_unexcused)."""
+    labels = np.asarray(labels).astype(np.int64)
+    ref_labels = np.asarray(ref_labels).astype(np.int64)
+    mism = np.flatnonzero(labels != ref_labels)
+    if mism.size == 0:
+        return 0, 0, mism
+    Xm = np.asarray(X, dtype=np.float64)[mism]
+    xx = (Xm * Xm).sum(1)
+    gap = np.asarray(second, dtype=np.float64)[mism] - np.asarray(best, dtype=np.float64)[mism]
+    bad = mism[gap >= gap_rel * np.maximum(xx, 1e-300)]
+    return int(mism.size), int(bad.size), bad
+
+
+def check_labels(labels, ref_labels, best, second, X, gap_rel=LABEL_GAP_REL, what="labels"):
+    n_m, n_bad, bad = label_mismatches(labels, ref_labels, best, second, X, gap_rel)
+    assert n_bad == 0, (
+        f"{what}: {n_bad} of {n_m} mismatching rows are not near-ties "
+        f"(first rows {bad[:8].tolist()})"
+    )
+    return n_m
+
+
+def center_rel_err(C, C_ref):
+    C = np.asarray(C, dtype=np.float64)
+    R = np.asarray(C_ref, dtype=np.float64)
+    num = np.abs(C - R).max(axis=1)
+    den = np.maximum(np.abs(R).max(axis=1), 1e-30)
+    return float((num / den).max())
+
+
+def check_centers(C, C_ref, rtol=CENTER_RTOL, what="centers"):
+    err = center_rel_err(C, C_ref)
+    assert err <= rtol, f"{what}: max row-relative error {err:.3e} > {rtol:.1e}"
+    return err
+
+
+def check_inertia(v, ref, rtol=INERTIA_RTOL, what="inertia"):
+    err = abs(float(v) - float(ref)) / max(abs(float(ref)), 1e-300)
+    assert err <= rtol, f"{what}: relative error {err:.3e} > {rtol:.1e} ({v} vs {ref})"
+    return err
+
+
+def near_ties(best, second, X, gap_rel=LABEL_GAP_REL):
+    """Rows whose best-vs-second gap is below gap_rel * ||x||^2."""
+    Xd = np.asarray(X, dtype=np.float64)
+    xx = (Xd * Xd).sum(1)
+    gap = np.asarray(second, dtype=np.float64) - np.asarray(best, dtype=np.float64)
+    return np.flatnonzero(gap < gap_rel * np.maximum(xx, 1e-300))
+
+
+def _match_relocated(C, C_ref, rows):
+    """Row-relative error after best-matching the given rows of C to those of C_ref."""
+    C = np.asarray(C, dtype=np.float64).copy()
+    R = np.asarray(C_ref, dtype=np.float64)
+    rows = list(rows)
+    free = list(rows)
+    for r in rows:
+        errs = [np.abs(C[f] - R[r]).max() for f in free]
+        f = free.pop(int(np.argmin(errs)))
+        C[r], C[f] = C[f].copy(), C[r].copy()
+    return center_rel_err(C, R)
+
+
+def check_lockstep(X, C_prev, C_next_ref, labels_ref, rtol=CENTER_RTOL, what="step"):
+    """One Lloyd step from C_prev checked against a reference step.
+
+    X and C_prev are in the coordinates the step runs in; labels_ref and
+    C_next_ref are the reference's E-step labels and M-step centres for that
+    step.  Labels must agree with the oracle's E-step up to near-ties; the
+    oracle's M-step applied to labels_ref must reproduce C_next_ref.  When
+    three or more clusters were empty, the reference may hand the relocated
+    points to the empty clusters in a different order, so those rows are
+    compared as a set.  Returns the number of label mismatches.
+    """
+    import oracle
+
+    labels, best, second = oracle.assign(X, C_prev, return_gap=True)
+    n_m = check_labels(labels_ref, labels, best, second, X, what=f"{what} labels")
+    C_new, _, n_empty = oracle.mstep(X, labels_ref, C_prev)
+    err = center_rel_err(C_new, C_next_ref)
+    if err > rtol and n_empty >= 3:
+        counts = np.bincount(np.asarray(labels_ref, dtype=np.int64), minlength=len(C_prev))
+        err = _match_relocated(C_new, C_next_ref, np.flatnonzero(counts == 0))
+    assert err <= rtol, f"{what}: centres row-relative error {err:.3e} > {rtol:.1e}"
+    return n_m
