@@ -1,0 +1,141 @@
+/*
+ * skmetal_hip.h -- C ABI of libskmetal_hip.so, the MI355X (gfx950) drop-in
+ * for libSkMetalBridge.dylib on skmetal's KMeans fit/predict path.
+ *
+ * Conventions (unchanged from the reference's ctypes binding,
+ * skmetal/_bridge.py:78-142, 345-363, 576-639):
+ *   - size_t arguments are 64-bit (Swift Int in the reference);
+ *   - X and centroids are float32, C-contiguous, row-major [n x d] / [k x d];
+ *   - labels ("assignments") are 32-bit integers in [0, k);
+ *   - the caller owns every buffer; no pointer is retained after a call
+ *     returns, and every call is synchronous (results are in the caller's
+ *     arrays on return);
+ *   - 0 means success; a non-zero return is one of the SKMETAL_E* codes below
+ *     (the reference returned 1 for every failure) and the message is
+ *     available from skmetal_hip_last_error().  The library never aborts.
+ *   - calls are serialised by an internal lock, so concurrent callers
+ *     (ctypes releases the GIL) are safe.
+ */
+#ifndef SKMETAL_HIP_H
+#define SKMETAL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__) || defined(__clang__)
+#define SKMETAL_API __attribute__((visibility("default")))
+#else
+#define SKMETAL_API
+#endif
+
+#define SKMETAL_OK 0
+#define SKMETAL_EINVAL 1   /* bad argument (null pointer, zero size, k > n ...) */
+#define SKMETAL_ENODEV 2   /* no usable gfx950 device / HIP runtime failed to start */
+#define SKMETAL_ENOMEM 3   /* device or pinned host allocation failed */
+#define SKMETAL_ELAUNCH 4  /* kernel launch failed */
+#define SKMETAL_EHIP 5     /* any other HIP runtime error */
+#define SKMETAL_ERANGE 6   /* a size exceeds what the library supports */
+
+/* ---- set-up: skmetal_bridge/Sources/SkMetalBridgeC/include/bridge.h:11-12,60;
+ *      Bridge.swift:19-48,52-144; bound at skmetal/_bridge.py:352-363 ---- */
+
+/* Create the device context (device 0 of the visible devices).  Idempotent. */
+SKMETAL_API int skmetal_init(void);
+
+/* Load and run every kernel of the path once on a tiny problem. */
+SKMETAL_API int skmetal_warmup(void);
+
+/* Device name, max threads per block, unified-memory flag (0 on MI355X),
+ * and total HBM bytes.  Replaces Bridge.swift:25-48 (bridge.h:12). */
+SKMETAL_API int skmetal_device_info(char* name, int name_capacity, size_t* max_threads,
+                        uint8_t* has_unified_memory, uint64_t* recommended_working_set_size);
+
+/* ---- the KMeans path ---- */
+
+/* E-step only: assignments[i] = argmin_j ||c_j||^2 - 2 x_i.c_j, lowest index on
+ * ties, evaluated on X as given.  Replaces skmetal_kmeans_assign
+ * (bridge.h:37; KMeansBridge.swift:138-181; _bridge.py:111-119, 576-578). */
+SKMETAL_API int skmetal_kmeans_assign(const void* X, const void* centroids, void* assignments,
+                          size_t n, size_t d, size_t k);
+
+/* Whole Lloyd fit, sklearn KMeans(init=centroids, n_init=1, algorithm="lloyd")
+ * semantics: X is centred on its column mean for the distance evaluations;
+ * the loop stops on strict label convergence, or when
+ * sum_j ||c_j_new - c_j_old||^2 <= tol (tol is sklearn's absolute `_tol`,
+ * i.e. mean feature variance x estimator tol; 0 disables the test), or after
+ * max_iter steps; empty clusters are relocated as sklearn does; a final E-step
+ * makes the labels match the returned centres.  centroids is in/out (initial
+ * centres in, final centres out, caller coordinates); assignments is out;
+ * *n_iter_out receives sklearn's n_iter_.  num_groups is accepted for ABI
+ * compatibility and ignored (the reference used it to size Metal threadgroup
+ * partials).  Replaces skmetal_kmeans_batch_fused (bridge.h:39;
+ * KMeansBridge.swift:187-320; _bridge.py:120-132, 591-617). */
+SKMETAL_API int skmetal_kmeans_batch_fused(const void* X, void* centroids, void* assignments,
+                               size_t n, size_t d, size_t k, size_t num_groups,
+                               size_t max_iter, float tol, int32_t* n_iter_out);
+
+/* sum_i ||x_i - c_{label_i}||^2 (fp64 accumulation, returned as float), or
+ * -1.0f on failure.  Replaces skmetal_kmeans_inertia (KMeansBridge.swift:324-373,
+ * bound lazily at _bridge.py:627-639; absent from the reference's bridge.h). */
+SKMETAL_API float skmetal_kmeans_inertia(const void* X, const void* centroids, const void* assignments,
+                             size_t n, size_t d, size_t k);
+
+/* dists[i] = ||x_i - c_{label_i}||^2 (fp32).  Replaces skmetal_compute_mindists
+ * (bridge.h:45; KMeansBridge.swift:89-134; _bridge.py:133-142, 620-624). */
+SKMETAL_API int skmetal_compute_mindists(const void* X, const void* centroids, const void* assignments,
+                             void* dists, size_t n, size_t d, size_t k);
+
+/* ---- additions without a counterpart in the reference ---- */
+
+/* Message of the last failure on the calling thread ("" if none). */
+SKMETAL_API const char* skmetal_hip_last_error(void);
+
+/* Release the device buffers the library keeps cached between calls. */
+SKMETAL_API int skmetal_hip_release_cache(void);
+
+/* skmetal_kmeans_batch_fused plus the final inertia (fp64), so a fit needs a
+ * single upload of X.  flags: SKMETAL_FIT_STRICT (stop on strict label
+ * convergence, as sklearn) -- pass it for sklearn semantics. */
+#define SKMETAL_FIT_STRICT 1
+SKMETAL_API int skmetal_hip_kmeans_fit(const float* X, float* centroids, int32_t* labels,
+                           size_t n, size_t d, size_t k, size_t max_iter, double tol,
+                           int flags, int32_t* n_iter_out, double* inertia_out);
+
+/* Device-resident Lloyd handle: X is uploaded (and optionally centred) once
+ * and stays in HBM across calls; used for timing a fixed number of
+ * iterations and for step-by-step checks.  Not thread-safe per handle. */
+typedef struct skmetal_hip_lloyd skmetal_hip_lloyd;
+
+SKMETAL_API int skmetal_hip_lloyd_create(size_t n, size_t d, size_t k, skmetal_hip_lloyd** out);
+SKMETAL_API int skmetal_hip_lloyd_destroy(skmetal_hip_lloyd* h);
+/* Upload X [n x d]; center != 0 subtracts the column mean on the device. */
+SKMETAL_API int skmetal_hip_lloyd_load(skmetal_hip_lloyd* h, const float* X, int center);
+/* Set the centres [k x d] (caller coordinates). */
+SKMETAL_API int skmetal_hip_lloyd_set_centers(skmetal_hip_lloyd* h, const float* C);
+/* Run exactly `iters` Lloyd steps (E-step + M-step, no convergence stop;
+ * empty clusters are still relocated).  If ms_out is not NULL it receives
+ * the elapsed time of the steps measured with HIP events on the handle's
+ * stream. */
+SKMETAL_API int skmetal_hip_lloyd_iterate(skmetal_hip_lloyd* h, size_t iters, float* ms_out);
+/* sklearn loop (see skmetal_hip_kmeans_fit) from the current centres,
+ * including the final E-step and inertia. */
+SKMETAL_API int skmetal_hip_lloyd_run(skmetal_hip_lloyd* h, size_t max_iter, double tol, int flags,
+                          int32_t* n_iter_out, double* inertia_out);
+/* Average time of one launch (ms) of the assign and the update kernels over
+ * `reps` back-to-back launches on the current centres (HIP events). */
+SKMETAL_API int skmetal_hip_lloyd_time_kernels(skmetal_hip_lloyd* h, size_t reps, float* ms_assign,
+                                   float* ms_update);
+SKMETAL_API int skmetal_hip_lloyd_get_centers(skmetal_hip_lloyd* h, float* C);
+SKMETAL_API int skmetal_hip_lloyd_get_labels(skmetal_hip_lloyd* h, int32_t* labels);
+/* Inertia of the current labels against the current centres (fp64). */
+SKMETAL_API int skmetal_hip_lloyd_inertia(skmetal_hip_lloyd* h, double* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SKMETAL_HIP_H */

@@ -58,9 +58,21 @@ def check_centers(C, C_ref, rtol=CENTER_RTOL, what="centers"):
     return err
 
 
-def check_inertia(v, ref, rtol=INERTIA_RTOL, what="inertia"):
-    err = abs(float(v) - float(ref)) / max(abs(float(ref)), 1e-300)
-    assert err <= rtol, f"{what}: relative error {err:.3e} > {rtol:.1e} ({v} vs {ref})"
+def centring_floor(X) -> float:
+    """Absolute inertia floor from fp32 centring: each element of X - mean carries
+    a rounding error up to eps*|x|, so two implementations that centre with
+    means differing in the last bit may differ by about n*d*(eps*max|x|)^2 even
+    when the true inertia is zero (all points on their centres)."""
+    X = np.asarray(X)
+    eps = float(np.finfo(np.float32).eps)
+    return 4.0 * X.size * (eps * float(np.abs(X).max(initial=0.0))) ** 2
+
+
+def check_inertia(v, ref, rtol=INERTIA_RTOL, atol=0.0, what="inertia"):
+    diff = abs(float(v) - float(ref))
+    err = diff / max(abs(float(ref)), 1e-300)
+    assert diff <= rtol * abs(float(ref)) + atol, (
+        f"{what}: relative error {err:.3e} > {rtol:.1e} ({v} vs {ref}, atol {atol:.1e})")
     return err
 
 

@@ -1,0 +1,290 @@
+"""ctypes bridge to libskmetal_hip.so (mirrors skmetal/_bridge.py on the KMeans path).
+
+Binds the reference's KMeans entry points with the reference's argtypes
+(skmetal/_bridge.py:111-142, 352-363, 627-639) plus this library's additions
+(``skmetal_hip_*``).  ``HIP_AVAILABLE`` (alias ``METAL_AVAILABLE``) is True
+only when the library loaded *and* a gfx950 device initialised.  Wrappers
+raise ``RuntimeError`` when the library is unavailable or a call fails; they
+never compute anything on the CPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import warnings
+from pathlib import Path
+
+import numpy as np
+
+_PKG = Path(__file__).resolve().parent
+LIB_NAME = "libskmetal_hip.so"
+
+
+def _find_library() -> str:
+    env = os.environ.get("SKMETAL_HIP_LIB")
+    candidates = [Path(env)] if env else []
+    candidates.append(_PKG / LIB_NAME)
+    for p in candidates:
+        if p.exists():
+            return str(p.resolve())
+    raise RuntimeError(f"{LIB_NAME} not found; build it with `python -m skmetal_amd._build`")
+
+
+_c_size = ctypes.c_size_t
+_vp = ctypes.c_void_p
+
+# (c_name, restype, argtypes...) -- the KMeans subset of the reference's registry
+_REGISTRY = [
+    ("skmetal_init", ctypes.c_int),
+    ("skmetal_warmup", ctypes.c_int),
+    ("skmetal_device_info", ctypes.c_int, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(ctypes.c_size_t),
+     ctypes.POINTER(ctypes.c_uint8), ctypes.POINTER(ctypes.c_uint64)),
+    ("skmetal_kmeans_assign", ctypes.c_int, _vp, _vp, _vp, _c_size, _c_size, _c_size),
+    ("skmetal_kmeans_batch_fused", ctypes.c_int, _vp, _vp, _vp, _c_size, _c_size, _c_size, _c_size, _c_size,
+     ctypes.c_float, ctypes.POINTER(ctypes.c_int32)),
+    ("skmetal_compute_mindists", ctypes.c_int, _vp, _vp, _vp, _vp, _c_size, _c_size, _c_size),
+    ("skmetal_kmeans_inertia", ctypes.c_float, _vp, _vp, _vp, _c_size, _c_size, _c_size),
+    ("skmetal_hip_last_error", ctypes.c_char_p),
+    ("skmetal_hip_release_cache", ctypes.c_int),
+    ("skmetal_hip_kmeans_fit", ctypes.c_int, _vp, _vp, _vp, _c_size, _c_size, _c_size, _c_size, ctypes.c_double,
+     ctypes.c_int, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_double)),
+    ("skmetal_hip_lloyd_create", ctypes.c_int, _c_size, _c_size, _c_size, ctypes.POINTER(_vp)),
+    ("skmetal_hip_lloyd_destroy", ctypes.c_int, _vp),
+    ("skmetal_hip_lloyd_load", ctypes.c_int, _vp, _vp, ctypes.c_int),
+    ("skmetal_hip_lloyd_set_centers", ctypes.c_int, _vp, _vp),
+    ("skmetal_hip_lloyd_iterate", ctypes.c_int, _vp, _c_size, ctypes.POINTER(ctypes.c_float)),
+    ("skmetal_hip_lloyd_run", ctypes.c_int, _vp, _c_size, ctypes.c_double, ctypes.c_int,
+     ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_double)),
+    ("skmetal_hip_lloyd_time_kernels", ctypes.c_int, _vp, _c_size, ctypes.POINTER(ctypes.c_float),
+     ctypes.POINTER(ctypes.c_float)),
+    ("skmetal_hip_lloyd_get_centers", ctypes.c_int, _vp, _vp),
+    ("skmetal_hip_lloyd_get_labels", ctypes.c_int, _vp, _vp),
+    ("skmetal_hip_lloyd_inertia", ctypes.c_int, _vp, ctypes.POINTER(ctypes.c_double)),
+]
+
+SKMETAL_FIT_STRICT = 1
+
+_lib = None
+_load_error = None
+HIP_AVAILABLE = False
+try:
+    _lib = ctypes.CDLL(_find_library())
+    for _name, _restype, *_argtypes in _REGISTRY:
+        _f = getattr(_lib, _name)
+        _f.argtypes = list(_argtypes)
+        _f.restype = _restype
+    _rc = _lib.skmetal_init()
+    if _rc != 0:
+        raise RuntimeError(f"skmetal_init failed with code {_rc}: {_lib.skmetal_hip_last_error().decode()}")
+    HIP_AVAILABLE = True
+except Exception as _err:  # noqa: BLE001 -- report and keep importing, like the reference
+    _load_error = _err
+    warnings.warn(
+        f"skmetal_amd: MI355X GPU path not available ({_err}). accelerate() leaves estimators on scikit-learn.",
+        stacklevel=2,
+    )
+
+METAL_AVAILABLE = HIP_AVAILABLE  # name kept for code written against skmetal
+
+_WARMUP_DONE = False
+
+
+def library_path() -> str | None:
+    return getattr(_lib, "_name", None) if _lib is not None else None
+
+
+def _require():
+    if _lib is None or not HIP_AVAILABLE:
+        raise RuntimeError(f"skmetal_amd GPU path unavailable: {_load_error}")
+
+
+def last_error() -> str:
+    return _lib.skmetal_hip_last_error().decode() if _lib is not None else str(_load_error)
+
+
+def ensure_warmed_up():
+    global _WARMUP_DONE
+    _require()
+    if not _WARMUP_DONE:
+        _check(_lib.skmetal_warmup(), "skmetal_warmup")
+        _WARMUP_DONE = True
+
+
+def _check(err: int, name: str, context: str = ""):
+    if err != 0:
+        msg = f"{name} failed with code {err}"
+        if context:
+            msg += f" ({context})"
+        detail = last_error()
+        if detail:
+            msg += f": {detail}"
+        raise RuntimeError(msg)
+
+
+def _bridge_call(c_func, *args, context=""):
+    """Call a C entry point converting numpy arrays / ints / floats as the reference does
+    (skmetal/_bridge.py:78-103); raise RuntimeError on a non-zero return."""
+    ensure_warmed_up()
+    c_args = []
+    for a in args:
+        if isinstance(a, np.ndarray):
+            c_args.append(a.ctypes.data)
+        elif isinstance(a, bool):
+            c_args.append(ctypes.c_int(int(a)))
+        elif isinstance(a, int):
+            c_args.append(ctypes.c_size_t(a))
+        elif isinstance(a, (float, np.floating)):
+            c_args.append(ctypes.c_float(a))
+        else:
+            c_args.append(a)
+    _check(c_func(*c_args), c_func.__name__, context)
+
+
+def _f32c(a, name):
+    if not (isinstance(a, np.ndarray) and a.dtype == np.float32 and a.flags.c_contiguous):
+        raise TypeError(f"{name} must be a C-contiguous float32 ndarray")
+    return a
+
+
+def _i32c(a, name):
+    if not (isinstance(a, np.ndarray) and a.dtype.itemsize == 4 and a.dtype.kind in "iu" and a.flags.c_contiguous):
+        raise TypeError(f"{name} must be a C-contiguous 32-bit integer ndarray")
+    return a
+
+
+# ---- the reference's KMeans wrappers (skmetal/_bridge.py:576-639) ----
+
+def kmeans_assign(X, centroids, assignments, n, d, k) -> None:
+    """E-step: assignments[i] = nearest centroid of X[i]."""
+    _f32c(X, "X"), _f32c(centroids, "centroids"), _i32c(assignments, "assignments")
+    _bridge_call(_lib.skmetal_kmeans_assign, X, centroids, assignments, n, d, k)
+
+
+def kmeans_batch_fused(X, centroids, assignments, n, d, k, num_groups, max_iter, tol) -> int:
+    """Lloyd fit on the GPU (centroids in/out); returns n_iter."""
+    _f32c(X, "X"), _f32c(centroids, "centroids"), _i32c(assignments, "assignments")
+    n_iter_out = ctypes.c_int32(0)
+    _bridge_call(_lib.skmetal_kmeans_batch_fused, X, centroids, assignments, n, d, k, num_groups, max_iter,
+                 ctypes.c_float(tol), ctypes.byref(n_iter_out))
+    return n_iter_out.value
+
+
+def compute_mindists(X, centroids, assignments, dists, n, d, k) -> None:
+    """dists[i] = ||X[i] - centroids[assignments[i]]||^2."""
+    _f32c(X, "X"), _f32c(centroids, "centroids"), _i32c(assignments, "assignments"), _f32c(dists, "dists")
+    _bridge_call(_lib.skmetal_compute_mindists, X, centroids, assignments, dists, n, d, k)
+
+
+def kmeans_inertia(X, centroids, assignments, n, d, k) -> float:
+    """Sum of squared distances to the assigned centroids (GPU); -1.0 on failure, as the reference."""
+    ensure_warmed_up()
+    return float(_lib.skmetal_kmeans_inertia(X.ctypes.data, centroids.ctypes.data, assignments.ctypes.data,
+                                             n, d, k))
+
+
+def device_info() -> dict:
+    _require()
+    name_buf = ctypes.create_string_buffer(256)
+    max_threads = ctypes.c_size_t()
+    unified = ctypes.c_uint8()
+    working_set = ctypes.c_uint64()
+    _check(_lib.skmetal_device_info(name_buf, 256, ctypes.byref(max_threads), ctypes.byref(unified),
+                                    ctypes.byref(working_set)), "skmetal_device_info")
+    return {
+        "name": name_buf.value.decode("utf-8") if name_buf.value else "unknown",
+        "max_threads_per_threadgroup": max_threads.value,
+        "has_unified_memory": bool(unified.value),
+        "recommended_working_set_size_bytes": working_set.value,
+    }
+
+
+# ---- additions ----
+
+def kmeans_fit(X, centroids, labels, max_iter, tol_abs, strict=True):
+    """Full sklearn-semantics Lloyd fit. centroids in/out, labels out.
+
+    Returns (n_iter, inertia)."""
+    _f32c(X, "X"), _f32c(centroids, "centroids"), _i32c(labels, "labels")
+    ensure_warmed_up()
+    n, d = X.shape
+    k = centroids.shape[0]
+    n_iter = ctypes.c_int32(0)
+    inertia = ctypes.c_double(0.0)
+    _check(_lib.skmetal_hip_kmeans_fit(X.ctypes.data, centroids.ctypes.data, labels.ctypes.data, n, d, k,
+                                       int(max_iter), float(tol_abs), SKMETAL_FIT_STRICT if strict else 0,
+                                       ctypes.byref(n_iter), ctypes.byref(inertia)), "skmetal_hip_kmeans_fit")
+    return int(n_iter.value), float(inertia.value)
+
+
+class LloydHandle:
+    """Device-resident Lloyd problem (X uploaded once, kept in HBM)."""
+
+    def __init__(self, n: int, d: int, k: int):
+        ensure_warmed_up()
+        self.n, self.d, self.k = int(n), int(d), int(k)
+        h = ctypes.c_void_p()
+        _check(_lib.skmetal_hip_lloyd_create(self.n, self.d, self.k, ctypes.byref(h)), "skmetal_hip_lloyd_create")
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            _lib.skmetal_hip_lloyd_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def load(self, X, center=True):
+        _f32c(X, "X")
+        assert X.shape == (self.n, self.d)
+        _check(_lib.skmetal_hip_lloyd_load(self._h, X.ctypes.data, int(bool(center))), "skmetal_hip_lloyd_load")
+
+    def set_centers(self, C):
+        _f32c(C, "C")
+        assert C.shape == (self.k, self.d)
+        _check(_lib.skmetal_hip_lloyd_set_centers(self._h, C.ctypes.data), "skmetal_hip_lloyd_set_centers")
+
+    def iterate(self, iters: int) -> float:
+        ms = ctypes.c_float(0.0)
+        _check(_lib.skmetal_hip_lloyd_iterate(self._h, int(iters), ctypes.byref(ms)), "skmetal_hip_lloyd_iterate")
+        return float(ms.value)
+
+    def run(self, max_iter: int, tol_abs: float = 0.0, strict: bool = True):
+        n_iter = ctypes.c_int32(0)
+        inertia = ctypes.c_double(0.0)
+        _check(_lib.skmetal_hip_lloyd_run(self._h, int(max_iter), float(tol_abs),
+                                          SKMETAL_FIT_STRICT if strict else 0, ctypes.byref(n_iter),
+                                          ctypes.byref(inertia)), "skmetal_hip_lloyd_run")
+        return int(n_iter.value), float(inertia.value)
+
+    def time_kernels(self, reps: int):
+        a = ctypes.c_float(0.0)
+        u = ctypes.c_float(0.0)
+        _check(_lib.skmetal_hip_lloyd_time_kernels(self._h, int(reps), ctypes.byref(a), ctypes.byref(u)),
+               "skmetal_hip_lloyd_time_kernels")
+        return float(a.value), float(u.value)
+
+    def centers(self):
+        out = np.empty((self.k, self.d), np.float32)
+        _check(_lib.skmetal_hip_lloyd_get_centers(self._h, out.ctypes.data), "skmetal_hip_lloyd_get_centers")
+        return out
+
+    def labels(self):
+        out = np.empty(self.n, np.int32)
+        _check(_lib.skmetal_hip_lloyd_get_labels(self._h, out.ctypes.data), "skmetal_hip_lloyd_get_labels")
+        return out
+
+    def inertia(self) -> float:
+        v = ctypes.c_double(0.0)
+        _check(_lib.skmetal_hip_lloyd_inertia(self._h, ctypes.byref(v)), "skmetal_hip_lloyd_inertia")
+        return float(v.value)

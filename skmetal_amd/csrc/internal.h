@@ -1,0 +1,91 @@
+// internal.h -- shared declarations between the KMeans kernels and the
+// host runtime of libskmetal_hip.so (gfx950 / MI355X).
+//
+// Device data layout for one Lloyd problem (n rows, d features, k clusters):
+//   X       fp32 [n x ld]   column-centred rows, ld = round_up(d, 4), pad = 0
+//   C[2]    fp32 [k x ld]   centres (double-buffered: old -> new each step)
+//   cnorm   fp32 [k]        ||c_j||^2 of the current centres
+//   labels  int32 [n]
+// Everything stays resident in HBM for the whole fit.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace skm {
+
+// Per-fit loop state, resident in device memory.  Every kernel of the
+// Lloyd loop reads `done` first and returns at once when it is non-zero,
+// so a whole batch of iterations can be enqueued without host round trips.
+struct LoopState {
+    int done;          // 0 run, 1 strict label convergence, 2 shift <= tol,
+                       // 3 empty cluster: host relocation needed at `halt_iter`
+    int n_iter;        // sklearn's n_iter_ (iterations completed)
+    int changed;       // labels changed by the E-step in flight
+    int last_changed;  // `changed` of the last finalised iteration
+    int halt_iter;     // iteration index at which `done` was set
+    int n_empty;       // empty clusters found by the last finalise
+    unsigned global_ctr;  // finalise: clusters completed in this iteration
+    unsigned rowdist_ctr; // row-distance reduction: blocks completed
+    double shift_tot;  // sum_j ||c_j_new - c_j_old||^2 of the last step
+    double inertia;    // result of the last row-distance reduction
+};
+
+enum StepFlags : int {
+    kStopStrict = 1,   // stop when an E-step changes no label (sklearn rule)
+};
+
+// ---- kernel launchers (kmeans_kernels.hip) -------------------------------
+// All return hipSuccess or the launch error; all enqueue on `s`.
+
+struct AssignArgs {
+    const float* X; long n; int ld;
+    const float* C; const float* cnorm; int k;
+    int* labels;
+    LoopState* state;      // nullable: no early exit, no change counting
+    int count_changes;     // compare with previous labels, add to state->changed
+};
+hipError_t launch_assign(const AssignArgs& a, int num_cu, hipStream_t s);
+
+struct UpdateArgs {
+    const float* X; long n; int ld; int d;
+    const int* labels; int k;
+    float* psum;           // [R x k x ld]
+    int* pcnt;             // [R x k]
+    LoopState* state;
+};
+struct UpdateGeom { int R; int G; int cg; long rows_per_range; int threads; size_t lds; };
+UpdateGeom update_geometry(long n, int d, int k, int num_cu);
+hipError_t launch_update(const UpdateArgs& a, const UpdateGeom& g, hipStream_t s);
+
+struct FinalizeArgs {
+    const float* psum; const int* pcnt; int R; int k; int d; int ld;
+    const float* C_old; float* C_new; float* cnorm;
+    double* sums;          // [k x ld] fp64 totals (kept for the relocation path)
+    int* counts;           // [k]
+    double* part;          // [k x nch x 2]
+    float* shift_sq;       // [k]
+    unsigned* cluster_ctr; // [k], zero between launches
+    LoopState* state;
+    int iter; double tol; int flags;
+};
+hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t s);
+inline int finalize_col_chunks(int d) { return (d + 31) / 32; }
+
+struct RowDistArgs {
+    const float* X; long n; int ld; int d;
+    const float* C; int k; const int* labels;  // rows with a label outside [0, k) count 0
+    float* out_rows;       // nullable: per-row squared distance
+    double* block_part;    // [grid]
+    LoopState* state;      // holds rowdist_ctr and receives `inertia`
+};
+int rowdist_grid(long n);
+hipError_t launch_rowdist(const RowDistArgs& a, hipStream_t s);
+
+hipError_t launch_colsum(const float* X, long n, int ld, int d, double* part, int nblk, hipStream_t s);
+int colsum_grid(long n);
+hipError_t launch_colmean(const double* part, int nblk, long n, int d, float* mean, hipStream_t s);
+hipError_t launch_center(float* X, long n, int ld, int d, const float* mean, hipStream_t s);
+hipError_t launch_cnorm(const float* C, int k, int ld, float* cnorm, hipStream_t s);
+
+}  // namespace skm

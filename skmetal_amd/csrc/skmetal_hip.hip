@@ -1,0 +1,896 @@
+// skmetal_hip.hip -- host runtime and C ABI of libskmetal_hip.so.
+//
+// Replaces the reference's Swift bridge on the KMeans path
+// (skmetal_bridge/Sources/SkMetalBridge/{MetalContext,Bridge,KMeansBridge}.swift):
+//   - MetalContext.shared (device, queue, buffer pool)  -> Context below
+//   - makeBuffer(bytesNoCopy:) zero-copy wrapping       -> hipMalloc'd device
+//     buffers, filled through pinned staging with hipMemcpyAsync; X stays
+//     resident in HBM for the whole fit
+//   - one command buffer + waitUntilCompleted per Lloyd iteration
+//     (KMeansBridge.swift:249-313)                      -> all iterations of a
+//     batch enqueued on one stream; kernels read a device-side `done` flag
+//     and return at once after the loop has stopped, so the host synchronises
+//     once per batch, not once per iteration.
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <numeric>
+#include <string>
+#include <vector>
+
+#include "../../include/skmetal_hip.h"
+#include "internal.h"
+
+using namespace skm;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what)
+{
+    int code = SKMETAL_EHIP;
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) code = SKMETAL_ENOMEM;
+    if (e == hipErrorLaunchFailure || e == hipErrorInvalidDeviceFunction || e == hipErrorLaunchOutOfResources)
+        code = SKMETAL_ELAUNCH;
+    return fail(code, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                       \
+    do {                                          \
+        hipError_t e_ = (expr);                   \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+#define TRY(expr)                \
+    do {                         \
+        int rc_ = (expr);        \
+        if (rc_ != 0) return rc_; \
+    } while (0)
+
+constexpr size_t kPinBytes = size_t(32) << 20;  // per staging buffer
+constexpr size_t kMaxDim = size_t(1) << 20;
+
+// ---------------------------------------------------------------------------
+// context: device, stream, pinned staging, size-keyed device buffer cache
+// (the analogue of MetalContext.reusableBuffer/recycleBuffer, :66-85)
+// ---------------------------------------------------------------------------
+struct Context {
+    std::recursive_mutex mu;
+    bool ready = false;
+    int dev = 0;
+    int num_cu = 0;
+    int max_threads = 0;
+    size_t total_mem = 0;
+    std::string name;
+    hipStream_t stream = nullptr;
+    void* pin[2] = {nullptr, nullptr};
+    hipEvent_t pin_ev[2] = {nullptr, nullptr};
+    std::multimap<size_t, void*> free_blocks;
+    std::map<void*, size_t> sizes;
+
+    int init()
+    {
+        if (ready) return 0;
+        int count = 0;
+        hipError_t e = hipGetDeviceCount(&count);
+        if (e != hipSuccess || count < 1)
+            return fail(SKMETAL_ENODEV, "no HIP device available (%s)", e == hipSuccess ? "0 devices" : hipGetErrorString(e));
+        HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
+        hipDeviceProp_t p;
+        HIP_TRY(hipGetDeviceProperties(&p, dev), "hipGetDeviceProperties");
+        if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0)
+            return fail(SKMETAL_ENODEV, "device %d is %s; this library is built for gfx950 (MI355X)", dev,
+                        p.gcnArchName);
+        num_cu = p.multiProcessorCount;
+        max_threads = p.maxThreadsPerBlock;
+        total_mem = p.totalGlobalMem;
+        name = p.name;
+        HIP_TRY(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
+        for (int i = 0; i < 2; ++i) {
+            HIP_TRY(hipHostMalloc(&pin[i], kPinBytes, hipHostMallocDefault), "hipHostMalloc(staging)");
+            HIP_TRY(hipEventCreateWithFlags(&pin_ev[i], hipEventDisableTiming), "hipEventCreate");
+        }
+        ready = true;
+        return 0;
+    }
+
+    int alloc(void** out, size_t bytes)
+    {
+        if (bytes == 0) bytes = 256;
+        bytes = (bytes + 255) & ~size_t(255);
+        auto it = free_blocks.lower_bound(bytes);
+        if (it != free_blocks.end() && it->first <= bytes + bytes / 4) {
+            *out = it->second;
+            free_blocks.erase(it);
+            return 0;
+        }
+        void* p = nullptr;
+        hipError_t e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) {
+            // drop the cache and retry once
+            hipGetLastError();
+            release_cache();
+            e = hipMalloc(&p, bytes);
+            if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+        }
+        sizes[p] = bytes;
+        *out = p;
+        return 0;
+    }
+
+    void release(void* p)
+    {
+        if (p == nullptr) return;
+        auto it = sizes.find(p);
+        if (it == sizes.end()) return;
+        free_blocks.emplace(it->second, p);
+    }
+
+    void release_cache()
+    {
+        for (auto& kv : free_blocks) {
+            sizes.erase(kv.second);
+            hipFree(kv.second);
+        }
+        free_blocks.clear();
+    }
+};
+
+Context& ctx()
+{
+    static Context* c = new Context();  // never destroyed: safe at process exit
+    return *c;
+}
+
+// Host -> device copy of `rows` rows of `cols` floats into rows of stride
+// `ld` floats (pad columns zeroed), through the two pinned staging buffers.
+int upload_rows(Context& C, const float* src, long rows, int cols, int ld, float* dst, hipStream_t s)
+{
+    const size_t row_bytes = size_t(ld) * sizeof(float);
+    const long chunk = std::max<long>(1, long(kPinBytes / row_bytes));
+    if (row_bytes > kPinBytes) return fail(SKMETAL_ERANGE, "row of %d floats exceeds the staging buffer", ld);
+    int b = 0;
+    for (long r = 0; r < rows; r += chunk, b ^= 1) {
+        const long m = std::min(chunk, rows - r);
+        HIP_TRY(hipEventSynchronize(C.pin_ev[b]), "hipEventSynchronize(staging)");
+        float* p = static_cast<float*>(C.pin[b]);
+        if (ld == cols) {
+            std::memcpy(p, src + r * cols, size_t(m) * row_bytes);
+        } else {
+            for (long i = 0; i < m; ++i) {
+                std::memcpy(p + i * ld, src + (r + i) * cols, size_t(cols) * sizeof(float));
+                std::memset(p + i * ld + cols, 0, size_t(ld - cols) * sizeof(float));
+            }
+        }
+        HIP_TRY(hipMemcpyAsync(dst + r * ld, p, size_t(m) * row_bytes, hipMemcpyHostToDevice, s), "hipMemcpyAsync(H2D)");
+        HIP_TRY(hipEventRecord(C.pin_ev[b], s), "hipEventRecord");
+    }
+    return 0;
+}
+
+// Device -> host copy of `rows` rows (stride ld on the device) keeping `cols`.
+int download_rows(Context& C, const float* src, long rows, int cols, int ld, float* dst, hipStream_t s)
+{
+    const size_t row_bytes = size_t(ld) * sizeof(float);
+    const long chunk = std::max<long>(1, long(kPinBytes / row_bytes));
+    for (long r = 0; r < rows; r += chunk) {
+        const long m = std::min(chunk, rows - r);
+        float* p = static_cast<float*>(C.pin[0]);
+        HIP_TRY(hipEventSynchronize(C.pin_ev[0]), "hipEventSynchronize(staging)");
+        HIP_TRY(hipEventSynchronize(C.pin_ev[1]), "hipEventSynchronize(staging)");
+        HIP_TRY(hipMemcpyAsync(p, src + r * ld, size_t(m) * row_bytes, hipMemcpyDeviceToHost, s), "hipMemcpyAsync(D2H)");
+        HIP_TRY(hipStreamSynchronize(s), "hipStreamSynchronize");
+        if (ld == cols) {
+            std::memcpy(dst + r * cols, p, size_t(m) * row_bytes);
+        } else {
+            for (long i = 0; i < m; ++i) std::memcpy(dst + (r + i) * cols, p + i * ld, size_t(cols) * sizeof(float));
+        }
+    }
+    return 0;
+}
+
+// Plain byte copies through staging (labels and small arrays).
+int upload_bytes(Context& C, const void* src, size_t bytes, void* dst, hipStream_t s)
+{
+    const char* sp = static_cast<const char*>(src);
+    char* dp = static_cast<char*>(dst);
+    int b = 0;
+    for (size_t o = 0; o < bytes; o += kPinBytes, b ^= 1) {
+        const size_t m = std::min(kPinBytes, bytes - o);
+        HIP_TRY(hipEventSynchronize(C.pin_ev[b]), "hipEventSynchronize(staging)");
+        std::memcpy(C.pin[b], sp + o, m);
+        HIP_TRY(hipMemcpyAsync(dp + o, C.pin[b], m, hipMemcpyHostToDevice, s), "hipMemcpyAsync(H2D)");
+        HIP_TRY(hipEventRecord(C.pin_ev[b], s), "hipEventRecord");
+    }
+    return 0;
+}
+
+int download_bytes(Context& C, const void* src, size_t bytes, void* dst, hipStream_t s)
+{
+    const char* sp = static_cast<const char*>(src);
+    char* dp = static_cast<char*>(dst);
+    for (size_t o = 0; o < bytes; o += kPinBytes) {
+        const size_t m = std::min(kPinBytes, bytes - o);
+        HIP_TRY(hipEventSynchronize(C.pin_ev[0]), "hipEventSynchronize(staging)");
+        HIP_TRY(hipEventSynchronize(C.pin_ev[1]), "hipEventSynchronize(staging)");
+        HIP_TRY(hipMemcpyAsync(C.pin[0], sp + o, m, hipMemcpyDeviceToHost, s), "hipMemcpyAsync(D2H)");
+        HIP_TRY(hipStreamSynchronize(s), "hipStreamSynchronize");
+        std::memcpy(dp + o, C.pin[0], m);
+    }
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// One Lloyd problem resident on the device.
+// ---------------------------------------------------------------------------
+struct Lloyd {
+    Context* C = nullptr;
+    long n = 0;
+    int d = 0, k = 0, ld = 0;
+    hipStream_t s = nullptr;
+    float* X = nullptr;
+    float* cen[2] = {nullptr, nullptr};
+    float* cnorm = nullptr;
+    float* mean = nullptr;
+    int* labels = nullptr;
+    float* psum = nullptr;
+    int* pcnt = nullptr;
+    double* sums = nullptr;
+    int* counts = nullptr;
+    double* part = nullptr;
+    float* shift_sq = nullptr;
+    unsigned* cctr = nullptr;
+    double* rowpart = nullptr;
+    float* rowout = nullptr;
+    double* colpart = nullptr;
+    LoopState* st = nullptr;
+    UpdateGeom ug{};
+    int cur = 0;            // index of the current centres in cen[]
+    bool centred = false;
+    std::vector<float> h_mean;
+    std::vector<void*> owned;
+
+    int grab(void** p, size_t bytes)
+    {
+        TRY(C->alloc(p, bytes));
+        owned.push_back(*p);
+        return 0;
+    }
+
+    int create(Context* c, long n_, int d_, int k_)
+    {
+        C = c;
+        n = n_;
+        d = d_;
+        k = k_;
+        ld = (d + 3) & ~3;
+        s = C->stream;
+        ug = update_geometry(n, d, k, C->num_cu);
+        const size_t kl = size_t(k) * ld;
+        TRY(grab((void**)&X, size_t(n) * ld * sizeof(float)));
+        TRY(grab((void**)&cen[0], kl * sizeof(float)));
+        TRY(grab((void**)&cen[1], kl * sizeof(float)));
+        TRY(grab((void**)&cnorm, size_t(k) * sizeof(float)));
+        TRY(grab((void**)&mean, size_t(ld) * sizeof(float)));
+        TRY(grab((void**)&labels, size_t(n) * sizeof(int)));
+        TRY(grab((void**)&psum, size_t(ug.R) * kl * sizeof(float)));
+        TRY(grab((void**)&pcnt, size_t(ug.R) * k * sizeof(int)));
+        TRY(grab((void**)&sums, kl * sizeof(double)));
+        TRY(grab((void**)&counts, size_t(k) * sizeof(int)));
+        TRY(grab((void**)&part, size_t(k) * finalize_col_chunks(d) * 2 * sizeof(double)));
+        TRY(grab((void**)&shift_sq, size_t(k) * sizeof(float)));
+        TRY(grab((void**)&cctr, size_t(k) * sizeof(unsigned)));
+        TRY(grab((void**)&rowpart, size_t(rowdist_grid(n)) * sizeof(double)));
+        TRY(grab((void**)&colpart, size_t(colsum_grid(n)) * d * sizeof(double)));
+        TRY(grab((void**)&st, sizeof(LoopState)));
+        HIP_TRY(hipMemsetAsync(cen[0], 0, kl * sizeof(float), s), "hipMemsetAsync");
+        HIP_TRY(hipMemsetAsync(cen[1], 0, kl * sizeof(float), s), "hipMemsetAsync");
+        HIP_TRY(hipMemsetAsync(mean, 0, size_t(ld) * sizeof(float), s), "hipMemsetAsync");
+        HIP_TRY(hipMemsetAsync(cctr, 0, size_t(k) * sizeof(unsigned), s), "hipMemsetAsync");
+        HIP_TRY(hipMemsetAsync(st, 0, sizeof(LoopState), s), "hipMemsetAsync");
+        HIP_TRY(hipMemsetAsync(labels, 0, size_t(n) * sizeof(int), s), "hipMemsetAsync");
+        h_mean.assign(size_t(ld), 0.f);
+        return 0;
+    }
+
+    void destroy()
+    {
+        if (s) hipStreamSynchronize(s);
+        for (void* p : owned) C->release(p);
+        owned.clear();
+    }
+
+    int load_X(const float* host, bool center)
+    {
+        TRY(upload_rows(*C, host, n, d, ld, X, s));
+        centred = center;
+        if (center) {
+            const int nb = colsum_grid(n);
+            HIP_TRY(launch_colsum(X, n, ld, d, colpart, nb, s), "colsum launch");
+            HIP_TRY(launch_colmean(colpart, nb, n, d, mean, s), "colmean launch");
+            HIP_TRY(launch_center(X, n, ld, d, mean, s), "center launch");
+            TRY(download_bytes(*C, mean, size_t(d) * sizeof(float), h_mean.data(), s));
+        } else {
+            std::fill(h_mean.begin(), h_mean.end(), 0.f);
+            HIP_TRY(hipMemsetAsync(mean, 0, size_t(ld) * sizeof(float), s), "hipMemsetAsync");
+        }
+        return 0;
+    }
+
+    // Centres given in caller coordinates -> device (centred like X).
+    int set_centers(const float* host)
+    {
+        TRY(upload_rows(*C, host, k, d, ld, cen[cur], s));
+        if (centred) HIP_TRY(launch_center(cen[cur], k, ld, d, mean, s), "center launch");
+        HIP_TRY(launch_cnorm(cen[cur], k, ld, cnorm, s), "cnorm launch");
+        return 0;
+    }
+
+    int get_centers(float* host)
+    {
+        TRY(download_rows(*C, cen[cur], k, d, ld, host, s));
+        if (centred)
+            for (int j = 0; j < k; ++j)
+                for (int c = 0; c < d; ++c) host[size_t(j) * d + c] = host[size_t(j) * d + c] + h_mean[c];
+        return 0;
+    }
+
+    int get_labels(int32_t* host) { return download_bytes(*C, labels, size_t(n) * sizeof(int), host, s); }
+
+    int read_state(LoopState* h)
+    {
+        HIP_TRY(hipMemcpyAsync(h, st, sizeof(LoopState), hipMemcpyDeviceToHost, s), "hipMemcpyAsync(state)");
+        HIP_TRY(hipStreamSynchronize(s), "hipStreamSynchronize");
+        return 0;
+    }
+
+    int write_state(const LoopState& h)
+    {
+        HIP_TRY(hipMemcpyAsync(st, &h, sizeof(LoopState), hipMemcpyHostToDevice, s), "hipMemcpyAsync(state)");
+        HIP_TRY(hipStreamSynchronize(s), "hipStreamSynchronize");
+        return 0;
+    }
+
+    int assign(const float* cents, LoopState* state, int count_changes)
+    {
+        AssignArgs a{X, n, ld, cents, cnorm, k, labels, state, count_changes};
+        HIP_TRY(launch_assign(a, C->num_cu, s), "assign launch");
+        return 0;
+    }
+
+    int update()
+    {
+        UpdateArgs u{X, n, ld, d, labels, k, psum, pcnt, st};
+        HIP_TRY(launch_update(u, ug, s), "update launch");
+        return 0;
+    }
+
+    // One Lloyd step, old centres cen[cur] -> new centres cen[cur ^ 1].
+    int enqueue_step(int iter, double tol, int flags)
+    {
+        TRY(assign(cen[cur], st, 1));
+        TRY(update());
+        FinalizeArgs f{psum, pcnt, ug.R, k, d, ld, cen[cur], cen[cur ^ 1], cnorm, sums, counts, part, shift_sq,
+                       cctr, st, iter, tol, flags};
+        HIP_TRY(launch_finalize(f, s), "finalize launch");
+        cur ^= 1;
+        return 0;
+    }
+
+    // Empty clusters at step t (old centres in cen[old]): sklearn's relocation
+    // (_k_means_common.pyx:167-211), averaging (:274-295) and shift on the host
+    // from the device's fp64 sums, then upload the new centres to cen[old^1].
+    int host_relocate(int t, int old, double tol, int flags, LoopState& hs)
+    {
+        const size_t kl = size_t(k) * ld;
+        std::vector<double> S(kl);
+        std::vector<int> cnt(static_cast<size_t>(k));
+        std::vector<int> lab(static_cast<size_t>(n));
+        std::vector<float> Cold(kl);
+        TRY(download_bytes(*C, sums, kl * sizeof(double), S.data(), s));
+        TRY(download_bytes(*C, counts, size_t(k) * sizeof(int), cnt.data(), s));
+        TRY(download_bytes(*C, labels, size_t(n) * sizeof(int), lab.data(), s));
+        TRY(download_bytes(*C, cen[old], kl * sizeof(float), Cold.data(), s));
+
+        std::vector<int> empties;
+        for (int j = 0; j < k; ++j)
+            if (cnt[size_t(j)] == 0) empties.push_back(j);
+        if (!empties.empty()) {
+            // distances of every row to its (old) centre, fp32 direct form
+            if (rowout == nullptr) TRY(grab((void**)&rowout, size_t(n) * sizeof(float)));
+            RowDistArgs r{X, n, ld, d, cen[old], k, labels, rowout, rowpart, st};
+            HIP_TRY(launch_rowdist(r, s), "rowdist launch");
+            std::vector<float> dist(static_cast<size_t>(n));
+            TRY(download_bytes(*C, rowout, size_t(n) * sizeof(float), dist.data(), s));
+            float dmax = 0.f;
+            for (float v : dist) dmax = std::max(dmax, v);
+            if (dmax > 0.f) {
+                const size_t ne = empties.size();
+                std::vector<long> idx(static_cast<size_t>(n));
+                std::iota(idx.begin(), idx.end(), 0L);
+                std::partial_sort(idx.begin(), idx.begin() + ne, idx.end(), [&](long a, long b) {
+                    return dist[size_t(a)] > dist[size_t(b)] || (dist[size_t(a)] == dist[size_t(b)] && a < b);
+                });
+                std::vector<float> xr(static_cast<size_t>(ld));
+                for (size_t e = 0; e < ne; ++e) {
+                    const int j = empties[e];
+                    const long far = idx[e];
+                    const int o = lab[size_t(far)];
+                    TRY(download_bytes(*C, X + far * ld, size_t(ld) * sizeof(float), xr.data(), s));
+                    for (int c = 0; c < d; ++c) {
+                        S[size_t(o) * ld + c] -= (double)xr[size_t(c)];
+                        S[size_t(j) * ld + c] = (double)xr[size_t(c)];
+                    }
+                    cnt[size_t(j)] = 1;
+                    cnt[size_t(o)] -= 1;
+                }
+            }
+        }
+        // _average_centers: heaviest cluster first, then rows in order
+        int amax = 0;
+        for (int j = 1; j < k; ++j)
+            if (cnt[size_t(j)] > cnt[size_t(amax)]) amax = j;
+        std::vector<double> cur_rows(S);
+        for (int j = 0; j < k; ++j) {
+            for (int c = 0; c < d; ++c) {
+                double& v = cur_rows[size_t(j) * ld + c];
+                if (cnt[size_t(j)] > 0)
+                    v = v / (double)cnt[size_t(j)];
+                else
+                    v = cur_rows[size_t(amax) * ld + c];
+            }
+        }
+        std::vector<float> Cn(kl, 0.f), cn(static_cast<size_t>(k));
+        double shift_tot = 0.0;
+        for (int j = 0; j < k; ++j) {
+            double sq = 0.0, nr = 0.0;
+            for (int c = 0; c < d; ++c) {
+                const float v = (float)cur_rows[size_t(j) * ld + c];
+                Cn[size_t(j) * ld + c] = v;
+                const double df = (double)v - (double)Cold[size_t(j) * ld + c];
+                sq += df * df;
+                nr += (double)v * (double)v;
+            }
+            shift_tot += (double)(float)sq;
+            cn[size_t(j)] = (float)nr;
+        }
+        TRY(upload_bytes(*C, Cn.data(), kl * sizeof(float), cen[old ^ 1], s));
+        TRY(upload_bytes(*C, cn.data(), size_t(k) * sizeof(float), cnorm, s));
+        int done = 0;
+        if ((flags & kStopStrict) && hs.last_changed == 0)
+            done = 1;
+        else if (tol > 0.0 && shift_tot <= tol)
+            done = 2;
+        hs.done = done;
+        hs.n_iter = t + 1;
+        hs.changed = 0;
+        hs.global_ctr = 0;
+        hs.shift_tot = shift_tot;
+        hs.halt_iter = t;
+        TRY(write_state(hs));
+        cur = old ^ 1;
+        return 0;
+    }
+
+    // Lloyd loop from the current centres.  With fixed != 0 exactly max_iter
+    // steps run (no convergence stop); otherwise sklearn's rules apply.
+    int run_loop(long max_iter, double tol, int flags, bool fixed, int* n_iter_out, int* done_out)
+    {
+        if (fixed) {
+            flags &= ~kStopStrict;
+            tol = 0.0;
+        }
+        LoopState hs{};
+        TRY(write_state(hs));
+        HIP_TRY(hipMemsetAsync(labels, 0xff, size_t(n) * sizeof(int), s), "hipMemsetAsync(labels)");
+        long it = 0;
+        long batch = fixed ? max_iter : 4;
+        int final_done = 0;
+        while (it < max_iter) {
+            const long nb = std::min(batch, max_iter - it);
+            const int c0 = cur;
+            for (long t = it; t < it + nb; ++t) TRY(enqueue_step((int)t, tol, flags));
+            TRY(read_state(&hs));
+            if (hs.done == 3) {
+                const int t = hs.halt_iter;
+                const int old = (c0 + (t - (int)it)) & 1;
+                TRY(host_relocate(t, old, tol, flags, hs));
+                it = t + 1;
+                if (hs.done != 0) {
+                    final_done = hs.done;
+                    break;
+                }
+                continue;
+            }
+            if (hs.done != 0) {
+                cur = (c0 + (hs.halt_iter - (int)it) + 1) & 1;
+                final_done = hs.done;
+                break;
+            }
+            it += nb;
+            if (!fixed) batch = std::min<long>(batch * 2, 64);
+        }
+        if (n_iter_out) *n_iter_out = max_iter > 0 ? hs.n_iter : 0;
+        if (done_out) *done_out = final_done;
+        return 0;
+    }
+
+    int inertia(double* out)
+    {
+        RowDistArgs r{X, n, ld, d, cen[cur], k, labels, nullptr, rowpart, st};
+        HIP_TRY(launch_rowdist(r, s), "rowdist launch");
+        LoopState hs{};
+        TRY(read_state(&hs));
+        *out = hs.inertia;
+        return 0;
+    }
+
+    // Full sklearn fit from the current centres: loop, final E-step, inertia.
+    int fit(long max_iter, double tol, int flags, int* n_iter_out, double* inertia_out)
+    {
+        int n_iter = 0, done = 0;
+        TRY(run_loop(max_iter, tol, flags, false, &n_iter, &done));
+        if (done != 1) TRY(assign(cen[cur], nullptr, 0));  // final E-step (_kmeans.py:736-748)
+        double in = 0.0;
+        TRY(inertia(&in));
+        if (n_iter_out) *n_iter_out = n_iter;
+        if (inertia_out) *inertia_out = in;
+        return 0;
+    }
+};
+
+int check_sizes(size_t n, size_t d, size_t k)
+{
+    if (n == 0 || d == 0 || k == 0) return fail(SKMETAL_EINVAL, "n, d and k must be positive (n=%zu d=%zu k=%zu)", n, d, k);
+    if (d > kMaxDim / 4 || k > kMaxDim) return fail(SKMETAL_ERANGE, "d=%zu or k=%zu exceeds the supported range", d, k);
+    if (n > (size_t(1) << 40)) return fail(SKMETAL_ERANGE, "n=%zu exceeds the supported range", n);
+    return 0;
+}
+
+struct Guard {
+    std::lock_guard<std::recursive_mutex> lk;
+    explicit Guard(Context& c) : lk(c.mu) { g_err.clear(); }
+};
+
+// RAII holder for per-call problems built on the shared context.
+struct Scoped {
+    Lloyd L;
+    ~Scoped() { L.destroy(); }
+};
+
+}  // namespace
+
+struct skmetal_hip_lloyd {
+    Lloyd L;
+};
+
+extern "C" {
+
+const char* skmetal_hip_last_error(void) { return g_err.c_str(); }
+
+int skmetal_init(void)
+{
+    Context& c = ctx();
+    Guard g(c);
+    return c.init();
+}
+
+int skmetal_warmup(void)
+{
+    Context& c = ctx();
+    Guard g(c);
+    TRY(c.init());
+    const long n = 300;
+    const int d = 6, k = 5;
+    std::vector<float> X(static_cast<size_t>(n) * d), C0(static_cast<size_t>(k) * d);
+    for (long i = 0; i < n; ++i)
+        for (int f = 0; f < d; ++f) X[size_t(i) * d + f] = float((i * 7 + f * 3) % 11) + 0.25f * float(i % k);
+    for (int j = 0; j < k; ++j)
+        for (int f = 0; f < d; ++f) C0[size_t(j) * d + f] = X[size_t(j * 3) * d + f];
+    Scoped sc;
+    TRY(sc.L.create(&c, n, d, k));
+    TRY(sc.L.load_X(X.data(), true));
+    TRY(sc.L.set_centers(C0.data()));
+    int it = 0;
+    double in = 0.0;
+    TRY(sc.L.fit(3, 0.0, kStopStrict, &it, &in));
+    HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+    return 0;
+}
+
+int skmetal_device_info(char* name, int name_capacity, size_t* max_threads, uint8_t* has_unified_memory,
+                        uint64_t* recommended_working_set_size)
+{
+    Context& c = ctx();
+    Guard g(c);
+    TRY(c.init());
+    if (name != nullptr && name_capacity > 0) {
+        const size_t m = std::min(c.name.size(), size_t(name_capacity - 1));
+        std::memcpy(name, c.name.data(), m);
+        name[m] = 0;
+    }
+    if (max_threads) *max_threads = size_t(c.max_threads);
+    if (has_unified_memory) *has_unified_memory = 0;
+    if (recommended_working_set_size) *recommended_working_set_size = uint64_t(c.total_mem);
+    return 0;
+}
+
+int skmetal_hip_release_cache(void)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (c.ready) {
+        hipStreamSynchronize(c.stream);
+        c.release_cache();
+    }
+    return 0;
+}
+
+int skmetal_kmeans_assign(const void* X, const void* centroids, void* assignments, size_t n, size_t d, size_t k)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!X || !centroids || !assignments) return fail(SKMETAL_EINVAL, "null pointer argument");
+    TRY(check_sizes(n, d, k));
+    TRY(c.init());
+    Scoped sc;
+    Lloyd& L = sc.L;
+    TRY(L.create(&c, (long)n, (int)d, (int)k));
+    TRY(L.load_X(static_cast<const float*>(X), false));
+    TRY(L.set_centers(static_cast<const float*>(centroids)));
+    TRY(L.assign(L.cen[L.cur], nullptr, 0));
+    TRY(L.get_labels(static_cast<int32_t*>(assignments)));
+    return 0;
+}
+
+int skmetal_hip_kmeans_fit(const float* X, float* centroids, int32_t* labels, size_t n, size_t d, size_t k,
+                           size_t max_iter, double tol, int flags, int32_t* n_iter_out, double* inertia_out)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!X || !centroids || !labels) return fail(SKMETAL_EINVAL, "null pointer argument");
+    TRY(check_sizes(n, d, k));
+    if (k > n) return fail(SKMETAL_EINVAL, "n_samples=%zu should be >= n_clusters=%zu", n, k);
+    if (!(tol >= 0.0)) return fail(SKMETAL_EINVAL, "tol must be >= 0");
+    if (max_iter > (size_t(1) << 30)) return fail(SKMETAL_ERANGE, "max_iter too large");
+    TRY(c.init());
+    Scoped sc;
+    Lloyd& L = sc.L;
+    TRY(L.create(&c, (long)n, (int)d, (int)k));
+    TRY(L.load_X(X, true));
+    TRY(L.set_centers(centroids));
+    int it = 0;
+    double in = 0.0;
+    TRY(L.fit((long)max_iter, tol, flags & SKMETAL_FIT_STRICT ? kStopStrict : 0, &it, &in));
+    TRY(L.get_labels(labels));
+    TRY(L.get_centers(centroids));
+    if (n_iter_out) *n_iter_out = it;
+    if (inertia_out) *inertia_out = in;
+    return 0;
+}
+
+int skmetal_kmeans_batch_fused(const void* X, void* centroids, void* assignments, size_t n, size_t d, size_t k,
+                               size_t num_groups, size_t max_iter, float tol, int32_t* n_iter_out)
+{
+    (void)num_groups;
+    int32_t it = 0;
+    const int rc = skmetal_hip_kmeans_fit(static_cast<const float*>(X), static_cast<float*>(centroids),
+                                          static_cast<int32_t*>(assignments), n, d, k, max_iter, (double)tol,
+                                          SKMETAL_FIT_STRICT, &it, nullptr);
+    if (rc == 0 && n_iter_out) *n_iter_out = it;
+    return rc;
+}
+
+static int rowdist_call(const void* X, const void* centroids, const void* assignments, void* dists, size_t n,
+                        size_t d, size_t k, double* total)
+{
+    Context& c = ctx();
+    if (!X || !centroids || !assignments) return fail(SKMETAL_EINVAL, "null pointer argument");
+    TRY(check_sizes(n, d, k));
+    TRY(c.init());
+    // labels are indices into the centroid rows: reject out-of-range values
+    const int32_t* lab = static_cast<const int32_t*>(assignments);
+    for (size_t i = 0; i < n; ++i)
+        if (lab[i] < 0 || size_t(lab[i]) >= k) return fail(SKMETAL_EINVAL, "assignments[%zu]=%d not in [0, %zu)", i, lab[i], k);
+    Scoped sc;
+    Lloyd& L = sc.L;
+    TRY(L.create(&c, (long)n, (int)d, (int)k));
+    TRY(L.load_X(static_cast<const float*>(X), false));
+    TRY(L.set_centers(static_cast<const float*>(centroids)));
+    TRY(upload_bytes(c, assignments, n * sizeof(int32_t), L.labels, L.s));
+    if (dists != nullptr) TRY(L.grab((void**)&L.rowout, n * sizeof(float)));
+    RowDistArgs r{L.X, L.n, L.ld, L.d, L.cen[L.cur], L.k, L.labels, dists ? L.rowout : nullptr, L.rowpart, L.st};
+    HIP_TRY(launch_rowdist(r, L.s), "rowdist launch");
+    LoopState hs{};
+    TRY(L.read_state(&hs));
+    if (total) *total = hs.inertia;
+    if (dists != nullptr) TRY(download_bytes(c, L.rowout, n * sizeof(float), dists, L.s));
+    return 0;
+}
+
+int skmetal_compute_mindists(const void* X, const void* centroids, const void* assignments, void* dists, size_t n,
+                             size_t d, size_t k)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!dists) return fail(SKMETAL_EINVAL, "null pointer argument");
+    return rowdist_call(X, centroids, assignments, dists, n, d, k, nullptr);
+}
+
+float skmetal_kmeans_inertia(const void* X, const void* centroids, const void* assignments, size_t n, size_t d,
+                             size_t k)
+{
+    Context& c = ctx();
+    Guard g(c);
+    double total = 0.0;
+    if (rowdist_call(X, centroids, assignments, nullptr, n, d, k, &total) != 0) return -1.0f;
+    return (float)total;
+}
+
+// ---- device-resident handle ----
+
+int skmetal_hip_lloyd_create(size_t n, size_t d, size_t k, skmetal_hip_lloyd** out)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!out) return fail(SKMETAL_EINVAL, "null pointer argument");
+    *out = nullptr;
+    TRY(check_sizes(n, d, k));
+    if (k > n) return fail(SKMETAL_EINVAL, "n_samples=%zu should be >= n_clusters=%zu", n, k);
+    TRY(c.init());
+    auto* h = new skmetal_hip_lloyd();
+    const int rc = h->L.create(&c, (long)n, (int)d, (int)k);
+    if (rc != 0) {
+        h->L.destroy();
+        delete h;
+        return rc;
+    }
+    *out = h;
+    return 0;
+}
+
+int skmetal_hip_lloyd_destroy(skmetal_hip_lloyd* h)
+{
+    if (!h) return 0;
+    Context& c = ctx();
+    Guard g(c);
+    h->L.destroy();
+    delete h;
+    return 0;
+}
+
+int skmetal_hip_lloyd_load(skmetal_hip_lloyd* h, const float* X, int center)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!h || !X) return fail(SKMETAL_EINVAL, "null pointer argument");
+    TRY(h->L.load_X(X, center != 0));
+    HIP_TRY(hipStreamSynchronize(h->L.s), "hipStreamSynchronize");
+    return 0;
+}
+
+int skmetal_hip_lloyd_set_centers(skmetal_hip_lloyd* h, const float* C)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!h || !C) return fail(SKMETAL_EINVAL, "null pointer argument");
+    TRY(h->L.set_centers(C));
+    HIP_TRY(hipStreamSynchronize(h->L.s), "hipStreamSynchronize");
+    return 0;
+}
+
+int skmetal_hip_lloyd_iterate(skmetal_hip_lloyd* h, size_t iters, float* ms_out)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!h) return fail(SKMETAL_EINVAL, "null pointer argument");
+    Lloyd& L = h->L;
+    hipEvent_t e0, e1;
+    HIP_TRY(hipEventCreate(&e0), "hipEventCreate");
+    HIP_TRY(hipEventCreate(&e1), "hipEventCreate");
+    int rc = 0;
+    // the loop resets the device state and labels before the timed region
+    LoopState hs{};
+    rc = L.write_state(hs);
+    if (rc == 0) {
+        hipEventRecord(e0, L.s);
+        int n_iter = 0, done = 0;
+        rc = L.run_loop((long)iters, 0.0, 0, true, &n_iter, &done);
+        hipEventRecord(e1, L.s);
+        hipError_t e = hipEventSynchronize(e1);
+        if (e != hipSuccess) rc = hip_fail(e, "hipEventSynchronize");
+        if (rc == 0 && ms_out) hipEventElapsedTime(ms_out, e0, e1);
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    return rc;
+}
+
+int skmetal_hip_lloyd_run(skmetal_hip_lloyd* h, size_t max_iter, double tol, int flags, int32_t* n_iter_out,
+                          double* inertia_out)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!h) return fail(SKMETAL_EINVAL, "null pointer argument");
+    int it = 0;
+    double in = 0.0;
+    TRY(h->L.fit((long)max_iter, tol, flags & SKMETAL_FIT_STRICT ? kStopStrict : 0, &it, &in));
+    if (n_iter_out) *n_iter_out = it;
+    if (inertia_out) *inertia_out = in;
+    return 0;
+}
+
+int skmetal_hip_lloyd_time_kernels(skmetal_hip_lloyd* h, size_t reps, float* ms_assign, float* ms_update)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!h || reps == 0) return fail(SKMETAL_EINVAL, "bad argument");
+    Lloyd& L = h->L;
+    LoopState hs{};
+    TRY(L.write_state(hs));
+    hipEvent_t e0, e1, e2;
+    HIP_TRY(hipEventCreate(&e0), "hipEventCreate");
+    HIP_TRY(hipEventCreate(&e1), "hipEventCreate");
+    HIP_TRY(hipEventCreate(&e2), "hipEventCreate");
+    int rc = 0;
+    TRY(L.assign(L.cen[L.cur], nullptr, 0));  // labels for the update timing
+    hipEventRecord(e0, L.s);
+    for (size_t r = 0; r < reps && rc == 0; ++r) rc = L.assign(L.cen[L.cur], nullptr, 0);
+    hipEventRecord(e1, L.s);
+    for (size_t r = 0; r < reps && rc == 0; ++r) rc = L.update();
+    hipEventRecord(e2, L.s);
+    hipError_t e = hipEventSynchronize(e2);
+    if (rc == 0 && e != hipSuccess) rc = hip_fail(e, "hipEventSynchronize");
+    float t01 = 0.f, t12 = 0.f;
+    hipEventElapsedTime(&t01, e0, e1);
+    hipEventElapsedTime(&t12, e1, e2);
+    if (ms_assign) *ms_assign = t01 / float(reps);
+    if (ms_update) *ms_update = t12 / float(reps);
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    hipEventDestroy(e2);
+    return rc;
+}
+
+int skmetal_hip_lloyd_get_centers(skmetal_hip_lloyd* h, float* C)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!h || !C) return fail(SKMETAL_EINVAL, "null pointer argument");
+    return h->L.get_centers(C);
+}
+
+int skmetal_hip_lloyd_get_labels(skmetal_hip_lloyd* h, int32_t* labels)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!h || !labels) return fail(SKMETAL_EINVAL, "null pointer argument");
+    return h->L.get_labels(labels);
+}
+
+int skmetal_hip_lloyd_inertia(skmetal_hip_lloyd* h, double* out)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!h || !out) return fail(SKMETAL_EINVAL, "null pointer argument");
+    return h->L.inertia(out);
+}
+
+}  // extern "C"

@@ -1,0 +1,177 @@
+"""KMeans on the MI355X: the Lloyd loop runs in libskmetal_hip.so.
+
+``HipKMeans`` takes the place of skmetal's ``MetalKMeans``
+(skmetal/estimators/cluster.py:18-146) and of ``MetalKMeansMLX``
+(skmetal/estimators/_mlx_kmeans.py:35-156) as the registered ``KMeans``
+implementation.  It follows scikit-learn's ``KMeans.fit``
+(sklearn/cluster/_kmeans.py:1427-1554) with ``algorithm="lloyd"``:
+
+* ``init`` may be an array (used as given, ``n_init`` forced to 1),
+  ``"k-means++"``, ``"random"`` or a callable, drawn from the estimator's
+  ``random_state`` in the same order scikit-learn draws them;
+* ``tol`` is scaled by the mean feature variance (``_tolerance``,
+  _kmeans.py:279-287) and the loop stops on strict label convergence;
+* for ``n_init > 1`` the run with the lowest inertia that is not the same
+  clustering as the best so far is kept (_kmeans.py:1516-1527).
+
+Estimator attributes set after ``fit``: ``cluster_centers_``, ``labels_``
+(int32), ``inertia_``, ``n_iter_``, ``n_features_in_``.
+"""
+
+from __future__ import annotations
+
+import warnings
+
+import numpy as np
+from sklearn.cluster import kmeans_plusplus
+from sklearn.exceptions import ConvergenceWarning
+from sklearn.utils.validation import check_array, check_random_state
+
+from .. import _bridge
+from .._config import get_config
+from ._base import BaseGPUEstimator
+
+
+def _tolerance(X: np.ndarray, tol: float) -> float:
+    """sklearn/cluster/_kmeans.py:279-287 for dense X."""
+    if tol == 0:
+        return 0.0
+    return float(np.mean(np.var(X, axis=0)) * tol)
+
+
+def _same_clustering(a: np.ndarray, b: np.ndarray, k: int) -> bool:
+    """True when two labelings are equal up to a permutation of cluster ids."""
+    mapping = np.full(k, -1, dtype=np.int64)
+    for i in range(a.shape[0]):
+        if mapping[a[i]] == -1:
+            mapping[a[i]] = b[i]
+        elif mapping[a[i]] != b[i]:
+            return False
+    return True
+
+
+class HipKMeans(BaseGPUEstimator):
+    """GPU KMeans (Lloyd) with X resident in MI355X HBM."""
+
+    def _resolve_n_init(self, init) -> int:
+        est = self._estimator
+        n_init = est.n_init
+        if n_init in ("auto", "warn"):
+            if isinstance(init, str) and init == "k-means++":
+                n_init = 1
+            elif isinstance(init, str) and init == "random":
+                n_init = 10
+            elif callable(init):
+                n_init = 10
+            else:
+                n_init = 1
+        if not isinstance(init, str) and not callable(init) and n_init != 1:
+            warnings.warn(
+                "Explicit initial center position passed: performing only one init in "
+                f"{type(est).__name__} instead of n_init={n_init}.",
+                RuntimeWarning,
+                stacklevel=3,
+            )
+            n_init = 1
+        return int(n_init)
+
+    def _initial_centers(self, X, init, k, random_state):
+        """sklearn/cluster/_kmeans.py:958-1029 (_init_centroids), unit weights."""
+        n = X.shape[0]
+        if isinstance(init, str) and init == "k-means++":
+            centers, _ = kmeans_plusplus(X, k, random_state=random_state)
+        elif isinstance(init, str) and init == "random":
+            seeds = random_state.choice(n, size=k, replace=False, p=np.full(n, 1.0 / n))
+            centers = X[seeds]
+        elif callable(init):
+            centers = init(X, k, random_state=random_state)
+        else:
+            centers = init
+        centers = check_array(centers, dtype=np.float32, order="C", copy=True)
+        if centers.shape != (k, X.shape[1]):
+            raise ValueError(
+                f"The shape of the initial centers {centers.shape} does not match "
+                f"the number of clusters {k} and features {X.shape[1]}."
+            )
+        return np.ascontiguousarray(centers, dtype=np.float32)
+
+    def fit(self, X, y=None, sample_weight=None):
+        X, _ = self._validate_data(X)
+        if sample_weight is not None:
+            if get_config().verbose:
+                print("[skmetal_amd] HipKMeans: device=cpu (sample_weight is not supported on the GPU path)")
+            return self._fallback_fit(X, y, sample_weight=sample_weight)
+        if not self._should_use_gpu(X):
+            return self._fallback_fit(X, y)
+
+        est = self._estimator
+        n, d = X.shape
+        k = int(est.n_clusters)
+        if n < k:
+            raise ValueError(f"n_samples={n} should be >= n_clusters={k}.")
+        init = est.init
+        n_init = self._resolve_n_init(init)
+        tol_abs = _tolerance(X, est.tol)
+        random_state = check_random_state(est.random_state)
+
+        best = None
+        for _ in range(n_init):
+            centers = self._initial_centers(X, init, k, random_state)
+            labels = np.empty(n, dtype=np.int32)
+            n_iter, inertia = _bridge.kmeans_fit(X, centers, labels, est.max_iter, tol_abs, strict=True)
+            if best is None or (inertia < best[2] and not _same_clustering(labels, best[1], k)):
+                best = (centers, labels, inertia, n_iter)
+
+        centers, labels, inertia, n_iter = best
+        if len(np.unique(labels)) < k:
+            warnings.warn(
+                f"Number of distinct clusters ({len(np.unique(labels))}) found smaller than "
+                f"n_clusters ({k}). Possibly due to duplicate points in X.",
+                ConvergenceWarning,
+                stacklevel=2,
+            )
+        est.cluster_centers_ = centers
+        est.labels_ = labels
+        est.inertia_ = float(inertia)
+        est.n_iter_ = int(n_iter)
+        est.n_features_in_ = d
+        est._n_features_out = k
+        est._n_threads = 1
+        self._fitted = True
+        return self
+
+    def _gpu_ready(self, X) -> bool:
+        return self._fitted and self._should_use_gpu(X) and hasattr(self._estimator, "cluster_centers_")
+
+    def predict(self, X):
+        X, _ = self._validate_data(X)
+        if not self._gpu_ready(X):
+            return self._fallback_predict(X)
+        n, d = X.shape
+        C = np.ascontiguousarray(self._estimator.cluster_centers_, dtype=np.float32)
+        out = np.empty(n, dtype=np.int32)
+        _bridge.kmeans_assign(X, C, out, n, d, C.shape[0])
+        return out
+
+    def fit_predict(self, X, y=None, sample_weight=None):
+        return self.fit(X, y, sample_weight=sample_weight)._estimator.labels_
+
+    def fit_transform(self, X, y=None, sample_weight=None):
+        return self.fit(X, y, sample_weight=sample_weight).transform(X)
+
+    def score(self, X, y=None, sample_weight=None):
+        X, _ = self._validate_data(X)
+        if sample_weight is not None or not self._gpu_ready(X):
+            return self._estimator.score(X, y, sample_weight=sample_weight)
+        n, d = X.shape
+        C = np.ascontiguousarray(self._estimator.cluster_centers_, dtype=np.float32)
+        lab = np.empty(n, dtype=np.int32)
+        _bridge.kmeans_assign(X, C, lab, n, d, C.shape[0])
+        v = _bridge.kmeans_inertia(X, C, lab, n, d, C.shape[0])
+        if v < 0:
+            raise RuntimeError(f"skmetal_kmeans_inertia failed: {_bridge.last_error()}")
+        return -float(v)
+
+
+# name kept for code written against skmetal
+MetalKMeans = HipKMeans

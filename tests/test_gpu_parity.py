@@ -1,0 +1,232 @@
+"""GPU parity: libskmetal_hip.so (through its C ABI) against the oracle.
+
+Every test here runs the HIP kernels on an MI355X and checks them with the
+rules of oracle/parity.py:
+  labels  -- equal except near-ties (gap < 1e-5 ||x||^2),
+  centres -- row-relative error <= 1e-4,
+  inertia -- relative error <= 1e-5 against an fp64 recomputation.
+"""
+
+from __future__ import annotations
+
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle import parity
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+@pytest.fixture(scope="module")
+def bridge():
+    from skmetal_amd import _bridge
+
+    if not _bridge.HIP_AVAILABLE:
+        pytest.fail(f"GPU path unavailable on a GPU run: {_bridge.last_error()}")
+    return _bridge
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def test_native_library_is_the_in_tree_build(bridge):
+    path = Path(bridge.library_path())
+    assert path.name == "libskmetal_hip.so"
+    assert path.parent == Path(bridge.__file__).resolve().parent
+    info = bridge.device_info()
+    assert info["has_unified_memory"] is False
+    assert info["recommended_working_set_size_bytes"] > 100 * 2**30
+
+
+def test_known_answer_assign(bridge):
+    # skmetal tests/test_kernels.py:93-99
+    X = np.array([[0.0, 0.0], [1.0, 1.0], [10.0, 10.0], [9.0, 9.0]], dtype=np.float32)
+    centroids = np.array([[0.0, 0.0], [10.0, 10.0]], dtype=np.float32)
+    assignments = np.empty(4, dtype=np.int32)
+    bridge.kmeans_assign(X, centroids, assignments, 4, 2, 2)
+    np.testing.assert_array_equal(assignments, [0, 0, 1, 1])
+
+
+ASSIGN_SHAPES = [
+    (1, 1, 1), (2, 3, 2), (63, 7, 5), (64, 4, 4), (65, 33, 9), (257, 2, 64), (1000, 32, 8),
+    (3001, 100, 50), (2048, 16, 65), (999, 20, 200), (4096, 129, 17), (1500, 300, 70),
+    (700, 5, 1024), (513, 768, 96),
+]
+
+
+@pytest.mark.parametrize("n,d,k", ASSIGN_SHAPES)
+def test_assign_vs_oracle(bridge, n, d, k):
+    _say(f"assign n={n} d={d} k={k}")
+    rng = np.random.default_rng(n * 131 + d * 7 + k)
+    X = (rng.standard_normal((n, d)) * 3).astype(np.float32)
+    C = (rng.standard_normal((k, d)) * 3).astype(np.float32)
+    out = np.full(n, -7, dtype=np.int32)
+    bridge.kmeans_assign(X, C, out, n, d, k)
+    ref, best, second = oracle.assign(X, C, return_gap=True)
+    assert out.min() >= 0 and out.max() < k
+    parity.check_labels(out, ref, best, second, X, what=f"assign {n}x{d} k={k}")
+
+
+def test_assign_one_hot_layout(bridge):
+    """Each row equals one centre exactly: checks the MFMA lane/register layout."""
+    k, d = 64, 64
+    C = np.eye(k, d, dtype=np.float32) * 10
+    rng = np.random.default_rng(0)
+    truth = rng.integers(0, k, 4096).astype(np.int32)
+    X = C[truth].copy()
+    out = np.empty(4096, np.int32)
+    bridge.kmeans_assign(X, C, out, 4096, d, k)
+    np.testing.assert_array_equal(out, truth)
+
+
+def test_assign_duplicate_centres_lowest_index(bridge):
+    rng = np.random.default_rng(1)
+    X = rng.standard_normal((3000, 12)).astype(np.float32)
+    base = rng.standard_normal((7, 12)).astype(np.float32)
+    C = np.concatenate([base, base, base])
+    out = np.empty(3000, np.int32)
+    bridge.kmeans_assign(X, C, out, 3000, 12, 21)
+    ref = oracle.assign(X, C)
+    np.testing.assert_array_equal(out, ref)
+    assert out.max() < 7
+
+
+def test_mindists_and_inertia_vs_oracle(bridge):
+    rng = np.random.default_rng(2)
+    n, d, k = 5000, 37, 13
+    X = (rng.standard_normal((n, d)) * 2).astype(np.float32)
+    C = rng.standard_normal((k, d)).astype(np.float32)
+    lab = rng.integers(0, k, n).astype(np.int32)
+    dists = np.empty(n, np.float32)
+    bridge.compute_mindists(X, C, lab, dists, n, d, k)
+    ref = oracle.mindists(X, C, lab)
+    np.testing.assert_allclose(dists, ref, rtol=2e-6, atol=1e-5)
+    v = bridge.kmeans_inertia(X, C, lab, n, d, k)
+    parity.check_inertia(v, oracle.inertia(X, C, lab), what="kmeans_inertia")
+
+
+def _lockstep_gpu(bridge, X, C0, steps, what):
+    """Run `steps` single GPU steps from C0, checking each against the oracle."""
+    n, d = X.shape
+    k = C0.shape[0]
+    mean = X.mean(axis=0)
+    Xc = X - mean
+    prev = C0
+    n_mism = 0
+    with bridge.LloydHandle(n, d, k) as h:
+        h.load(X, center=True)
+        for m in range(steps):
+            h.set_centers(prev)
+            h.iterate(1)
+            lab = h.labels()
+            Cn = h.centers()
+            n_mism += parity.check_lockstep(Xc, prev - mean, Cn - mean, lab, what=f"{what} step {m + 1}")
+            prev = Cn
+    return n_mism
+
+
+def _golden_names():
+    return [c["name"] for c in json.loads((GOLDEN / "manifest.json").read_text())["cases"]]
+
+
+def _load_golden(name):
+    from golden_io import load_golden
+
+    return load_golden(name)
+
+
+@pytest.mark.parametrize("name", _golden_names())
+def test_lockstep_golden(bridge, name):
+    g = _load_golden(name)
+    _say(f"lockstep golden {name} {g['X'].shape}")
+    _lockstep_gpu(bridge, g["X"], g["C0"], min(len(g["trace"]), 6), name)
+
+
+@pytest.mark.parametrize("name", _golden_names())
+def test_fit_vs_sklearn_golden(bridge, name):
+    """Full GPU fit vs sklearn's recorded fit and the oracle."""
+    g = _load_golden(name)
+    X, C0 = g["X"], g["C0"]
+    _say(f"fit golden {name} {X.shape} k={C0.shape[0]}")
+    n, d = X.shape
+    k = C0.shape[0]
+    tol_abs = oracle.sklearn_tolerance(X, float(g["tol"])) if "tol" in g else 0.0
+    C = C0.copy()
+    lab = np.empty(n, np.int32)
+    n_iter, inertia = bridge.kmeans_fit(X, C, lab, int(g["max_iter"]), tol_abs, strict=True)
+    mean = X.mean(axis=0)
+    Xc = X - mean
+    # final labels are the E-step of the final centres
+    ref_lab, best, second = oracle.assign(Xc, C - mean, return_gap=True)
+    parity.check_labels(lab, ref_lab, best, second, Xc, what=f"{name} final E-step")
+    parity.check_inertia(inertia, oracle.inertia(Xc, C - mean, lab), atol=parity.centring_floor(X),
+                         what=f"{name} inertia")
+    # end to end against sklearn whenever the oracle's own trajectory matches sklearn's
+    out = oracle.lloyd(X, C0, int(g["max_iter"]), tol_abs)
+    if out["n_iter"] == int(g["n_iter"]) and parity.center_rel_err(out["centers"], g["centers"]) <= 1e-5:
+        assert n_iter == int(g["n_iter"]), f"{name}: n_iter {n_iter} vs sklearn {int(g['n_iter'])}"
+        parity.check_centers(C, g["centers"], what=f"{name} centres vs sklearn")
+        _, best, second = oracle.assign(Xc, g["centers"] - mean, return_gap=True)
+        parity.check_labels(lab, g["labels"], best, second, Xc, what=f"{name} labels vs sklearn")
+
+
+def test_fit_is_deterministic(bridge):
+    from skmetal_amd import _synth
+
+    X, C0 = _synth.generate("c2", seed=3, scale=0.05)
+    outs = []
+    for _ in range(2):
+        C = C0.copy()
+        lab = np.empty(X.shape[0], np.int32)
+        n_iter, inertia = bridge.kmeans_fit(X, C, lab, 15, 0.0, strict=False)
+        outs.append((C, lab, n_iter, inertia))
+    assert np.array_equal(outs[0][0], outs[1][0])
+    assert np.array_equal(outs[0][1], outs[1][1])
+    assert outs[0][2:] == outs[1][2:]
+
+
+def test_empty_cluster_relocation_matches_oracle(bridge):
+    g = _load_golden("empty_1000x10_k20")
+    X, C0 = g["X"], g["C0"]
+    C = C0.copy()
+    lab = np.empty(X.shape[0], np.int32)
+    n_iter, inertia = bridge.kmeans_fit(X, C, lab, 300, 0.0, strict=True)
+    assert np.all(np.isfinite(C))
+    assert len(np.unique(lab)) == 20
+    out = oracle.lloyd(X, C0, 300)
+    assert n_iter == out["n_iter"]
+    parity.check_centers(C, out["centers"], what="relocation fit")
+
+
+@pytest.mark.parametrize("wl,steps", [("c1", 4), ("c2", 3)])
+def test_workload_lockstep_full_size(bridge, wl, steps):
+    from skmetal_amd import _synth
+
+    X, C0 = _synth.generate(wl, seed=0)
+    _say(f"lockstep {wl} {X.shape} k={C0.shape[0]}")
+    _lockstep_gpu(bridge, X, C0, steps, wl)
+
+
+def test_c2_fixed_iterations_inertia_monotone(bridge):
+    from skmetal_amd import _synth
+
+    X, C0 = _synth.generate("c2", seed=0)
+    n, d = X.shape
+    prev = np.inf
+    with bridge.LloydHandle(n, d, C0.shape[0]) as h:
+        h.load(X, center=True)
+        h.set_centers(C0)
+        for _ in range(6):
+            h.iterate(1)
+            v = h.inertia()  # labels of this E-step against the centres of its M-step
+            assert v <= prev * (1 + 1e-6)
+            prev = v

@@ -22,6 +22,7 @@ import numpy as np
 import pytest
 
 import oracle
+from golden_io import load_golden
 from oracle import parity
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
@@ -156,21 +157,6 @@ def test_c_and_numpy_restatements_agree():
 def _golden_cases():
     manifest = json.loads((GOLDEN / "manifest.json").read_text())
     return [c["name"] for c in manifest["cases"]]
-
-
-def load_golden(name):
-    """Load a golden case, regenerating workload inputs from their seed (SHA-256 checked)."""
-    with np.load(GOLDEN / f"{name}.npz") as z:
-        g = {key: z[key] for key in z.files}
-    if "X" not in g:
-        from skmetal_amd import _synth
-
-        X, C0 = _synth.generate(str(g["workload"]), seed=int(g["seed"]), scale=float(g["scale"]))
-        assert _synth.sha256(X) == str(g["sha256"]), "workload generator no longer reproduces the fixture input"
-        np.testing.assert_array_equal(C0, g["C0"])
-        g["X"] = X
-    g["labels"] = g["labels"].astype(np.int32)
-    return g
 
 
 @pytest.mark.parametrize("name", _golden_cases())
