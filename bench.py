@@ -1,0 +1,160 @@
+"""Benchmark: KMeans Lloyd iterations/s on one MI355X.
+
+Workload: 500,000 x 100 fp32 from 50 isotropic Gaussian blobs (centres
+~U[-10,10]^100, sigma 1), k = 50, seeded random-row init -- the shape of
+skmetal's README headline.  A "step" is one Lloyd iteration (fused E-step on
+fp32 MFMA, per-cluster sums, finalize) over all 500,000 rows, with X already
+resident in HBM.  The steps are timed with HIP events on the library's stream
+(skmetal_hip_lloyd_iterate); the assign kernel is also timed alone
+(skmetal_hip_lloyd_time_kernels) for its roofline fraction.
+
+cpu_baseline: scikit-learn's KMeans(algorithm="lloyd") -- the CPU
+implementation skmetal routes KMeans to -- on the same workload, same init, on
+this machine's cores; per-iteration time from fits of N and 1 iterations.
+
+Prints one JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBPS = 8000.0
+
+
+def _traffic_from_profile(name: str):
+    """HBM bytes per assign launch, from the committed rocprofv3 PMC summary."""
+    p = ROOT / "profiles" / name
+    if not p.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(X, C0, iters: int, reps: int = 3):
+    """sklearn Lloyd on this host: seconds per iteration (median of reps)."""
+    try:
+        import sklearn
+        from sklearn.cluster import KMeans
+    except ImportError:  # pragma: no cover - sklearn is part of the image
+        return None
+    cores = len(os.sched_getaffinity(0))
+
+    def fit(m):
+        km = KMeans(n_clusters=C0.shape[0], init=C0, n_init=1, max_iter=m, tol=0.0, algorithm="lloyd")
+        t = time.perf_counter()
+        km.fit(X)
+        return time.perf_counter() - t, km.n_iter_
+
+    per = []
+    for _ in range(reps):
+        tn, it_n = fit(iters)
+        t1, _ = fit(1)
+        per.append((tn - t1) / (it_n - 1) if it_n == iters and iters > 1 else tn / it_n)
+    s = float(np.median(per))
+    return dict(
+        value=1.0 / s,
+        unit="Lloyd iters/s",
+        cores=cores,
+        kind="reference",
+        sample=(f"sklearn {sklearn.__version__} KMeans(algorithm='lloyd', init=same {C0.shape[0]} rows, n_init=1, "
+                f"tol=0) on the full {X.shape[0]}x{X.shape[1]} workload; per-iteration time = "
+                f"(t_fit(max_iter={iters}) - t_fit(max_iter=1))/({iters}-1), median of {reps}; "
+                f"OMP threads={os.environ.get('OMP_NUM_THREADS', 'default')}"),
+    )
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="c2")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the sklearn CPU baseline")
+    ap.add_argument("--cpu-iters", type=int, default=8)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the multi-GPU sharding design is described in DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+
+    from skmetal_amd import _bridge, _synth
+
+    if not _bridge.HIP_AVAILABLE:
+        raise SystemExit(f"GPU path unavailable: {_bridge.last_error()}")
+    wl = _synth.WORKLOADS[args.workload]
+    X, C0 = _synth.generate(args.workload, seed=0)
+    n, d = X.shape
+    k = C0.shape[0]
+
+    with _bridge.LloydHandle(n, d, k) as h:
+        t = time.perf_counter()
+        h.load(X, center=True)
+        h2d_s = time.perf_counter() - t
+        h.set_centers(C0)
+        h.iterate(args.warmup)
+        h.set_centers(C0)
+        t = time.perf_counter()
+        ms = h.iterate(args.steps)
+        wall = time.perf_counter() - t
+        ms_assign, ms_update = h.time_kernels(max(20, args.steps // 2))
+
+    step_s = ms / 1e3 / args.steps
+    it_s = 1.0 / step_s
+    flops = 2.0 * n * k * d
+    assign_s = ms_assign / 1e3
+    achieved = flops / assign_s / 1e12
+    traffic = _traffic_from_profile(f"assign_{args.workload}_pmc.txt")
+
+    cpu = None if args.no_cpu else cpu_baseline(X, C0, args.cpu_iters)
+
+    out = {
+        "metric": "Lloyd iters/s + dist-evals/s at 500k x100,k=50 fp32; % of roofline",
+        "value": round(it_s, 2),
+        "unit": "Lloyd iters/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"KMeans Lloyd {n}x{d} fp32, k={k}, {wl.description}, seeded random-row init, "
+                               f"fixed iterations (no convergence stop)",
+                   "n": n, "d": d, "k": k},
+        "dist_evals_per_s": round(n * k * it_s, 1),
+        "wall_s_timed": round(wall, 4),
+        "h2d_s": round(h2d_s, 4),
+        "kernels_ms": {"assign": round(ms_assign, 5), "update": round(ms_update, 5)},
+        "roofline": {
+            "kernel": "assign (fused ||c||^2-2x.c MFMA + argmin)",
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_FP32_MFMA_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+    }
+    if cpu:
+        out["speedup_vs_cpu"] = round(it_s / cpu["value"], 1)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

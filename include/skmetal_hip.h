@@ -125,10 +125,15 @@ SKMETAL_API int skmetal_hip_lloyd_iterate(skmetal_hip_lloyd* h, size_t iters, fl
  * including the final E-step and inertia. */
 SKMETAL_API int skmetal_hip_lloyd_run(skmetal_hip_lloyd* h, size_t max_iter, double tol, int flags,
                           int32_t* n_iter_out, double* inertia_out);
-/* Average time of one launch (ms) of the assign and the update kernels over
- * `reps` back-to-back launches on the current centres (HIP events). */
+/* Average time of one launch (ms) over `reps` back-to-back launches on the
+ * current centres (HIP events): *ms_assign receives the E-step kernel (the
+ * fused E-step + per-cluster-sum kernel when the handle uses it),
+ * *ms_update the separate update kernel (0 in fused mode). */
 SKMETAL_API int skmetal_hip_lloyd_time_kernels(skmetal_hip_lloyd* h, size_t reps, float* ms_assign,
                                    float* ms_update);
+/* *fused = 1 when a step runs as one fused E-step + sums kernel (k <= 64,
+ * padded d <= 128); *partials = per-step partial sums the finalize reduces. */
+SKMETAL_API int skmetal_hip_lloyd_info(skmetal_hip_lloyd* h, int* fused, int* partials);
 SKMETAL_API int skmetal_hip_lloyd_get_centers(skmetal_hip_lloyd* h, float* C);
 SKMETAL_API int skmetal_hip_lloyd_get_labels(skmetal_hip_lloyd* h, int32_t* labels);
 /* Inertia of the current labels against the current centres (fp64). */

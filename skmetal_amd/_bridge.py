@@ -58,6 +58,7 @@ _REGISTRY = [
      ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_double)),
     ("skmetal_hip_lloyd_time_kernels", ctypes.c_int, _vp, _c_size, ctypes.POINTER(ctypes.c_float),
      ctypes.POINTER(ctypes.c_float)),
+    ("skmetal_hip_lloyd_info", ctypes.c_int, _vp, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)),
     ("skmetal_hip_lloyd_get_centers", ctypes.c_int, _vp, _vp),
     ("skmetal_hip_lloyd_get_labels", ctypes.c_int, _vp, _vp),
     ("skmetal_hip_lloyd_inertia", ctypes.c_int, _vp, ctypes.POINTER(ctypes.c_double)),
@@ -273,6 +274,13 @@ class LloydHandle:
         _check(_lib.skmetal_hip_lloyd_time_kernels(self._h, int(reps), ctypes.byref(a), ctypes.byref(u)),
                "skmetal_hip_lloyd_time_kernels")
         return float(a.value), float(u.value)
+
+    def info(self):
+        fused = ctypes.c_int(0)
+        partials = ctypes.c_int(0)
+        _check(_lib.skmetal_hip_lloyd_info(self._h, ctypes.byref(fused), ctypes.byref(partials)),
+               "skmetal_hip_lloyd_info")
+        return dict(fused=bool(fused.value), partials=int(partials.value))
 
     def centers(self):
         out = np.empty((self.k, self.d), np.float32)

@@ -28,6 +28,9 @@ HIPCC_FLAGS = [
     "-Wall",
     # keep the compiler from emitting packed fp32 VALU ops (v_pk_*_f32)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: keeps loop-carried accumulators in place
+    # instead of rotating them through AGPRs with v_accvgpr_* copies
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

@@ -47,6 +47,21 @@ struct AssignArgs {
 };
 hipError_t launch_assign(const AssignArgs& a, int num_cu, hipStream_t s);
 
+// Fused E-step + per-cluster sums (k <= 64, ld <= 128, tables fit in LDS).
+struct FusedArgs {
+    const float* X; long n; int ld;
+    const float* C; const float* cnorm; int k;
+    int* labels;
+    float* psum;           // [blocks x k x ld]
+    int* pcnt;             // [blocks x k]
+    LoopState* state;      // required: early exit and change counting
+    int blocks;
+};
+// Number of blocks (= partials) of the fused kernel for this shape, or 0 when
+// the shape does not qualify.
+int fused_blocks(long n, int d, int k, int num_cu);
+hipError_t launch_fused(const FusedArgs& a, hipStream_t s);
+
 struct UpdateArgs {
     const float* X; long n; int ld; int d;
     const int* labels; int k;
@@ -54,7 +69,7 @@ struct UpdateArgs {
     int* pcnt;             // [R x k]
     LoopState* state;
 };
-struct UpdateGeom { int R; int G; int cg; long rows_per_range; int threads; size_t lds; };
+struct UpdateGeom { int R; int G; int Z; int cg; int nslots; int ncp; int W; long rows_per_range; int threads; size_t lds; };
 UpdateGeom update_geometry(long n, int d, int k, int num_cu);
 hipError_t launch_update(const UpdateArgs& a, const UpdateGeom& g, hipStream_t s);
 
@@ -68,9 +83,18 @@ struct FinalizeArgs {
     unsigned* cluster_ctr; // [k], zero between launches
     LoopState* state;
     int iter; double tol; int flags;
+    int cw;                // columns per finalize block: finalize_cols(R)
 };
 hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t s);
-inline int finalize_col_chunks(int d) { return (d + 31) / 32; }
+// A finalize block is 256 threads = cw columns x (256/cw) partial-sum lanes,
+// sized so that each thread reads at most about 8 of the R partials.
+inline int finalize_cols(int R)
+{
+    int rs = 1;
+    while (rs < 64 && rs * 8 < R) rs *= 2;
+    return 256 / rs;
+}
+inline int finalize_col_chunks(int d, int R) { const int cw = finalize_cols(R); return (d + cw - 1) / cw; }
 
 struct RowDistArgs {
     const float* X; long n; int ld; int d;

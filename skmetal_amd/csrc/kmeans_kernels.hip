@@ -17,6 +17,7 @@
 //   sklearn/cluster/_k_means_common.pyx:94-124, :274-311 (inertia, average,
 //   shift); the relocation of empty clusters runs on the host.
 #include <math.h>
+#include <stdlib.h>
 
 #include "internal.h"
 
@@ -39,6 +40,26 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 // Centres are staged through LDS per (chunk, feature segment); X rows are read
 // straight from HBM into registers (one row per lane, 16-byte loads).
 
+// Loads NQ float4s of this lane's row (row0 + lane) starting at feature f0,
+// with no branches: the buffer descriptor covers exactly the valid rows, so a
+// lane past the last row, and any float4 at or past `nq`, reads 0 without a
+// memory access.  All NQ loads stay in flight together.
+template <int NQ>
+__device__ __forceinline__ void load_row_quads(float4* xv, const float* X, long row0, long n, int ld, int f0,
+                                               int nq, int lane)
+{
+    const long rows = n - row0 < 64 ? (n - row0 > 0 ? n - row0 : 0) : 64;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(X + (rows > 0 ? row0 * ld + f0 : 0)), (short)0, (int)(rows * ld * 4), 0x00020000);
+    const int base = lane * ld * 4;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const int off = q < nq ? base + 16 * q : 0x7ffffff0;
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+        xv[q] = *reinterpret_cast<const float4*>(&v);
+    }
+}
+
 template <int KG, int G = 0>
 __device__ __forceinline__ void mfma_groups(v4f* acc, float a, float b)
 {
@@ -49,7 +70,7 @@ __device__ __forceinline__ void mfma_groups(v4f* acc, float a, float b)
 }
 
 template <int KG, int NQ>
-__global__ __launch_bounds__(256, 2) void k_assign(const float* __restrict__ X, long n, int ld,
+__global__ __launch_bounds__(256, 1) void k_assign(const float* __restrict__ X, long n, int ld,
                                                    const float* __restrict__ C,
                                                    const float* __restrict__ cnorm, int k,
                                                    int* __restrict__ labels, LoopState* st,
@@ -64,7 +85,7 @@ __global__ __launch_bounds__(256, 2) void k_assign(const float* __restrict__ X, 
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps descriptors scalar
     const int nchunk = (k + CPC - 1) / CPC;
     const int nseg = (ld + SEG - 1) / SEG;
     const bool single = (nchunk == 1) && (nseg == 1);
@@ -96,9 +117,8 @@ __global__ __launch_bounds__(256, 2) void k_assign(const float* __restrict__ X, 
 
     const long stride = (long)gridDim.x * 256;
     for (long base = (long)blockIdx.x * 256; base < n; base += stride) {
-        const long row = base + wave * 64 + lane;
-        const long rr = row < n ? row : n - 1;
-        const float* xrow = X + rr * ld;
+        const long row0 = base + wave * 64;
+        const long row = row0 + lane;
         float best = INFINITY;
         int bidx = 0;
         for (int ch = 0; ch < nchunk; ++ch) {
@@ -114,18 +134,15 @@ __global__ __launch_bounds__(256, 2) void k_assign(const float* __restrict__ X, 
                 const int f0 = sg * SEG;
                 const int nq = min(NQ, (ld - f0) >> 2);
                 float4 xv[NQ];
-#pragma unroll
-                for (int q = 0; q < NQ; ++q)
-                    if (q < nq) xv[q] = *reinterpret_cast<const float4*>(xrow + f0 + 4 * q);
+                load_row_quads<NQ>(xv, X, row0, n, ld, f0, nq, lane);
+                // past nq both operands are 0 (zero-filled stage, zero loads)
 #pragma unroll
                 for (int q = 0; q < NQ; ++q) {
-                    if (q < nq) {
-                        const float4 cv = *reinterpret_cast<const float4*>(&sC[crow * LS + 4 * q]);
-                        mfma_groups<KG>(acc, cv.x, xv[q].x);
-                        mfma_groups<KG>(acc, cv.y, xv[q].y);
-                        mfma_groups<KG>(acc, cv.z, xv[q].z);
-                        mfma_groups<KG>(acc, cv.w, xv[q].w);
-                    }
+                    const float4 cv = *reinterpret_cast<const float4*>(&sC[crow * LS + 4 * q]);
+                    mfma_groups<KG>(acc, cv.x, xv[q].x);
+                    mfma_groups<KG>(acc, cv.y, xv[q].y);
+                    mfma_groups<KG>(acc, cv.z, xv[q].z);
+                    mfma_groups<KG>(acc, cv.w, xv[q].w);
                 }
             }
             // ||c||^2 - 2 x.c, first minimum wins (_k_means_lloyd.pyx:196-212)
@@ -212,81 +229,394 @@ hipError_t launch_assign(const AssignArgs& a, int num_cu, hipStream_t s)
 }
 
 // ---------------------------------------------------------------------------
-// update: per-(row range, cluster group) sums and counts
+// fused Lloyd step for small k*d: E-step and per-cluster sums in one pass
 // ---------------------------------------------------------------------------
 //
-// Block (r, g) walks rows [r*rpr, (r+1)*rpr) in order and adds every row whose
-// label falls in cluster group g into an LDS table S[cg x d].  Column c of S is
-// only ever touched by thread c mod blockDim, so every partial sum is formed
-// in row order: bitwise reproducible.  X is read once overall (each row is
-// used by the one group owning its label); labels are read once per group.
+// When k <= 64 and ld <= 4*NQ <= 128, one kernel both assigns and
+// accumulates, reading X from HBM once per Lloyd step.  Each wave owns 64-row
+// tiles and stages the tile in its own LDS region (row r at r*xs floats, xs/4
+// odd so 16-byte reads of 8 different rows hit 8 different bank groups).
+//   E-step: exactly as k_assign, with lane l's operands read from row l.
+//   sums:   lane j owns cluster j; its running sum of the cluster's rows stays
+//           in registers (float4 S[NQ]).  ballot(label == j) hands lane j the
+//           bitmask of this tile's rows in cluster j, and every lane then walks
+//           its own bits, adding those rows from LDS -- all clusters in
+//           parallel, rows in increasing order, no atomics.
+// The next tile's rows are loaded into registers while this tile is
+// processed.  At the end the four waves' sums are combined in wave order, one
+// partial per block (one block per CU): bitwise reproducible.
 
+template <int KG, int NQ>
+__global__ __launch_bounds__(256, 1) void k_fused(const float* __restrict__ X, long n, int ld,
+                                                  const float* __restrict__ C,
+                                                  const float* __restrict__ cnorm, int k,
+                                                  int* __restrict__ labels, float* __restrict__ psum,
+                                                  int* __restrict__ pcnt, LoopState* st)
+{
+    if (st->done != 0) return;
+    constexpr int CPC = 4 * KG;
+    constexpr int SEG = 4 * NQ;
+    constexpr int LS = SEG + 4;
+    constexpr int XS = (NQ & 1) ? SEG : SEG + 4;  // X tile row stride: XS/4 odd
+    extern __shared__ __attribute__((aligned(16))) float xt[];  // 4 waves x 64 rows x XS
+    __shared__ __attribute__((aligned(16))) float sC[CPC * LS];
+    __shared__ float sN[CPC];
+    __shared__ int sCnt[4][64];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps descriptors scalar
+    const int nq = ld >> 2;
+    float* xw = xt + wave * 64 * XS;
+
+    for (int idx = tid; idx < CPC * NQ; idx += 256) {
+        const int cl = idx / NQ;
+        const int q = idx - cl * NQ;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (cl < k && q < nq) v = *reinterpret_cast<const float4*>(C + (long)cl * ld + 4 * q);
+        *reinterpret_cast<float4*>(&sC[cl * LS + 4 * q]) = v;
+    }
+    for (int i = tid; i < CPC; i += 256) sN[i] = i < k ? cnorm[i] : 0.f;
+    __syncthreads();
+
+    const int crow = lane < CPC ? lane : CPC - 1;
+    const long ntiles = (n + 63) / 64;
+    const long tstride = (long)gridDim.x * 4;
+    float4 S[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) S[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+    int cnt = 0;
+    float4 xn[NQ];
+    float* my_row = xw + lane * XS;
+
+    long t = (long)blockIdx.x * 4 + wave;
+    load_row_quads<NQ>(xn, X, t * 64, n, ld, 0, nq, lane);
+    while (t < ntiles) {
+        const long row = t * 64 + lane;
+        const bool valid = row < n;
+        const int old = valid ? labels[row] : -1;  // issued before the prefetch below
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) *reinterpret_cast<float4*>(my_row + 4 * q) = xn[q];
+        const long tn = t + tstride;
+        load_row_quads<NQ>(xn, X, tn * 64, n, ld, 0, nq, lane);  // empty when tn is past the end
+
+        v4f acc[KG];
+#pragma unroll
+        for (int g = 0; g < KG; ++g) acc[g] = v4f{0.f, 0.f, 0.f, 0.f};
+        // operands of feature quad q+1 are read from LDS while quad q's MFMAs run
+        float4 xv = *reinterpret_cast<const float4*>(my_row);
+        float4 cv = *reinterpret_cast<const float4*>(&sC[crow * LS]);
+        for (int q = 0; q < nq; ++q) {
+            const int qn = q + 1 < nq ? q + 1 : q;
+            const float4 xv2 = *reinterpret_cast<const float4*>(my_row + 4 * qn);
+            const float4 cv2 = *reinterpret_cast<const float4*>(&sC[crow * LS + 4 * qn]);
+            mfma_groups<KG>(acc, cv.x, xv.x);
+            mfma_groups<KG>(acc, cv.y, xv.y);
+            mfma_groups<KG>(acc, cv.z, xv.z);
+            mfma_groups<KG>(acc, cv.w, xv.w);
+            xv = xv2;
+            cv = cv2;
+        }
+        float best = INFINITY;
+        int bidx = 0;
+#pragma unroll
+        for (int g = 0; g < KG; ++g) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int j = 4 * g + r;
+                const float dist = fmaf(-2.0f, acc[g][r], sN[j]);
+                if (j < k && dist < best) {
+                    best = dist;
+                    bidx = j;
+                }
+            }
+        }
+        if (valid) labels[row] = bidx;
+        const unsigned long long mv = __ballot(valid && old != bidx);
+        if (lane == 0 && mv != 0ull) atomicAdd(&st->changed, (int)__popcll(mv));
+
+        // cluster-owner sums: lane j collects the rows of cluster j
+        unsigned long long mine = 0ull;
+#pragma unroll
+        for (int j = 0; j < CPC; ++j) {
+            const unsigned long long m = __ballot(valid && bidx == j);
+            if (lane == j) mine = m;
+        }
+        cnt += __popcll(mine);
+        while (mine != 0ull) {
+            const int r = __ffsll((long long)mine) - 1;
+            mine &= mine - 1ull;
+            const float* src = xw + r * XS;
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                const float4 v = *reinterpret_cast<const float4*>(src + 4 * q);
+                S[q].x += v.x;
+                S[q].y += v.y;
+                S[q].z += v.z;
+                S[q].w += v.w;
+            }
+        }
+        t = tn;
+    }
+
+    // combine the four waves' sums in wave order
+    __syncthreads();
+    if (lane < k) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) *reinterpret_cast<float4*>(my_row + 4 * q) = S[q];
+    }
+    sCnt[wave][lane] = cnt;
+    __syncthreads();
+    const int wstride = 64 * XS;
+    for (int idx = tid; idx < k * ld; idx += 256) {
+        const int j = idx / ld;
+        const int c = idx - j * ld;
+        const int i = j * XS + c;
+        psum[(long)blockIdx.x * k * ld + idx] =
+            ((xt[i] + xt[wstride + i]) + xt[2 * wstride + i]) + xt[3 * wstride + i];
+    }
+    for (int j = tid; j < k; j += 256)
+        pcnt[(long)blockIdx.x * k + j] = sCnt[0][j] + sCnt[1][j] + sCnt[2][j] + sCnt[3][j];
+}
+
+typedef void (*fused_fn)(const float*, long, int, const float*, const float*, int, int*, float*, int*, LoopState*);
+
+template <int NQ, int... KGs>
+struct FusedTable {
+    static fused_fn get(int kg)
+    {
+        fused_fn f = nullptr;
+        ((kg == KGs ? (f = &k_fused<KGs, NQ>, 0) : 0), ...);
+        return f;
+    }
+};
+
+template <int NQ>
+static fused_fn pick_fused(int kg)
+{
+    return FusedTable<NQ, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16>::get(kg);
+}
+
+static int fused_nq(int ld)
+{
+    const int q = ld / 4;
+    return q <= 4 ? 4 : ((q + 3) / 4) * 4;
+}
+
+static fused_fn fused_kernel(int k, int ld)
+{
+    if (k > 64 || ld > 128) return nullptr;
+    const int kg = (k + 3) / 4;
+    switch (fused_nq(ld)) {
+    case 4: return pick_fused<4>(kg);
+    case 8: return pick_fused<8>(kg);
+    case 12: return pick_fused<12>(kg);
+    case 16: return pick_fused<16>(kg);
+    case 20: return pick_fused<20>(kg);
+    case 24: return pick_fused<24>(kg);
+    case 28: return pick_fused<28>(kg);
+    case 32: return pick_fused<32>(kg);
+    default: return nullptr;
+    }
+}
+
+static size_t fused_dyn_lds(int k, int ld)
+{
+    (void)k;
+    const int nq = fused_nq(ld);
+    const int xs = (nq & 1) ? 4 * nq : 4 * nq + 4;
+    return (size_t)4 * 64 * xs * sizeof(float);
+}
+
+int fused_blocks(long n, int d, int k, int num_cu)
+{
+    // SKMETAL_HIP_FUSED=0 selects the separate assign/update kernels for every shape
+    const char* env = getenv("SKMETAL_HIP_FUSED");
+    if (env != nullptr && env[0] == '0') return 0;
+    const int ld = (d + 3) & ~3;
+    fused_fn f = fused_kernel(k, ld);
+    if (f == nullptr) return 0;
+    const size_t dyn = fused_dyn_lds(k, ld);
+    const int nq = fused_nq(ld);
+    const size_t stat = (size_t)4 * ((k + 3) / 4) * (4 * nq + 4) * sizeof(float) + 64 * sizeof(float) + 1024;
+    if (dyn + stat > 150 * 1024) return 0;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(f), hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) !=
+        hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    long blocks = num_cu;
+    const long tiles4 = ((n + 63) / 64 + 3) / 4;
+    if (blocks > tiles4) blocks = tiles4;
+    return (int)(blocks < 1 ? 1 : blocks);
+}
+
+hipError_t launch_fused(const FusedArgs& a, hipStream_t s)
+{
+    fused_fn f = fused_kernel(a.k, a.ld);
+    if (f == nullptr || a.blocks < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(f, dim3(a.blocks), dim3(256), fused_dyn_lds(a.k, a.ld), s, a.X, a.n, a.ld, a.C, a.cnorm, a.k,
+                       a.labels, a.psum, a.pcnt, a.state);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// update: per-(row range, cluster group, column tile) sums and counts
+// ---------------------------------------------------------------------------
+//
+// Block (r, g, z) handles rows [r*rpr, (r+1)*rpr), clusters [g*cg, (g+1)*cg)
+// and columns [z*W, (z+1)*W).  Its threads form `nslots` row slots of `ct`
+// column threads; slot s owns a contiguous half/quarter of the rows and its
+// own LDS table S_s[cg x dt].  A slot walks its rows in batches of kUB: the
+// batch's labels are uniform across the slot, so duplicates inside a batch are
+// folded in registers first (in row order) and every distinct label then costs
+// one LDS read-modify-write -- one LDS round trip per batch instead of per row,
+// and the kUB row loads of a batch are all in flight together.  Column c of
+// S_s is only touched by one thread, and the slots are summed in slot order at
+// the end, so each partial is bitwise reproducible.  Rows outside the group
+// are skipped without loading X, so X is read once overall.
+
+constexpr int kUB = 8;     // rows per batch
+constexpr int kLCH = 256;  // labels staged per slot and chunk
+
+template <int NCP>
 __global__ __launch_bounds__(256) void k_update(const float* __restrict__ X, long n, int ld, int d,
                                                 const int* __restrict__ labels, int k, int cg, long rpr,
-                                                float* __restrict__ psum, int* __restrict__ pcnt,
-                                                const LoopState* st)
+                                                int nslots, int W, float* __restrict__ psum,
+                                                int* __restrict__ pcnt, const LoopState* st)
 {
     if (st != nullptr && st->done != 0) return;
-    extern __shared__ float sS[];
-    constexpr int LCH = 256;
-    __shared__ int sLab[LCH];
-    int* sCnt = reinterpret_cast<int*>(sS + (long)cg * d);
+    extern __shared__ float smem[];
+    const int T = blockDim.x;
+    const int ct = T / nslots;
+    const int slot = threadIdx.x / ct;
+    const int lt = threadIdx.x - slot * ct;
     const int r = blockIdx.x;
-    const int g = blockIdx.y;
-    const int j0 = g * cg;
+    const int j0 = blockIdx.y * cg;
     const int j1 = min(k, j0 + cg);
+    const int col0 = blockIdx.z * W;
+    const int dt = min(d - col0, W);
     const long row0 = (long)r * rpr;
     const long row1 = min(n, row0 + rpr);
-    const int T = blockDim.x;
-    for (int i = threadIdx.x; i < cg * d; i += T) sS[i] = 0.f;
-    for (int i = threadIdx.x; i < cg; i += T) sCnt[i] = 0;
-    for (long c0 = row0; c0 < row1; c0 += LCH) {
-        const int m = (int)min((long)LCH, row1 - c0);
+    const long per = (row1 - row0 + nslots - 1) / nslots;
+    const long a = min(row1, row0 + (long)slot * per);
+    const long b = min(row1, a + per);
+    float* S = smem + (long)slot * cg * dt;
+    int* cnt_all = reinterpret_cast<int*>(smem + (long)nslots * cg * dt);
+    int* cnt = cnt_all + slot * cg;
+    int* sLab = cnt_all + nslots * cg + slot * kLCH;
+    for (int i = threadIdx.x; i < nslots * cg * dt; i += T) smem[i] = 0.f;
+    for (int i = threadIdx.x; i < nslots * cg; i += T) cnt_all[i] = 0;
+
+    for (long base = 0; base < per; base += kLCH) {
         __syncthreads();
-        for (int i = threadIdx.x; i < m; i += T) sLab[i] = labels[c0 + i];
+        for (int i = lt; i < kLCH; i += ct) {
+            const long row = a + base + i;
+            int lab = -1;
+            if (row < b) {
+                lab = labels[row];
+                lab = (lab >= j0 && lab < j1) ? lab - j0 : -1;
+            }
+            sLab[i] = lab;
+        }
         __syncthreads();
-        for (int i = 0; i < m; ++i) {
-            const int lab = sLab[i];
-            if (lab >= j0 && lab < j1) {
-                float* srow = sS + (long)(lab - j0) * d;
-                const float* xr = X + (c0 + i) * ld;
-                for (int c = threadIdx.x; c < d; c += T) srow[c] += xr[c];
-                if (threadIdx.x == 0) sCnt[lab - j0] += 1;
+        const int m = (int)min((long)kLCH, max(0L, b - a - base));
+        for (int i0 = 0; i0 < m; i0 += kUB) {
+            int lj[kUB], dup[kUB];
+#pragma unroll
+            for (int u = 0; u < kUB; ++u) lj[u] = __builtin_amdgcn_readfirstlane(i0 + u < m ? sLab[i0 + u] : -1);
+#pragma unroll
+            for (int u = 0; u < kUB; ++u) {
+                dup[u] = -1;
+#pragma unroll
+                for (int v = 0; v < u; ++v)
+                    if (dup[u] < 0 && lj[u] >= 0 && dup[v] < 0 && lj[v] == lj[u]) dup[u] = v;
+            }
+            if (lt == 0) {
+#pragma unroll
+                for (int u = 0; u < kUB; ++u)
+                    if (lj[u] >= 0) cnt[lj[u]] += 1;
+            }
+            const float* xb = X + (a + base + i0) * ld + col0;
+#pragma unroll
+            for (int p = 0; p < NCP; ++p) {
+                const int c = lt + p * ct;
+                if (c < dt) {
+                    float v[kUB];
+#pragma unroll
+                    for (int u = 0; u < kUB; ++u) v[u] = lj[u] >= 0 ? xb[(long)u * ld + c] : 0.f;
+#pragma unroll
+                    for (int u = 1; u < kUB; ++u) {
+#pragma unroll
+                        for (int w = 0; w < u; ++w)
+                            if (dup[u] == w) v[w] += v[u];
+                    }
+                    float o[kUB];
+#pragma unroll
+                    for (int u = 0; u < kUB; ++u)
+                        if (lj[u] >= 0 && dup[u] < 0) o[u] = S[lj[u] * dt + c];
+#pragma unroll
+                    for (int u = 0; u < kUB; ++u)
+                        if (lj[u] >= 0 && dup[u] < 0) S[lj[u] * dt + c] = o[u] + v[u];
+                }
             }
         }
     }
     __syncthreads();
-    for (int jl = 0; jl < j1 - j0; ++jl) {
-        float* dst = psum + ((long)r * k + j0 + jl) * ld;
-        for (int c = threadIdx.x; c < d; c += T) dst[c] = sS[(long)jl * d + c];
+    const int ncl = j1 - j0;
+    for (int idx = threadIdx.x; idx < ncl * dt; idx += T) {
+        const int jl = idx / dt;
+        const int c = idx - jl * dt;
+        float acc = 0.f;
+        for (int q = 0; q < nslots; ++q) acc += smem[(long)q * cg * dt + idx];
+        psum[((long)r * k + j0 + jl) * ld + col0 + c] = acc;
     }
-    for (int jl = threadIdx.x; jl < j1 - j0; jl += T) pcnt[(long)r * k + j0 + jl] = sCnt[jl];
+    if (blockIdx.z == 0) {
+        for (int jl = threadIdx.x; jl < ncl; jl += T) {
+            int c2 = 0;
+            for (int q = 0; q < nslots; ++q) c2 += cnt_all[q * cg + jl];
+            pcnt[(long)r * k + j0 + jl] = c2;
+        }
+    }
 }
 
 UpdateGeom update_geometry(long n, int d, int k, int num_cu)
 {
     UpdateGeom g{};
-    const long lds_words = 12 * 1024;  // 48 KB of sums + counts per block
-    g.cg = (int)max(1L, min((long)k, lds_words / (long)(d + 1)));
+    const int ct = d >= 256 ? 256 : ((d + 63) / 64) * 64;
+    g.nslots = 256 / ct;
+    g.ncp = d <= ct ? 1 : d <= 2 * ct ? 2 : 4;
+    g.W = ct * g.ncp;
+    g.Z = (d + g.W - 1) / g.W;
+    const long words = 16 * 1024 - (long)g.nslots * kLCH;  // 64 KB of LDS per block
+    g.cg = (int)max(1L, min((long)k, words / ((long)g.nslots * (min(d, g.W) + 1))));
     g.G = (k + g.cg - 1) / g.cg;
-    g.threads = d >= 256 ? 256 : ((d + 63) / 64) * 64;
-    const long target = (long)num_cu * 8;
-    long R = target / g.G;
+    g.threads = 256;
+    long R = (2L * num_cu) / ((long)g.G * g.Z);
+    const long min_r = (n + 32767) / 32768;  // bound the label scan of one block
+    if (R < min_r) R = min_r;
     if (R < 1) R = 1;
     const long max_r = (n + 255) / 256;
     if (R > max_r) R = max_r;
-    if (R > 4096) R = 4096;
     g.R = (int)R;
     g.rows_per_range = (n + R - 1) / R;
-    g.lds = (size_t)g.cg * d * sizeof(float) + (size_t)g.cg * sizeof(int);
+    const int dt = min(d, g.W);
+    g.lds = ((size_t)g.nslots * g.cg * dt + (size_t)g.nslots * g.cg + (size_t)g.nslots * kLCH) * 4;
     return g;
 }
 
 hipError_t launch_update(const UpdateArgs& a, const UpdateGeom& g, hipStream_t s)
 {
     if (a.n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_update, dim3(g.R, g.G), dim3(g.threads), g.lds, s, a.X, a.n, a.ld, a.d, a.labels, a.k,
-                       g.cg, g.rows_per_range, a.psum, a.pcnt, a.state);
+    const dim3 grid(g.R, g.G, g.Z);
+    if (g.ncp == 1)
+        hipLaunchKernelGGL(k_update<1>, grid, dim3(g.threads), g.lds, s, a.X, a.n, a.ld, a.d, a.labels, a.k, g.cg,
+                           g.rows_per_range, g.nslots, g.W, a.psum, a.pcnt, a.state);
+    else if (g.ncp == 2)
+        hipLaunchKernelGGL(k_update<2>, grid, dim3(g.threads), g.lds, s, a.X, a.n, a.ld, a.d, a.labels, a.k, g.cg,
+                           g.rows_per_range, g.nslots, g.W, a.psum, a.pcnt, a.state);
+    else
+        hipLaunchKernelGGL(k_update<4>, grid, dim3(g.threads), g.lds, s, a.X, a.n, a.ld, a.d, a.labels, a.k, g.cg,
+                           g.rows_per_range, g.nslots, g.W, a.psum, a.pcnt, a.state);
     return hipGetLastError();
 }
 
@@ -314,31 +644,37 @@ __global__ __launch_bounds__(256) void k_finalize(FinalizeArgs a)
     const int cc = blockIdx.y;
     const int nch = gridDim.y;
     const int tid = threadIdx.x;
-    const int cl = tid & 31;
-    const int rs = tid >> 5;
-    const int col = cc * 32 + cl;
-    __shared__ double red[8][33];
+    const int CW = a.cw;            // columns per block
+    const int RS = 256 / CW;        // partial-sum lanes per column (power of two)
+    const int cl = tid % CW;
+    const int rs = tid / CW;
+    const int col = cc * CW + cl;
+    __shared__ double red[256];
     __shared__ int cred[256];
-    __shared__ double pr[2][32];
+    __shared__ double pr[2][256];
 
     int cnt = 0;
     for (int r = tid; r < a.R; r += 256) cnt += a.pcnt[(long)r * a.k + j];
     cred[tid] = cnt;
     double s = 0.0;
     if (col < a.d)
-        for (int r = rs; r < a.R; r += 8) s += (double)a.psum[((long)r * a.k + j) * a.ld + col];
-    red[rs][cl] = s;
+        for (int r = rs; r < a.R; r += RS) s += (double)a.psum[((long)r * a.k + j) * a.ld + col];
+    red[tid] = s;
     __syncthreads();
     for (int w = 128; w > 0; w >>= 1) {
         if (tid < w) cred[tid] += cred[tid + w];
+        __syncthreads();
+    }
+    // fixed-order tree over the RS lanes of each column
+    for (int w = RS / 2; w > 0; w >>= 1) {
+        if (rs < w) red[tid] += red[tid + w * CW];
         __syncthreads();
     }
     const int count = cred[0];
     if (rs == 0) {
         double sq = 0.0, nrm = 0.0;
         if (col < a.d) {
-            double tot = 0.0;
-            for (int t = 0; t < 8; ++t) tot += red[t][cl];
+            const double tot = red[cl];
             a.sums[(long)j * a.ld + col] = tot;
             if (count > 0) {
                 const float cn = (float)(tot / (double)count);
@@ -354,7 +690,7 @@ __global__ __launch_bounds__(256) void k_finalize(FinalizeArgs a)
     __syncthreads();
     if (tid == 0) {
         double ssq = 0.0, snr = 0.0;
-        for (int t = 0; t < 32; ++t) {
+        for (int t = 0; t < CW; ++t) {
             ssq += pr[0][t];
             snr += pr[1][t];
         }
@@ -407,7 +743,7 @@ __global__ __launch_bounds__(256) void k_finalize(FinalizeArgs a)
 
 hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t s)
 {
-    hipLaunchKernelGGL(k_finalize, dim3(a.k, finalize_col_chunks(a.d)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(k_finalize, dim3(a.k, finalize_col_chunks(a.d, a.R)), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

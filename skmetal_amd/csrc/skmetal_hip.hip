@@ -262,6 +262,7 @@ struct Lloyd {
     double* colpart = nullptr;
     LoopState* st = nullptr;
     UpdateGeom ug{};
+    int fblocks = 0;        // > 0: fused E-step + sums kernel with this many partials
     int cur = 0;            // index of the current centres in cen[]
     bool centred = false;
     std::vector<float> h_mean;
@@ -283,6 +284,9 @@ struct Lloyd {
         ld = (d + 3) & ~3;
         s = C->stream;
         ug = update_geometry(n, d, k, C->num_cu);
+        fblocks = fused_blocks(n, d, k, C->num_cu);
+        const int Rmax = std::max(ug.R, fblocks);
+        const int chunks = std::max(finalize_col_chunks(d, ug.R), fblocks > 0 ? finalize_col_chunks(d, fblocks) : 0);
         const size_t kl = size_t(k) * ld;
         TRY(grab((void**)&X, size_t(n) * ld * sizeof(float)));
         TRY(grab((void**)&cen[0], kl * sizeof(float)));
@@ -290,11 +294,11 @@ struct Lloyd {
         TRY(grab((void**)&cnorm, size_t(k) * sizeof(float)));
         TRY(grab((void**)&mean, size_t(ld) * sizeof(float)));
         TRY(grab((void**)&labels, size_t(n) * sizeof(int)));
-        TRY(grab((void**)&psum, size_t(ug.R) * kl * sizeof(float)));
-        TRY(grab((void**)&pcnt, size_t(ug.R) * k * sizeof(int)));
+        TRY(grab((void**)&psum, size_t(Rmax) * kl * sizeof(float)));
+        TRY(grab((void**)&pcnt, size_t(Rmax) * k * sizeof(int)));
         TRY(grab((void**)&sums, kl * sizeof(double)));
         TRY(grab((void**)&counts, size_t(k) * sizeof(int)));
-        TRY(grab((void**)&part, size_t(k) * finalize_col_chunks(d) * 2 * sizeof(double)));
+        TRY(grab((void**)&part, size_t(k) * chunks * 2 * sizeof(double)));
         TRY(grab((void**)&shift_sq, size_t(k) * sizeof(float)));
         TRY(grab((void**)&cctr, size_t(k) * sizeof(unsigned)));
         TRY(grab((void**)&rowpart, size_t(rowdist_grid(n)) * sizeof(double)));
@@ -382,13 +386,26 @@ struct Lloyd {
         return 0;
     }
 
+    int fused_step()
+    {
+        FusedArgs a{X, n, ld, cen[cur], cnorm, k, labels, psum, pcnt, st, fblocks};
+        HIP_TRY(launch_fused(a, s), "fused launch");
+        return 0;
+    }
+
     // One Lloyd step, old centres cen[cur] -> new centres cen[cur ^ 1].
     int enqueue_step(int iter, double tol, int flags)
     {
-        TRY(assign(cen[cur], st, 1));
-        TRY(update());
-        FinalizeArgs f{psum, pcnt, ug.R, k, d, ld, cen[cur], cen[cur ^ 1], cnorm, sums, counts, part, shift_sq,
-                       cctr, st, iter, tol, flags};
+        int R = ug.R;
+        if (fblocks > 0) {
+            TRY(fused_step());
+            R = fblocks;
+        } else {
+            TRY(assign(cen[cur], st, 1));
+            TRY(update());
+        }
+        FinalizeArgs f{psum, pcnt, R, k, d, ld, cen[cur], cen[cur ^ 1], cnorm, sums, counts, part, shift_sq,
+                       cctr, st, iter, tol, flags, finalize_cols(R)};
         HIP_TRY(launch_finalize(f, s), "finalize launch");
         cur ^= 1;
         return 0;
@@ -852,9 +869,9 @@ int skmetal_hip_lloyd_time_kernels(skmetal_hip_lloyd* h, size_t reps, float* ms_
     int rc = 0;
     TRY(L.assign(L.cen[L.cur], nullptr, 0));  // labels for the update timing
     hipEventRecord(e0, L.s);
-    for (size_t r = 0; r < reps && rc == 0; ++r) rc = L.assign(L.cen[L.cur], nullptr, 0);
+    for (size_t r = 0; r < reps && rc == 0; ++r) rc = L.fblocks > 0 ? L.fused_step() : L.assign(L.cen[L.cur], nullptr, 0);
     hipEventRecord(e1, L.s);
-    for (size_t r = 0; r < reps && rc == 0; ++r) rc = L.update();
+    for (size_t r = 0; r < reps && rc == 0 && L.fblocks == 0; ++r) rc = L.update();
     hipEventRecord(e2, L.s);
     hipError_t e = hipEventSynchronize(e2);
     if (rc == 0 && e != hipSuccess) rc = hip_fail(e, "hipEventSynchronize");
@@ -867,6 +884,14 @@ int skmetal_hip_lloyd_time_kernels(skmetal_hip_lloyd* h, size_t reps, float* ms_
     hipEventDestroy(e1);
     hipEventDestroy(e2);
     return rc;
+}
+
+int skmetal_hip_lloyd_info(skmetal_hip_lloyd* h, int* fused, int* partials)
+{
+    if (!h) return fail(SKMETAL_EINVAL, "null pointer argument");
+    if (fused) *fused = h->L.fblocks > 0;
+    if (partials) *partials = h->L.fblocks > 0 ? h->L.fblocks : h->L.ug.R;
+    return 0;
 }
 
 int skmetal_hip_lloyd_get_centers(skmetal_hip_lloyd* h, float* C)

@@ -230,3 +230,25 @@ def test_c2_fixed_iterations_inertia_monotone(bridge):
             v = h.inertia()  # labels of this E-step against the centres of its M-step
             assert v <= prev * (1 + 1e-6)
             prev = v
+
+
+@pytest.mark.parametrize("n,d,k,blobs", [(3000, 1, 5, 4), (5000, 2000, 30, 12), (20000, 64, 300, 90),
+                                         (8000, 129, 130, 60), (50000, 32, 8, 8)])
+def test_lockstep_update_geometries(bridge, n, d, k, blobs):
+    """Column tiles (d > 1024), several cluster groups, d = 1, many row ranges."""
+    _say(f"lockstep geometry n={n} d={d} k={k}")
+    rng = np.random.default_rng(n + d + k)
+    cen = rng.uniform(-5, 5, (blobs, d))
+    X = (cen[rng.integers(0, blobs, n)] + rng.standard_normal((n, d))).astype(np.float32)
+    C0 = X[np.sort(rng.choice(n, k, replace=False))]
+    _lockstep_gpu(bridge, X, C0, 3, f"geometry {n}x{d} k={k}")
+
+
+def test_step_mode_selection(bridge):
+    """k <= 64 and padded d <= 128 take the fused E-step + sums kernel; others the generic path."""
+    with bridge.LloydHandle(500_000, 100, 50) as h:
+        assert h.info()["fused"] is True
+    with bridge.LloydHandle(10_000, 16, 100) as h:
+        assert h.info()["fused"] is False
+    with bridge.LloydHandle(10_000, 200, 8) as h:
+        assert h.info()["fused"] is False
