@@ -43,6 +43,22 @@ def _traffic_from_profile(name: str):
     return float(m.group(1)) if m else None
 
 
+def copy_probe(mib: int) -> None:
+    """One device-to-device copy of `mib` MiB (hipMemcpy), a known-size kernel the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE counters are calibrated against."""
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so.7")  # the runtime libskmetal_hip.so already loaded
+    nbytes = ctypes.c_size_t(mib << 20)
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    assert hip.hipMalloc(ctypes.byref(a), nbytes) == 0 and hip.hipMalloc(ctypes.byref(b), nbytes) == 0
+    assert hip.hipMemset(a, 1, nbytes) == 0
+    assert hip.hipMemcpy(b, a, nbytes, 3) == 0  # hipMemcpyDeviceToDevice
+    assert hip.hipDeviceSynchronize() == 0
+    hip.hipFree(a)
+    hip.hipFree(b)
+
+
 def cpu_baseline(X, C0, iters: int, reps: int = 3):
     """sklearn Lloyd on this host: seconds per iteration (median of reps)."""
     try:
@@ -84,6 +100,8 @@ def main():
     ap.add_argument("--workload", default="c2")
     ap.add_argument("--no-cpu", action="store_true", help="skip the sklearn CPU baseline")
     ap.add_argument("--cpu-iters", type=int, default=8)
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
+                    help="also run one device-to-device copy of MIB MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -110,13 +128,18 @@ def main():
         ms = h.iterate(args.steps)
         wall = time.perf_counter() - t
         ms_assign, ms_update = h.time_kernels(max(20, args.steps // 2))
+        mode = h.info()
+    if args.calib_copy:
+        copy_probe(args.calib_copy)
 
     step_s = ms / 1e3 / args.steps
     it_s = 1.0 / step_s
     flops = 2.0 * n * k * d
     assign_s = ms_assign / 1e3
     achieved = flops / assign_s / 1e12
-    traffic = _traffic_from_profile(f"assign_{args.workload}_pmc.txt")
+    fused = mode["fused"]
+    kname = "k_fused" if fused else "k_assign"
+    traffic = _traffic_from_profile(f"{kname}_{args.workload}_pmc.txt")
 
     cpu = None if args.no_cpu else cpu_baseline(X, C0, args.cpu_iters)
 
@@ -139,9 +162,14 @@ def main():
         "dist_evals_per_s": round(n * k * it_s, 1),
         "wall_s_timed": round(wall, 4),
         "h2d_s": round(h2d_s, 4),
-        "kernels_ms": {"assign": round(ms_assign, 5), "update": round(ms_update, 5)},
+        "step_mode": ("fused: k_fused (E-step + per-cluster sums) + k_finalize" if fused
+                      else "k_assign + k_update + k_finalize"),
+        "partials": mode["partials"],
+        "kernels_ms": ({"k_fused": round(ms_assign, 5)} if fused
+                       else {"k_assign": round(ms_assign, 5), "k_update": round(ms_update, 5)}),
         "roofline": {
-            "kernel": "assign (fused ||c||^2-2x.c MFMA + argmin)",
+            "kernel": (f"{kname}: ||c||^2 - 2 x.c on fp32 MFMA + argmin"
+                       + (" + per-cluster sums" if fused else "")),
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": PEAK_FP32_MFMA_TFLOPS,

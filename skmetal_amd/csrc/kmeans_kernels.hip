@@ -233,18 +233,20 @@ hipError_t launch_assign(const AssignArgs& a, int num_cu, hipStream_t s)
 // ---------------------------------------------------------------------------
 //
 // When k <= 64 and ld <= 4*NQ <= 128, one kernel both assigns and
-// accumulates, reading X from HBM once per Lloyd step.  Each wave owns 64-row
-// tiles and stages the tile in its own LDS region (row r at r*xs floats, xs/4
+// accumulates, reading X from HBM once per Lloyd step.  A block (4 waves, one
+// per SIMD, one block per CU) works in rounds of 256 rows; wave w owns the
+// round's w-th 64-row tile and stages it in LDS (row r at r*XS floats, XS/4
 // odd so 16-byte reads of 8 different rows hit 8 different bank groups).
-//   E-step: exactly as k_assign, with lane l's operands read from row l.
-//   sums:   lane j owns cluster j; its running sum of the cluster's rows stays
-//           in registers (float4 S[NQ]).  ballot(label == j) hands lane j the
-//           bitmask of this tile's rows in cluster j, and every lane then walks
-//           its own bits, adding those rows from LDS -- all clusters in
-//           parallel, rows in increasing order, no atomics.
-// The next tile's rows are loaded into registers while this tile is
-// processed.  At the end the four waves' sums are combined in wave order, one
-// partial per block (one block per CU): bitwise reproducible.
+//   E-step: as k_assign, lane l's MFMA operands read from row l of the tile;
+//           the next round's rows are loaded into registers meanwhile.
+//   sums:   after a block barrier, wave w owns column slice w (QW float4s)
+//           for all 256 rows and lane j owns cluster j, keeping the slice of
+//           the cluster's running sum in registers.  Per-cluster row masks
+//           (ballot(label == j), one per tile) are exchanged through LDS and
+//           lane j walks its bits -- tile 0 rows ascending, then tile 1, ...
+//           -- adding its slice of each row.  No atomics.
+// Every (cluster, column) partial is owned by exactly one lane of the block
+// and written from registers at the end: bitwise reproducible.
 
 template <int KG, int NQ>
 __global__ __launch_bounds__(256, 1) void k_fused(const float* __restrict__ X, long n, int ld,
@@ -257,16 +259,17 @@ __global__ __launch_bounds__(256, 1) void k_fused(const float* __restrict__ X, l
     constexpr int CPC = 4 * KG;
     constexpr int SEG = 4 * NQ;
     constexpr int LS = SEG + 4;
-    constexpr int XS = (NQ & 1) ? SEG : SEG + 4;  // X tile row stride: XS/4 odd
-    extern __shared__ __attribute__((aligned(16))) float xt[];  // 4 waves x 64 rows x XS
+    constexpr int QW = (NQ + 3) / 4;                     // float4 columns per wave slice
+    constexpr int XQ = 4 * QW;                            // float4 columns staged per row
+    constexpr int XS = (XQ & 1) ? 4 * XQ : 4 * XQ + 4;   // row stride, XS/4 odd
+    extern __shared__ __attribute__((aligned(16))) float xt[];  // 4 tiles x 64 rows x XS
     __shared__ __attribute__((aligned(16))) float sC[CPC * LS];
     __shared__ float sN[CPC];
-    __shared__ int sCnt[4][64];
+    __shared__ unsigned long long sMask[4][CPC];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps descriptors scalar
     const int nq = ld >> 2;
-    float* xw = xt + wave * 64 * XS;
 
     for (int idx = tid; idx < CPC * NQ; idx += 256) {
         const int cl = idx / NQ;
@@ -279,42 +282,36 @@ __global__ __launch_bounds__(256, 1) void k_fused(const float* __restrict__ X, l
     __syncthreads();
 
     const int crow = lane < CPC ? lane : CPC - 1;
-    const long ntiles = (n + 63) / 64;
-    const long tstride = (long)gridDim.x * 4;
-    float4 S[NQ];
+    float* my_row = xt + (wave * 64 + lane) * XS;
+    float4 S[QW];
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) S[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int q = 0; q < QW; ++q) S[q] = make_float4(0.f, 0.f, 0.f, 0.f);
     int cnt = 0;
     float4 xn[NQ];
-    float* my_row = xw + lane * XS;
 
-    long t = (long)blockIdx.x * 4 + wave;
-    load_row_quads<NQ>(xn, X, t * 64, n, ld, 0, nq, lane);
-    while (t < ntiles) {
-        const long row = t * 64 + lane;
+    long rb = blockIdx.x;  // round = rows [rb*256, rb*256 + 256)
+    load_row_quads<NQ>(xn, X, (rb * 4 + wave) * 64, n, ld, 0, nq, lane);
+    while (rb * 256 < n) {
+        const long row = (rb * 4 + wave) * 64 + lane;
         const bool valid = row < n;
         const int old = valid ? labels[row] : -1;  // issued before the prefetch below
 #pragma unroll
         for (int q = 0; q < NQ; ++q) *reinterpret_cast<float4*>(my_row + 4 * q) = xn[q];
-        const long tn = t + tstride;
-        load_row_quads<NQ>(xn, X, tn * 64, n, ld, 0, nq, lane);  // empty when tn is past the end
+#pragma unroll
+        for (int q = NQ; q < XQ; ++q) *reinterpret_cast<float4*>(my_row + 4 * q) = make_float4(0.f, 0.f, 0.f, 0.f);
+        const long rn = rb + gridDim.x;
+        load_row_quads<NQ>(xn, X, (rn * 4 + wave) * 64, n, ld, 0, nq, lane);  // empty past the end
 
         v4f acc[KG];
 #pragma unroll
         for (int g = 0; g < KG; ++g) acc[g] = v4f{0.f, 0.f, 0.f, 0.f};
-        // operands of feature quad q+1 are read from LDS while quad q's MFMAs run
-        float4 xv = *reinterpret_cast<const float4*>(my_row);
-        float4 cv = *reinterpret_cast<const float4*>(&sC[crow * LS]);
         for (int q = 0; q < nq; ++q) {
-            const int qn = q + 1 < nq ? q + 1 : q;
-            const float4 xv2 = *reinterpret_cast<const float4*>(my_row + 4 * qn);
-            const float4 cv2 = *reinterpret_cast<const float4*>(&sC[crow * LS + 4 * qn]);
+            const float4 xv = *reinterpret_cast<const float4*>(my_row + 4 * q);
+            const float4 cv = *reinterpret_cast<const float4*>(&sC[crow * LS + 4 * q]);
             mfma_groups<KG>(acc, cv.x, xv.x);
             mfma_groups<KG>(acc, cv.y, xv.y);
             mfma_groups<KG>(acc, cv.z, xv.z);
             mfma_groups<KG>(acc, cv.w, xv.w);
-            xv = xv2;
-            cv = cv2;
         }
         float best = INFINITY;
         int bidx = 0;
@@ -333,49 +330,48 @@ __global__ __launch_bounds__(256, 1) void k_fused(const float* __restrict__ X, l
         if (valid) labels[row] = bidx;
         const unsigned long long mv = __ballot(valid && old != bidx);
         if (lane == 0 && mv != 0ull) atomicAdd(&st->changed, (int)__popcll(mv));
-
-        // cluster-owner sums: lane j collects the rows of cluster j
-        unsigned long long mine = 0ull;
 #pragma unroll
         for (int j = 0; j < CPC; ++j) {
             const unsigned long long m = __ballot(valid && bidx == j);
-            if (lane == j) mine = m;
+            if (lane == j) sMask[wave][j] = m;
         }
-        cnt += __popcll(mine);
-        while (mine != 0ull) {
-            const int r = __ffsll((long long)mine) - 1;
-            mine &= mine - 1ull;
-            const float* src = xw + r * XS;
+        __syncthreads();
+
+        // sums: wave = column slice, lane = cluster, rows in (tile, row) order
+        if (lane < CPC) {
 #pragma unroll
-            for (int q = 0; q < NQ; ++q) {
-                const float4 v = *reinterpret_cast<const float4*>(src + 4 * q);
-                S[q].x += v.x;
-                S[q].y += v.y;
-                S[q].z += v.z;
-                S[q].w += v.w;
+            for (int tw = 0; tw < 4; ++tw) {
+                unsigned long long m = sMask[tw][lane];
+                cnt += __popcll(m);
+                const float* tile = xt + tw * 64 * XS + wave * QW * 4;
+                while (m != 0ull) {
+                    const int r = __ffsll((long long)m) - 1;
+                    m &= m - 1ull;
+                    const float* src = tile + r * XS;
+#pragma unroll
+                    for (int q = 0; q < QW; ++q) {
+                        const float4 v = *reinterpret_cast<const float4*>(src + 4 * q);
+                        S[q].x += v.x;
+                        S[q].y += v.y;
+                        S[q].z += v.z;
+                        S[q].w += v.w;
+                    }
+                }
             }
         }
-        t = tn;
+        __syncthreads();
+        rb = rn;
     }
 
-    // combine the four waves' sums in wave order
-    __syncthreads();
     if (lane < k) {
+        float* dst = psum + ((long)blockIdx.x * k + lane) * ld;
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) *reinterpret_cast<float4*>(my_row + 4 * q) = S[q];
+        for (int q = 0; q < QW; ++q) {
+            const int c = 4 * (wave * QW + q);
+            if (c < ld) *reinterpret_cast<float4*>(dst + c) = S[q];
+        }
+        if (wave == 0) pcnt[(long)blockIdx.x * k + lane] = cnt;
     }
-    sCnt[wave][lane] = cnt;
-    __syncthreads();
-    const int wstride = 64 * XS;
-    for (int idx = tid; idx < k * ld; idx += 256) {
-        const int j = idx / ld;
-        const int c = idx - j * ld;
-        const int i = j * XS + c;
-        psum[(long)blockIdx.x * k * ld + idx] =
-            ((xt[i] + xt[wstride + i]) + xt[2 * wstride + i]) + xt[3 * wstride + i];
-    }
-    for (int j = tid; j < k; j += 256)
-        pcnt[(long)blockIdx.x * k + j] = sCnt[0][j] + sCnt[1][j] + sCnt[2][j] + sCnt[3][j];
 }
 
 typedef void (*fused_fn)(const float*, long, int, const float*, const float*, int, int*, float*, int*, LoopState*);
@@ -422,8 +418,8 @@ static fused_fn fused_kernel(int k, int ld)
 static size_t fused_dyn_lds(int k, int ld)
 {
     (void)k;
-    const int nq = fused_nq(ld);
-    const int xs = (nq & 1) ? 4 * nq : 4 * nq + 4;
+    const int xq = 4 * ((fused_nq(ld) + 3) / 4);
+    const int xs = (xq & 1) ? 4 * xq : 4 * xq + 4;
     return (size_t)4 * 64 * xs * sizeof(float);
 }
 
@@ -437,7 +433,7 @@ int fused_blocks(long n, int d, int k, int num_cu)
     if (f == nullptr) return 0;
     const size_t dyn = fused_dyn_lds(k, ld);
     const int nq = fused_nq(ld);
-    const size_t stat = (size_t)4 * ((k + 3) / 4) * (4 * nq + 4) * sizeof(float) + 64 * sizeof(float) + 1024;
+    const size_t stat = (size_t)4 * ((k + 3) / 4) * (4 * nq + 4) * sizeof(float) + 64 * sizeof(float) + 4 * 64 * 8;
     if (dyn + stat > 150 * 1024) return 0;
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(f), hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) !=
         hipSuccess) {
@@ -445,7 +441,7 @@ int fused_blocks(long n, int d, int k, int num_cu)
         return 0;
     }
     long blocks = num_cu;
-    const long tiles4 = ((n + 63) / 64 + 3) / 4;
+    const long tiles4 = (n + 255) / 256;
     if (blocks > tiles4) blocks = tiles4;
     return (int)(blocks < 1 ? 1 : blocks);
 }
