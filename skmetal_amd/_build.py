@@ -9,13 +9,13 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libskmetal_hip.so"
-SOURCES = ["kmeans_kernels.hip", "skmetal_hip.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -23,14 +23,20 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-fvisibility=hidden",
     "-Wall",
     # keep the compiler from emitting packed fp32 VALU ops (v_pk_*_f32)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # MFMA accumulators in VGPRs: keeps loop-carried accumulators in place
-    # instead of rotating them through AGPRs with v_accvgpr_* copies
-    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+]
+# MFMA accumulators in VGPRs: keeps the runtime-loop-carried accumulators of
+# the assign kernel in place instead of rotating them through AGPRs with
+# v_accvgpr_* copies
+VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+# (source, extra flags): the fused kernel keeps its accumulators in AGPRs
+SOURCES = [
+    ("kmeans_kernels.hip", VGPR_FORM),
+    ("fused_kernels.hip", []),
+    ("skmetal_hip.hip", VGPR_FORM),
 ]
 
 
@@ -41,18 +47,35 @@ def hipcc() -> str:
     return path
 
 
-def build(verbose: bool = False) -> Path:
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{ROOT / 'include'}", *[str(CSRC / s) for s in SOURCES], "-o", str(tmp)]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
+    return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+
+
+def _finish(proc, verbose):
+    out, _ = proc.communicate()
     noise = "is not a recognized feature for this target"
-    msgs = [ln for ln in (res.stdout + res.stderr).splitlines() if noise not in ln and ln.strip()]
-    if res.returncode != 0:
+    msgs = [ln for ln in out.splitlines() if noise not in ln and ln.strip()]
+    if proc.returncode != 0:
         raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
     if verbose and msgs:
         print("\n".join(msgs))
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every source to an object (in parallel), then link the library."""
+    tmp = LIB.with_suffix(".so.tmp")
+    with tempfile.TemporaryDirectory(prefix="skmetal_hip_build_") as bdir:
+        objs, procs = [], []
+        for src, extra in SOURCES:
+            obj = str(Path(bdir) / (Path(src).stem + ".o"))
+            objs.append(obj)
+            procs.append(_run([hipcc(), *HIPCC_FLAGS, *extra, f"-I{ROOT / 'include'}", "-c", str(CSRC / src),
+                               "-o", obj], verbose))
+        for p in procs:
+            _finish(p, verbose)
+        _finish(_run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)], verbose), verbose)
     os.replace(tmp, LIB)
     return LIB
 

@@ -1,0 +1,418 @@
+// fused_kernels.hip -- one-pass Lloyd step for small k*d on gfx950 (MI355X):
+// the E-step (sklearn/cluster/_k_means_lloyd.pyx:196-212) and the
+// per-cluster sums and counts of the M-step (:214-218) in one kernel that
+// reads X from HBM once per step.
+//
+// Used when k <= 64 and d <= 100; X's row stride ld is then padded (with
+// zeros) to 4*NQ floats for one of the compiled NQ, so the kernel's loops over
+// the row's float4s have no bounds.  The separate assign / update kernels
+// cover every other shape.
+//
+// Built without -amdgpu-mfma-vgpr-form: the MFMA accumulators live in AGPRs,
+// next to the VGPRs that hold the tile's rows.
+#include <math.h>
+#include <stdlib.h>
+
+#include "device.h"
+
+namespace skm {
+
+// A block is 8 waves, two per SIMD: MFMA waves 0-3 and walker waves 4-7.
+// MFMA wave p and walker wave 4+p form pair p and share one 64-row LDS tile;
+// pair p of block b handles tiles t = 4b + p + r*P (P = 4 * blocks) in
+// rounds r.  A wave cannot issue VALU work while its own MFMAs run, but the
+// other wave on the same SIMD can, so the walker's adds overlap the MFMA
+// wave's E-step.  The two waves of a pair hand tiles over through LDS flags;
+// there is no block barrier until the end.
+//
+//   MFMA wave  holds tile t's row in registers (one row per lane) and runs
+//              the E-step as k_assign does: x.c on v_mfma_f32_4x4x1_16b_f32
+//              (B = this lane's row, A = centres from LDS, lane j = cluster
+//              j), ||c||^2 - 2 x.c and the first minimum in the lane.  From
+//              chunk K on (once the walker has finished tile t - P) each
+//              chunk is written to the pair's LDS tile right after its MFMAs
+//              and its registers are reloaded with tile t + P, so the HBM
+//              reads spread over the E-step.  Chunks [0, K) are held in one
+//              of two register sets (by round parity), written out after the
+//              argmin and reloaded with tile t + 2P.  Then the tile's rows of
+//              each cluster go to LDS as bit masks (an LDS atomic OR of
+//              1 << lane into mask[label]; OR does not depend on the order the
+//              lanes land in) and the tile is flagged ready.
+//   walker     lane j adds the ready tile's rows of cluster j to its running
+//              sums of every column, in registers: the lowest WS bits of its
+//              mask become LDS row offsets (unused ones point at a row of
+//              zeros, so the walk is a fixed sequence), rows past the first
+//              WS by a loop; then it flags the tile walked.
+//
+// Rows are added in ascending row order per cluster (the first WS rows after
+// the others), tiles in round order, and the four walkers are combined in
+// wave order: bitwise reproducible.
+
+// Rows per (cluster, tile) walked without a loop: about the mean 64/k plus
+// three standard deviations for balanced clusters.
+template <int KG>
+__host__ __device__ constexpr int walk_steps()
+{
+    return KG >= 12 ? 6 : KG >= 8 ? 8 : KG >= 4 ? 12 : 16;
+}
+
+// Floats per LDS row for a row of NQ float4s: an odd number of float4s, so
+// 16-byte accesses of different rows at the same column fall in different
+// bank groups.
+__host__ __device__ constexpr int fused_stride(int nq) { return 4 * (nq | 1); }
+
+// Buffer descriptor over the rows of tile t (none past the last row: loads
+// there return 0 without a memory access).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const float* X, long t, long n, int ld)
+{
+    const long r0 = t * 64;
+    const long rows = n - r0 < 64 ? (n - r0 > 0 ? n - r0 : 0) : 64;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(X + (rows > 0 ? r0 * ld : 0)), (short)0,
+                                             (int)(rows * ld * 4), 0x00020000);
+}
+
+__device__ __forceinline__ float4 load_quad(__amdgpu_buffer_rsrc_t rs, int off)
+{
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+    return *reinterpret_cast<const float4*>(&v);
+}
+
+// Waits (polling LDS) until *flag >= v.  Flags are written by the other wave
+// of the pair; LDS operations of one wave are performed in issue order, so a
+// wave that sees the flag also sees the LDS writes issued before it.
+__device__ __forceinline__ void wait_flag(int* flag, int v)
+{
+    while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < v) __builtin_amdgcn_s_sleep(1);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // no LDS access moves above the wait
+}
+
+__device__ __forceinline__ void set_flag(int* flag, int v)
+{
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // every LDS access above stays above
+    __hip_atomic_store(flag, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// First minimum of d[0..N) with its index, as a pairwise tree in which the
+// lower-index side wins ties -- the same result as scanning j upward with a
+// strict '<' from +inf (NaN never wins: leaves are clamped to +inf first).
+template <int N>
+__device__ __forceinline__ int argmin_tree(float* d)
+{
+    int ix[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        d[j] = fminf(d[j], INFINITY);
+        ix[j] = j;
+    }
+#pragma unroll
+    for (int w = 1; w < N; w *= 2) {
+#pragma unroll
+        for (int j = 0; j + w < N; j += 2 * w) {
+            const bool take = d[j + w] < d[j];
+            d[j] = take ? d[j + w] : d[j];
+            ix[j] = take ? ix[j + w] : ix[j];
+        }
+    }
+    return ix[0];
+}
+
+template <int KG, int NQ>
+__global__ __launch_bounds__(512, 1) void k_fused(const float* __restrict__ X, long n, int ld,
+                                                  const float* __restrict__ C,
+                                                  const float* __restrict__ cnorm, int k,
+                                                  int* __restrict__ labels, float* __restrict__ psum,
+                                                  int* __restrict__ pcnt, LoopState* st)
+{
+    if (st->done != 0) return;
+    constexpr int CPC = 4 * KG;
+    constexpr int WS = walk_steps<KG>();
+    constexpr int XS = fused_stride(NQ);      // ld == 4 * NQ
+    constexpr int K = NQ >= 12 ? 6 : NQ / 2;  // chunks computed before the LDS tile is reused
+    constexpr int KA = K > 0 ? K : 1;
+    // LDS: centres [CPC x XS] | zero row [XS] | 4 pair tiles [64 x XS]
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    __shared__ unsigned long long sMask[4][64];
+    __shared__ int sCnt[4][64];
+    __shared__ __attribute__((aligned(16))) float sN[CPC];
+    __shared__ int sReady[4];   // tiles the MFMA wave has put in LDS
+    __shared__ int sWalked[4];  // tiles the walker has finished
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps descriptors scalar
+    const int pair = wave & 3;
+
+    float* sC = lds;
+    float* zrow = lds + CPC * XS;
+    float* tile = zrow + XS + pair * 64 * XS;
+    const int zoff = CPC * XS * 4;  // byte offsets from `lds`
+    const int toff = (CPC + 1 + pair * 64) * XS * 4;
+    const char* lbase = reinterpret_cast<const char*>(lds);
+
+    for (int idx = tid; idx < CPC * NQ; idx += 512) {
+        const int cl = idx / NQ;
+        const int q = idx - cl * NQ;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (cl < k) v = *reinterpret_cast<const float4*>(C + (long)cl * ld + 4 * q);
+        *reinterpret_cast<float4*>(&sC[cl * XS + 4 * q]) = v;
+    }
+    for (int i = tid; i < XS; i += 512) zrow[i] = 0.f;
+    // padding clusters get ||c||^2 = +inf: their distance never wins
+    for (int i = tid; i < CPC; i += 512) sN[i] = i < k ? cnorm[i] : INFINITY;
+    if (tid < 4) {
+        sReady[tid] = 0;
+        sWalked[tid] = 0;
+    }
+
+    const long ntiles = (n + 63) >> 6;
+    const long P = (long)gridDim.x * 4;
+    const long t0 = (long)blockIdx.x * 4 + pair;
+    const int rounds = t0 < ntiles ? (int)((ntiles - t0 + P - 1) / P) : 0;  // this pair's tiles
+    const int xoff = lane * ld * 4;  // this lane's row inside a tile of X
+    __syncthreads();
+
+    if (wave < 4) {
+        // MFMA wave.  Tile t's row: chunks [0, K) in pre (two sets, one per
+        // round parity, loaded a round ahead), chunks [K, NQ) in xv.
+        const char* cbase = reinterpret_cast<const char*>(sC + (lane < CPC ? lane : CPC - 1) * XS);
+        float* myrow = tile + lane * XS;
+        int changed = 0;
+        float4 preA[KA], preB[KA], xv[NQ - K];
+
+        auto round = [&](int r, float4* pre) {
+            const long t = t0 + (long)r * P;
+            const long nrow = n - t * 64 < 64 ? n - t * 64 : 64;
+            const bool valid = lane < nrow;
+            // the tile's labels; lanes past the last row fall outside the
+            // descriptor (the load returns 0, the store is dropped)
+            const __amdgpu_buffer_rsrc_t rl =
+                __builtin_amdgcn_make_buffer_rsrc(labels + t * 64, (short)0, (int)(nrow * 4), 0x00020000);
+            const int old = __builtin_amdgcn_raw_buffer_load_b32(rl, lane * 4, 0, 0);
+            const __amdgpu_buffer_rsrc_t rn = tile_rsrc(X, t + P, n, ld);
+            v4f acc[KG];
+#pragma unroll
+            for (int g = 0; g < KG; ++g) acc[g] = v4f{0.f, 0.f, 0.f, 0.f};
+            float4 cv = *reinterpret_cast<const float4*>(cbase);
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                if (q == K) wait_flag(&sWalked[pair], r);  // the walker is done with tile t - P
+                const float4 cvn = *reinterpret_cast<const float4*>(cbase + 16 * (q + 1 < NQ ? q + 1 : 0));
+                const float4 x = q < K ? pre[q < K ? q : 0] : xv[q < K ? 0 : q - K];
+                mfma_groups<KG>(acc, cv.x, x.x);
+                mfma_groups<KG>(acc, cv.y, x.y);
+                mfma_groups<KG>(acc, cv.z, x.z);
+                mfma_groups<KG>(acc, cv.w, x.w);
+                if (q >= K) {
+                    *reinterpret_cast<float4*>(myrow + 4 * q) = x;
+                    xv[q - K] = load_quad(rn, xoff + 16 * q);  // tile t + P
+                }
+                cv = cvn;
+            }
+            if (K == 0) wait_flag(&sWalked[pair], r);
+            // ||c||^2 - 2 x.c, first minimum wins (_k_means_lloyd.pyx:196-212)
+            float d[CPC];
+#pragma unroll
+            for (int g = 0; g < KG; ++g) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) d[4 * g + i] = fmaf(-2.0f, acc[g][i], sN[4 * g + i]);
+            }
+            const int bidx = argmin_tree<CPC>(d);
+            __builtin_amdgcn_raw_buffer_store_b32(bidx, rl, lane * 4, 0, 0);
+            changed += (int)__popcll(__ballot(valid && old != bidx));
+            // held chunks to LDS, then their registers take tile t + 2P
+            const __amdgpu_buffer_rsrc_t rn2 = tile_rsrc(X, t + 2 * P, n, ld);
+#pragma unroll
+            for (int q = 0; q < K; ++q) {
+                *reinterpret_cast<float4*>(myrow + 4 * q) = pre[q];
+                pre[q] = load_quad(rn2, xoff + 16 * q);
+            }
+            // the tile's rows of each cluster
+            if (lane < CPC) sMask[pair][lane] = 0ull;
+            if (valid) atomicOr(&sMask[pair][bidx], 1ull << lane);
+            set_flag(&sReady[pair], r + 1);
+        };
+
+        {
+            const __amdgpu_buffer_rsrc_t r0 = tile_rsrc(X, t0, n, ld);
+            const __amdgpu_buffer_rsrc_t r1 = tile_rsrc(X, t0 + P, n, ld);
+#pragma unroll
+            for (int q = 0; q < K; ++q) preA[q] = load_quad(r0, xoff + 16 * q);
+#pragma unroll
+            for (int q = K; q < NQ; ++q) xv[q - K] = load_quad(r0, xoff + 16 * q);
+#pragma unroll
+            for (int q = 0; q < K; ++q) preB[q] = load_quad(r1, xoff + 16 * q);
+        }
+        int r = 0;
+        for (; r + 1 < rounds; r += 2) {
+            round(r, preA);
+            round(r + 1, preB);
+        }
+        if (r < rounds) round(r, preA);
+        if (lane == 0 && changed != 0) atomicAdd(&st->changed, changed);
+        __syncthreads();  // every pair's walker is done: the tile area is free
+        __syncthreads();  // the walkers' sums are in LDS
+    } else {
+        // walker
+        float4 S[NQ];
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) S[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+        int cnt = 0;
+        for (int r = 0; r < rounds; ++r) {
+            wait_flag(&sReady[pair], r + 1);
+            unsigned long long m = lane < CPC ? sMask[pair][lane] : 0ull;
+            cnt += (int)__popcll(m);
+            int ro[WS];
+#pragma unroll
+            for (int s = 0; s < WS; ++s) {
+                const int rr = __ffsll((long long)m) - 1;
+                ro[s] = m != 0ull ? toff + rr * XS * 4 : zoff;
+                m &= m - 1ull;
+            }
+            // rows past the first WS (ascending) first, then the first WS:
+            // a fixed order either way
+            if (__ballot(m != 0ull) != 0ull) {
+                while (m != 0ull) {
+                    const int rr = __ffsll((long long)m) - 1;
+                    m &= m - 1ull;
+                    const char* src = lbase + toff + rr * XS * 4;
+#pragma unroll
+                    for (int q = 0; q < NQ; ++q) {
+                        const float4 v = *reinterpret_cast<const float4*>(src + 16 * q);
+                        S[q].x += v.x;
+                        S[q].y += v.y;
+                        S[q].z += v.z;
+                        S[q].w += v.w;
+                    }
+                }
+            }
+            float4 wv[WS];
+#pragma unroll
+            for (int s = 0; s < WS; ++s) wv[s] = *reinterpret_cast<const float4*>(lbase + ro[s]);
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                float4 wn[WS];
+                if (q + 1 < NQ) {
+#pragma unroll
+                    for (int s = 0; s < WS; ++s) wn[s] = *reinterpret_cast<const float4*>(lbase + ro[s] + 16 * (q + 1));
+                }
+#pragma unroll
+                for (int s = 0; s < WS; ++s) {
+                    S[q].x += wv[s].x;
+                    S[q].y += wv[s].y;
+                    S[q].z += wv[s].z;
+                    S[q].w += wv[s].w;
+                }
+                if (q + 1 < NQ) {
+#pragma unroll
+                    for (int s = 0; s < WS; ++s) wv[s] = wn[s];
+                }
+            }
+            set_flag(&sWalked[pair], r + 1);
+        }
+        __syncthreads();  // every pair is done with its tile
+        // this walker's sums, combined below in walker order: [4][CPC][ld]
+        // over the tile area
+        float* red = zrow + XS;
+        if (lane < CPC) {
+            float* dst = red + (pair * CPC + lane) * ld;
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) *reinterpret_cast<float4*>(dst + 4 * q) = S[q];
+            sCnt[pair][lane] = cnt;
+        }
+        __syncthreads();
+    }
+    const int kl = k * ld;
+    const float* red = zrow + XS;
+    float* out = psum + (long)blockIdx.x * kl;
+    for (int i = tid; i < kl; i += 512) {
+        const int j = i / ld;
+        const int col = i - j * ld;
+        const float* p = red + j * ld + col;
+        out[i] = ((p[0] + p[CPC * ld]) + p[2 * CPC * ld]) + p[3 * CPC * ld];
+    }
+    if (tid < k) pcnt[(long)blockIdx.x * k + tid] = ((sCnt[0][tid] + sCnt[1][tid]) + sCnt[2][tid]) + sCnt[3][tid];
+}
+
+typedef void (*fused_fn)(const float*, long, int, const float*, const float*, int, int*, float*, int*, LoopState*);
+
+template <int NQ, int... KGs>
+struct FusedTable {
+    static fused_fn get(int kg)
+    {
+        fused_fn f = nullptr;
+        ((kg == KGs ? (f = &k_fused<KGs, NQ>, 0) : 0), ...);
+        return f;
+    }
+};
+
+template <int NQ>
+static fused_fn pick_fused(int kg)
+{
+    return FusedTable<NQ, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16>::get(kg);
+}
+
+// Compiled row sizes (float4s); ld = 4 * NQ.
+static fused_fn fused_kernel(int k, int ld)
+{
+    if (k < 1 || k > 64) return nullptr;
+    const int kg = (k + 3) / 4;
+    switch (ld) {
+    case 4: return pick_fused<1>(kg);
+    case 8: return pick_fused<2>(kg);
+    case 16: return pick_fused<4>(kg);
+    case 32: return pick_fused<8>(kg);
+    case 48: return pick_fused<12>(kg);
+    case 64: return pick_fused<16>(kg);
+    case 80: return pick_fused<20>(kg);
+    case 100: return pick_fused<25>(kg);
+    default: return nullptr;
+    }
+}
+
+static size_t fused_dyn_lds(int k, int ld)
+{
+    const int cpc = 4 * ((k + 3) / 4);
+    return (size_t)(cpc + 1 + 4 * 64) * fused_stride(ld / 4) * sizeof(float);
+}
+
+int fused_ld(int d, int k)
+{
+    // SKMETAL_HIP_FUSED=0 selects the separate assign/update kernels for every shape
+    const char* env = getenv("SKMETAL_HIP_FUSED");
+    if (env != nullptr && env[0] == '0') return 0;
+    if (d < 1 || k < 1 || k > 64) return 0;
+    static const int kLds[] = {4, 8, 16, 32, 48, 64, 80, 100};
+    for (int ld : kLds) {
+        if (ld < d) continue;
+        fused_fn f = fused_kernel(k, ld);
+        const size_t dyn = fused_dyn_lds(k, ld);
+        const size_t stat = 4 * 64 * (sizeof(unsigned long long) + sizeof(int)) + 64 * sizeof(float);  // sMask, sCnt, sN
+        if (f == nullptr || dyn + stat > 160 * 1024) return 0;
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(f), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)dyn) != hipSuccess) {
+            (void)hipGetLastError();
+            return 0;
+        }
+        return ld;
+    }
+    return 0;
+}
+
+int fused_blocks(long n, int ld, int k, int num_cu)
+{
+    if (fused_kernel(k, ld) == nullptr) return 0;
+    const long tiles = (n + 63) / 64;
+    long blocks = (tiles + 3) / 4;
+    if (blocks > num_cu) blocks = num_cu;
+    return (int)(blocks < 1 ? 1 : blocks);
+}
+
+hipError_t launch_fused(const FusedArgs& a, hipStream_t s)
+{
+    fused_fn f = fused_kernel(a.k, a.ld);
+    if (f == nullptr || a.blocks < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(f, dim3(a.blocks), dim3(512), fused_dyn_lds(a.k, a.ld), s, a.X, a.n, a.ld, a.C, a.cnorm, a.k,
+                       a.labels, a.psum, a.pcnt, a.state);
+    return hipGetLastError();
+}
+
+}  // namespace skm

@@ -25,8 +25,8 @@ struct LoopState {
     int last_changed;  // `changed` of the last finalised iteration
     int halt_iter;     // iteration index at which `done` was set
     int n_empty;       // empty clusters found by the last finalise
-    unsigned global_ctr;  // finalise: clusters completed in this iteration
     unsigned rowdist_ctr; // row-distance reduction: blocks completed
+    unsigned pad_;
     double shift_tot;  // sum_j ||c_j_new - c_j_old||^2 of the last step
     double inertia;    // result of the last row-distance reduction
 };
@@ -47,7 +47,7 @@ struct AssignArgs {
 };
 hipError_t launch_assign(const AssignArgs& a, int num_cu, hipStream_t s);
 
-// Fused E-step + per-cluster sums (k <= 64, ld <= 128, tables fit in LDS).
+// Fused E-step + per-cluster sums (k <= 64, d <= 100).
 struct FusedArgs {
     const float* X; long n; int ld;
     const float* C; const float* cnorm; int k;
@@ -57,9 +57,11 @@ struct FusedArgs {
     LoopState* state;      // required: early exit and change counting
     int blocks;
 };
-// Number of blocks (= partials) of the fused kernel for this shape, or 0 when
-// the shape does not qualify.
-int fused_blocks(long n, int d, int k, int num_cu);
+// Row stride (floats) X must have for the fused kernel, or 0 when (d, k) does
+// not qualify; the pad columns are zero.
+int fused_ld(int d, int k);
+// Number of blocks (= partials) of the fused kernel for n rows of stride ld.
+int fused_blocks(long n, int ld, int k, int num_cu);
 hipError_t launch_fused(const FusedArgs& a, hipStream_t s);
 
 struct UpdateArgs {
@@ -80,11 +82,11 @@ struct FinalizeArgs {
     int* counts;           // [k]
     double* part;          // [k x nch x 2]
     float* shift_sq;       // [k]
-    unsigned* cluster_ctr; // [k], zero between launches
     LoopState* state;
     int iter; double tol; int flags;
     int cw;                // columns per finalize block: finalize_cols(R)
 };
+// Two launches: per-(cluster, column chunk) totals, then the loop decision.
 hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t s);
 // A finalize block is 256 threads = cw columns x (256/cw) partial-sum lanes,
 // sized so that each thread reads at most about 8 of the R partials.

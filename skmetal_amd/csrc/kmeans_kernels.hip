@@ -19,11 +19,9 @@
 #include <math.h>
 #include <stdlib.h>
 
-#include "internal.h"
+#include "device.h"
 
 namespace skm {
-
-typedef float v4f __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
 // assign
@@ -39,35 +37,6 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 //
 // Centres are staged through LDS per (chunk, feature segment); X rows are read
 // straight from HBM into registers (one row per lane, 16-byte loads).
-
-// Loads NQ float4s of this lane's row (row0 + lane) starting at feature f0,
-// with no branches: the buffer descriptor covers exactly the valid rows, so a
-// lane past the last row, and any float4 at or past `nq`, reads 0 without a
-// memory access.  All NQ loads stay in flight together.
-template <int NQ>
-__device__ __forceinline__ void load_row_quads(float4* xv, const float* X, long row0, long n, int ld, int f0,
-                                               int nq, int lane)
-{
-    const long rows = n - row0 < 64 ? (n - row0 > 0 ? n - row0 : 0) : 64;
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(X + (rows > 0 ? row0 * ld + f0 : 0)), (short)0, (int)(rows * ld * 4), 0x00020000);
-    const int base = lane * ld * 4;
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-        const int off = q < nq ? base + 16 * q : 0x7ffffff0;
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
-        xv[q] = *reinterpret_cast<const float4*>(&v);
-    }
-}
-
-template <int KG, int G = 0>
-__device__ __forceinline__ void mfma_groups(v4f* acc, float a, float b)
-{
-    if constexpr (G < KG) {
-        acc[G] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, acc[G], 4, G, 0);
-        mfma_groups<KG, G + 1>(acc, a, b);
-    }
-}
 
 template <int KG, int NQ>
 __global__ __launch_bounds__(256, 1) void k_assign(const float* __restrict__ X, long n, int ld,
@@ -225,233 +194,6 @@ hipError_t launch_assign(const AssignArgs& a, int num_cu, hipStream_t s)
     if (blocks < 1) blocks = 1;
     hipLaunchKernelGGL(f, dim3((unsigned)blocks), dim3(256), 0, s, a.X, a.n, a.ld, a.C, a.cnorm, a.k, a.labels,
                        a.state, a.count_changes);
-    return hipGetLastError();
-}
-
-// ---------------------------------------------------------------------------
-// fused Lloyd step for small k*d: E-step and per-cluster sums in one pass
-// ---------------------------------------------------------------------------
-//
-// When k <= 64 and ld <= 4*NQ <= 128, one kernel both assigns and
-// accumulates, reading X from HBM once per Lloyd step.  A block (4 waves, one
-// per SIMD, one block per CU) works in rounds of 256 rows; wave w owns the
-// round's w-th 64-row tile and stages it in LDS (row r at r*XS floats, XS/4
-// odd so 16-byte reads of 8 different rows hit 8 different bank groups).
-//   E-step: as k_assign, lane l's MFMA operands read from row l of the tile;
-//           the next round's rows are loaded into registers meanwhile.
-//   sums:   after a block barrier, wave w owns column slice w (QW float4s)
-//           for all 256 rows and lane j owns cluster j, keeping the slice of
-//           the cluster's running sum in registers.  Per-cluster row masks
-//           (ballot(label == j), one per tile) are exchanged through LDS and
-//           lane j walks its bits -- tile 0 rows ascending, then tile 1, ...
-//           -- adding its slice of each row.  No atomics.
-// Every (cluster, column) partial is owned by exactly one lane of the block
-// and written from registers at the end: bitwise reproducible.
-
-template <int KG, int NQ>
-__global__ __launch_bounds__(256, 1) void k_fused(const float* __restrict__ X, long n, int ld,
-                                                  const float* __restrict__ C,
-                                                  const float* __restrict__ cnorm, int k,
-                                                  int* __restrict__ labels, float* __restrict__ psum,
-                                                  int* __restrict__ pcnt, LoopState* st)
-{
-    if (st->done != 0) return;
-    constexpr int CPC = 4 * KG;
-    constexpr int SEG = 4 * NQ;
-    constexpr int LS = SEG + 4;
-    constexpr int QW = (NQ + 3) / 4;                     // float4 columns per wave slice
-    constexpr int XQ = 4 * QW;                            // float4 columns staged per row
-    constexpr int XS = (XQ & 1) ? 4 * XQ : 4 * XQ + 4;   // row stride, XS/4 odd
-    extern __shared__ __attribute__((aligned(16))) float xt[];  // 4 tiles x 64 rows x XS
-    __shared__ __attribute__((aligned(16))) float sC[CPC * LS];
-    __shared__ float sN[CPC];
-    __shared__ unsigned long long sMask[4][CPC];
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps descriptors scalar
-    const int nq = ld >> 2;
-
-    for (int idx = tid; idx < CPC * NQ; idx += 256) {
-        const int cl = idx / NQ;
-        const int q = idx - cl * NQ;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (cl < k && q < nq) v = *reinterpret_cast<const float4*>(C + (long)cl * ld + 4 * q);
-        *reinterpret_cast<float4*>(&sC[cl * LS + 4 * q]) = v;
-    }
-    for (int i = tid; i < CPC; i += 256) sN[i] = i < k ? cnorm[i] : 0.f;
-    __syncthreads();
-
-    const int crow = lane < CPC ? lane : CPC - 1;
-    float* my_row = xt + (wave * 64 + lane) * XS;
-    float4 S[QW];
-#pragma unroll
-    for (int q = 0; q < QW; ++q) S[q] = make_float4(0.f, 0.f, 0.f, 0.f);
-    int cnt = 0;
-    float4 xn[NQ];
-
-    long rb = blockIdx.x;  // round = rows [rb*256, rb*256 + 256)
-    load_row_quads<NQ>(xn, X, (rb * 4 + wave) * 64, n, ld, 0, nq, lane);
-    while (rb * 256 < n) {
-        const long row = (rb * 4 + wave) * 64 + lane;
-        const bool valid = row < n;
-        const int old = valid ? labels[row] : -1;  // issued before the prefetch below
-#pragma unroll
-        for (int q = 0; q < NQ; ++q) *reinterpret_cast<float4*>(my_row + 4 * q) = xn[q];
-#pragma unroll
-        for (int q = NQ; q < XQ; ++q) *reinterpret_cast<float4*>(my_row + 4 * q) = make_float4(0.f, 0.f, 0.f, 0.f);
-        const long rn = rb + gridDim.x;
-        load_row_quads<NQ>(xn, X, (rn * 4 + wave) * 64, n, ld, 0, nq, lane);  // empty past the end
-
-        v4f acc[KG];
-#pragma unroll
-        for (int g = 0; g < KG; ++g) acc[g] = v4f{0.f, 0.f, 0.f, 0.f};
-        for (int q = 0; q < nq; ++q) {
-            const float4 xv = *reinterpret_cast<const float4*>(my_row + 4 * q);
-            const float4 cv = *reinterpret_cast<const float4*>(&sC[crow * LS + 4 * q]);
-            mfma_groups<KG>(acc, cv.x, xv.x);
-            mfma_groups<KG>(acc, cv.y, xv.y);
-            mfma_groups<KG>(acc, cv.z, xv.z);
-            mfma_groups<KG>(acc, cv.w, xv.w);
-        }
-        float best = INFINITY;
-        int bidx = 0;
-#pragma unroll
-        for (int g = 0; g < KG; ++g) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int j = 4 * g + r;
-                const float dist = fmaf(-2.0f, acc[g][r], sN[j]);
-                if (j < k && dist < best) {
-                    best = dist;
-                    bidx = j;
-                }
-            }
-        }
-        if (valid) labels[row] = bidx;
-        const unsigned long long mv = __ballot(valid && old != bidx);
-        if (lane == 0 && mv != 0ull) atomicAdd(&st->changed, (int)__popcll(mv));
-#pragma unroll
-        for (int j = 0; j < CPC; ++j) {
-            const unsigned long long m = __ballot(valid && bidx == j);
-            if (lane == j) sMask[wave][j] = m;
-        }
-        __syncthreads();
-
-        // sums: wave = column slice, lane = cluster, rows in (tile, row) order
-        if (lane < CPC) {
-#pragma unroll
-            for (int tw = 0; tw < 4; ++tw) {
-                unsigned long long m = sMask[tw][lane];
-                cnt += __popcll(m);
-                const float* tile = xt + tw * 64 * XS + wave * QW * 4;
-                while (m != 0ull) {
-                    const int r = __ffsll((long long)m) - 1;
-                    m &= m - 1ull;
-                    const float* src = tile + r * XS;
-#pragma unroll
-                    for (int q = 0; q < QW; ++q) {
-                        const float4 v = *reinterpret_cast<const float4*>(src + 4 * q);
-                        S[q].x += v.x;
-                        S[q].y += v.y;
-                        S[q].z += v.z;
-                        S[q].w += v.w;
-                    }
-                }
-            }
-        }
-        __syncthreads();
-        rb = rn;
-    }
-
-    if (lane < k) {
-        float* dst = psum + ((long)blockIdx.x * k + lane) * ld;
-#pragma unroll
-        for (int q = 0; q < QW; ++q) {
-            const int c = 4 * (wave * QW + q);
-            if (c < ld) *reinterpret_cast<float4*>(dst + c) = S[q];
-        }
-        if (wave == 0) pcnt[(long)blockIdx.x * k + lane] = cnt;
-    }
-}
-
-typedef void (*fused_fn)(const float*, long, int, const float*, const float*, int, int*, float*, int*, LoopState*);
-
-template <int NQ, int... KGs>
-struct FusedTable {
-    static fused_fn get(int kg)
-    {
-        fused_fn f = nullptr;
-        ((kg == KGs ? (f = &k_fused<KGs, NQ>, 0) : 0), ...);
-        return f;
-    }
-};
-
-template <int NQ>
-static fused_fn pick_fused(int kg)
-{
-    return FusedTable<NQ, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16>::get(kg);
-}
-
-static int fused_nq(int ld)
-{
-    const int q = ld / 4;
-    return q <= 4 ? 4 : ((q + 3) / 4) * 4;
-}
-
-static fused_fn fused_kernel(int k, int ld)
-{
-    if (k > 64 || ld > 128) return nullptr;
-    const int kg = (k + 3) / 4;
-    switch (fused_nq(ld)) {
-    case 4: return pick_fused<4>(kg);
-    case 8: return pick_fused<8>(kg);
-    case 12: return pick_fused<12>(kg);
-    case 16: return pick_fused<16>(kg);
-    case 20: return pick_fused<20>(kg);
-    case 24: return pick_fused<24>(kg);
-    case 28: return pick_fused<28>(kg);
-    case 32: return pick_fused<32>(kg);
-    default: return nullptr;
-    }
-}
-
-static size_t fused_dyn_lds(int k, int ld)
-{
-    (void)k;
-    const int xq = 4 * ((fused_nq(ld) + 3) / 4);
-    const int xs = (xq & 1) ? 4 * xq : 4 * xq + 4;
-    return (size_t)4 * 64 * xs * sizeof(float);
-}
-
-int fused_blocks(long n, int d, int k, int num_cu)
-{
-    // SKMETAL_HIP_FUSED=0 selects the separate assign/update kernels for every shape
-    const char* env = getenv("SKMETAL_HIP_FUSED");
-    if (env != nullptr && env[0] == '0') return 0;
-    const int ld = (d + 3) & ~3;
-    fused_fn f = fused_kernel(k, ld);
-    if (f == nullptr) return 0;
-    const size_t dyn = fused_dyn_lds(k, ld);
-    const int nq = fused_nq(ld);
-    const size_t stat = (size_t)4 * ((k + 3) / 4) * (4 * nq + 4) * sizeof(float) + 64 * sizeof(float) + 4 * 64 * 8;
-    if (dyn + stat > 150 * 1024) return 0;
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(f), hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) !=
-        hipSuccess) {
-        (void)hipGetLastError();
-        return 0;
-    }
-    long blocks = num_cu;
-    const long tiles4 = (n + 255) / 256;
-    if (blocks > tiles4) blocks = tiles4;
-    return (int)(blocks < 1 ? 1 : blocks);
-}
-
-hipError_t launch_fused(const FusedArgs& a, hipStream_t s)
-{
-    fused_fn f = fused_kernel(a.k, a.ld);
-    if (f == nullptr || a.blocks < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(f, dim3(a.blocks), dim3(256), fused_dyn_lds(a.k, a.ld), s, a.X, a.n, a.ld, a.C, a.cnorm, a.k,
-                       a.labels, a.psum, a.pcnt, a.state);
     return hipGetLastError();
 }
 
@@ -617,129 +359,157 @@ hipError_t launch_update(const UpdateArgs& a, const UpdateGeom& g, hipStream_t s
 }
 
 // ---------------------------------------------------------------------------
-// finalize
+// finalize: two kernels, no cross-block atomics or fences
 // ---------------------------------------------------------------------------
 //
-// Block (j, cc) reduces the R partial sums of cluster j, columns
-// [32cc, 32cc+32), in a fixed order (8 interleaved fp64 lanes per column, then
-// those 8 in order).  The last block to finish cluster j folds the per-chunk
-// shift^2 and ||c||^2 partials; the last cluster to finish evaluates the
-// loop's stopping rules (_kmeans.py:717-732) and flags empty clusters.
+// k_finalize_cols, block (j, cc): the R partial sums of cluster j, columns
+// [cc*CW, cc*CW + CW), reduced in a fixed order -- each of the RS lanes of a
+// column adds partials rs, rs+RS, ... in fp64, the lanes of a wave are
+// combined by an xor butterfly (every lane ends with bitwise the same value)
+// and the four waves in wave order -- then the new centre, and the chunk's
+// shift^2 and ||c||^2 partials.
+// k_finalize_loop, one block: folds each cluster's chunk partials in chunk
+// order and evaluates the loop's stopping rules (_kmeans.py:717-732).
+// The kernel boundary makes the first kernel's stores visible to the second;
+// agent-scope fences inside one kernel would write back and invalidate the
+// L2 of every XCD for each block.
 
+// Sum over the 64 lanes of a wave by xor butterfly; all lanes get the total.
 template <typename T>
-__device__ __forceinline__ T coherent_load(const T* p)
+__device__ __forceinline__ T wave_sum(T v)
 {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+    return v;
 }
 
-__global__ __launch_bounds__(256) void k_finalize(FinalizeArgs a)
+// Sum over a 256-thread block in a fixed order (wave butterflies, then waves
+// 0..3); every thread gets the total.  `sh` holds 4 elements; the call ends
+// with a barrier, so it may be reused right after.
+template <typename T>
+__device__ __forceinline__ T block_sum(T v, T* sh)
 {
-    LoopState* st = a.state;
-    if (st->done != 0) return;
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const T t = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+    __syncthreads();
+    return t;
+}
+
+constexpr int kFinUnroll = 8;  // partials in flight per thread
+
+__global__ __launch_bounds__(256) void k_finalize_cols(FinalizeArgs a)
+{
+    if (a.state->done != 0) return;
     const int j = blockIdx.x;
     const int cc = blockIdx.y;
     const int nch = gridDim.y;
     const int tid = threadIdx.x;
-    const int CW = a.cw;            // columns per block
-    const int RS = 256 / CW;        // partial-sum lanes per column (power of two)
+    const int CW = a.cw;            // columns per block (power of two)
+    const int RS = 256 / CW;        // partial-sum lanes per column
     const int cl = tid % CW;
     const int rs = tid / CW;
     const int col = cc * CW + cl;
     __shared__ double red[256];
-    __shared__ int cred[256];
-    __shared__ double pr[2][256];
+    __shared__ double shd[2][4];
+    __shared__ int shi[4];
 
     int cnt = 0;
     for (int r = tid; r < a.R; r += 256) cnt += a.pcnt[(long)r * a.k + j];
-    cred[tid] = cnt;
     double s = 0.0;
-    if (col < a.d)
-        for (int r = rs; r < a.R; r += RS) s += (double)a.psum[((long)r * a.k + j) * a.ld + col];
+    if (col < a.d) {
+        const float* src = a.psum + (long)j * a.ld + col;
+        const long step = (long)a.k * a.ld;
+        for (int r0 = rs; r0 < a.R; r0 += kFinUnroll * RS) {
+            float v[kFinUnroll];
+#pragma unroll
+            for (int u = 0; u < kFinUnroll; ++u) {
+                const int r = r0 + u * RS;
+                v[u] = src[(long)(r < a.R ? r : a.R - 1) * step];  // unconditional: all in flight
+            }
+#pragma unroll
+            for (int u = 0; u < kFinUnroll; ++u)
+                if (r0 + u * RS < a.R) s += (double)v[u];
+        }
+    }
+    // lanes of one column inside a wave: xor offsets CW, 2CW, ... < 64
+    for (int off = CW; off < 64; off <<= 1) s += __shfl_xor(s, off, 64);
     red[tid] = s;
-    __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if (tid < w) cred[tid] += cred[tid + w];
-        __syncthreads();
-    }
-    // fixed-order tree over the RS lanes of each column
-    for (int w = RS / 2; w > 0; w >>= 1) {
-        if (rs < w) red[tid] += red[tid + w * CW];
-        __syncthreads();
-    }
-    const int count = cred[0];
-    if (rs == 0) {
-        double sq = 0.0, nrm = 0.0;
-        if (col < a.d) {
-            const double tot = red[cl];
-            a.sums[(long)j * a.ld + col] = tot;
-            if (count > 0) {
-                const float cn = (float)(tot / (double)count);
-                a.C_new[(long)j * a.ld + col] = cn;
-                const double df = (double)cn - (double)a.C_old[(long)j * a.ld + col];
-                sq = df * df;
-                nrm = (double)cn * (double)cn;
-            }
+    const int count = block_sum(cnt, shi);  // its barrier also publishes red[]
+
+    double sq = 0.0, nrm = 0.0;
+    if (tid < CW && col < a.d) {
+        const int stride = CW < 64 ? 64 : CW;
+        double tot = 0.0;
+        for (int t = cl; t < 256; t += stride) tot += red[t];
+        a.sums[(long)j * a.ld + col] = tot;
+        if (count > 0) {
+            const float cn = (float)(tot / (double)count);
+            a.C_new[(long)j * a.ld + col] = cn;
+            const double df = (double)cn - (double)a.C_old[(long)j * a.ld + col];
+            sq = df * df;
+            nrm = (double)cn * (double)cn;
         }
-        pr[0][cl] = sq;
-        pr[1][cl] = nrm;
     }
-    __syncthreads();
+    sq = block_sum(sq, shd[0]);
+    nrm = block_sum(nrm, shd[1]);
     if (tid == 0) {
-        double ssq = 0.0, snr = 0.0;
-        for (int t = 0; t < CW; ++t) {
-            ssq += pr[0][t];
-            snr += pr[1][t];
+        a.part[((long)j * nch + cc) * 2 + 0] = sq;
+        a.part[((long)j * nch + cc) * 2 + 1] = nrm;
+        if (cc == 0) a.counts[j] = count;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_finalize_loop(FinalizeArgs a, int nch)
+{
+    LoopState* st = a.state;
+    if (st->done != 0) return;
+    const int tid = threadIdx.x;
+    __shared__ double shd[4];
+    __shared__ int shi[4];
+    int n_empty = 0;
+    double tot = 0.0;
+    for (int j = tid; j < a.k; j += 256) {
+        double tsq = 0.0, tnr = 0.0;
+        for (int c = 0; c < nch; ++c) {
+            tsq += a.part[((long)j * nch + c) * 2 + 0];
+            tnr += a.part[((long)j * nch + c) * 2 + 1];
         }
-        a.part[((long)j * nch + cc) * 2 + 0] = ssq;
-        a.part[((long)j * nch + cc) * 2 + 1] = snr;
-        __threadfence();
-        const unsigned prev = atomicAdd(&a.cluster_ctr[j], 1u);
-        if (prev == (unsigned)(nch - 1)) {
-            __threadfence();
-            double tsq = 0.0, tnr = 0.0;
-            for (int c2 = 0; c2 < nch; ++c2) {
-                tsq += coherent_load(&a.part[((long)j * nch + c2) * 2 + 0]);
-                tnr += coherent_load(&a.part[((long)j * nch + c2) * 2 + 1]);
-            }
-            a.shift_sq[j] = (float)tsq;
-            if (count > 0) a.cnorm[j] = (float)tnr;
-            a.counts[j] = count;
-            a.cluster_ctr[j] = 0u;
-            __threadfence();
-            const unsigned done_clusters = atomicAdd(&st->global_ctr, 1u);
-            if (done_clusters == (unsigned)(a.k - 1)) {
-                __threadfence();
-                int n_empty = 0;
-                double tot = 0.0;
-                for (int jj = 0; jj < a.k; ++jj) {
-                    n_empty += coherent_load(&a.counts[jj]) == 0;
-                    tot += (double)coherent_load(&a.shift_sq[jj]);
-                }
-                const int changed = coherent_load(&st->changed);
-                st->n_empty = n_empty;
-                st->shift_tot = tot;
-                st->last_changed = changed;
-                st->changed = 0;
-                st->global_ctr = 0u;
-                st->n_iter = a.iter + 1;
-                int done = 0;
-                if (n_empty > 0)
-                    done = 3;
-                else if ((a.flags & kStopStrict) && changed == 0)
-                    done = 1;
-                else if (a.tol > 0.0 && tot <= a.tol)
-                    done = 2;
-                if (done != 0) st->halt_iter = a.iter;
-                __threadfence();
-                st->done = done;
-            }
-        }
+        const int count = a.counts[j];
+        a.shift_sq[j] = (float)tsq;
+        if (count > 0) a.cnorm[j] = (float)tnr;
+        n_empty += count == 0;
+        tot += (double)(float)tsq;
+    }
+    n_empty = block_sum(n_empty, shi);
+    tot = block_sum(tot, shd);
+    if (tid == 0) {
+        const int changed = st->changed;
+        st->n_empty = n_empty;
+        st->shift_tot = tot;
+        st->last_changed = changed;
+        st->changed = 0;
+        st->n_iter = a.iter + 1;
+        int done = 0;
+        if (n_empty > 0)
+            done = 3;
+        else if ((a.flags & kStopStrict) && changed == 0)
+            done = 1;
+        else if (a.tol > 0.0 && tot <= a.tol)
+            done = 2;
+        if (done != 0) st->halt_iter = a.iter;
+        st->done = done;
     }
 }
 
 hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t s)
 {
-    hipLaunchKernelGGL(k_finalize, dim3(a.k, finalize_col_chunks(a.d, a.R)), dim3(256), 0, s, a);
+    const int nch = finalize_col_chunks(a.d, a.R);
+    hipLaunchKernelGGL(k_finalize_cols, dim3(a.k, nch), dim3(256), 0, s, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_finalize_loop, dim3(1), dim3(256), 0, s, a, nch);
     return hipGetLastError();
 }
 

@@ -23,7 +23,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/skmetal_hip.h"
+#include "skmetal_hip.h"
 #include "internal.h"
 
 using namespace skm;
@@ -256,7 +256,6 @@ struct Lloyd {
     int* counts = nullptr;
     double* part = nullptr;
     float* shift_sq = nullptr;
-    unsigned* cctr = nullptr;
     double* rowpart = nullptr;
     float* rowout = nullptr;
     double* colpart = nullptr;
@@ -281,10 +280,11 @@ struct Lloyd {
         n = n_;
         d = d_;
         k = k_;
-        ld = (d + 3) & ~3;
+        const int lf = fused_ld(d, k);
+        ld = lf > 0 ? lf : (d + 3) & ~3;
         s = C->stream;
         ug = update_geometry(n, d, k, C->num_cu);
-        fblocks = fused_blocks(n, d, k, C->num_cu);
+        fblocks = lf > 0 ? fused_blocks(n, ld, k, C->num_cu) : 0;
         const int Rmax = std::max(ug.R, fblocks);
         const int chunks = std::max(finalize_col_chunks(d, ug.R), fblocks > 0 ? finalize_col_chunks(d, fblocks) : 0);
         const size_t kl = size_t(k) * ld;
@@ -300,14 +300,12 @@ struct Lloyd {
         TRY(grab((void**)&counts, size_t(k) * sizeof(int)));
         TRY(grab((void**)&part, size_t(k) * chunks * 2 * sizeof(double)));
         TRY(grab((void**)&shift_sq, size_t(k) * sizeof(float)));
-        TRY(grab((void**)&cctr, size_t(k) * sizeof(unsigned)));
         TRY(grab((void**)&rowpart, size_t(rowdist_grid(n)) * sizeof(double)));
         TRY(grab((void**)&colpart, size_t(colsum_grid(n)) * d * sizeof(double)));
         TRY(grab((void**)&st, sizeof(LoopState)));
         HIP_TRY(hipMemsetAsync(cen[0], 0, kl * sizeof(float), s), "hipMemsetAsync");
         HIP_TRY(hipMemsetAsync(cen[1], 0, kl * sizeof(float), s), "hipMemsetAsync");
         HIP_TRY(hipMemsetAsync(mean, 0, size_t(ld) * sizeof(float), s), "hipMemsetAsync");
-        HIP_TRY(hipMemsetAsync(cctr, 0, size_t(k) * sizeof(unsigned), s), "hipMemsetAsync");
         HIP_TRY(hipMemsetAsync(st, 0, sizeof(LoopState), s), "hipMemsetAsync");
         HIP_TRY(hipMemsetAsync(labels, 0, size_t(n) * sizeof(int), s), "hipMemsetAsync");
         h_mean.assign(size_t(ld), 0.f);
@@ -405,7 +403,7 @@ struct Lloyd {
             TRY(update());
         }
         FinalizeArgs f{psum, pcnt, R, k, d, ld, cen[cur], cen[cur ^ 1], cnorm, sums, counts, part, shift_sq,
-                       cctr, st, iter, tol, flags, finalize_cols(R)};
+                       st, iter, tol, flags, finalize_cols(R)};
         HIP_TRY(launch_finalize(f, s), "finalize launch");
         cur ^= 1;
         return 0;
@@ -498,7 +496,6 @@ struct Lloyd {
         hs.done = done;
         hs.n_iter = t + 1;
         hs.changed = 0;
-        hs.global_ctr = 0;
         hs.shift_tot = shift_tot;
         hs.halt_iter = t;
         TRY(write_state(hs));
@@ -518,7 +515,10 @@ struct Lloyd {
         TRY(write_state(hs));
         HIP_TRY(hipMemsetAsync(labels, 0xff, size_t(n) * sizeof(int), s), "hipMemsetAsync(labels)");
         long it = 0;
-        long batch = fixed ? max_iter : 4;
+        // Steps are enqueued in growing batches and the loop state is read
+        // back after each: a halt (convergence, or an empty cluster that the
+        // host relocates) then skips at most one batch of launches.
+        long batch = fixed ? 8 : 4;
         int final_done = 0;
         while (it < max_iter) {
             const long nb = std::min(batch, max_iter - it);
@@ -542,7 +542,7 @@ struct Lloyd {
                 break;
             }
             it += nb;
-            if (!fixed) batch = std::min<long>(batch * 2, 64);
+            batch = std::min<long>(batch * 2, fixed ? 1024 : 64);
         }
         if (n_iter_out) *n_iter_out = max_iter > 0 ? hs.n_iter : 0;
         if (done_out) *done_out = final_done;
