@@ -29,10 +29,11 @@ namespace skm {
 //              the E-step as k_assign does: x.c on v_mfma_f32_4x4x1_16b_f32
 //              (B = this lane's row, A = centres from LDS, lane j = cluster
 //              j), ||c||^2 - 2 x.c and the first minimum in the lane.  From
-//              chunk K on (once the walker has finished tile t - P) each
-//              chunk is written to the pair's LDS tile right after its MFMAs
-//              and its registers are reloaded with tile t + P, so the HBM
-//              reads spread over the E-step.  Chunks [0, K) are held in one
+//              chunk K on, each chunk is written to the pair's LDS tile right
+//              after its MFMAs (once the walker has read that chunk of tile
+//              t - P: it publishes its progress per chunk) and its registers
+//              are reloaded with tile t + P, so the HBM reads spread over the
+//              E-step.  Chunks [0, K) are held in one
 //              of two register sets (by round parity), written out after the
 //              argmin and reloaded with tile t + 2P.  Then the tile's rows of
 //              each cluster go to LDS as bit masks (an LDS atomic OR of
@@ -42,7 +43,8 @@ namespace skm {
 //              sums of every column, in registers: the lowest WS bits of its
 //              mask become LDS row offsets (unused ones point at a row of
 //              zeros, so the walk is a fixed sequence), rows past the first
-//              WS by a loop; then it flags the tile walked.
+//              WS by a loop; it flags each chunk as soon as its reads are
+//              issued.
 //
 // Rows are added in ascending row order per cluster (the first WS rows after
 // the others), tiles in round order, and the four walkers are combined in
@@ -77,13 +79,17 @@ __device__ __forceinline__ float4 load_quad(__amdgpu_buffer_rsrc_t rs, int off)
     return *reinterpret_cast<const float4*>(&v);
 }
 
-// Waits (polling LDS) until *flag >= v.  Flags are written by the other wave
-// of the pair; LDS operations of one wave are performed in issue order, so a
-// wave that sees the flag also sees the LDS writes issued before it.
-__device__ __forceinline__ void wait_flag(int* flag, int v)
+// Waits (polling LDS) until *flag >= v and returns the value seen.  Flags are
+// written by the other wave of the pair; LDS operations of one wave are
+// performed in issue order, so a wave that sees a flag value also sees the
+// LDS writes issued before it, and LDS reads issued before it are done.
+__device__ __forceinline__ int wait_flag(int* flag, int v)
 {
-    while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < v) __builtin_amdgcn_s_sleep(1);
+    int seen;
+    while ((seen = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < v)
+        __builtin_amdgcn_s_sleep(1);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);  // no LDS access moves above the wait
+    return seen;
 }
 
 __device__ __forceinline__ void set_flag(int* flag, int v)
@@ -127,15 +133,16 @@ __global__ __launch_bounds__(512, 1) void k_fused(const float* __restrict__ X, l
     constexpr int CPC = 4 * KG;
     constexpr int WS = walk_steps<KG>();
     constexpr int XS = fused_stride(NQ);      // ld == 4 * NQ
-    constexpr int K = NQ >= 12 ? 6 : NQ / 2;  // chunks computed before the LDS tile is reused
+    constexpr int K = NQ >= 8 ? 3 : NQ / 2;  // chunks computed before the LDS tile is reused
     constexpr int KA = K > 0 ? K : 1;
+    constexpr int LB = 8;                     // chunks per burst of HBM loads
     // LDS: centres [CPC x XS] | zero row [XS] | 4 pair tiles [64 x XS]
     extern __shared__ __attribute__((aligned(16))) float lds[];
     __shared__ unsigned long long sMask[4][64];
     __shared__ int sCnt[4][64];
     __shared__ __attribute__((aligned(16))) float sN[CPC];
-    __shared__ int sReady[4];   // tiles the MFMA wave has put in LDS
-    __shared__ int sWalked[4];  // tiles the walker has finished
+    __shared__ int sReady[4];  // tiles the MFMA wave has put in LDS
+    __shared__ int sProg[4];   // chunks the walker has read: tile * NQ + chunk
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps descriptors scalar
@@ -160,7 +167,7 @@ __global__ __launch_bounds__(512, 1) void k_fused(const float* __restrict__ X, l
     for (int i = tid; i < CPC; i += 512) sN[i] = i < k ? cnorm[i] : INFINITY;
     if (tid < 4) {
         sReady[tid] = 0;
-        sWalked[tid] = 0;
+        sProg[tid] = 0;
     }
 
     const long ntiles = (n + 63) >> 6;
@@ -192,9 +199,15 @@ __global__ __launch_bounds__(512, 1) void k_fused(const float* __restrict__ X, l
 #pragma unroll
             for (int g = 0; g < KG; ++g) acc[g] = v4f{0.f, 0.f, 0.f, 0.f};
             float4 cv = *reinterpret_cast<const float4*>(cbase);
+            int seen = 0;  // walker progress last read
 #pragma unroll
             for (int q = 0; q < NQ; ++q) {
-                if (q == K) wait_flag(&sWalked[pair], r);  // the walker is done with tile t - P
+                // chunk q of the LDS tile is rewritten below once the walker
+                // has read it for tile t - P (it runs well ahead: few polls)
+                if (q >= K && r > 0) {
+                    const int need = (r - 1) * NQ + q + 1;
+                    if (seen < need) seen = wait_flag(&sProg[pair], need);
+                }
                 const float4 cvn = *reinterpret_cast<const float4*>(cbase + 16 * (q + 1 < NQ ? q + 1 : 0));
                 const float4 x = q < K ? pre[q < K ? q : 0] : xv[q < K ? 0 : q - K];
                 mfma_groups<KG>(acc, cv.x, x.x);
@@ -203,11 +216,19 @@ __global__ __launch_bounds__(512, 1) void k_fused(const float* __restrict__ X, l
                 mfma_groups<KG>(acc, cv.w, x.w);
                 if (q >= K) {
                     *reinterpret_cast<float4*>(myrow + 4 * q) = x;
-                    xv[q - K] = load_quad(rn, xoff + 16 * q);  // tile t + P
+                    // tile t + P into the registers of the last LB chunks,
+                    // back to back: the loads of one row's 16-byte pieces
+                    // then meet the same cache lines together
+                    if ((q - K) % LB == LB - 1 || q == NQ - 1) {
+#pragma unroll
+                        for (int qq = q - (q - K) % LB; qq <= q; ++qq) xv[qq - K] = load_quad(rn, xoff + 16 * qq);
+                    }
                 }
                 cv = cvn;
+                // one chunk per scheduling region: keeps each chunk's load
+                // in its chunk, spreading the HBM reads over the E-step
+                __builtin_amdgcn_sched_barrier(0);
             }
-            if (K == 0) wait_flag(&sWalked[pair], r);
             // ||c||^2 - 2 x.c, first minimum wins (_k_means_lloyd.pyx:196-212)
             float d[CPC];
 #pragma unroll
@@ -287,12 +308,14 @@ __global__ __launch_bounds__(512, 1) void k_fused(const float* __restrict__ X, l
             float4 wv[WS];
 #pragma unroll
             for (int s = 0; s < WS; ++s) wv[s] = *reinterpret_cast<const float4*>(lbase + ro[s]);
+            set_flag(&sProg[pair], r * NQ + 1);
 #pragma unroll
             for (int q = 0; q < NQ; ++q) {
                 float4 wn[WS];
                 if (q + 1 < NQ) {
 #pragma unroll
                     for (int s = 0; s < WS; ++s) wn[s] = *reinterpret_cast<const float4*>(lbase + ro[s] + 16 * (q + 1));
+                    set_flag(&sProg[pair], r * NQ + q + 2);  // reads issued: LDS keeps their order
                 }
 #pragma unroll
                 for (int s = 0; s < WS; ++s) {
@@ -306,7 +329,6 @@ __global__ __launch_bounds__(512, 1) void k_fused(const float* __restrict__ X, l
                     for (int s = 0; s < WS; ++s) wv[s] = wn[s];
                 }
             }
-            set_flag(&sWalked[pair], r + 1);
         }
         __syncthreads();  // every pair is done with its tile
         // this walker's sums, combined below in walker order: [4][CPC][ld]
