@@ -252,3 +252,101 @@ def test_step_mode_selection(bridge):
         assert h.info()["fused"] is False
     with bridge.LloydHandle(10_000, 200, 8) as h:
         assert h.info()["fused"] is False
+
+
+def _sampled_steps(bridge, X, C0, steps, sample, seed, what):
+    """Full-size GPU steps from C0.  Labels are checked against the oracle's
+    E-step on a row sample (the full n x k oracle E-step would take minutes);
+    centres are checked in full: the oracle's M-step (sums, relocation,
+    averaging) applied to the GPU's labels must reproduce the GPU's centres."""
+    n, d = X.shape
+    k = C0.shape[0]
+    mean = X.mean(axis=0)
+    Xc = X - mean
+    idx = np.sort(np.random.default_rng(seed).choice(n, size=min(sample, n), replace=False))
+    prev = C0
+    with bridge.LloydHandle(n, d, k) as h:
+        h.load(X, center=True)
+        for m in range(steps):
+            _say(f"{what} step {m + 1}")
+            h.set_centers(prev)
+            h.iterate(1)
+            lab = h.labels()
+            Cn = h.centers()
+            assert lab.min() >= 0 and lab.max() < k
+            ref, best, second = oracle.assign(Xc[idx], prev - mean, return_gap=True)
+            parity.check_labels(lab[idx], ref, best, second, Xc[idx], what=f"{what} step {m + 1} sampled labels")
+            C_ref, _, n_empty = oracle.mstep(Xc, lab, prev - mean)
+            err = parity.center_rel_err(C_ref, Cn - mean)
+            if err > parity.CENTER_RTOL and n_empty >= 3:
+                counts = np.bincount(lab, minlength=k)
+                err = parity._match_relocated(C_ref, Cn - mean, np.flatnonzero(counts == 0))
+            assert err <= parity.CENTER_RTOL, f"{what} step {m + 1}: centres error {err:.3e}"
+            prev = Cn
+
+
+@pytest.mark.parametrize("wl,scale,steps", [("c3", 1.0, 2), ("c4", 1.0, 2), ("c5", 0.25, 1)])
+def test_workload_sampled_full_size(bridge, wl, scale, steps):
+    """The large-k workloads (generic assign/update path) at their real shapes:
+    1M x 128 k=256, 4M x 64 k=1024 (Zipf-skewed clusters), and the
+    768-feature k=4096 embedding workload on a quarter of its rows."""
+    from skmetal_amd import _synth
+
+    X, C0 = _synth.generate(wl, seed=0, scale=scale)
+    _say(f"sampled lockstep {wl} {X.shape} k={C0.shape[0]}")
+    _sampled_steps(bridge, X, C0, steps, 20000, 7, wl)
+
+
+def _separated_blobs(n, d, k, seed):
+    """k well-separated blobs (centres ~U[-10,10]^d, sigma 1) and one initial
+    centre per blob: scikit-learn's trajectory has no near-ties to diverge on."""
+    rng = np.random.default_rng(seed)
+    cen = rng.uniform(-10, 10, (k, d))
+    ids = rng.integers(0, k, n)
+    X = (cen[ids] + rng.standard_normal((n, d))).astype(np.float32)
+    C0 = np.stack([X[np.flatnonzero(ids == j)[0]] for j in range(k)])
+    return X, C0
+
+
+def test_accelerate_kmeans_matches_sklearn(bridge):
+    """skmetal's user-facing path: accelerate(KMeans(...)).fit/predict/score on the
+    GPU against scikit-learn's own KMeans from the same initial centres."""
+    from sklearn.cluster import KMeans
+
+    import skmetal_amd
+    from skmetal_amd.estimators.cluster import HipKMeans
+
+    X, C0 = _separated_blobs(20000, 32, 8, 11)
+    kw = dict(n_clusters=8, init=C0, n_init=1, max_iter=100, tol=1e-4)
+    model = skmetal_amd.accelerate(KMeans(**kw))
+    assert isinstance(model, HipKMeans)
+    model.fit(X)
+    ref = KMeans(**kw).fit(X)
+    parity.check_centers(model.cluster_centers_, ref.cluster_centers_, what="accelerate centres")
+    mean = X.mean(axis=0)
+    _, best, second = oracle.assign(X - mean, ref.cluster_centers_ - mean, return_gap=True)
+    parity.check_labels(model.labels_, ref.labels_, best, second, X - mean, what="accelerate labels")
+    assert model.n_iter_ == ref.n_iter_
+    parity.check_inertia(model.inertia_, ref.inertia_, rtol=1e-5, atol=parity.centring_floor(X),
+                         what="accelerate inertia")
+    Y, _ = _separated_blobs(5000, 32, 8, 12)
+    pred = model.predict(Y)
+    ref_pred = ref.predict(Y)
+    _, best, second = oracle.assign(Y, ref.cluster_centers_, return_gap=True)
+    parity.check_labels(pred, ref_pred, best, second, Y, what="accelerate predict")
+    assert model.score(Y) == pytest.approx(ref.score(Y), rel=1e-5)
+
+
+def test_accelerate_kmeans_plusplus_same_draws_as_sklearn(bridge):
+    """k-means++ init is drawn from the estimator's random_state exactly as
+    scikit-learn draws it, so a seeded fit reproduces scikit-learn's."""
+    from sklearn.cluster import KMeans
+
+    import skmetal_amd
+
+    X, _ = _separated_blobs(10000, 32, 8, 13)
+    kw = dict(n_clusters=8, init="k-means++", n_init=1, max_iter=50, random_state=3)
+    model = skmetal_amd.accelerate(KMeans(**kw)).fit(X)
+    ref = KMeans(**kw).fit(X)
+    parity.check_centers(model.cluster_centers_, ref.cluster_centers_, what="k-means++ centres")
+    assert model.n_iter_ == ref.n_iter_
