@@ -75,8 +75,44 @@ struct UpdateGeom { int R; int G; int Z; int cg; int nslots; int ncp; int W; lon
 UpdateGeom update_geometry(long n, int d, int k, int num_cu);
 hipError_t launch_update(const UpdateArgs& a, const UpdateGeom& g, hipStream_t s);
 
+// Sorted update for the generic path: rows are ordered by label with a
+// counting sort (per-range histograms, scan, scatter), then chunks of the
+// sorted order are summed segment by segment; cluster j's partial sums are
+// the records rec_off[j] .. rec_off[j] + rec_cnt[j] - 1 (chunk order).
+struct SortGeom {
+    bool on = false;
+    int wr = 0;            // rows per range (one wave each)
+    int nw = 0;            // ranges
+    int nseg = 0;          // scan segments of kSortSeg ranges
+    int B = 0;             // sorted rows per chunk
+    long nchunks = 0;
+    int G = 0;             // threads per chunk group (covers the row's columns)
+    long max_records = 0;  // k + nchunks
+};
+constexpr int kSortSeg = 32;
+SortGeom sort_geometry(long n, int d, int ld, int k);
+struct SortArgs {
+    const float* X; long n; int ld; int d;
+    const int* labels; int k;
+    int* hist;             // [nw x k]: range histograms, then range offsets
+    int* segsum;           // [nseg x k]
+    int* counts;           // [k]  rows per cluster
+    int* start;            // [k]  first sorted position of cluster j
+    int* rec_off;          // [k]  first record of cluster j
+    int* rec_cnt;          // [k]  records of cluster j
+    int* perm;             // [n]  row ids in sorted order
+    int* slab;             // [n]  labels in sorted order
+    float* rec;            // [max_records x ld]
+    LoopState* state;
+};
+hipError_t launch_sorted_update(const SortArgs& a, const SortGeom& g, hipStream_t s);
+
 struct FinalizeArgs {
     const float* psum; const int* pcnt; int R; int k; int d; int ld;
+    // record mode (sorted update): cluster j's partials are the records
+    // rec_off[j] .. + rec_cnt[j] of psum and its count is cnt_in[j]; null
+    // otherwise (partials r*k + j for r < R, counts summed from pcnt)
+    const int* rec_off; const int* rec_cnt; const int* cnt_in;
     const float* C_old; float* C_new; float* cnorm;
     double* sums;          // [k x ld] fp64 totals (kept for the relocation path)
     int* counts;           // [k]

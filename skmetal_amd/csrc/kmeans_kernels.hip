@@ -359,6 +359,268 @@ hipError_t launch_update(const UpdateArgs& a, const UpdateGeom& g, hipStream_t s
 }
 
 // ---------------------------------------------------------------------------
+// sorted update (generic path): counting sort by label + segmented sums
+// ---------------------------------------------------------------------------
+//
+// 1. k_label_hist   one wave per range of wr rows: LDS histogram of labels.
+// 2. k_label_segs   column sums of the range histograms per segment of
+//                   kSortSeg ranges.
+// 3. k_label_scan   one block: per-cluster counts, exclusive scan over
+//                   clusters (first sorted position), chunk spans and record
+//                   offsets, and per-segment bases.
+// 4. k_label_offs   range offsets: start_j + rows of cluster j in earlier
+//                   ranges.
+// 5. k_label_scatter one wave per range: row ids and labels to their sorted
+//                   positions (ranges in order; inside a wave instruction the
+//                   LDS atomic hands out the positions).
+// 6. k_segsum       a group of G threads sums one chunk of B sorted rows,
+//                   segment by segment (the rows of one cluster are
+//                   consecutive), gathering each X row once; a segment's sum
+//                   is the record (cluster, chunk).
+// The finalize then folds cluster j's records in chunk order.  X is read
+// once; labels a few times (4 bytes per row).
+
+__global__ __launch_bounds__(64) void k_label_hist(SortArgs a, int wr)
+{
+    if (a.state->done != 0) return;
+    extern __shared__ int h[];
+    for (int j = threadIdx.x; j < a.k; j += 64) h[j] = 0;
+    __syncthreads();
+    const long r0 = (long)blockIdx.x * wr;
+    const long r1 = min(a.n, r0 + wr);
+    for (long r = r0 + threadIdx.x; r < r1; r += 64) atomicAdd(&h[a.labels[r]], 1);
+    __syncthreads();
+    int* out = a.hist + (long)blockIdx.x * a.k;
+    for (int j = threadIdx.x; j < a.k; j += 64) out[j] = h[j];
+}
+
+__global__ __launch_bounds__(256) void k_label_segs(SortArgs a, int nw)
+{
+    if (a.state->done != 0) return;
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    if (j >= a.k) return;
+    const int w0 = blockIdx.y * kSortSeg;
+    const int w1 = min(nw, w0 + kSortSeg);
+    int v[kSortSeg];
+#pragma unroll
+    for (int i = 0; i < kSortSeg; ++i) v[i] = a.hist[(long)min(w0 + i, w1 - 1) * a.k + j];  // all in flight
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < kSortSeg; ++i) s += w0 + i < w1 ? v[i] : 0;
+    a.segsum[(long)blockIdx.y * a.k + j] = s;
+}
+
+// Exclusive scan of v over the 1024 threads of the block (v per thread).
+__device__ int block_exclusive_scan(int v, int* sh)
+{
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    int x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    if (lane == 63) sh[tid >> 6] = x;
+    __syncthreads();
+    if (tid < 16) {
+        int w = sh[tid];
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) {
+            const int y = __shfl_up(w, off, 16);
+            if (tid >= off) w += y;
+        }
+        sh[16 + tid] = w;
+    }
+    __syncthreads();
+    const int base = (tid >> 6) > 0 ? sh[16 + (tid >> 6) - 1] : 0;
+    __syncthreads();
+    return base + x - v;
+}
+
+__global__ __launch_bounds__(1024) void k_label_scan(SortArgs a, int nseg, int B)
+{
+    if (a.state->done != 0) return;
+    __shared__ int sh[32];
+    const int tid = threadIdx.x;
+    const int per = (a.k + 1023) / 1024;  // clusters per thread, contiguous
+    const int j0 = tid * per;
+    const int j1 = min(a.k, j0 + per);
+    // counts, and per-segment bases relative to the cluster's start
+    int tot = 0;
+    for (int j = j0; j < j1; ++j) {
+        int v[kSortSeg];
+#pragma unroll
+        for (int s = 0; s < kSortSeg; ++s) v[s] = a.segsum[(long)min(s, nseg - 1) * a.k + j];  // all in flight
+        int run = 0;
+#pragma unroll
+        for (int s = 0; s < kSortSeg; ++s) {
+            if (s < nseg) {
+                a.segsum[(long)s * a.k + j] = run;
+                run += v[s];
+            }
+        }
+        a.counts[j] = run;
+        tot += run;
+    }
+    int pos = block_exclusive_scan(tot, sh);
+    int spans = 0;
+    for (int j = j0; j < j1; ++j) {
+        a.start[j] = pos;
+        const int c = a.counts[j];
+        const int span = c > 0 ? (pos + c - 1) / B - pos / B + 1 : 0;
+        a.rec_cnt[j] = span;
+        spans += span;
+        pos += c;
+    }
+    int rec = block_exclusive_scan(spans, sh);
+    for (int j = j0; j < j1; ++j) {
+        a.rec_off[j] = rec;
+        rec += a.rec_cnt[j];
+    }
+}
+
+__global__ __launch_bounds__(256) void k_label_offs(SortArgs a, int nw)
+{
+    if (a.state->done != 0) return;
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    if (j >= a.k) return;
+    const int w0 = blockIdx.y * kSortSeg;
+    const int w1 = min(nw, w0 + kSortSeg);
+    int v[kSortSeg];
+#pragma unroll
+    for (int i = 0; i < kSortSeg; ++i) v[i] = a.hist[(long)min(w0 + i, w1 - 1) * a.k + j];  // all in flight
+    int run = a.start[j] + a.segsum[(long)blockIdx.y * a.k + j];
+#pragma unroll
+    for (int i = 0; i < kSortSeg; ++i) {
+        if (w0 + i < w1) a.hist[(long)(w0 + i) * a.k + j] = run;
+        run += v[i];
+    }
+}
+
+__global__ __launch_bounds__(64) void k_label_scatter(SortArgs a, int wr)
+{
+    if (a.state->done != 0) return;
+    extern __shared__ int ctr[];
+    const int* off = a.hist + (long)blockIdx.x * a.k;
+    for (int j = threadIdx.x; j < a.k; j += 64) ctr[j] = off[j];
+    __syncthreads();
+    const long r0 = (long)blockIdx.x * wr;
+    const long r1 = min(a.n, r0 + wr);
+    for (long r = r0 + threadIdx.x; r < r1; r += 64) {
+        const int l = a.labels[r];
+        const int p = atomicAdd(&ctr[l], 1);
+        a.perm[p] = (int)r;
+        a.slab[p] = l;
+    }
+}
+
+// Columns per thread: CPT * G >= the tile's columns (<= 1024 per grid row).
+template <int CPT>
+__global__ __launch_bounds__(256) void k_segsum(SortArgs a, int B, int G)
+{
+    if (a.state->done != 0) return;
+    constexpr int U = 8;  // sorted rows in flight
+    const int groups = 256 / G;
+    const int grp = threadIdx.x / G;
+    const int t = threadIdx.x - grp * G;
+    const long c = (long)blockIdx.x * groups + grp;
+    const long p0 = c * B;
+    if (p0 >= a.n) return;
+    const long p1 = min(a.n, p0 + B);
+    const int col0 = blockIdx.y * 1024;
+    int cols[CPT];
+    bool on[CPT];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+        cols[i] = col0 + t + i * G;
+        on[i] = cols[i] < a.d && t + i * G < 1024;
+    }
+    float acc[CPT];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) acc[i] = 0.f;
+    int cur = a.slab[p0];
+    auto flush = [&](int j) {
+        const long rec = a.rec_off[j] + (c - a.start[j] / B);
+        float* dst = a.rec + rec * a.ld;
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            if (on[i]) dst[cols[i]] = acc[i];
+            acc[i] = 0.f;
+        }
+    };
+    for (long p = p0; p < p1; p += U) {
+        int lab[U];
+        float v[U][CPT];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const long q = p + u < p1 ? p + u : p1 - 1;
+            lab[u] = p + u < p1 ? a.slab[q] : cur;
+            const float* row = a.X + (long)a.perm[q] * a.ld;
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) v[u][i] = on[i] ? row[cols[i]] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (p + u >= p1) break;
+            if (lab[u] != cur) {
+                flush(cur);
+                cur = lab[u];
+            }
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) acc[i] += v[u][i];
+        }
+    }
+    flush(cur);
+}
+
+SortGeom sort_geometry(long n, int d, int ld, int k)
+{
+    SortGeom g;
+    if (k > 16384 || n < 1) return g;  // LDS histogram of one wave: 64 KB
+    long wr = (n + 1023) / 1024;
+    wr = ((wr + 63) / 64) * 64;
+    if (wr < 256) wr = 256;
+    g.wr = (int)wr;
+    g.nw = (int)((n + wr - 1) / wr);
+    if ((long)g.nw * k > (64L << 20)) return g;
+    g.nseg = (g.nw + kSortSeg - 1) / kSortSeg;
+    const int dcols = ld < 1024 ? ld : 1024;
+    g.G = dcols <= 64 ? 64 : dcols <= 128 ? 128 : 256;
+    long B = (n + 2047) / 2048;
+    B = ((B + 63) / 64) * 64;
+    if (B < 64) B = 64;
+    g.B = (int)B;
+    g.nchunks = (n + B - 1) / B;
+    g.max_records = k + g.nchunks;
+    g.on = true;
+    return g;
+}
+
+hipError_t launch_sorted_update(const SortArgs& a, const SortGeom& g, hipStream_t s)
+{
+    if (!g.on) return hipErrorInvalidValue;
+    const size_t hlds = (size_t)a.k * sizeof(int);
+    const unsigned kb = (unsigned)((a.k + 255) / 256);
+    hipLaunchKernelGGL(k_label_hist, dim3(g.nw), dim3(64), hlds, s, a, g.wr);
+    hipLaunchKernelGGL(k_label_segs, dim3(kb, g.nseg), dim3(256), 0, s, a, g.nw);
+    hipLaunchKernelGGL(k_label_scan, dim3(1), dim3(1024), 0, s, a, g.nseg, g.B);
+    hipLaunchKernelGGL(k_label_offs, dim3(kb, g.nseg), dim3(256), 0, s, a, g.nw);
+    hipLaunchKernelGGL(k_label_scatter, dim3(g.nw), dim3(64), hlds, s, a, g.wr);
+    const int groups = 256 / g.G;
+    const int dcols = a.d < 1024 ? a.d : 1024;
+    const int cpt = (dcols + g.G - 1) / g.G;
+    const dim3 grid((unsigned)((g.nchunks + groups - 1) / groups), (unsigned)((a.d + 1023) / 1024));
+    if (cpt <= 1)
+        hipLaunchKernelGGL(k_segsum<1>, grid, dim3(256), 0, s, a, g.B, g.G);
+    else if (cpt == 2)
+        hipLaunchKernelGGL(k_segsum<2>, grid, dim3(256), 0, s, a, g.B, g.G);
+    else
+        hipLaunchKernelGGL(k_segsum<4>, grid, dim3(256), 0, s, a, g.B, g.G);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // finalize: two kernels, no cross-block atomics or fences
 // ---------------------------------------------------------------------------
 //
@@ -415,22 +677,29 @@ __global__ __launch_bounds__(256) void k_finalize_cols(FinalizeArgs a)
     __shared__ double shd[2][4];
     __shared__ int shi[4];
 
+    // partials of cluster j: R of them at r*k + j, or its records
+    const bool recs = a.rec_off != nullptr;
+    const int R = recs ? a.rec_cnt[j] : a.R;
+    const float* src = a.psum + (recs ? (long)a.rec_off[j] * a.ld : (long)j * a.ld) + col;
+    const long step = recs ? (long)a.ld : (long)a.k * a.ld;
     int cnt = 0;
-    for (int r = tid; r < a.R; r += 256) cnt += a.pcnt[(long)r * a.k + j];
+    if (recs) {
+        cnt = tid == 0 ? a.cnt_in[j] : 0;
+    } else {
+        for (int r = tid; r < a.R; r += 256) cnt += a.pcnt[(long)r * a.k + j];
+    }
     double s = 0.0;
-    if (col < a.d) {
-        const float* src = a.psum + (long)j * a.ld + col;
-        const long step = (long)a.k * a.ld;
-        for (int r0 = rs; r0 < a.R; r0 += kFinUnroll * RS) {
+    if (col < a.d && R > 0) {
+        for (int r0 = rs; r0 < R; r0 += kFinUnroll * RS) {
             float v[kFinUnroll];
 #pragma unroll
             for (int u = 0; u < kFinUnroll; ++u) {
                 const int r = r0 + u * RS;
-                v[u] = src[(long)(r < a.R ? r : a.R - 1) * step];  // unconditional: all in flight
+                v[u] = src[(long)(r < R ? r : R - 1) * step];  // unconditional: all in flight
             }
 #pragma unroll
             for (int u = 0; u < kFinUnroll; ++u)
-                if (r0 + u * RS < a.R) s += (double)v[u];
+                if (r0 + u * RS < R) s += (double)v[u];
         }
     }
     // lanes of one column inside a wave: xor offsets CW, 2CW, ... < 64

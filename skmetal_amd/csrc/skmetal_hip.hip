@@ -65,6 +65,9 @@ int hip_fail(hipError_t e, const char* what)
     } while (0)
 
 constexpr size_t kPinBytes = size_t(32) << 20;  // per staging buffer
+// finalize in record mode (sorted update): sized as for 128 partials, i.e.
+// 16 columns x 16 lanes per block; a cluster's records are read in batches
+constexpr int kRecR = 128;
 constexpr size_t kMaxDim = size_t(1) << 20;
 
 // ---------------------------------------------------------------------------
@@ -261,6 +264,16 @@ struct Lloyd {
     double* colpart = nullptr;
     LoopState* st = nullptr;
     UpdateGeom ug{};
+    SortGeom sg{};          // sorted update (generic path), when it applies
+    int* s_hist = nullptr;
+    int* s_seg = nullptr;
+    int* s_counts = nullptr;
+    int* s_start = nullptr;
+    int* s_roff = nullptr;
+    int* s_rcnt = nullptr;
+    int* s_perm = nullptr;
+    int* s_slab = nullptr;
+    float* s_rec = nullptr;
     int fblocks = 0;        // > 0: fused E-step + sums kernel with this many partials
     int cur = 0;            // index of the current centres in cen[]
     bool centred = false;
@@ -285,8 +298,10 @@ struct Lloyd {
         s = C->stream;
         ug = update_geometry(n, d, k, C->num_cu);
         fblocks = lf > 0 ? fused_blocks(n, ld, k, C->num_cu) : 0;
-        const int Rmax = std::max(ug.R, fblocks);
-        const int chunks = std::max(finalize_col_chunks(d, ug.R), fblocks > 0 ? finalize_col_chunks(d, fblocks) : 0);
+        if (fblocks == 0) sg = sort_geometry(n, d, ld, k);
+        const int Rmax = sg.on ? 1 : std::max(ug.R, fblocks);
+        const int chunks = std::max({finalize_col_chunks(d, ug.R), fblocks > 0 ? finalize_col_chunks(d, fblocks) : 0,
+                                     finalize_col_chunks(d, kRecR)});
         const size_t kl = size_t(k) * ld;
         TRY(grab((void**)&X, size_t(n) * ld * sizeof(float)));
         TRY(grab((void**)&cen[0], kl * sizeof(float)));
@@ -303,6 +318,17 @@ struct Lloyd {
         TRY(grab((void**)&rowpart, size_t(rowdist_grid(n)) * sizeof(double)));
         TRY(grab((void**)&colpart, size_t(colsum_grid(n)) * d * sizeof(double)));
         TRY(grab((void**)&st, sizeof(LoopState)));
+        if (sg.on) {
+            TRY(grab((void**)&s_hist, size_t(sg.nw) * k * sizeof(int)));
+            TRY(grab((void**)&s_seg, size_t(sg.nseg) * k * sizeof(int)));
+            TRY(grab((void**)&s_counts, size_t(k) * sizeof(int)));
+            TRY(grab((void**)&s_start, size_t(k) * sizeof(int)));
+            TRY(grab((void**)&s_roff, size_t(k) * sizeof(int)));
+            TRY(grab((void**)&s_rcnt, size_t(k) * sizeof(int)));
+            TRY(grab((void**)&s_perm, size_t(n) * sizeof(int)));
+            TRY(grab((void**)&s_slab, size_t(n) * sizeof(int)));
+            TRY(grab((void**)&s_rec, size_t(sg.max_records) * ld * sizeof(float)));
+        }
         HIP_TRY(hipMemsetAsync(cen[0], 0, kl * sizeof(float), s), "hipMemsetAsync");
         HIP_TRY(hipMemsetAsync(cen[1], 0, kl * sizeof(float), s), "hipMemsetAsync");
         HIP_TRY(hipMemsetAsync(mean, 0, size_t(ld) * sizeof(float), s), "hipMemsetAsync");
@@ -379,6 +405,12 @@ struct Lloyd {
 
     int update()
     {
+        if (sg.on) {
+            SortArgs a{X, n, ld, d, labels, k, s_hist, s_seg, s_counts, s_start, s_roff, s_rcnt, s_perm, s_slab, s_rec,
+                       st};
+            HIP_TRY(launch_sorted_update(a, sg, s), "sorted update launch");
+            return 0;
+        }
         UpdateArgs u{X, n, ld, d, labels, k, psum, pcnt, st};
         HIP_TRY(launch_update(u, ug, s), "update launch");
         return 0;
@@ -402,7 +434,11 @@ struct Lloyd {
             TRY(assign(cen[cur], st, 1));
             TRY(update());
         }
-        FinalizeArgs f{psum, pcnt, R, k, d, ld, cen[cur], cen[cur ^ 1], cnorm, sums, counts, part, shift_sq,
+        const bool recs = fblocks == 0 && sg.on;
+        if (recs) R = kRecR;
+        FinalizeArgs f{recs ? s_rec : psum, pcnt, R, k, d, ld,
+                       recs ? s_roff : nullptr, recs ? s_rcnt : nullptr, recs ? s_counts : nullptr,
+                       cen[cur], cen[cur ^ 1], cnorm, sums, counts, part, shift_sq,
                        st, iter, tol, flags, finalize_cols(R)};
         HIP_TRY(launch_finalize(f, s), "finalize launch");
         cur ^= 1;
@@ -890,7 +926,7 @@ int skmetal_hip_lloyd_info(skmetal_hip_lloyd* h, int* fused, int* partials)
 {
     if (!h) return fail(SKMETAL_EINVAL, "null pointer argument");
     if (fused) *fused = h->L.fblocks > 0;
-    if (partials) *partials = h->L.fblocks > 0 ? h->L.fblocks : h->L.ug.R;
+    if (partials) *partials = h->L.fblocks > 0 ? h->L.fblocks : h->L.sg.on ? (int)h->L.sg.nchunks : h->L.ug.R;
     return 0;
 }
 

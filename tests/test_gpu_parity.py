@@ -194,6 +194,23 @@ def test_fit_is_deterministic(bridge):
     assert outs[0][2:] == outs[1][2:]
 
 
+def test_fit_is_deterministic_generic_path(bridge):
+    """k > 64: assign + sorted update + record finalize, bitwise equal across runs."""
+    rng = np.random.default_rng(21)
+    cen = rng.uniform(-5, 5, (150, 40))
+    X = (cen[rng.integers(0, 150, 60000)] + rng.standard_normal((60000, 40))).astype(np.float32)
+    C0 = X[np.sort(rng.choice(60000, 120, replace=False))]
+    outs = []
+    for _ in range(2):
+        C = C0.copy()
+        lab = np.empty(X.shape[0], np.int32)
+        n_iter, inertia = bridge.kmeans_fit(X, C, lab, 12, 0.0, strict=False)
+        outs.append((C, lab, n_iter, inertia))
+    assert np.array_equal(outs[0][0], outs[1][0])
+    assert np.array_equal(outs[0][1], outs[1][1])
+    assert outs[0][2:] == outs[1][2:]
+
+
 def test_empty_cluster_relocation_matches_oracle(bridge):
     g = _load_golden("empty_1000x10_k20")
     X, C0 = g["X"], g["C0"]
