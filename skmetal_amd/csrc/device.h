@@ -38,6 +38,15 @@ __device__ __forceinline__ void mfma_groups(v4f* acc, float a, float b)
     }
 }
 
+// Sum over the 64 lanes of a wave by xor butterfly; all lanes get the total.
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v)
+{
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
 // Load that sees stores other blocks made visible with __threadfence().
 template <typename T>
 __device__ __forceinline__ T coherent_load(const T* p)

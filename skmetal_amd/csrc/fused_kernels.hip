@@ -123,12 +123,17 @@ __device__ __forceinline__ int argmin_tree(float* d)
 }
 
 template <int KG, int NQ>
-__global__ __launch_bounds__(512, 1) void k_fused(const float* __restrict__ X, long n, int ld,
-                                                  const float* __restrict__ C,
-                                                  const float* __restrict__ cnorm, int k,
-                                                  int* __restrict__ labels, float* __restrict__ psum,
-                                                  int* __restrict__ pcnt, LoopState* st)
+__global__ __launch_bounds__(512, 1) void k_fused(FusedArgs a)
 {
+    const float* __restrict__ X = a.X;
+    const long n = a.n;
+    const int ld = a.ld;
+    const float* __restrict__ C = a.C;
+    const int k = a.k;
+    int* __restrict__ labels = a.labels;
+    float* __restrict__ psum = a.psum;
+    int* __restrict__ pcnt = a.pcnt;
+    LoopState* st = a.state;
     if (st->done != 0) return;
     constexpr int CPC = 4 * KG;
     constexpr int WS = walk_steps<KG>();
@@ -163,8 +168,71 @@ __global__ __launch_bounds__(512, 1) void k_fused(const float* __restrict__ X, l
         *reinterpret_cast<float4*>(&sC[cl * XS + 4 * q]) = v;
     }
     for (int i = tid; i < XS; i += 512) zrow[i] = 0.f;
-    // padding clusters get ||c||^2 = +inf: their distance never wins
-    for (int i = tid; i < CPC; i += 512) sN[i] = i < k ? cnorm[i] : INFINITY;
+    if (a.decide) {
+        // the previous step's stopping rules, evaluated identically by every
+        // block (same loads, same order as k_finalize_loop for k <= 64)
+        __shared__ int sDone;
+        if (wave == 0) {
+            const int j = lane;
+            double tsq = 0.0, tnr = 0.0;
+            int count = 1;
+            if (j < k) {
+                // all chunk partials in flight at once (the sum order is the
+                // finalize's: chunk 0, 1, ...)
+                const double* pj = a.part + (long)j * a.nch * 2;
+                constexpr int NB = 16;
+                for (int c0 = 0; c0 < a.nch; c0 += NB) {
+                    double v[2 * NB];
+#pragma unroll
+                    for (int u = 0; u < NB; ++u) {
+                        const int c = min(c0 + u, a.nch - 1);
+                        v[2 * u] = pj[2 * c];
+                        v[2 * u + 1] = pj[2 * c + 1];
+                    }
+#pragma unroll
+                    for (int u = 0; u < NB; ++u) {
+                        if (c0 + u < a.nch) {
+                            tsq += v[2 * u];
+                            tnr += v[2 * u + 1];
+                        }
+                    }
+                }
+                count = a.counts[j];
+            }
+            const int n_empty = wave_sum(j < k && count == 0 ? 1 : 0);
+            const double tot = wave_sum(j < k ? (double)(float)tsq : 0.0);
+            const int chg = *a.prev_changed;
+            int done = 0;
+            if (n_empty > 0)
+                done = 3;
+            else if ((a.flags & kStopStrict) && chg == 0)
+                done = 1;
+            else if (a.tol > 0.0 && tot <= a.tol)
+                done = 2;
+            if (blockIdx.x == 0) {
+                if (j < k) {
+                    a.shift_sq[j] = (float)tsq;
+                    if (count > 0) a.cnorm_out[j] = (float)tnr;
+                }
+                if (lane == 0) {
+                    st->n_empty = n_empty;
+                    st->shift_tot = tot;
+                    st->last_changed = chg;
+                    st->n_iter = a.iter;
+                    if (done != 0) st->halt_iter = a.iter - 1;
+                    st->done = done;
+                }
+            }
+            // padding clusters get ||c||^2 = +inf: their distance never wins
+            if (j < CPC) sN[j] = j < k ? (float)tnr : INFINITY;
+            if (lane == 0) sDone = done;
+        }
+        __syncthreads();
+        if (sDone != 0) return;
+    } else {
+        // padding clusters get ||c||^2 = +inf: their distance never wins
+        for (int i = tid; i < CPC; i += 512) sN[i] = i < k ? a.cnorm[i] : INFINITY;
+    }
     if (tid < 4) {
         sReady[tid] = 0;
         sProg[tid] = 0;
@@ -268,7 +336,7 @@ __global__ __launch_bounds__(512, 1) void k_fused(const float* __restrict__ X, l
             round(r + 1, preB);
         }
         if (r < rounds) round(r, preA);
-        if (lane == 0 && changed != 0) atomicAdd(&st->changed, changed);
+        if (lane == 0 && changed != 0) atomicAdd(a.changed, changed);
         __syncthreads();  // every pair's walker is done: the tile area is free
         __syncthreads();  // the walkers' sums are in LDS
     } else {
@@ -354,7 +422,7 @@ __global__ __launch_bounds__(512, 1) void k_fused(const float* __restrict__ X, l
     if (tid < k) pcnt[(long)blockIdx.x * k + tid] = ((sCnt[0][tid] + sCnt[1][tid]) + sCnt[2][tid]) + sCnt[3][tid];
 }
 
-typedef void (*fused_fn)(const float*, long, int, const float*, const float*, int, int*, float*, int*, LoopState*);
+typedef void (*fused_fn)(FusedArgs);
 
 template <int NQ, int... KGs>
 struct FusedTable {
@@ -432,8 +500,7 @@ hipError_t launch_fused(const FusedArgs& a, hipStream_t s)
 {
     fused_fn f = fused_kernel(a.k, a.ld);
     if (f == nullptr || a.blocks < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(f, dim3(a.blocks), dim3(512), fused_dyn_lds(a.k, a.ld), s, a.X, a.n, a.ld, a.C, a.cnorm, a.k,
-                       a.labels, a.psum, a.pcnt, a.state);
+    hipLaunchKernelGGL(f, dim3(a.blocks), dim3(512), fused_dyn_lds(a.k, a.ld), s, a);
     return hipGetLastError();
 }
 

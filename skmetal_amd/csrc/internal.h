@@ -21,8 +21,8 @@ struct LoopState {
     int done;          // 0 run, 1 strict label convergence, 2 shift <= tol,
                        // 3 empty cluster: host relocation needed at `halt_iter`
     int n_iter;        // sklearn's n_iter_ (iterations completed)
-    int changed;       // labels changed by the E-step in flight
-    int last_changed;  // `changed` of the last finalised iteration
+    int chg[2];        // labels changed by the E-step of iteration i: chg[i & 1]
+    int last_changed;  // changes of the last decided iteration
     int halt_iter;     // iteration index at which `done` was set
     int n_empty;       // empty clusters found by the last finalise
     unsigned rowdist_ctr; // row-distance reduction: blocks completed
@@ -42,8 +42,8 @@ struct AssignArgs {
     const float* X; long n; int ld;
     const float* C; const float* cnorm; int k;
     int* labels;
-    LoopState* state;      // nullable: no early exit, no change counting
-    int count_changes;     // compare with previous labels, add to state->changed
+    LoopState* state;      // nullable: no early exit
+    int* changed;          // nullable: compare with previous labels, add the changes here
 };
 hipError_t launch_assign(const AssignArgs& a, int num_cu, hipStream_t s);
 
@@ -54,8 +54,16 @@ struct FusedArgs {
     int* labels;
     float* psum;           // [blocks x k x ld]
     int* pcnt;             // [blocks x k]
-    LoopState* state;      // required: early exit and change counting
+    LoopState* state;      // required: early exit
     int blocks;
+    int* changed;          // this E-step's changed labels (added)
+    // decide = 1: every block first evaluates the stopping rules of the
+    // previous step (iteration iter - 1) from the finalize's chunk partials,
+    // as k_finalize_loop does, and block 0 records the decision; the step's
+    // ||c||^2 then come from those partials instead of `cnorm`
+    int decide; int iter; double tol; int flags;
+    const double* part; int nch; const int* counts; const int* prev_changed;
+    float* cnorm_out; float* shift_sq;
 };
 // Row stride (floats) X must have for the fused kernel, or 0 when (d, k) does
 // not qualify; the pad columns are zero.
@@ -121,9 +129,13 @@ struct FinalizeArgs {
     LoopState* state;
     int iter; double tol; int flags;
     int cw;                // columns per finalize block: finalize_cols(R)
+    const int* chg_cur;    // changes of this step's E-step
+    int* chg_next;         // cleared for the next step's E-step
 };
-// Two launches: per-(cluster, column chunk) totals, then the loop decision.
-hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t s);
+// Per-(cluster, column chunk) totals, then (with_loop) the loop decision.
+hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t s, bool with_loop);
+// The loop decision alone (after a fused step whose successor is not enqueued).
+hipError_t launch_finalize_loop(const FinalizeArgs& a, hipStream_t s);
 // A finalize block is 256 threads = cw columns x (256/cw) partial-sum lanes,
 // sized so that each thread reads at most about 8 of the R partials.
 inline int finalize_cols(int R)

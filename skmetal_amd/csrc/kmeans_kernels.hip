@@ -43,7 +43,7 @@ __global__ __launch_bounds__(256, 1) void k_assign(const float* __restrict__ X, 
                                                    const float* __restrict__ C,
                                                    const float* __restrict__ cnorm, int k,
                                                    int* __restrict__ labels, LoopState* st,
-                                                   int count_changes)
+                                                   int* changed)
 {
     if (st != nullptr && st->done != 0) return;
     constexpr int CPC = 4 * KG;   // clusters per chunk
@@ -131,17 +131,17 @@ __global__ __launch_bounds__(256, 1) void k_assign(const float* __restrict__ X, 
         }
         if (row < n) {
             int moved = 0;
-            if (count_changes) moved = labels[row] != bidx;
+            if (changed != nullptr) moved = labels[row] != bidx;
             labels[row] = bidx;
-            if (count_changes) {
+            if (changed != nullptr) {
                 const unsigned long long m = __ballot(moved);
-                if (lane == 0 && m != 0ull) atomicAdd(&st->changed, (int)__popcll(m));
+                if (lane == 0 && m != 0ull) atomicAdd(changed, (int)__popcll(m));
             }
         }
     }
 }
 
-typedef void (*assign_fn)(const float*, long, int, const float*, const float*, int, int*, LoopState*, int);
+typedef void (*assign_fn)(const float*, long, int, const float*, const float*, int, int*, LoopState*, int*);
 
 template <int NQ, int... KGs>
 struct AssignTable {
@@ -193,7 +193,7 @@ hipError_t launch_assign(const AssignArgs& a, int num_cu, hipStream_t s)
     if (blocks > tiles) blocks = tiles;
     if (blocks < 1) blocks = 1;
     hipLaunchKernelGGL(f, dim3((unsigned)blocks), dim3(256), 0, s, a.X, a.n, a.ld, a.C, a.cnorm, a.k, a.labels,
-                       a.state, a.count_changes);
+                       a.state, a.changed);
     return hipGetLastError();
 }
 
@@ -636,15 +636,6 @@ hipError_t launch_sorted_update(const SortArgs& a, const SortGeom& g, hipStream_
 // agent-scope fences inside one kernel would write back and invalidate the
 // L2 of every XCD for each block.
 
-// Sum over the 64 lanes of a wave by xor butterfly; all lanes get the total.
-template <typename T>
-__device__ __forceinline__ T wave_sum(T v)
-{
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
 // Sum over a 256-thread block in a fixed order (wave butterflies, then waves
 // 0..3); every thread gets the total.  `sh` holds 4 elements; the call ends
 // with a barrier, so it may be reused right after.
@@ -727,6 +718,7 @@ __global__ __launch_bounds__(256) void k_finalize_cols(FinalizeArgs a)
         a.part[((long)j * nch + cc) * 2 + 0] = sq;
         a.part[((long)j * nch + cc) * 2 + 1] = nrm;
         if (cc == 0) a.counts[j] = count;
+        if (j == 0 && cc == 0 && a.chg_next != nullptr) *a.chg_next = 0;
     }
 }
 
@@ -754,11 +746,10 @@ __global__ __launch_bounds__(256) void k_finalize_loop(FinalizeArgs a, int nch)
     n_empty = block_sum(n_empty, shi);
     tot = block_sum(tot, shd);
     if (tid == 0) {
-        const int changed = st->changed;
+        const int changed = *a.chg_cur;
         st->n_empty = n_empty;
         st->shift_tot = tot;
         st->last_changed = changed;
-        st->changed = 0;
         st->n_iter = a.iter + 1;
         int done = 0;
         if (n_empty > 0)
@@ -772,13 +763,18 @@ __global__ __launch_bounds__(256) void k_finalize_loop(FinalizeArgs a, int nch)
     }
 }
 
-hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t s)
+hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t s, bool with_loop)
 {
     const int nch = finalize_col_chunks(a.d, a.R);
     hipLaunchKernelGGL(k_finalize_cols, dim3(a.k, nch), dim3(256), 0, s, a);
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_finalize_loop, dim3(1), dim3(256), 0, s, a, nch);
+    if (e != hipSuccess || !with_loop) return e;
+    return launch_finalize_loop(a, s);
+}
+
+hipError_t launch_finalize_loop(const FinalizeArgs& a, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_finalize_loop, dim3(1), dim3(256), 0, s, a, finalize_col_chunks(a.d, a.R));
     return hipGetLastError();
 }
 

@@ -396,9 +396,9 @@ struct Lloyd {
         return 0;
     }
 
-    int assign(const float* cents, LoopState* state, int count_changes)
+    int assign(const float* cents, LoopState* state, int* changed)
     {
-        AssignArgs a{X, n, ld, cents, cnorm, k, labels, state, count_changes};
+        AssignArgs a{X, n, ld, cents, cnorm, k, labels, state, changed};
         HIP_TRY(launch_assign(a, C->num_cu, s), "assign launch");
         return 0;
     }
@@ -416,31 +416,41 @@ struct Lloyd {
         return 0;
     }
 
-    int fused_step()
+    // Fused E-step + sums of iteration `iter`; with decide, its blocks first
+    // evaluate the stopping rules of iteration iter - 1.
+    int fused_step(int iter = 0, bool decide = false, double tol = 0.0, int flags = 0)
     {
-        FusedArgs a{X, n, ld, cen[cur], cnorm, k, labels, psum, pcnt, st, fblocks};
+        FusedArgs a{X, n, ld, cen[cur], cnorm, k, labels, psum, pcnt, st, fblocks, &st->chg[iter & 1],
+                    decide ? 1 : 0, iter, tol, flags, part, finalize_col_chunks(d, fblocks), counts,
+                    &st->chg[(iter + 1) & 1], cnorm, shift_sq};
         HIP_TRY(launch_fused(a, s), "fused launch");
         return 0;
     }
 
-    // One Lloyd step, old centres cen[cur] -> new centres cen[cur ^ 1].
-    int enqueue_step(int iter, double tol, int flags)
+    FinalizeArgs finalize_args(int iter, double tol, int flags)
     {
-        int R = ug.R;
+        const bool recs = fblocks == 0 && sg.on;
+        const int R = fblocks > 0 ? fblocks : recs ? kRecR : ug.R;
+        return FinalizeArgs{recs ? s_rec : psum, pcnt, R, k, d, ld,
+                            recs ? s_roff : nullptr, recs ? s_rcnt : nullptr, recs ? s_counts : nullptr,
+                            cen[cur], cen[cur ^ 1], cnorm, sums, counts, part, shift_sq,
+                            st, iter, tol, flags, finalize_cols(R), &st->chg[iter & 1], &st->chg[(iter + 1) & 1]};
+    }
+
+    // One Lloyd step, old centres cen[cur] -> new centres cen[cur ^ 1].  On
+    // the fused path the stopping rules of a step are evaluated by the next
+    // step's kernel (decide) or, for the last step of a batch (last), by
+    // k_finalize_loop; on the generic path by k_finalize_loop every step.
+    int enqueue_step(int iter, double tol, int flags, bool decide, bool last)
+    {
         if (fblocks > 0) {
-            TRY(fused_step());
-            R = fblocks;
+            TRY(fused_step(iter, decide, tol, flags));
         } else {
-            TRY(assign(cen[cur], st, 1));
+            TRY(assign(cen[cur], st, &st->chg[iter & 1]));
             TRY(update());
         }
-        const bool recs = fblocks == 0 && sg.on;
-        if (recs) R = kRecR;
-        FinalizeArgs f{recs ? s_rec : psum, pcnt, R, k, d, ld,
-                       recs ? s_roff : nullptr, recs ? s_rcnt : nullptr, recs ? s_counts : nullptr,
-                       cen[cur], cen[cur ^ 1], cnorm, sums, counts, part, shift_sq,
-                       st, iter, tol, flags, finalize_cols(R)};
-        HIP_TRY(launch_finalize(f, s), "finalize launch");
+        const FinalizeArgs f = finalize_args(iter, tol, flags);
+        HIP_TRY(launch_finalize(f, s, fblocks == 0 || last), "finalize launch");
         cur ^= 1;
         return 0;
     }
@@ -531,7 +541,7 @@ struct Lloyd {
             done = 2;
         hs.done = done;
         hs.n_iter = t + 1;
-        hs.changed = 0;
+        hs.chg[0] = hs.chg[1] = 0;
         hs.shift_tot = shift_tot;
         hs.halt_iter = t;
         TRY(write_state(hs));
@@ -559,7 +569,7 @@ struct Lloyd {
         while (it < max_iter) {
             const long nb = std::min(batch, max_iter - it);
             const int c0 = cur;
-            for (long t = it; t < it + nb; ++t) TRY(enqueue_step((int)t, tol, flags));
+            for (long t = it; t < it + nb; ++t) TRY(enqueue_step((int)t, tol, flags, t > it, t + 1 == it + nb));
             TRY(read_state(&hs));
             if (hs.done == 3) {
                 const int t = hs.halt_iter;
@@ -600,7 +610,7 @@ struct Lloyd {
     {
         int n_iter = 0, done = 0;
         TRY(run_loop(max_iter, tol, flags, false, &n_iter, &done));
-        if (done != 1) TRY(assign(cen[cur], nullptr, 0));  // final E-step (_kmeans.py:736-748)
+        if (done != 1) TRY(assign(cen[cur], nullptr, nullptr));  // final E-step (_kmeans.py:736-748)
         double in = 0.0;
         TRY(inertia(&in));
         if (n_iter_out) *n_iter_out = n_iter;
@@ -708,7 +718,7 @@ int skmetal_kmeans_assign(const void* X, const void* centroids, void* assignment
     TRY(L.create(&c, (long)n, (int)d, (int)k));
     TRY(L.load_X(static_cast<const float*>(X), false));
     TRY(L.set_centers(static_cast<const float*>(centroids)));
-    TRY(L.assign(L.cen[L.cur], nullptr, 0));
+    TRY(L.assign(L.cen[L.cur], nullptr, nullptr));
     TRY(L.get_labels(static_cast<int32_t*>(assignments)));
     return 0;
 }
@@ -903,9 +913,9 @@ int skmetal_hip_lloyd_time_kernels(skmetal_hip_lloyd* h, size_t reps, float* ms_
     HIP_TRY(hipEventCreate(&e1), "hipEventCreate");
     HIP_TRY(hipEventCreate(&e2), "hipEventCreate");
     int rc = 0;
-    TRY(L.assign(L.cen[L.cur], nullptr, 0));  // labels for the update timing
+    TRY(L.assign(L.cen[L.cur], nullptr, nullptr));  // labels for the update timing
     hipEventRecord(e0, L.s);
-    for (size_t r = 0; r < reps && rc == 0; ++r) rc = L.fblocks > 0 ? L.fused_step() : L.assign(L.cen[L.cur], nullptr, 0);
+    for (size_t r = 0; r < reps && rc == 0; ++r) rc = L.fblocks > 0 ? L.fused_step() : L.assign(L.cen[L.cur], nullptr, nullptr);
     hipEventRecord(e1, L.s);
     for (size_t r = 0; r < reps && rc == 0 && L.fblocks == 0; ++r) rc = L.update();
     hipEventRecord(e2, L.s);
