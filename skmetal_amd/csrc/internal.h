@@ -131,11 +131,14 @@ struct FinalizeArgs {
     int cw;                // columns per finalize block: finalize_cols(R)
     const int* chg_cur;    // changes of this step's E-step
     int* chg_next;         // cleared for the next step's E-step
+    int after_reloc = 0;   // loop decision right after a relocation: empty
+                           // clusters do not stop the loop, every ||c||^2 is set
 };
 // Per-(cluster, column chunk) totals, then (with_loop) the loop decision.
 hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t s, bool with_loop);
 // The loop decision alone (after a fused step whose successor is not enqueued).
-hipError_t launch_finalize_loop(const FinalizeArgs& a, hipStream_t s);
+// nch: the chunk count the partials were written with (0: that of a.R).
+hipError_t launch_finalize_loop(const FinalizeArgs& a, hipStream_t s, int nch = 0);
 // A finalize block is 256 threads = cw columns x (256/cw) partial-sum lanes,
 // sized so that each thread reads at most about 8 of the R partials.
 inline int finalize_cols(int R)
@@ -154,7 +157,28 @@ struct RowDistArgs {
     LoopState* state;      // holds rowdist_ctr and receives `inertia`
 };
 int rowdist_grid(long n);
+// Row distances and their fixed-order total (two launches).
 hipError_t launch_rowdist(const RowDistArgs& a, hipStream_t s);
+
+// Device relocation of up to kMaxReloc empty clusters at once (see
+// kmeans_kernels.hip); more go through the host.
+constexpr int kMaxReloc = 64;
+constexpr int kRelocBlocks = 256;   // candidate blocks
+constexpr int kRelocCW = 64;        // columns per k_finalize_sums block
+struct RelocArgs {
+    const float* X; long n; int ld; int d; int k;
+    const int* labels;
+    const float* dist;     // [n] k_rowdist's per-row distances to the old centres
+    float* cand_d;         // [kRelocBlocks x E]
+    long* cand_i;          // [kRelocBlocks x E]
+    double* sums;          // [k x ld] fp64 totals, updated in place
+    int* counts;           // [k], updated in place
+    int* amax;             // [1] heaviest cluster after the moves
+    const float* C_old; float* C_new;
+    double* part;          // [k x nch x 2], nch = ceil(d / kRelocCW)
+};
+// E = number of empty clusters (1 <= E <= kMaxReloc).
+hipError_t launch_relocate(const RelocArgs& a, int E, hipStream_t s);
 
 hipError_t launch_colsum(const float* X, long n, int ld, int d, double* part, int nblk, hipStream_t s);
 int colsum_grid(long n);

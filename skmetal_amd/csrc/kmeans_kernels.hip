@@ -739,7 +739,7 @@ __global__ __launch_bounds__(256) void k_finalize_loop(FinalizeArgs a, int nch)
         }
         const int count = a.counts[j];
         a.shift_sq[j] = (float)tsq;
-        if (count > 0) a.cnorm[j] = (float)tnr;
+        if (count > 0 || a.after_reloc) a.cnorm[j] = (float)tnr;
         n_empty += count == 0;
         tot += (double)(float)tsq;
     }
@@ -752,7 +752,7 @@ __global__ __launch_bounds__(256) void k_finalize_loop(FinalizeArgs a, int nch)
         st->last_changed = changed;
         st->n_iter = a.iter + 1;
         int done = 0;
-        if (n_empty > 0)
+        if (n_empty > 0 && !a.after_reloc)
             done = 3;
         else if ((a.flags & kStopStrict) && changed == 0)
             done = 1;
@@ -772,9 +772,9 @@ hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t s, bool with_loop)
     return launch_finalize_loop(a, s);
 }
 
-hipError_t launch_finalize_loop(const FinalizeArgs& a, hipStream_t s)
+hipError_t launch_finalize_loop(const FinalizeArgs& a, hipStream_t s, int nch)
 {
-    hipLaunchKernelGGL(k_finalize_loop, dim3(1), dim3(256), 0, s, a, finalize_col_chunks(a.d, a.R));
+    hipLaunchKernelGGL(k_finalize_loop, dim3(1), dim3(256), 0, s, a, nch > 0 ? nch : finalize_col_chunks(a.d, a.R));
     return hipGetLastError();
 }
 
@@ -817,34 +817,216 @@ __global__ __launch_bounds__(256) void k_rowdist(RowDistArgs a)
         if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
         __syncthreads();
     }
-    __shared__ bool last;
-    if (threadIdx.x == 0) {
-        a.block_part[blockIdx.x] = red[0];
-        __threadfence();
-        last = atomicAdd(&a.state->rowdist_ctr, 1u) == gridDim.x - 1;
-    }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
+    if (threadIdx.x == 0) a.block_part[blockIdx.x] = red[0];
+}
+
+// Fixed-order total of the block partials (a second launch: the kernel
+// boundary replaces a cross-block fence).
+__global__ __launch_bounds__(256) void k_rowdist_total(RowDistArgs a, int nblk)
+{
+    __shared__ double red[256];
     double t = 0.0;
-    for (int b = threadIdx.x; b < (int)gridDim.x; b += 256) t += coherent_load(&a.block_part[b]);
+    for (int b = threadIdx.x; b < nblk; b += 256) t += a.block_part[b];
     red[threadIdx.x] = t;
     __syncthreads();
     for (int w = 128; w > 0; w >>= 1) {
         if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
         __syncthreads();
     }
-    if (threadIdx.x == 0) {
-        a.state->inertia = red[0];
-        a.state->rowdist_ctr = 0u;
-    }
+    if (threadIdx.x == 0) a.state->inertia = red[0];
 }
 
 int rowdist_grid(long n) { return (int)max(1L, (n + 255) / 256); }
 
 hipError_t launch_rowdist(const RowDistArgs& a, hipStream_t s)
 {
-    hipLaunchKernelGGL(k_rowdist, dim3(rowdist_grid(a.n)), dim3(256), 0, s, a);
+    const int nblk = rowdist_grid(a.n);
+    hipLaunchKernelGGL(k_rowdist, dim3(nblk), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(k_rowdist_total, dim3(1), dim3(256), 0, s, a, nblk);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// relocation of empty clusters on the device
+// ---------------------------------------------------------------------------
+//
+// sklearn's _relocate_empty_clusters_dense (_k_means_common.pyx:167-211):
+// the n_empty rows farthest from their centre (fp32 direct-form distances from
+// k_rowdist; descending distance, lower row index first on ties) move, in
+// that order, to the empty clusters in ascending cluster order; each moves its
+// row out of its old cluster's sums.  Then the centres are re-averaged from
+// the fp64 sums with _average_centers' handling of still-empty clusters
+// (:274-295) and the shift / ||c||^2 partials feed k_finalize_loop.
+
+// (d, row) order: larger distance first, then lower row index.
+__device__ __forceinline__ bool far_before(float d1, long i1, float d2, long i2)
+{
+    return d1 > d2 || (d1 == d2 && i1 < i2);
+}
+
+// One step of a selection: the best candidate strictly after (dl, il).
+__device__ __forceinline__ void far_pick(float& bd, long& bi, float d, long i, float dl, long il)
+{
+    if (far_before(dl, il, d, i) && (bi < 0 || far_before(d, i, bd, bi))) {
+        bd = d;
+        bi = i;
+    }
+}
+
+__device__ void far_block_reduce(float& bd, long& bi, float* sd, long* si)
+{
+    sd[threadIdx.x] = bd;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (threadIdx.x < w) {
+            const float d2 = sd[threadIdx.x + w];
+            const long i2 = si[threadIdx.x + w];
+            if (i2 >= 0 && (si[threadIdx.x] < 0 || far_before(d2, i2, sd[threadIdx.x], si[threadIdx.x]))) {
+                sd[threadIdx.x] = d2;
+                si[threadIdx.x] = i2;
+            }
+        }
+        __syncthreads();
+    }
+    bd = sd[0];
+    bi = si[0];
+    __syncthreads();
+}
+
+// Block b: its E farthest rows, in order, among rows [b*rpb, (b+1)*rpb).
+__global__ __launch_bounds__(256) void k_far_select(RelocArgs a, int E, long rpb)
+{
+    __shared__ float sd[256];
+    __shared__ long si[256];
+    const long r0 = (long)blockIdx.x * rpb;
+    const long r1 = min(a.n, r0 + rpb);
+    float dl = INFINITY;
+    long il = -1;
+    for (int e = 0; e < E; ++e) {
+        float bd = 0.f;
+        long bi = -1;
+        for (long r = r0 + threadIdx.x; r < r1; r += 256) far_pick(bd, bi, a.dist[r], r, dl, il);
+        far_block_reduce(bd, bi, sd, si);
+        if (threadIdx.x == 0) {
+            a.cand_d[(long)blockIdx.x * E + e] = bd;
+            a.cand_i[(long)blockIdx.x * E + e] = bi;
+        }
+        if (bi < 0) {
+            // this block has no more rows: pad the rest
+            for (int e2 = e + 1 + threadIdx.x; e2 < E; e2 += 256) {
+                a.cand_d[(long)blockIdx.x * E + e2] = 0.f;
+                a.cand_i[(long)blockIdx.x * E + e2] = -1;
+            }
+            return;
+        }
+        dl = bd;
+        il = bi;
+    }
+}
+
+// One block: merge the candidates, move the rows, then the heaviest cluster.
+__global__ __launch_bounds__(256) void k_far_apply(RelocArgs a, int E, int nb)
+{
+    __shared__ float sd[256];
+    __shared__ long si[256];
+    __shared__ long far[kMaxReloc];
+    __shared__ int empt[kMaxReloc];
+    __shared__ int ne_s;
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        int ne = 0;
+        for (int j = 0; j < a.k && ne < E; ++j)
+            if (a.counts[j] == 0) empt[ne++] = j;
+        ne_s = ne;
+    }
+    float dl = INFINITY;
+    long il = -1;
+    for (int e = 0; e < E; ++e) {
+        float bd = 0.f;
+        long bi = -1;
+        for (int c = tid; c < nb * E; c += 256) {
+            const long i = a.cand_i[c];
+            if (i >= 0) far_pick(bd, bi, a.cand_d[c], i, dl, il);
+        }
+        far_block_reduce(bd, bi, sd, si);
+        if (tid == 0) far[e] = bi;
+        dl = bd;
+        il = bi;
+        // the farthest distance decides whether anything moves (all zero: no)
+        if (e == 0 && tid == 0 && (bi < 0 || bd <= 0.f)) ne_s = 0;
+    }
+    __syncthreads();
+    const int ne = ne_s;
+    for (int e = 0; e < ne; ++e) {
+        const long fr = far[e];
+        const int j = empt[e];
+        const int o = a.labels[fr];
+        const float* x = a.X + fr * a.ld;
+        for (int c = tid; c < a.d; c += 256) {
+            a.sums[(long)o * a.ld + c] -= (double)x[c];
+            a.sums[(long)j * a.ld + c] = (double)x[c];
+        }
+        __syncthreads();
+        if (tid == 0) {
+            a.counts[j] = 1;
+            a.counts[o] -= 1;
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        int amax = 0;
+        for (int j = 1; j < a.k; ++j)
+            if (a.counts[j] > a.counts[amax]) amax = j;
+        *a.amax = amax;
+    }
+}
+
+// Centres from the fp64 sums (block (j, cc): columns [cc*CW, cc*CW + CW)),
+// and the shift^2 / ||c||^2 chunk partials, as k_finalize_cols.
+__global__ __launch_bounds__(256) void k_finalize_sums(RelocArgs a, int CW)
+{
+    const int j = blockIdx.x;
+    const int cc = blockIdx.y;
+    const int nch = gridDim.y;
+    const int tid = threadIdx.x;
+    __shared__ double shd[2][4];
+    const int col = cc * CW + tid;
+    const int cnt = a.counts[j];
+    const int amax = *a.amax;
+    double sq = 0.0, nrm = 0.0;
+    if (tid < CW && col < a.d) {
+        double v;
+        if (cnt > 0) {
+            v = a.sums[(long)j * a.ld + col] / (double)cnt;
+        } else {
+            // _average_centers: the heaviest cluster's row as the loop has it
+            // -- already divided when it comes before j, still a sum after
+            const double sa = a.sums[(long)amax * a.ld + col];
+            v = amax < j ? sa / (double)a.counts[amax] : sa;
+        }
+        const float cn = (float)v;
+        a.C_new[(long)j * a.ld + col] = cn;
+        const double df = (double)cn - (double)a.C_old[(long)j * a.ld + col];
+        sq = df * df;
+        nrm = (double)cn * (double)cn;
+    }
+    sq = block_sum(sq, shd[0]);
+    nrm = block_sum(nrm, shd[1]);
+    if (tid == 0) {
+        a.part[((long)j * nch + cc) * 2 + 0] = sq;
+        a.part[((long)j * nch + cc) * 2 + 1] = nrm;
+    }
+}
+
+hipError_t launch_relocate(const RelocArgs& a, int E, hipStream_t s)
+{
+    if (E < 1 || E > kMaxReloc) return hipErrorInvalidValue;
+    const int nb = kRelocBlocks;
+    const long rpb = (a.n + nb - 1) / nb;
+    hipLaunchKernelGGL(k_far_select, dim3(nb), dim3(256), 0, s, a, E, rpb);
+    hipLaunchKernelGGL(k_far_apply, dim3(1), dim3(256), 0, s, a, E, nb);
+    hipLaunchKernelGGL(k_finalize_sums, dim3(a.k, (a.d + kRelocCW - 1) / kRelocCW), dim3(256), 0, s, a, kRelocCW);
     return hipGetLastError();
 }
 

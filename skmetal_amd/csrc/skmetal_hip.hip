@@ -455,6 +455,39 @@ struct Lloyd {
         return 0;
     }
 
+    // Empty clusters at step t (old centres in cen[old]), on the device: the
+    // farthest rows move to the empty clusters, the centres are re-averaged
+    // from the fp64 sums and the loop decision is taken again (empty clusters
+    // no longer stop it).  hs is the state read at the halt; on return it
+    // holds the new decision.
+    float* r_cand_d = nullptr;
+    long* r_cand_i = nullptr;
+    int* r_amax = nullptr;
+    int device_relocate(int t, int old, double tol, int flags, LoopState& hs)
+    {
+        if (rowout == nullptr) TRY(grab((void**)&rowout, size_t(n) * sizeof(float)));
+        if (r_cand_d == nullptr) {
+            TRY(grab((void**)&r_cand_d, size_t(kRelocBlocks) * kMaxReloc * sizeof(float)));
+            TRY(grab((void**)&r_cand_i, size_t(kRelocBlocks) * kMaxReloc * sizeof(long)));
+            TRY(grab((void**)&r_amax, sizeof(int)));
+        }
+        LoopState w = hs;
+        w.done = 0;
+        TRY(write_state(w));
+        RowDistArgs r{X, n, ld, d, cen[old], k, labels, rowout, rowpart, st};
+        HIP_TRY(launch_rowdist(r, s), "rowdist launch");
+        RelocArgs ra{X, n, ld, d, k, labels, rowout, r_cand_d, r_cand_i, sums, counts, r_amax,
+                     cen[old], cen[old ^ 1], part};
+        HIP_TRY(launch_relocate(ra, hs.n_empty, s), "relocate launch");
+        cur = old;
+        FinalizeArgs f = finalize_args(t, tol, flags);
+        f.after_reloc = 1;
+        HIP_TRY(launch_finalize_loop(f, s, (d + kRelocCW - 1) / kRelocCW), "finalize launch");
+        cur = old ^ 1;
+        TRY(read_state(&hs));
+        return 0;
+    }
+
     // Empty clusters at step t (old centres in cen[old]): sklearn's relocation
     // (_k_means_common.pyx:167-211), averaging (:274-295) and shift on the host
     // from the device's fp64 sums, then upload the new centres to cen[old^1].
@@ -574,7 +607,13 @@ struct Lloyd {
             if (hs.done == 3) {
                 const int t = hs.halt_iter;
                 const int old = (c0 + (t - (int)it)) & 1;
-                TRY(host_relocate(t, old, tol, flags, hs));
+                // SKMETAL_HIP_HOST_RELOCATE=1 keeps the host path (A/B checks)
+                const char* env = getenv("SKMETAL_HIP_HOST_RELOCATE");
+                const bool on_host = (env != nullptr && env[0] == '1') || hs.n_empty < 1 || hs.n_empty > kMaxReloc;
+                if (on_host)
+                    TRY(host_relocate(t, old, tol, flags, hs));
+                else
+                    TRY(device_relocate(t, old, tol, flags, hs));
                 it = t + 1;
                 if (hs.done != 0) {
                     final_done = hs.done;

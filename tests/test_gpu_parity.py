@@ -224,6 +224,31 @@ def test_empty_cluster_relocation_matches_oracle(bridge):
     parity.check_centers(C, out["centers"], what="relocation fit")
 
 
+@pytest.mark.parametrize("n_dup", [1, 4, 9])
+def test_relocation_of_several_empty_clusters(bridge, n_dup, monkeypatch):
+    """Duplicated initial centres leave n_dup clusters empty after the first
+    E-step (lowest index wins ties); the device relocation must follow the
+    oracle's (sklearn's) rule, and agree with the host relocation path."""
+    rng = np.random.default_rng(40 + n_dup)
+    cen = rng.uniform(-8, 8, (6, 8))
+    X = (cen[rng.integers(0, 6, 6000)] + rng.standard_normal((6000, 8))).astype(np.float32)
+    base = X[np.sort(rng.choice(6000, 12, replace=False))]
+    C0 = np.concatenate([base, base[:n_dup]])  # the copies come later: they get no rows
+    out = oracle.lloyd(X, C0, 60)
+    res = {}
+    for where in ("device", "host"):
+        if where == "host":
+            monkeypatch.setenv("SKMETAL_HIP_HOST_RELOCATE", "1")
+        C = C0.copy()
+        lab = np.empty(X.shape[0], np.int32)
+        res[where] = bridge.kmeans_fit(X, C, lab, 60, 0.0, strict=True) + (C,)
+    monkeypatch.delenv("SKMETAL_HIP_HOST_RELOCATE", raising=False)
+    for where, (n_iter, inertia, C) in res.items():
+        assert n_iter == out["n_iter"], f"{where}: n_iter {n_iter} vs oracle {out['n_iter']}"
+        parity.check_centers(C, out["centers"], what=f"{where} relocation n_dup={n_dup}")
+    parity.check_centers(res["device"][2], res["host"][2], rtol=1e-5, what="device vs host relocation")
+
+
 @pytest.mark.parametrize("wl,steps", [("c1", 4), ("c2", 3)])
 def test_workload_lockstep_full_size(bridge, wl, steps):
     from skmetal_amd import _synth
