@@ -5,8 +5,10 @@ Workload: 500,000 x 100 fp32 from 50 isotropic Gaussian blobs (centres
 skmetal's README headline.  A "step" is one Lloyd iteration (fused E-step on
 fp32 MFMA, per-cluster sums, finalize) over all 500,000 rows, with X already
 resident in HBM.  The steps are timed with HIP events on the library's stream
-(skmetal_hip_lloyd_iterate); the assign kernel is also timed alone
-(skmetal_hip_lloyd_time_kernels) for its roofline fraction.
+(skmetal_hip_lloyd_iterate).  The same steps are then run again from the same
+initial centres with each step's kernels bracketed by HIP events on that
+stream: the dominant kernel's average launch time over those steps gives its
+roofline fraction.
 
 cpu_baseline: scikit-learn's KMeans(algorithm="lloyd") -- the CPU
 implementation skmetal routes KMeans to -- on the same workload, same init, on
@@ -96,7 +98,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--workload", default="c2")
     ap.add_argument("--no-cpu", action="store_true", help="skip the sklearn CPU baseline")
     ap.add_argument("--cpu-iters", type=int, default=8)
@@ -127,7 +129,11 @@ def main():
         t = time.perf_counter()
         ms = h.iterate(args.steps)
         wall = time.perf_counter() - t
-        ms_assign, ms_update = h.time_kernels(max(20, args.steps // 2))
+        # the same steps again from the same centres, each kernel bracketed by
+        # HIP events (a marker costs a few microseconds of queue time, so the
+        # step time above is measured without them)
+        h.set_centers(C0)
+        _, (ms_assign, ms_update, ms_final) = h.iterate(args.steps, kernel_times=True)
         mode = h.info()
     if args.calib_copy:
         copy_probe(args.calib_copy)
@@ -165,8 +171,9 @@ def main():
         "step_mode": ("fused: k_fused (E-step + per-cluster sums) + k_finalize" if fused
                       else "k_assign + k_update + k_finalize"),
         "partials": mode["partials"],
-        "kernels_ms": ({"k_fused": round(ms_assign, 5)} if fused
-                       else {"k_assign": round(ms_assign, 5), "k_update": round(ms_update, 5)}),
+        "kernels_ms": ({"k_fused": round(ms_assign, 5), "k_finalize": round(ms_final, 5)} if fused
+                       else {"k_assign": round(ms_assign, 5), "update": round(ms_update, 5),
+                             "k_finalize": round(ms_final, 5)}),
         "roofline": {
             "kernel": (f"{kname}: ||c||^2 - 2 x.c on fp32 MFMA + argmin"
                        + (" + per-cluster sums" if fused else "")),

@@ -119,18 +119,17 @@ SKMETAL_API int skmetal_hip_lloyd_set_centers(skmetal_hip_lloyd* h, const float*
 /* Run exactly `iters` Lloyd steps (E-step + M-step, no convergence stop;
  * empty clusters are still relocated).  If ms_out is not NULL it receives
  * the elapsed time of the steps measured with HIP events on the handle's
- * stream. */
-SKMETAL_API int skmetal_hip_lloyd_iterate(skmetal_hip_lloyd* h, size_t iters, float* ms_out);
+ * stream.  If kernel_ms is not NULL (iters <= 4096) each step is also
+ * bracketed by HIP events and kernel_ms[0..2] receive the average time per
+ * step (ms) of the E-step kernel (the fused E-step + sums kernel when the
+ * handle uses it), of the separate update kernels (0 when fused) and of the
+ * finalize. */
+SKMETAL_API int skmetal_hip_lloyd_iterate(skmetal_hip_lloyd* h, size_t iters, float* ms_out,
+                                          float* kernel_ms);
 /* sklearn loop (see skmetal_hip_kmeans_fit) from the current centres,
  * including the final E-step and inertia. */
 SKMETAL_API int skmetal_hip_lloyd_run(skmetal_hip_lloyd* h, size_t max_iter, double tol, int flags,
                           int32_t* n_iter_out, double* inertia_out);
-/* Average time of one launch (ms) over `reps` back-to-back launches on the
- * current centres (HIP events): *ms_assign receives the E-step kernel (the
- * fused E-step + per-cluster-sum kernel when the handle uses it),
- * *ms_update the separate update kernel (0 in fused mode). */
-SKMETAL_API int skmetal_hip_lloyd_time_kernels(skmetal_hip_lloyd* h, size_t reps, float* ms_assign,
-                                   float* ms_update);
 /* *fused = 1 when a step runs as one fused E-step + sums kernel (k <= 64,
  * padded d <= 128); *partials = per-step partial sums the finalize reduces. */
 SKMETAL_API int skmetal_hip_lloyd_info(skmetal_hip_lloyd* h, int* fused, int* partials);

@@ -53,11 +53,10 @@ _REGISTRY = [
     ("skmetal_hip_lloyd_destroy", ctypes.c_int, _vp),
     ("skmetal_hip_lloyd_load", ctypes.c_int, _vp, _vp, ctypes.c_int),
     ("skmetal_hip_lloyd_set_centers", ctypes.c_int, _vp, _vp),
-    ("skmetal_hip_lloyd_iterate", ctypes.c_int, _vp, _c_size, ctypes.POINTER(ctypes.c_float)),
+    ("skmetal_hip_lloyd_iterate", ctypes.c_int, _vp, _c_size, ctypes.POINTER(ctypes.c_float),
+     ctypes.POINTER(ctypes.c_float)),
     ("skmetal_hip_lloyd_run", ctypes.c_int, _vp, _c_size, ctypes.c_double, ctypes.c_int,
      ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_double)),
-    ("skmetal_hip_lloyd_time_kernels", ctypes.c_int, _vp, _c_size, ctypes.POINTER(ctypes.c_float),
-     ctypes.POINTER(ctypes.c_float)),
     ("skmetal_hip_lloyd_info", ctypes.c_int, _vp, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)),
     ("skmetal_hip_lloyd_get_centers", ctypes.c_int, _vp, _vp),
     ("skmetal_hip_lloyd_get_labels", ctypes.c_int, _vp, _vp),
@@ -255,9 +254,16 @@ class LloydHandle:
         assert C.shape == (self.k, self.d)
         _check(_lib.skmetal_hip_lloyd_set_centers(self._h, C.ctypes.data), "skmetal_hip_lloyd_set_centers")
 
-    def iterate(self, iters: int) -> float:
+    def iterate(self, iters: int, kernel_times: bool = False):
+        """Run `iters` fixed Lloyd steps; returns their time (ms), or with
+        kernel_times (ms, (main, update, finalize)) where the second item holds
+        the average per-step kernel times measured inside the same run."""
         ms = ctypes.c_float(0.0)
-        _check(_lib.skmetal_hip_lloyd_iterate(self._h, int(iters), ctypes.byref(ms)), "skmetal_hip_lloyd_iterate")
+        km = (ctypes.c_float * 3)()
+        _check(_lib.skmetal_hip_lloyd_iterate(self._h, int(iters), ctypes.byref(ms), km if kernel_times else None),
+               "skmetal_hip_lloyd_iterate")
+        if kernel_times:
+            return float(ms.value), tuple(float(v) for v in km)
         return float(ms.value)
 
     def run(self, max_iter: int, tol_abs: float = 0.0, strict: bool = True):
@@ -267,13 +273,6 @@ class LloydHandle:
                                           SKMETAL_FIT_STRICT if strict else 0, ctypes.byref(n_iter),
                                           ctypes.byref(inertia)), "skmetal_hip_lloyd_run")
         return int(n_iter.value), float(inertia.value)
-
-    def time_kernels(self, reps: int):
-        a = ctypes.c_float(0.0)
-        u = ctypes.c_float(0.0)
-        _check(_lib.skmetal_hip_lloyd_time_kernels(self._h, int(reps), ctypes.byref(a), ctypes.byref(u)),
-               "skmetal_hip_lloyd_time_kernels")
-        return float(a.value), float(u.value)
 
     def info(self):
         fused = ctypes.c_int(0)

@@ -134,7 +134,6 @@ __global__ __launch_bounds__(512, 1) void k_fused(FusedArgs a)
     float* __restrict__ psum = a.psum;
     int* __restrict__ pcnt = a.pcnt;
     LoopState* st = a.state;
-    if (st->done != 0) return;
     constexpr int CPC = 4 * KG;
     constexpr int WS = walk_steps<KG>();
     constexpr int XS = fused_stride(NQ);      // ld == 4 * NQ
@@ -148,6 +147,7 @@ __global__ __launch_bounds__(512, 1) void k_fused(FusedArgs a)
     __shared__ __attribute__((aligned(16))) float sN[CPC];
     __shared__ int sReady[4];  // tiles the MFMA wave has put in LDS
     __shared__ int sProg[4];   // chunks the walker has read: tile * NQ + chunk
+    __shared__ int sDone;      // nonzero: the loop has halted, nothing to do
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps descriptors scalar
@@ -160,98 +160,31 @@ __global__ __launch_bounds__(512, 1) void k_fused(FusedArgs a)
     const int toff = (CPC + 1 + pair * 64) * XS * 4;
     const char* lbase = reinterpret_cast<const char*>(lds);
 
-    for (int idx = tid; idx < CPC * NQ; idx += 512) {
-        const int cl = idx / NQ;
-        const int q = idx - cl * NQ;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (cl < k) v = *reinterpret_cast<const float4*>(C + (long)cl * ld + 4 * q);
-        *reinterpret_cast<float4*>(&sC[cl * XS + 4 * q]) = v;
-    }
-    for (int i = tid; i < XS; i += 512) zrow[i] = 0.f;
-    if (a.decide) {
-        // the previous step's stopping rules, evaluated identically by every
-        // block (same loads, same order as k_finalize_loop for k <= 64)
-        __shared__ int sDone;
-        if (wave == 0) {
-            const int j = lane;
-            double tsq = 0.0, tnr = 0.0;
-            int count = 1;
-            if (j < k) {
-                // all chunk partials in flight at once (the sum order is the
-                // finalize's: chunk 0, 1, ...)
-                const double* pj = a.part + (long)j * a.nch * 2;
-                constexpr int NB = 16;
-                for (int c0 = 0; c0 < a.nch; c0 += NB) {
-                    double v[2 * NB];
-#pragma unroll
-                    for (int u = 0; u < NB; ++u) {
-                        const int c = min(c0 + u, a.nch - 1);
-                        v[2 * u] = pj[2 * c];
-                        v[2 * u + 1] = pj[2 * c + 1];
-                    }
-#pragma unroll
-                    for (int u = 0; u < NB; ++u) {
-                        if (c0 + u < a.nch) {
-                            tsq += v[2 * u];
-                            tnr += v[2 * u + 1];
-                        }
-                    }
-                }
-                count = a.counts[j];
-            }
-            const int n_empty = wave_sum(j < k && count == 0 ? 1 : 0);
-            const double tot = wave_sum(j < k ? (double)(float)tsq : 0.0);
-            const int chg = *a.prev_changed;
-            int done = 0;
-            if (n_empty > 0)
-                done = 3;
-            else if ((a.flags & kStopStrict) && chg == 0)
-                done = 1;
-            else if (a.tol > 0.0 && tot <= a.tol)
-                done = 2;
-            if (blockIdx.x == 0) {
-                if (j < k) {
-                    a.shift_sq[j] = (float)tsq;
-                    if (count > 0) a.cnorm_out[j] = (float)tnr;
-                }
-                if (lane == 0) {
-                    st->n_empty = n_empty;
-                    st->shift_tot = tot;
-                    st->last_changed = chg;
-                    st->n_iter = a.iter;
-                    if (done != 0) st->halt_iter = a.iter - 1;
-                    st->done = done;
-                }
-            }
-            // padding clusters get ||c||^2 = +inf: their distance never wins
-            if (j < CPC) sN[j] = j < k ? (float)tnr : INFINITY;
-            if (lane == 0) sDone = done;
-        }
-        __syncthreads();
-        if (sDone != 0) return;
-    } else {
-        // padding clusters get ||c||^2 = +inf: their distance never wins
-        for (int i = tid; i < CPC; i += 512) sN[i] = i < k ? a.cnorm[i] : INFINITY;
-    }
-    if (tid < 4) {
-        sReady[tid] = 0;
-        sProg[tid] = 0;
-    }
-
     const long ntiles = (n + 63) >> 6;
     const long P = (long)gridDim.x * 4;
     const long t0 = (long)blockIdx.x * 4 + pair;
     const int rounds = t0 < ntiles ? (int)((ntiles - t0 + P - 1) / P) : 0;  // this pair's tiles
     const int xoff = lane * ld * 4;  // this lane's row inside a tile of X
-    __syncthreads();
 
     if (wave < 4) {
         // MFMA wave.  Tile t's row: chunks [0, K) in pre (two sets, one per
-        // round parity, loaded a round ahead), chunks [K, NQ) in xv.
+        // round parity, loaded a round ahead), chunks [K, NQ) in xv.  The
+        // first tiles are requested before anything else: their HBM latency
+        // overlaps the walkers' set-up.
+        float4 preA[KA], preB[KA], xv[NQ - K];
+        const __amdgpu_buffer_rsrc_t r0 = tile_rsrc(X, t0, n, ld);
+        const __amdgpu_buffer_rsrc_t r1 = tile_rsrc(X, t0 + P, n, ld);
+#pragma unroll
+        for (int q = 0; q < K; ++q) preA[q] = load_quad(r0, xoff + 16 * q);
+#pragma unroll
+        for (int q = K; q < NQ; ++q) xv[q - K] = load_quad(r0, xoff + 16 * q);
+#pragma unroll
+        for (int q = 0; q < K; ++q) preB[q] = load_quad(r1, xoff + 16 * q);
+        __syncthreads();  // LDS set up by the walkers
+        if (sDone != 0) return;
         const char* cbase = reinterpret_cast<const char*>(sC + (lane < CPC ? lane : CPC - 1) * XS);
         float* myrow = tile + lane * XS;
         int changed = 0;
-        float4 preA[KA], preB[KA], xv[NQ - K];
 
         auto round = [&](int r, float4* pre) {
             const long t = t0 + (long)r * P;
@@ -320,16 +253,6 @@ __global__ __launch_bounds__(512, 1) void k_fused(FusedArgs a)
             set_flag(&sReady[pair], r + 1);
         };
 
-        {
-            const __amdgpu_buffer_rsrc_t r0 = tile_rsrc(X, t0, n, ld);
-            const __amdgpu_buffer_rsrc_t r1 = tile_rsrc(X, t0 + P, n, ld);
-#pragma unroll
-            for (int q = 0; q < K; ++q) preA[q] = load_quad(r0, xoff + 16 * q);
-#pragma unroll
-            for (int q = K; q < NQ; ++q) xv[q - K] = load_quad(r0, xoff + 16 * q);
-#pragma unroll
-            for (int q = 0; q < K; ++q) preB[q] = load_quad(r1, xoff + 16 * q);
-        }
         int r = 0;
         for (; r + 1 < rounds; r += 2) {
             round(r, preA);
@@ -340,6 +263,103 @@ __global__ __launch_bounds__(512, 1) void k_fused(FusedArgs a)
         __syncthreads();  // every pair's walker is done: the tile area is free
         __syncthreads();  // the walkers' sums are in LDS
     } else {
+        // walker waves: the halt test, then centres and the zero row into
+        // LDS (all loads in flight at once) and ||c||^2
+        const int prev = st->done;  // an earlier step halted the loop
+        if (prev != 0) {
+            if (tid == 256) sDone = prev;
+            __syncthreads();
+            return;
+        }
+        const int wt = tid - 256;
+        constexpr int NF = (CPC * NQ + 255) / 256;
+        float4 cf[NF];
+#pragma unroll
+        for (int u = 0; u < NF; ++u) {
+            const int idx = wt + 256 * u;
+            const int cl = idx / NQ;
+            const int q = idx - cl * NQ;
+            cf[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (idx < CPC * NQ && cl < k) cf[u] = *reinterpret_cast<const float4*>(C + (long)cl * ld + 4 * q);
+        }
+#pragma unroll
+        for (int u = 0; u < NF; ++u) {
+            const int idx = wt + 256 * u;
+            const int cl = idx / NQ;
+            const int q = idx - cl * NQ;
+            if (idx < CPC * NQ) *reinterpret_cast<float4*>(&sC[cl * XS + 4 * q]) = cf[u];
+        }
+        for (int i = wt; i < XS; i += 256) zrow[i] = 0.f;
+        if (wt < 4) {
+            sReady[wt] = 0;
+            sProg[wt] = 0;
+        }
+        if (wave == 4) {
+            const int j = lane;
+            if (a.decide) {
+                // the previous step's stopping rules, evaluated identically by
+                // every block (same loads, same order as k_finalize_loop for
+                // k <= 64)
+                double tsq = 0.0, tnr = 0.0;
+                int count = 1;
+                if (j < k) {
+                    // all chunk partials in flight at once (the sum order is
+                    // the finalize's: chunk 0, 1, ...)
+                    const double* pj = a.part + (long)j * a.nch * 2;
+                    constexpr int NB = 16;
+                    for (int c0 = 0; c0 < a.nch; c0 += NB) {
+                        double v[2 * NB];
+#pragma unroll
+                        for (int u = 0; u < NB; ++u) {
+                            const int c = min(c0 + u, a.nch - 1);
+                            v[2 * u] = pj[2 * c];
+                            v[2 * u + 1] = pj[2 * c + 1];
+                        }
+#pragma unroll
+                        for (int u = 0; u < NB; ++u) {
+                            if (c0 + u < a.nch) {
+                                tsq += v[2 * u];
+                                tnr += v[2 * u + 1];
+                            }
+                        }
+                    }
+                    count = a.counts[j];
+                }
+                const int n_empty = wave_sum(j < k && count == 0 ? 1 : 0);
+                const double tot = wave_sum(j < k ? (double)(float)tsq : 0.0);
+                const int chg = *a.prev_changed;
+                int done = 0;
+                if (n_empty > 0)
+                    done = 3;
+                else if ((a.flags & kStopStrict) && chg == 0)
+                    done = 1;
+                else if (a.tol > 0.0 && tot <= a.tol)
+                    done = 2;
+                if (blockIdx.x == 0) {
+                    if (j < k) {
+                        a.shift_sq[j] = (float)tsq;
+                        if (count > 0) a.cnorm_out[j] = (float)tnr;
+                    }
+                    if (lane == 0) {
+                        st->n_empty = n_empty;
+                        st->shift_tot = tot;
+                        st->last_changed = chg;
+                        st->n_iter = a.iter;
+                        if (done != 0) st->halt_iter = a.iter - 1;
+                        st->done = done;
+                    }
+                }
+                // padding clusters get ||c||^2 = +inf: their distance never wins
+                if (j < CPC) sN[j] = j < k ? (float)tnr : INFINITY;
+                if (lane == 0) sDone = done;
+            } else {
+                // padding clusters get ||c||^2 = +inf: their distance never wins
+                if (j < CPC) sN[j] = j < k ? a.cnorm[j] : INFINITY;
+                if (lane == 0) sDone = 0;
+            }
+        }
+        __syncthreads();
+        if (sDone != 0) return;
         // walker
         float4 S[NQ];
 #pragma unroll

@@ -69,6 +69,7 @@ constexpr size_t kPinBytes = size_t(32) << 20;  // per staging buffer
 // 16 columns x 16 lanes per block; a cluster's records are read in batches
 constexpr int kRecR = 128;
 constexpr size_t kMaxDim = size_t(1) << 20;
+constexpr size_t kMaxTimedSteps = 4096;  // steps skmetal_hip_lloyd_iterate can time per kernel
 
 // ---------------------------------------------------------------------------
 // context: device, stream, pinned staging, size-keyed device buffer cache
@@ -338,11 +339,20 @@ struct Lloyd {
         return 0;
     }
 
+    // Per-step kernel timing: when kev_base >= 0, step kev_base + i records
+    // kev[4i .. 4i+3] before its E-step (or fused) kernel, after it, after
+    // the update kernels and after the finalize.  A step enqueued again
+    // (after a halt) records again.
+    std::vector<hipEvent_t> kev;
+    long kev_base = -1;
+
     void destroy()
     {
         if (s) hipStreamSynchronize(s);
         for (void* p : owned) C->release(p);
         owned.clear();
+        for (hipEvent_t e : kev) hipEventDestroy(e);
+        kev.clear();
     }
 
     int load_X(const float* host, bool center)
@@ -443,14 +453,22 @@ struct Lloyd {
     // k_finalize_loop; on the generic path by k_finalize_loop every step.
     int enqueue_step(int iter, double tol, int flags, bool decide, bool last)
     {
+        hipEvent_t* ev = nullptr;
+        if (kev_base >= 0 && iter >= kev_base && 4 * (iter - kev_base + 1) <= (long)kev.size())
+            ev = &kev[4 * (iter - kev_base)];
+        if (ev) HIP_TRY(hipEventRecord(ev[0], s), "hipEventRecord");
         if (fblocks > 0) {
             TRY(fused_step(iter, decide, tol, flags));
+            if (ev) HIP_TRY(hipEventRecord(ev[1], s), "hipEventRecord");
         } else {
             TRY(assign(cen[cur], st, &st->chg[iter & 1]));
+            if (ev) HIP_TRY(hipEventRecord(ev[1], s), "hipEventRecord");
             TRY(update());
         }
+        if (ev) HIP_TRY(hipEventRecord(ev[2], s), "hipEventRecord");
         const FinalizeArgs f = finalize_args(iter, tol, flags);
         HIP_TRY(launch_finalize(f, s, fblocks == 0 || last), "finalize launch");
+        if (ev) HIP_TRY(hipEventRecord(ev[3], s), "hipEventRecord");
         cur ^= 1;
         return 0;
     }
@@ -898,12 +916,20 @@ int skmetal_hip_lloyd_set_centers(skmetal_hip_lloyd* h, const float* C)
     return 0;
 }
 
-int skmetal_hip_lloyd_iterate(skmetal_hip_lloyd* h, size_t iters, float* ms_out)
+int skmetal_hip_lloyd_iterate(skmetal_hip_lloyd* h, size_t iters, float* ms_out, float* kernel_ms)
 {
     Context& c = ctx();
     Guard g(c);
     if (!h) return fail(SKMETAL_EINVAL, "null pointer argument");
     Lloyd& L = h->L;
+    if (kernel_ms) {
+        if (iters > kMaxTimedSteps) return fail(SKMETAL_ERANGE, "iterate: kernel timing covers at most 4096 steps");
+        while (L.kev.size() < 4 * iters) {
+            hipEvent_t e;
+            HIP_TRY(hipEventCreate(&e), "hipEventCreate");
+            L.kev.push_back(e);
+        }
+    }
     hipEvent_t e0, e1;
     HIP_TRY(hipEventCreate(&e0), "hipEventCreate");
     HIP_TRY(hipEventCreate(&e1), "hipEventCreate");
@@ -912,13 +938,28 @@ int skmetal_hip_lloyd_iterate(skmetal_hip_lloyd* h, size_t iters, float* ms_out)
     LoopState hs{};
     rc = L.write_state(hs);
     if (rc == 0) {
+        L.kev_base = kernel_ms ? 0 : -1;
         hipEventRecord(e0, L.s);
         int n_iter = 0, done = 0;
         rc = L.run_loop((long)iters, 0.0, 0, true, &n_iter, &done);
         hipEventRecord(e1, L.s);
+        L.kev_base = -1;
         hipError_t e = hipEventSynchronize(e1);
-        if (e != hipSuccess) rc = hip_fail(e, "hipEventSynchronize");
+        if (rc == 0 && e != hipSuccess) rc = hip_fail(e, "hipEventSynchronize");
         if (rc == 0 && ms_out) hipEventElapsedTime(ms_out, e0, e1);
+        if (rc == 0 && kernel_ms) {
+            // averages over the steps: main kernel, update kernels, finalize
+            double sum[3] = {0.0, 0.0, 0.0};
+            for (size_t i = 0; i < iters && rc == 0; ++i) {
+                for (int j = 0; j < 3; ++j) {
+                    float t = 0.f;
+                    const hipError_t ee = hipEventElapsedTime(&t, L.kev[4 * i + j], L.kev[4 * i + j + 1]);
+                    if (ee != hipSuccess) rc = hip_fail(ee, "hipEventElapsedTime");
+                    sum[j] += t;
+                }
+            }
+            for (int j = 0; j < 3; ++j) kernel_ms[j] = iters ? float(sum[j] / double(iters)) : 0.f;
+        }
     }
     hipEventDestroy(e0);
     hipEventDestroy(e1);
@@ -937,38 +978,6 @@ int skmetal_hip_lloyd_run(skmetal_hip_lloyd* h, size_t max_iter, double tol, int
     if (n_iter_out) *n_iter_out = it;
     if (inertia_out) *inertia_out = in;
     return 0;
-}
-
-int skmetal_hip_lloyd_time_kernels(skmetal_hip_lloyd* h, size_t reps, float* ms_assign, float* ms_update)
-{
-    Context& c = ctx();
-    Guard g(c);
-    if (!h || reps == 0) return fail(SKMETAL_EINVAL, "bad argument");
-    Lloyd& L = h->L;
-    LoopState hs{};
-    TRY(L.write_state(hs));
-    hipEvent_t e0, e1, e2;
-    HIP_TRY(hipEventCreate(&e0), "hipEventCreate");
-    HIP_TRY(hipEventCreate(&e1), "hipEventCreate");
-    HIP_TRY(hipEventCreate(&e2), "hipEventCreate");
-    int rc = 0;
-    TRY(L.assign(L.cen[L.cur], nullptr, nullptr));  // labels for the update timing
-    hipEventRecord(e0, L.s);
-    for (size_t r = 0; r < reps && rc == 0; ++r) rc = L.fblocks > 0 ? L.fused_step() : L.assign(L.cen[L.cur], nullptr, nullptr);
-    hipEventRecord(e1, L.s);
-    for (size_t r = 0; r < reps && rc == 0 && L.fblocks == 0; ++r) rc = L.update();
-    hipEventRecord(e2, L.s);
-    hipError_t e = hipEventSynchronize(e2);
-    if (rc == 0 && e != hipSuccess) rc = hip_fail(e, "hipEventSynchronize");
-    float t01 = 0.f, t12 = 0.f;
-    hipEventElapsedTime(&t01, e0, e1);
-    hipEventElapsedTime(&t12, e1, e2);
-    if (ms_assign) *ms_assign = t01 / float(reps);
-    if (ms_update) *ms_update = t12 / float(reps);
-    hipEventDestroy(e0);
-    hipEventDestroy(e1);
-    hipEventDestroy(e2);
-    return rc;
 }
 
 int skmetal_hip_lloyd_info(skmetal_hip_lloyd* h, int* fused, int* partials)
