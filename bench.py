@@ -3,7 +3,7 @@
 Workload: 500,000 x 100 fp32 from 50 isotropic Gaussian blobs (centres
 ~U[-10,10]^100, sigma 1), k = 50, seeded random-row init -- the shape of
 skmetal's README headline.  A "step" is one Lloyd iteration (fused E-step on
-fp32 MFMA, per-cluster sums, finalize) over all 500,000 rows, with X already
+fp16x2-split MFMA, per-cluster sums, finalize) over all 500,000 rows, with X already
 resident in HBM.  The steps are timed with HIP events on the library's stream
 (skmetal_hip_lloyd_iterate).  The same steps are then run again from the same
 initial centres with each step's kernels bracketed by HIP events on that
@@ -142,10 +142,36 @@ def main():
     it_s = 1.0 / step_s
     flops = 2.0 * n * k * d
     assign_s = ms_assign / 1e3
-    achieved = flops / assign_s / 1e12
-    fused = mode["fused"]
-    kname = "k_fused" if fused else "k_assign"
+    fused, f16 = mode["fused"], mode["f16"]
+    kname = "k_fused16" if f16 else "k_fused" if fused else "k_assign"
     traffic = _traffic_from_profile(f"{kname}_{args.workload}_pmc.txt")
+    if f16:
+        # HBM roofline: the bytes one launch must move -- X once, the labels
+        # read and written, the per-block partial sums and counts written
+        nbytes = 4.0 * n * d + 8.0 * n + 4.0 * mode["partials"] * k * (d + 1)
+        roofline = {
+            "kernel": "k_fused16: E-step (||c||^2 - 2 x.c, fp16x2-split MFMA) + argmin + per-cluster sums",
+            "bound": "hbm",
+            "achieved": round(nbytes / assign_s / 1e9, 1),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(nbytes / assign_s / 1e9 / PEAK_HBM_GBPS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes": nbytes,
+            "fp32_equiv_tflops": round(flops / assign_s / 1e12, 2),
+        }
+    else:
+        achieved = flops / assign_s / 1e12
+        roofline = {
+            "kernel": (f"{kname}: ||c||^2 - 2 x.c on fp32 MFMA + argmin"
+                       + (" + per-cluster sums" if fused else "")),
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_FP32_MFMA_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+            "traffic": traffic,
+        }
 
     cpu = None if args.no_cpu else cpu_baseline(X, C0, args.cpu_iters)
 
@@ -168,22 +194,15 @@ def main():
         "dist_evals_per_s": round(n * k * it_s, 1),
         "wall_s_timed": round(wall, 4),
         "h2d_s": round(h2d_s, 4),
-        "step_mode": ("fused: k_fused (E-step + per-cluster sums) + k_finalize" if fused
+        "step_mode": (f"fused: {kname} (E-step + per-cluster sums) + k_finalize" if fused
                       else "k_assign + k_update + k_finalize"),
+        "e_step": ("fp16x2 split (x, c scaled by 2^s; hi/lo parts), v_mfma_f32_16x16x32_f16, fp32 accumulate"
+                   if f16 else "fp32 MFMA (v_mfma_f32_4x4x1_16b_f32)"),
         "partials": mode["partials"],
-        "kernels_ms": ({"k_fused": round(ms_assign, 5), "k_finalize": round(ms_final, 5)} if fused
+        "kernels_ms": ({kname: round(ms_assign, 5), "k_finalize": round(ms_final, 5)} if fused
                        else {"k_assign": round(ms_assign, 5), "update": round(ms_update, 5),
                              "k_finalize": round(ms_final, 5)}),
-        "roofline": {
-            "kernel": (f"{kname}: ||c||^2 - 2 x.c on fp32 MFMA + argmin"
-                       + (" + per-cluster sums" if fused else "")),
-            "bound": "mfma",
-            "achieved": round(achieved, 2),
-            "peak": PEAK_FP32_MFMA_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
-            "traffic": traffic,
-        },
+        "roofline": roofline,
         "cpu_baseline": cpu,
     }
     if cpu:

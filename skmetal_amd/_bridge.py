@@ -279,7 +279,7 @@ class LloydHandle:
         partials = ctypes.c_int(0)
         _check(_lib.skmetal_hip_lloyd_info(self._h, ctypes.byref(fused), ctypes.byref(partials)),
                "skmetal_hip_lloyd_info")
-        return dict(fused=bool(fused.value), partials=int(partials.value))
+        return dict(fused=bool(fused.value), f16=fused.value == 2, partials=int(partials.value))
 
     def centers(self):
         out = np.empty((self.k, self.d), np.float32)

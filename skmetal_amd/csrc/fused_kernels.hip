@@ -122,6 +122,170 @@ __device__ __forceinline__ int argmin_tree(float* d)
     return ix[0];
 }
 
+// Wave 4 of every block: the previous step's stopping rules when a.decide
+// (evaluated identically by every block: same loads, same order as
+// k_finalize_loop for k <= 64; block 0 records the decision), else nothing
+// to decide.  Writes ||c||^2 of this step's centres to sN (padding clusters
+// j >= k get +inf: their distance never wins) and the decision to *sDone.
+template <int CPC>
+__device__ __forceinline__ void step_norms(const FusedArgs& a, int lane, float* sN, int* sDone)
+{
+    const int k = a.k;
+    const int j = lane;
+    if (a.decide) {
+        double tsq = 0.0, tnr = 0.0;
+        int count = 1;
+        if (j < k) {
+            // all chunk partials in flight at once (the sum order is the
+            // finalize's: chunk 0, 1, ...)
+            const double* pj = a.part + (long)j * a.nch * 2;
+            constexpr int NB = 16;
+            for (int c0 = 0; c0 < a.nch; c0 += NB) {
+                double v[2 * NB];
+#pragma unroll
+                for (int u = 0; u < NB; ++u) {
+                    const int c = min(c0 + u, a.nch - 1);
+                    v[2 * u] = pj[2 * c];
+                    v[2 * u + 1] = pj[2 * c + 1];
+                }
+#pragma unroll
+                for (int u = 0; u < NB; ++u) {
+                    if (c0 + u < a.nch) {
+                        tsq += v[2 * u];
+                        tnr += v[2 * u + 1];
+                    }
+                }
+            }
+            count = a.counts[j];
+        }
+        const int n_empty = wave_sum(j < k && count == 0 ? 1 : 0);
+        const double tot = wave_sum(j < k ? (double)(float)tsq : 0.0);
+        const int chg = *a.prev_changed;
+        int done = 0;
+        if (n_empty > 0)
+            done = 3;
+        else if ((a.flags & kStopStrict) && chg == 0)
+            done = 1;
+        else if (a.tol > 0.0 && tot <= a.tol)
+            done = 2;
+        if (blockIdx.x == 0) {
+            LoopState* st = a.state;
+            if (j < k) {
+                a.shift_sq[j] = (float)tsq;
+                if (count > 0) a.cnorm_out[j] = (float)tnr;
+            }
+            if (lane == 0) {
+                st->n_empty = n_empty;
+                st->shift_tot = tot;
+                st->last_changed = chg;
+                st->n_iter = a.iter;
+                if (done != 0) st->halt_iter = a.iter - 1;
+                st->done = done;
+            }
+        }
+        if (j < CPC) sN[j] = j < k ? (float)tnr : INFINITY;
+        if (lane == 0) *sDone = done;
+    } else {
+        if (j < CPC) sN[j] = j < k ? a.cnorm[j] : INFINITY;
+        if (lane == 0) *sDone = 0;
+    }
+}
+
+// The walker wave of a pair: for every round, waits for the tile, then lane j
+// adds the tile's rows of cluster j (its mask) to S, publishing its progress
+// per chunk; cnt counts the rows.
+template <int CPC, int WS, int NQ, int XS>
+__device__ __forceinline__ void walk_tiles(float4 (&S)[NQ], int& cnt, int rounds, int lane, int* ready, int* prog,
+                                           const unsigned long long* mask, const char* lbase, int toff, int zoff)
+{
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) S[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+    cnt = 0;
+    for (int r = 0; r < rounds; ++r) {
+        wait_flag(ready, r + 1);
+        unsigned long long m = lane < CPC ? mask[lane] : 0ull;
+        cnt += (int)__popcll(m);
+        int ro[WS];
+#pragma unroll
+        for (int s = 0; s < WS; ++s) {
+            const int rr = __ffsll((long long)m) - 1;
+            ro[s] = m != 0ull ? toff + rr * XS * 4 : zoff;
+            m &= m - 1ull;
+        }
+        // rows past the first WS (ascending) first, then the first WS: a
+        // fixed order either way
+        if (__ballot(m != 0ull) != 0ull) {
+            while (m != 0ull) {
+                const int rr = __ffsll((long long)m) - 1;
+                m &= m - 1ull;
+                const char* src = lbase + toff + rr * XS * 4;
+#pragma unroll
+                for (int q = 0; q < NQ; ++q) {
+                    const float4 v = *reinterpret_cast<const float4*>(src + 16 * q);
+                    S[q].x += v.x;
+                    S[q].y += v.y;
+                    S[q].z += v.z;
+                    S[q].w += v.w;
+                }
+            }
+        }
+        float4 wv[WS];
+#pragma unroll
+        for (int s = 0; s < WS; ++s) wv[s] = *reinterpret_cast<const float4*>(lbase + ro[s]);
+        set_flag(prog, r * NQ + 1);
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            float4 wn[WS];
+            if (q + 1 < NQ) {
+#pragma unroll
+                for (int s = 0; s < WS; ++s) wn[s] = *reinterpret_cast<const float4*>(lbase + ro[s] + 16 * (q + 1));
+                set_flag(prog, r * NQ + q + 2);  // reads issued: LDS keeps their order
+            }
+#pragma unroll
+            for (int s = 0; s < WS; ++s) {
+                S[q].x += wv[s].x;
+                S[q].y += wv[s].y;
+                S[q].z += wv[s].z;
+                S[q].w += wv[s].w;
+            }
+            if (q + 1 < NQ) {
+#pragma unroll
+                for (int s = 0; s < WS; ++s) wv[s] = wn[s];
+            }
+        }
+    }
+}
+
+// After the tiles: every walker's sums into red = [4][CPC][ld] (over the tile
+// area, once every pair is done with it), then the block's partial sums and
+// counts, the four walkers combined in wave order.
+template <int CPC, int NQ>
+__device__ __forceinline__ void publish_sums(const float4 (&S)[NQ], int cnt, float* red, int ld, int pair, int lane,
+                                             int (*sCnt)[64])
+{
+    if (lane < CPC) {
+        float* dst = red + (pair * CPC + lane) * ld;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) *reinterpret_cast<float4*>(dst + 4 * q) = S[q];
+        sCnt[pair][lane] = cnt;
+    }
+}
+
+template <int CPC>
+__device__ __forceinline__ void combine_sums(const float* red, int ld, int k, float* psum, int* pcnt, int (*sCnt)[64],
+                                             int tid)
+{
+    const int kl = k * ld;
+    float* out = psum + (long)blockIdx.x * kl;
+    for (int i = tid; i < kl; i += 512) {
+        const int j = i / ld;
+        const int col = i - j * ld;
+        const float* p = red + j * ld + col;
+        out[i] = ((p[0] + p[CPC * ld]) + p[2 * CPC * ld]) + p[3 * CPC * ld];
+    }
+    if (tid < k) pcnt[(long)blockIdx.x * k + tid] = ((sCnt[0][tid] + sCnt[1][tid]) + sCnt[2][tid]) + sCnt[3][tid];
+}
+
 template <int KG, int NQ>
 __global__ __launch_bounds__(512, 1) void k_fused(FusedArgs a)
 {
@@ -294,152 +458,316 @@ __global__ __launch_bounds__(512, 1) void k_fused(FusedArgs a)
             sReady[wt] = 0;
             sProg[wt] = 0;
         }
-        if (wave == 4) {
-            const int j = lane;
-            if (a.decide) {
-                // the previous step's stopping rules, evaluated identically by
-                // every block (same loads, same order as k_finalize_loop for
-                // k <= 64)
-                double tsq = 0.0, tnr = 0.0;
-                int count = 1;
-                if (j < k) {
-                    // all chunk partials in flight at once (the sum order is
-                    // the finalize's: chunk 0, 1, ...)
-                    const double* pj = a.part + (long)j * a.nch * 2;
-                    constexpr int NB = 16;
-                    for (int c0 = 0; c0 < a.nch; c0 += NB) {
-                        double v[2 * NB];
-#pragma unroll
-                        for (int u = 0; u < NB; ++u) {
-                            const int c = min(c0 + u, a.nch - 1);
-                            v[2 * u] = pj[2 * c];
-                            v[2 * u + 1] = pj[2 * c + 1];
-                        }
-#pragma unroll
-                        for (int u = 0; u < NB; ++u) {
-                            if (c0 + u < a.nch) {
-                                tsq += v[2 * u];
-                                tnr += v[2 * u + 1];
-                            }
-                        }
-                    }
-                    count = a.counts[j];
-                }
-                const int n_empty = wave_sum(j < k && count == 0 ? 1 : 0);
-                const double tot = wave_sum(j < k ? (double)(float)tsq : 0.0);
-                const int chg = *a.prev_changed;
-                int done = 0;
-                if (n_empty > 0)
-                    done = 3;
-                else if ((a.flags & kStopStrict) && chg == 0)
-                    done = 1;
-                else if (a.tol > 0.0 && tot <= a.tol)
-                    done = 2;
-                if (blockIdx.x == 0) {
-                    if (j < k) {
-                        a.shift_sq[j] = (float)tsq;
-                        if (count > 0) a.cnorm_out[j] = (float)tnr;
-                    }
-                    if (lane == 0) {
-                        st->n_empty = n_empty;
-                        st->shift_tot = tot;
-                        st->last_changed = chg;
-                        st->n_iter = a.iter;
-                        if (done != 0) st->halt_iter = a.iter - 1;
-                        st->done = done;
-                    }
-                }
-                // padding clusters get ||c||^2 = +inf: their distance never wins
-                if (j < CPC) sN[j] = j < k ? (float)tnr : INFINITY;
-                if (lane == 0) sDone = done;
-            } else {
-                // padding clusters get ||c||^2 = +inf: their distance never wins
-                if (j < CPC) sN[j] = j < k ? a.cnorm[j] : INFINITY;
-                if (lane == 0) sDone = 0;
-            }
-        }
+        if (wave == 4) step_norms<CPC>(a, lane, sN, &sDone);
         __syncthreads();
         if (sDone != 0) return;
         // walker
         float4 S[NQ];
-#pragma unroll
-        for (int q = 0; q < NQ; ++q) S[q] = make_float4(0.f, 0.f, 0.f, 0.f);
-        int cnt = 0;
-        for (int r = 0; r < rounds; ++r) {
-            wait_flag(&sReady[pair], r + 1);
-            unsigned long long m = lane < CPC ? sMask[pair][lane] : 0ull;
-            cnt += (int)__popcll(m);
-            int ro[WS];
-#pragma unroll
-            for (int s = 0; s < WS; ++s) {
-                const int rr = __ffsll((long long)m) - 1;
-                ro[s] = m != 0ull ? toff + rr * XS * 4 : zoff;
-                m &= m - 1ull;
-            }
-            // rows past the first WS (ascending) first, then the first WS:
-            // a fixed order either way
-            if (__ballot(m != 0ull) != 0ull) {
-                while (m != 0ull) {
-                    const int rr = __ffsll((long long)m) - 1;
-                    m &= m - 1ull;
-                    const char* src = lbase + toff + rr * XS * 4;
-#pragma unroll
-                    for (int q = 0; q < NQ; ++q) {
-                        const float4 v = *reinterpret_cast<const float4*>(src + 16 * q);
-                        S[q].x += v.x;
-                        S[q].y += v.y;
-                        S[q].z += v.z;
-                        S[q].w += v.w;
-                    }
-                }
-            }
-            float4 wv[WS];
-#pragma unroll
-            for (int s = 0; s < WS; ++s) wv[s] = *reinterpret_cast<const float4*>(lbase + ro[s]);
-            set_flag(&sProg[pair], r * NQ + 1);
-#pragma unroll
-            for (int q = 0; q < NQ; ++q) {
-                float4 wn[WS];
-                if (q + 1 < NQ) {
-#pragma unroll
-                    for (int s = 0; s < WS; ++s) wn[s] = *reinterpret_cast<const float4*>(lbase + ro[s] + 16 * (q + 1));
-                    set_flag(&sProg[pair], r * NQ + q + 2);  // reads issued: LDS keeps their order
-                }
-#pragma unroll
-                for (int s = 0; s < WS; ++s) {
-                    S[q].x += wv[s].x;
-                    S[q].y += wv[s].y;
-                    S[q].z += wv[s].z;
-                    S[q].w += wv[s].w;
-                }
-                if (q + 1 < NQ) {
-#pragma unroll
-                    for (int s = 0; s < WS; ++s) wv[s] = wn[s];
-                }
-            }
-        }
+        int cnt;
+        walk_tiles<CPC, WS, NQ, XS>(S, cnt, rounds, lane, &sReady[pair], &sProg[pair], sMask[pair], lbase, toff,
+                                    zoff);
         __syncthreads();  // every pair is done with its tile
-        // this walker's sums, combined below in walker order: [4][CPC][ld]
-        // over the tile area
-        float* red = zrow + XS;
-        if (lane < CPC) {
-            float* dst = red + (pair * CPC + lane) * ld;
-#pragma unroll
-            for (int q = 0; q < NQ; ++q) *reinterpret_cast<float4*>(dst + 4 * q) = S[q];
-            sCnt[pair][lane] = cnt;
-        }
+        publish_sums<CPC, NQ>(S, cnt, zrow + XS, ld, pair, lane, sCnt);
         __syncthreads();
     }
-    const int kl = k * ld;
-    const float* red = zrow + XS;
-    float* out = psum + (long)blockIdx.x * kl;
-    for (int i = tid; i < kl; i += 512) {
-        const int j = i / ld;
-        const int col = i - j * ld;
-        const float* p = red + j * ld + col;
-        out[i] = ((p[0] + p[CPC * ld]) + p[2 * CPC * ld]) + p[3 * CPC * ld];
+    combine_sums<CPC>(zrow + XS, ld, k, psum, pcnt, sCnt, tid);
+}
+
+// ---------------------------------------------------------------------------
+// k_fused16: the same step (same pairs, walker, LDS hand-over and sums) with
+// the E-step on v_mfma_f32_16x16x32_f16 (v_mfma_f32_16x16x16_f16 for a last
+// 4-, 8- or 16-feature slice).  x and c are scaled by 2^s (s from the largest
+// |x| and |c|, so scaled values stay below 2^14) and split in two fp16
+// parts, hi = fp16(v 2^s) and lo = fp16(v 2^s - hi), both rounded to
+// nearest: v 2^s = hi + lo + e with |e| <= 2^-22 |v 2^s|.  Then
+//   x.c = 2^-2s (xh.ch + xl.ch + xh.cl) + O(3 * 2^-22 sum_i |x_i c_i|),
+// the dropped xl.cl and the residuals being of the order of fp32's own
+// rounding in a dot product of d terms; the products are exact in the fp32
+// accumulators.
+//
+// MFMA operand layout (16x16x32, checked on the device): lane l holds A[m =
+// l%16][kk = 8(l/16) + j] and B[kk = 8(l/16) + j][n = l%16], j < 8, and
+// receives D[m = 4(l/16) + i][n = l%16], i < 4; 16x16x16 the same with 4
+// values per lane.  Here A = 16 centres (block cb, hi/lo parts from LDS) and
+// B = 16 rows of the tile (group g, from registers), so lane l ends with the
+// distances of row 16g + l%16 to centres 16cb + 4(l/16) + i: the first
+// minimum over the lane's 4 CB centres, then over the four lanes l%16 + 16h
+// (lower index wins ties: the first minimum over all centres), and lane 16g +
+// r keeps row 16g + r's label -- lane = row again for the labels, masks and
+// walker.
+//
+// Each lane loads its 8 (K32 step) or 4 (tail) features of its rows straight
+// from HBM into registers (one 128-byte piece of each of 16 rows per pair of
+// loads), writes them to the pair's LDS tile for the walker and reloads them
+// with tile t + P; the walker is k_fused's.
+
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ void split4(float4 v, float sc, v4h& hi, v4h& lo)
+{
+    const v4f x = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
+    hi = __builtin_convertvector(x, v4h);
+    lo = __builtin_convertvector(x - __builtin_convertvector(hi, v4f), v4h);
+}
+
+__device__ __forceinline__ void split8(float4 u, float4 v, float sc, v8h& hi, v8h& lo)
+{
+    v4h h0, l0, h1, l1;
+    split4(u, sc, h0, l0);
+    split4(v, sc, h1, l1);
+    hi = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+    lo = __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+template <int CB, int NQ>
+__global__ __launch_bounds__(512, 1) void k_fused16(FusedArgs a)
+{
+    const float* __restrict__ X = a.X;
+    const long n = a.n;
+    const int ld = a.ld;
+    const float* __restrict__ C = a.C;
+    const int k = a.k;
+    int* __restrict__ labels = a.labels;
+    LoopState* st = a.state;
+    constexpr int CPC = 16 * CB;                 // clusters padded to 16-centre blocks
+    constexpr int LDX = 4 * NQ;                  // == ld
+    constexpr int NK = LDX / 32;                 // 32-feature K steps
+    constexpr int TAIL = LDX - 32 * NK;          // features of the last, 16-wide step (0: none)
+    constexpr int NS = NK + (TAIL > 0 ? 1 : 0);  // K steps
+    constexpr int QG = 2 * NK + (TAIL > 0 ? 1 : 0);  // float4s per lane per 16-row group
+    constexpr int KP = 32 * NK + (TAIL > 0 ? 16 : 0);
+    constexpr int CSTR = KP + 8;                 // halves per centre row: an odd number of 16-byte units
+    constexpr int WS = walk_steps<4 * CB - 3>();
+    constexpr int XS = fused_stride(KP / 4);     // LDS row: >= KP floats (tail lanes write zeros past ld)
+    static_assert(TAIL == 0 || TAIL == 4 || TAIL == 8 || TAIL == 16, "one 16-wide step covers the tail");
+    // LDS: zero row [XS] | 4 pair tiles [64 x XS] | centre hi parts [CPC x
+    // CSTR] halves | centre lo parts
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    __shared__ unsigned long long sMask[4][64];
+    __shared__ int sCnt[4][64];
+    __shared__ __attribute__((aligned(16))) float sN[CPC];
+    __shared__ int sReady[4];
+    __shared__ int sProg[4];
+    __shared__ int sDone;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pair = wave & 3;
+    const int h = lane >> 4;    // this lane's K slice / centre quad in the MFMA layout
+    const int r16 = lane & 15;  // this lane's row of a 16-row group / centre of a block
+
+    float* zrow = lds;
+    float* tiles = lds + XS;
+    _Float16* sCH = reinterpret_cast<_Float16*>(tiles + 4 * 64 * XS);
+    _Float16* sCL = sCH + CPC * CSTR;
+    const int zoff = 0;
+    const int toff = (XS + pair * 64 * XS) * 4;
+    const char* lbase = reinterpret_cast<const char*>(lds);
+
+    const long ntiles = (n + 63) >> 6;
+    const long P = (long)gridDim.x * 4;
+    const long t0 = (long)blockIdx.x * 4 + pair;
+    const int rounds = t0 < ntiles ? (int)((ntiles - t0 + P - 1) / P) : 0;
+
+    if (wave < 4) {
+        // MFMA wave.  xr[g] holds this lane's features of row 16g + l%16:
+        // K32 step s in xr[g][2s], xr[g][2s + 1] (features 32s + 8h + 0..7),
+        // the tail in xr[g][2NK] (features 32NK + 4h + 0..3; lanes past the
+        // row's last feature load nothing: zeros)
+        float4 xr[4][QG];
+        auto load_step = [&](__amdgpu_buffer_rsrc_t rs, int g, int s) {
+            if (s < NK) {
+                const int o = ((16 * g + r16) * LDX + 32 * s + 8 * h) * 4;
+                xr[g][2 * s] = load_quad(rs, o);
+                xr[g][2 * s + 1] = load_quad(rs, o + 16);
+            } else {
+                const int o = ((16 * g + r16) * LDX + 32 * NK + 4 * h) * 4;
+                xr[g][2 * NK] = load_quad(rs, 4 * h < TAIL ? o : 0x40000000);
+            }
+        };
+        {
+            // in the order of the reloads in the rounds below
+            const __amdgpu_buffer_rsrc_t r0 = tile_rsrc(X, t0, n, ld);
+#pragma unroll
+            for (int gp = 0; gp < 2; ++gp) {
+#pragma unroll
+                for (int s = 0; s < NS; ++s) {
+                    load_step(r0, 2 * gp, s);
+                    load_step(r0, 2 * gp + 1, s);
+                }
+            }
+        }
+        __syncthreads();  // LDS set up by the walkers
+        if (sDone != 0) return;
+        const float sc = a.xscale;
+        const float f2 = a.dscale;  // -2 * 2^-2s
+        float* const trow = tiles + pair * 64 * XS + r16 * XS;  // group 0's row of this lane
+        int changed = 0;
+        for (int r = 0; r < rounds; ++r) {
+            const long t = t0 + (long)r * P;
+            const long nrow = n - t * 64 < 64 ? n - t * 64 : 64;
+            const bool valid = lane < nrow;
+            const __amdgpu_buffer_rsrc_t rl =
+                __builtin_amdgcn_make_buffer_rsrc(labels + t * 64, (short)0, (int)(nrow * 4), 0x00020000);
+            const int old = __builtin_amdgcn_raw_buffer_load_b32(rl, lane * 4, 0, 0);
+            const __amdgpu_buffer_rsrc_t rn = tile_rsrc(X, t + P, n, ld);
+            int mylab = 0;
+            int seen = 0;  // walker progress last read
+#pragma unroll
+            for (int gp = 0; gp < 2; ++gp) {
+                // groups 2gp and 2gp + 1
+                v4f acc[2][CB];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+#pragma unroll
+                    for (int cb = 0; cb < CB; ++cb) acc[e][cb] = v4f{0.f, 0.f, 0.f, 0.f};
+                }
+#pragma unroll
+                for (int s = 0; s < NS; ++s) {
+                    // the columns of step s are rewritten below once the
+                    // walker has read them for tile t - P
+                    if (gp == 0 && r > 0) {
+                        const int need = (r - 1) * NQ + (s < NK ? min(NQ, 8 * s + 8) : NQ);
+                        if (seen < need) seen = wait_flag(&sProg[pair], need);
+                    }
+                    if (s < NK) {
+                        v8h xh[2], xl[2];
+#pragma unroll
+                        for (int e = 0; e < 2; ++e) {
+                            const int g = 2 * gp + e;
+                            float* dst = trow + 16 * g * XS + 32 * s + 8 * h;
+                            *reinterpret_cast<float4*>(dst) = xr[g][2 * s];
+                            *reinterpret_cast<float4*>(dst + 4) = xr[g][2 * s + 1];
+                            split8(xr[g][2 * s], xr[g][2 * s + 1], sc, xh[e], xl[e]);
+                            load_step(rn, g, s);
+                        }
+#pragma unroll
+                        for (int cb = 0; cb < CB; ++cb) {
+                            const int co = (16 * cb + r16) * CSTR + 32 * s + 8 * h;
+                            const v8h ah = *reinterpret_cast<const v8h*>(sCH + co);
+                            const v8h al = *reinterpret_cast<const v8h*>(sCL + co);
+#pragma unroll
+                            for (int e = 0; e < 2; ++e) {
+                                acc[e][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, xh[e], acc[e][cb], 0, 0, 0);
+                                acc[e][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, xh[e], acc[e][cb], 0, 0, 0);
+                                acc[e][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, xl[e], acc[e][cb], 0, 0, 0);
+                            }
+                        }
+                    } else {
+                        v4h xh[2], xl[2];
+#pragma unroll
+                        for (int e = 0; e < 2; ++e) {
+                            const int g = 2 * gp + e;
+                            *reinterpret_cast<float4*>(trow + 16 * g * XS + 32 * NK + 4 * h) = xr[g][2 * NK];
+                            split4(xr[g][2 * NK], sc, xh[e], xl[e]);
+                            load_step(rn, g, s);
+                        }
+#pragma unroll
+                        for (int cb = 0; cb < CB; ++cb) {
+                            const int co = (16 * cb + r16) * CSTR + 32 * NK + 4 * h;
+                            const v4h ah = *reinterpret_cast<const v4h*>(sCH + co);
+                            const v4h al = *reinterpret_cast<const v4h*>(sCL + co);
+#pragma unroll
+                            for (int e = 0; e < 2; ++e) {
+                                acc[e][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, xh[e], acc[e][cb], 0, 0, 0);
+                                acc[e][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(al, xh[e], acc[e][cb], 0, 0, 0);
+                                acc[e][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, xl[e], acc[e][cb], 0, 0, 0);
+                            }
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                // ||c||^2 - 2 x.c, first minimum wins (_k_means_lloyd.pyx:196-212)
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    float bd = INFINITY;
+                    int bi = 4 * h;
+#pragma unroll
+                    for (int cb = 0; cb < CB; ++cb) {
+                        const float4 c4 = *reinterpret_cast<const float4*>(&sN[16 * cb + 4 * h]);
+                        const float cn[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const float dd = fminf(fmaf(f2, acc[e][cb][i], cn[i]), INFINITY);
+                            const bool take = dd < bd;
+                            bd = take ? dd : bd;
+                            bi = take ? 16 * cb + 4 * h + i : bi;
+                        }
+                    }
+#pragma unroll
+                    for (int m = 16; m <= 32; m *= 2) {
+                        const float od = __shfl_xor(bd, m);
+                        const int oi = __shfl_xor(bi, m);
+                        const bool take = (od < bd) | ((od == bd) & (oi < bi));  // no branch
+                        bd = take ? od : bd;
+                        bi = take ? oi : bi;
+                    }
+                    if (h == 2 * gp + e) mylab = bi;
+                }
+            }
+            __builtin_amdgcn_raw_buffer_store_b32(mylab, rl, lane * 4, 0, 0);
+            changed += (int)__popcll(__ballot(valid && old != mylab));
+            // the tile's rows of each cluster
+            if (lane < CPC) sMask[pair][lane] = 0ull;
+            if (valid) atomicOr(&sMask[pair][mylab], 1ull << lane);
+            set_flag(&sReady[pair], r + 1);
+        }
+        if (lane == 0 && changed != 0) atomicAdd(a.changed, changed);
+        __syncthreads();  // every pair's walker is done: the tile area is free
+        __syncthreads();  // the walkers' sums are in LDS
+    } else {
+        // walker waves: the halt test, then the centres' scaled fp16 parts
+        // (rows >= k and columns >= ld zero), the zero row and ||c||^2
+        const int prev = st->done;
+        if (prev != 0) {
+            if (tid == 256) sDone = prev;
+            __syncthreads();
+            return;
+        }
+        const int wt = tid - 256;
+        constexpr int CQ = KP / 4;
+        constexpr int NF = (CPC * CQ + 255) / 256;
+        const float sc = a.xscale;
+        float4 cf[NF];
+#pragma unroll
+        for (int u = 0; u < NF; ++u) {
+            const int idx = wt + 256 * u;
+            const int cl = idx / CQ;
+            const int q = idx - cl * CQ;
+            cf[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (idx < CPC * CQ && cl < k && 4 * q < LDX)
+                cf[u] = *reinterpret_cast<const float4*>(C + (long)cl * ld + 4 * q);
+        }
+#pragma unroll
+        for (int u = 0; u < NF; ++u) {
+            const int idx = wt + 256 * u;
+            const int cl = idx / CQ;
+            const int q = idx - cl * CQ;
+            if (idx < CPC * CQ) {
+                v4h hi, lo;
+                split4(cf[u], sc, hi, lo);
+                *reinterpret_cast<v4h*>(sCH + cl * CSTR + 4 * q) = hi;
+                *reinterpret_cast<v4h*>(sCL + cl * CSTR + 4 * q) = lo;
+            }
+        }
+        for (int i = wt; i < XS; i += 256) zrow[i] = 0.f;
+        if (wt < 4) {
+            sReady[wt] = 0;
+            sProg[wt] = 0;
+        }
+        if (wave == 4) step_norms<CPC>(a, lane, sN, &sDone);
+        __syncthreads();
+        if (sDone != 0) return;
+        float4 S[NQ];
+        int cnt;
+        walk_tiles<CPC, WS, NQ, XS>(S, cnt, rounds, lane, &sReady[pair], &sProg[pair], sMask[pair], lbase, toff,
+                                    zoff);
+        __syncthreads();  // every pair is done with its tile
+        publish_sums<CPC, NQ>(S, cnt, tiles, ld, pair, lane, sCnt);
+        __syncthreads();
     }
-    if (tid < k) pcnt[(long)blockIdx.x * k + tid] = ((sCnt[0][tid] + sCnt[1][tid]) + sCnt[2][tid]) + sCnt[3][tid];
+    combine_sums<CPC>(tiles, ld, k, a.psum, a.pcnt, sCnt, tid);
 }
 
 typedef void (*fused_fn)(FusedArgs);
@@ -476,6 +804,58 @@ static fused_fn fused_kernel(int k, int ld)
     case 100: return pick_fused<25>(kg);
     default: return nullptr;
     }
+}
+
+template <int NQ, int... CBs>
+struct Fused16Table {
+    static fused_fn get(int cb)
+    {
+        fused_fn f = nullptr;
+        ((cb == CBs ? (f = &k_fused16<CBs, NQ>, 0) : 0), ...);
+        return f;
+    }
+};
+
+// The fp16-split kernel for row strides of 32 floats and more (below that
+// the K steps would be mostly padding).
+static fused_fn fused16_kernel(int k, int ld)
+{
+    if (k < 1 || k > 64) return nullptr;
+    const int cb = (k + 15) / 16;
+    switch (ld) {
+    case 32: return Fused16Table<8, 1, 2, 3, 4>::get(cb);
+    case 48: return Fused16Table<12, 1, 2, 3, 4>::get(cb);
+    case 64: return Fused16Table<16, 1, 2, 3, 4>::get(cb);
+    case 80: return Fused16Table<20, 1, 2, 3, 4>::get(cb);
+    case 100: return Fused16Table<25, 1, 2, 3, 4>::get(cb);
+    default: return nullptr;
+    }
+}
+
+static size_t fused16_dyn_lds(int k, int ld)
+{
+    const int cpc = 16 * ((k + 15) / 16);
+    const int nk = ld / 32;
+    const int kp = 32 * nk + (ld > 32 * nk ? 16 : 0);
+    return (size_t)(1 + 4 * 64) * fused_stride(kp / 4) * sizeof(float) + (size_t)2 * cpc * (kp + 8) * sizeof(_Float16);
+}
+
+int fused16_ready(int k, int ld)
+{
+    // SKMETAL_HIP_F16=0 keeps the fp32 MFMA E-step for every shape
+    const char* env = getenv("SKMETAL_HIP_F16");
+    if (env != nullptr && env[0] == '0') return 0;
+    fused_fn f = fused16_kernel(k, ld);
+    if (f == nullptr) return 0;
+    const size_t dyn = fused16_dyn_lds(k, ld);
+    const size_t stat = 4 * 64 * (sizeof(unsigned long long) + sizeof(int)) + 64 * sizeof(float) + 64;
+    if (dyn + stat > 160 * 1024) return 0;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(f), hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) !=
+        hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return 1;
 }
 
 static size_t fused_dyn_lds(int k, int ld)
@@ -518,9 +898,10 @@ int fused_blocks(long n, int ld, int k, int num_cu)
 
 hipError_t launch_fused(const FusedArgs& a, hipStream_t s)
 {
-    fused_fn f = fused_kernel(a.k, a.ld);
+    fused_fn f = a.f16 ? fused16_kernel(a.k, a.ld) : fused_kernel(a.k, a.ld);
     if (f == nullptr || a.blocks < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(f, dim3(a.blocks), dim3(512), fused_dyn_lds(a.k, a.ld), s, a);
+    const size_t dyn = a.f16 ? fused16_dyn_lds(a.k, a.ld) : fused_dyn_lds(a.k, a.ld);
+    hipLaunchKernelGGL(f, dim3(a.blocks), dim3(512), dyn, s, a);
     return hipGetLastError();
 }
 

@@ -64,12 +64,18 @@ struct FusedArgs {
     int decide; int iter; double tol; int flags;
     const double* part; int nch; const int* counts; const int* prev_changed;
     float* cnorm_out; float* shift_sq;
+    // f16 = 1: the E-step on fp16 MFMAs with x and c split in two scaled
+    // parts (xscale = 2^s, dscale = -2 * 2^-2s); see fused16_ready
+    int f16 = 0; float xscale = 1.f; float dscale = -2.f;
 };
 // Row stride (floats) X must have for the fused kernel, or 0 when (d, k) does
 // not qualify; the pad columns are zero.
 int fused_ld(int d, int k);
 // Number of blocks (= partials) of the fused kernel for n rows of stride ld.
 int fused_blocks(long n, int ld, int k, int num_cu);
+// 1 when the fp16-split fused kernel exists for (k, ld) and fits in LDS (sets
+// its LDS attribute); the caller still needs a valid scale for the data.
+int fused16_ready(int k, int ld);
 hipError_t launch_fused(const FusedArgs& a, hipStream_t s);
 
 struct UpdateArgs {
@@ -184,6 +190,8 @@ hipError_t launch_colsum(const float* X, long n, int ld, int d, double* part, in
 int colsum_grid(long n);
 hipError_t launch_colmean(const double* part, int nblk, long n, int d, float* mean, hipStream_t s);
 hipError_t launch_center(float* X, long n, int ld, int d, const float* mean, hipStream_t s);
+// max |x| over count floats (NaN as +inf) into *out as float bits
+hipError_t launch_absmax(const float* X, long count, unsigned* out, hipStream_t s);
 hipError_t launch_cnorm(const float* C, int k, int ld, float* cnorm, hipStream_t s);
 
 }  // namespace skm

@@ -1090,6 +1090,33 @@ hipError_t launch_center(float* X, long n, int ld, int d, const float* mean, hip
     return hipGetLastError();
 }
 
+// Largest |x| over `count` floats (NaN counts as +inf) into *out as float
+// bits: non-negative floats order like their bit patterns, so an unsigned
+// atomic max per wave combines them.
+__global__ __launch_bounds__(256) void k_absmax(const float* __restrict__ X, long count, unsigned* out)
+{
+    float m = 0.f;
+    const long stride = (long)gridDim.x * 256;
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < count; i += stride) {
+        const float v = fabsf(X[i]);
+        m = v != v ? INFINITY : fmaxf(m, v);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((threadIdx.x & 63) == 0) atomicMax(out, __float_as_uint(m));
+}
+
+hipError_t launch_absmax(const float* X, long count, unsigned* out, hipStream_t s)
+{
+    const hipError_t e = hipMemsetAsync(out, 0, sizeof(unsigned), s);
+    if (e != hipSuccess) return e;
+    long blocks = (count + 255) / 256;
+    if (blocks > 1024) blocks = 1024;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(k_absmax, dim3((unsigned)blocks), dim3(256), 0, s, X, count, out);
+    return hipGetLastError();
+}
+
 __global__ void k_cnorm(const float* __restrict__ C, int k, int ld, float* __restrict__ cnorm)
 {
     const int j = blockIdx.x * blockDim.x + threadIdx.x;

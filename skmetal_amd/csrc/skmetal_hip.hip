@@ -276,6 +276,14 @@ struct Lloyd {
     int* s_slab = nullptr;
     float* s_rec = nullptr;
     int fblocks = 0;        // > 0: fused E-step + sums kernel with this many partials
+    // fp16-split E-step of the fused kernel: available for this shape
+    // (f16cap) and used while the data's scale allows it (f16_on); xmax/cmax
+    // are the largest |x| of X and of the centres last set, in device
+    // coordinates
+    int f16cap = 0;
+    bool f16_on = false;
+    float xmax = 0.f, cmax = 0.f, xscale = 1.f, dscale = -2.f;
+    unsigned* absmax = nullptr;
     int cur = 0;            // index of the current centres in cen[]
     bool centred = false;
     std::vector<float> h_mean;
@@ -299,6 +307,7 @@ struct Lloyd {
         s = C->stream;
         ug = update_geometry(n, d, k, C->num_cu);
         fblocks = lf > 0 ? fused_blocks(n, ld, k, C->num_cu) : 0;
+        f16cap = fblocks > 0 ? fused16_ready(k, ld) : 0;
         if (fblocks == 0) sg = sort_geometry(n, d, ld, k);
         const int Rmax = sg.on ? 1 : std::max(ug.R, fblocks);
         const int chunks = std::max({finalize_col_chunks(d, ug.R), fblocks > 0 ? finalize_col_chunks(d, fblocks) : 0,
@@ -319,6 +328,7 @@ struct Lloyd {
         TRY(grab((void**)&rowpart, size_t(rowdist_grid(n)) * sizeof(double)));
         TRY(grab((void**)&colpart, size_t(colsum_grid(n)) * d * sizeof(double)));
         TRY(grab((void**)&st, sizeof(LoopState)));
+        TRY(grab((void**)&absmax, sizeof(unsigned)));
         if (sg.on) {
             TRY(grab((void**)&s_hist, size_t(sg.nw) * k * sizeof(int)));
             TRY(grab((void**)&s_seg, size_t(sg.nseg) * k * sizeof(int)));
@@ -369,12 +379,45 @@ struct Lloyd {
             std::fill(h_mean.begin(), h_mean.end(), 0.f);
             HIP_TRY(hipMemsetAsync(mean, 0, size_t(ld) * sizeof(float), s), "hipMemsetAsync");
         }
+        if (f16cap) {
+            unsigned bits = 0;
+            HIP_TRY(launch_absmax(X, n * (long)ld, absmax, s), "absmax launch");
+            TRY(download_bytes(*C, absmax, sizeof(unsigned), &bits, s));
+            std::memcpy(&xmax, &bits, sizeof(float));
+            update_scale();
+        }
         return 0;
+    }
+
+    // x and c are scaled by 2^s for the fp16 split: the largest |x|, |c|
+    // lands in [2^13, 2^14], far from fp16's overflow (65504) and with the
+    // smallest normal fp16 2^-14 at 2^-27 of it.  Non-finite data, or a
+    // scale whose 2^(1-2s) would leave fp32's normal range, keep the fp32
+    // E-step.
+    void update_scale()
+    {
+        const float m = std::max(xmax, cmax);
+        int e = 0;
+        if (m > 0.f && std::isfinite(m)) std::frexp(m, &e);  // m = f 2^e, f in [0.5, 1)
+        const int sh = m > 0.f ? 14 - e : 0;
+        f16_on = f16cap != 0 && std::isfinite(m) && sh >= -60 && sh <= 60;
+        xscale = std::ldexp(1.f, sh);
+        dscale = -std::ldexp(1.f, 1 - 2 * sh);
     }
 
     // Centres given in caller coordinates -> device (centred like X).
     int set_centers(const float* host)
     {
+        if (f16cap) {
+            double m = 0.0;
+            for (int j = 0; j < k; ++j)
+                for (int c = 0; c < d; ++c) {
+                    const double v = std::fabs(double(host[size_t(j) * d + c]) - (centred ? double(h_mean[c]) : 0.0));
+                    m = v != v ? INFINITY : std::max(m, v);
+                }
+            cmax = float(m * (1.0 + 1e-6));
+            update_scale();
+        }
         TRY(upload_rows(*C, host, k, d, ld, cen[cur], s));
         if (centred) HIP_TRY(launch_center(cen[cur], k, ld, d, mean, s), "center launch");
         HIP_TRY(launch_cnorm(cen[cur], k, ld, cnorm, s), "cnorm launch");
@@ -433,6 +476,9 @@ struct Lloyd {
         FusedArgs a{X, n, ld, cen[cur], cnorm, k, labels, psum, pcnt, st, fblocks, &st->chg[iter & 1],
                     decide ? 1 : 0, iter, tol, flags, part, finalize_col_chunks(d, fblocks), counts,
                     &st->chg[(iter + 1) & 1], cnorm, shift_sq};
+        a.f16 = f16_on ? 1 : 0;
+        a.xscale = xscale;
+        a.dscale = dscale;
         HIP_TRY(launch_fused(a, s), "fused launch");
         return 0;
     }
@@ -983,7 +1029,7 @@ int skmetal_hip_lloyd_run(skmetal_hip_lloyd* h, size_t max_iter, double tol, int
 int skmetal_hip_lloyd_info(skmetal_hip_lloyd* h, int* fused, int* partials)
 {
     if (!h) return fail(SKMETAL_EINVAL, "null pointer argument");
-    if (fused) *fused = h->L.fblocks > 0;
+    if (fused) *fused = h->L.fblocks > 0 ? (h->L.f16_on ? 2 : 1) : 0;
     if (partials) *partials = h->L.fblocks > 0 ? h->L.fblocks : h->L.sg.on ? (int)h->L.sg.nchunks : h->L.ug.R;
     return 0;
 }

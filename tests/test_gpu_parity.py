@@ -134,6 +134,65 @@ def _lockstep_gpu(bridge, X, C0, steps, what):
     return n_mism
 
 
+# (n, d, k) covering every row stride of the fp16x2-split E-step (with and
+# without a 16-wide K tail, pad columns) and 1..4 blocks of 16 centres
+F16_SHAPES = [(3000, 17, 5), (4100, 33, 16), (5000, 64, 17), (6000, 80, 48), (20000, 97, 50), (7000, 100, 64)]
+
+
+def _blob_problem(n, d, k, seed, scale=1.0):
+    rng = np.random.default_rng(seed)
+    cen = rng.uniform(-6, 6, (k, d))
+    X = ((cen[rng.integers(0, k, n)] + rng.standard_normal((n, d))) * scale).astype(np.float32)
+    C0 = X[np.sort(rng.choice(n, k, replace=False))].copy()
+    return X, C0
+
+
+def _f16_engaged(bridge, X, C0):
+    n, d = X.shape
+    with bridge.LloydHandle(n, d, C0.shape[0]) as h:
+        h.load(X, center=True)
+        h.set_centers(C0)
+        return h.info()
+
+
+@pytest.mark.parametrize("n,d,k", F16_SHAPES)
+def test_f16_estep_lockstep(bridge, n, d, k):
+    """Fused steps with the E-step on fp16 MFMA (x, c split in two scaled
+    fp16 parts) against the oracle, step by step."""
+    _say(f"f16 lockstep n={n} d={d} k={k}")
+    X, C0 = _blob_problem(n, d, k, seed=n + d + k)
+    info = _f16_engaged(bridge, X, C0)
+    assert info["fused"] and info["f16"], info
+    _lockstep_gpu(bridge, X, C0, 3, what=f"f16 {n}x{d} k={k}")
+
+
+@pytest.mark.parametrize("scale", [1e-15, 1e-3, 1e4, 1e15])
+def test_f16_estep_scaled_data(bridge, scale):
+    """The 2^s scaling keeps the fp16 parts in range for any data magnitude."""
+    _say(f"f16 scale {scale}")
+    X, C0 = _blob_problem(6000, 40, 30, seed=5, scale=scale)
+    assert _f16_engaged(bridge, X, C0)["f16"]
+    _lockstep_gpu(bridge, X, C0, 2, what=f"f16 scale {scale}")
+
+
+def test_f16_switched_off_by_env(bridge, monkeypatch):
+    """SKMETAL_HIP_F16=0 keeps the fp32 MFMA E-step; both agree with the oracle."""
+    monkeypatch.setenv("SKMETAL_HIP_F16", "0")
+    X, C0 = _blob_problem(8000, 100, 50, seed=9)
+    info = _f16_engaged(bridge, X, C0)
+    assert info["fused"] and not info["f16"], info
+    _lockstep_gpu(bridge, X, C0, 2, what="fp32 E-step")
+
+
+def test_f16_off_for_non_finite_data(bridge):
+    X, C0 = _blob_problem(3000, 40, 8, seed=3)
+    X[17, 5] = np.inf
+    with bridge.LloydHandle(3000, 40, 8) as h:
+        h.load(X, center=False)
+        h.set_centers(C0)
+        assert not h.info()["f16"]
+
+
 def _golden_names():
     return [c["name"] for c in json.loads((GOLDEN / "manifest.json").read_text())["cases"]]
 
