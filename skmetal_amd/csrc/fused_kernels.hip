@@ -504,23 +504,25 @@ __global__ __launch_bounds__(512, 1) void k_fused(FusedArgs a)
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
+template <bool SC>
 __device__ __forceinline__ void split4(float4 v, float sc, v4h& hi, v4h& lo)
 {
-    const v4f x = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
+    const v4f x = SC ? v4f{v.x * sc, v.y * sc, v.z * sc, v.w * sc} : v4f{v.x, v.y, v.z, v.w};
     hi = __builtin_convertvector(x, v4h);
     lo = __builtin_convertvector(x - __builtin_convertvector(hi, v4f), v4h);
 }
 
+template <bool SC>
 __device__ __forceinline__ void split8(float4 u, float4 v, float sc, v8h& hi, v8h& lo)
 {
     v4h h0, l0, h1, l1;
-    split4(u, sc, h0, l0);
-    split4(v, sc, h1, l1);
+    split4<SC>(u, sc, h0, l0);
+    split4<SC>(v, sc, h1, l1);
     hi = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
     lo = __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-template <int CB, int NQ>
+template <int CB, int NQ, bool SC>
 __global__ __launch_bounds__(512, 1) void k_fused16(FusedArgs a)
 {
     const float* __restrict__ X = a.X;
@@ -639,7 +641,7 @@ __global__ __launch_bounds__(512, 1) void k_fused16(FusedArgs a)
                             float* dst = trow + 16 * g * XS + 32 * s + 8 * h;
                             *reinterpret_cast<float4*>(dst) = xr[g][2 * s];
                             *reinterpret_cast<float4*>(dst + 4) = xr[g][2 * s + 1];
-                            split8(xr[g][2 * s], xr[g][2 * s + 1], sc, xh[e], xl[e]);
+                            split8<SC>(xr[g][2 * s], xr[g][2 * s + 1], sc, xh[e], xl[e]);
                             load_step(rn, g, s);
                         }
 #pragma unroll
@@ -660,7 +662,7 @@ __global__ __launch_bounds__(512, 1) void k_fused16(FusedArgs a)
                         for (int e = 0; e < 2; ++e) {
                             const int g = 2 * gp + e;
                             *reinterpret_cast<float4*>(trow + 16 * g * XS + 32 * NK + 4 * h) = xr[g][2 * NK];
-                            split4(xr[g][2 * NK], sc, xh[e], xl[e]);
+                            split4<SC>(xr[g][2 * NK], sc, xh[e], xl[e]);
                             load_step(rn, g, s);
                         }
 #pragma unroll
@@ -689,7 +691,8 @@ __global__ __launch_bounds__(512, 1) void k_fused16(FusedArgs a)
                         const float cn[4] = {c4.x, c4.y, c4.z, c4.w};
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            const float dd = fminf(fmaf(f2, acc[e][cb][i], cn[i]), INFINITY);
+                            // a NaN distance compares false: it never wins
+                            const float dd = fmaf(f2, acc[e][cb][i], cn[i]);
                             const bool take = dd < bd;
                             bd = take ? dd : bd;
                             bi = take ? 16 * cb + 4 * h + i : bi;
@@ -746,7 +749,7 @@ __global__ __launch_bounds__(512, 1) void k_fused16(FusedArgs a)
             const int q = idx - cl * CQ;
             if (idx < CPC * CQ) {
                 v4h hi, lo;
-                split4(cf[u], sc, hi, lo);
+                split4<SC>(cf[u], sc, hi, lo);
                 *reinterpret_cast<v4h*>(sCH + cl * CSTR + 4 * q) = hi;
                 *reinterpret_cast<v4h*>(sCL + cl * CSTR + 4 * q) = lo;
             }
@@ -808,26 +811,26 @@ static fused_fn fused_kernel(int k, int ld)
 
 template <int NQ, int... CBs>
 struct Fused16Table {
-    static fused_fn get(int cb)
+    static fused_fn get(int cb, bool scaled)
     {
         fused_fn f = nullptr;
-        ((cb == CBs ? (f = &k_fused16<CBs, NQ>, 0) : 0), ...);
+        ((cb == CBs ? (f = scaled ? &k_fused16<CBs, NQ, true> : &k_fused16<CBs, NQ, false>, 0) : 0), ...);
         return f;
     }
 };
 
 // The fp16-split kernel for row strides of 32 floats and more (below that
 // the K steps would be mostly padding).
-static fused_fn fused16_kernel(int k, int ld)
+static fused_fn fused16_kernel(int k, int ld, bool scaled)
 {
     if (k < 1 || k > 64) return nullptr;
     const int cb = (k + 15) / 16;
     switch (ld) {
-    case 32: return Fused16Table<8, 1, 2, 3, 4>::get(cb);
-    case 48: return Fused16Table<12, 1, 2, 3, 4>::get(cb);
-    case 64: return Fused16Table<16, 1, 2, 3, 4>::get(cb);
-    case 80: return Fused16Table<20, 1, 2, 3, 4>::get(cb);
-    case 100: return Fused16Table<25, 1, 2, 3, 4>::get(cb);
+    case 32: return Fused16Table<8, 1, 2, 3, 4>::get(cb, scaled);
+    case 48: return Fused16Table<12, 1, 2, 3, 4>::get(cb, scaled);
+    case 64: return Fused16Table<16, 1, 2, 3, 4>::get(cb, scaled);
+    case 80: return Fused16Table<20, 1, 2, 3, 4>::get(cb, scaled);
+    case 100: return Fused16Table<25, 1, 2, 3, 4>::get(cb, scaled);
     default: return nullptr;
     }
 }
@@ -845,15 +848,17 @@ int fused16_ready(int k, int ld)
     // SKMETAL_HIP_F16=0 keeps the fp32 MFMA E-step for every shape
     const char* env = getenv("SKMETAL_HIP_F16");
     if (env != nullptr && env[0] == '0') return 0;
-    fused_fn f = fused16_kernel(k, ld);
-    if (f == nullptr) return 0;
     const size_t dyn = fused16_dyn_lds(k, ld);
     const size_t stat = 4 * 64 * (sizeof(unsigned long long) + sizeof(int)) + 64 * sizeof(float) + 64;
     if (dyn + stat > 160 * 1024) return 0;
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(f), hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) !=
-        hipSuccess) {
-        (void)hipGetLastError();
-        return 0;
+    for (const bool scaled : {false, true}) {
+        fused_fn f = fused16_kernel(k, ld, scaled);
+        if (f == nullptr) return 0;
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(f), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)dyn) != hipSuccess) {
+            (void)hipGetLastError();
+            return 0;
+        }
     }
     return 1;
 }
@@ -898,7 +903,7 @@ int fused_blocks(long n, int ld, int k, int num_cu)
 
 hipError_t launch_fused(const FusedArgs& a, hipStream_t s)
 {
-    fused_fn f = a.f16 ? fused16_kernel(a.k, a.ld) : fused_kernel(a.k, a.ld);
+    fused_fn f = a.f16 ? fused16_kernel(a.k, a.ld, a.xscale != 1.f) : fused_kernel(a.k, a.ld);
     if (f == nullptr || a.blocks < 1) return hipErrorInvalidValue;
     const size_t dyn = a.f16 ? fused16_dyn_lds(a.k, a.ld) : fused_dyn_lds(a.k, a.ld);
     hipLaunchKernelGGL(f, dim3(a.blocks), dim3(512), dyn, s, a);

@@ -389,17 +389,20 @@ struct Lloyd {
         return 0;
     }
 
-    // x and c are scaled by 2^s for the fp16 split: the largest |x|, |c|
-    // lands in [2^13, 2^14], far from fp16's overflow (65504) and with the
-    // smallest normal fp16 2^-14 at 2^-27 of it.  Non-finite data, or a
-    // scale whose 2^(1-2s) would leave fp32's normal range, keep the fp32
-    // E-step.
+    // x and c are scaled by 2^s for the fp16 split so that the largest |x|,
+    // |c| (m) stays below 2^14, far from fp16's overflow (65504), and above
+    // 2^-3: a split part that falls below fp16's smallest normal (2^-14) then
+    // errs by at most 2^-25 absolute, under 2^-22 m, the same order as the
+    // relative error of the split.  s = 0 whenever m is already in
+    // [2^-3, 2^14) (no scaling multiply in the kernel), else m lands in
+    // [2^13, 2^14).  Non-finite data, or a scale whose 2^(1-2s) would leave
+    // fp32's normal range, keep the fp32 E-step.
     void update_scale()
     {
         const float m = std::max(xmax, cmax);
         int e = 0;
         if (m > 0.f && std::isfinite(m)) std::frexp(m, &e);  // m = f 2^e, f in [0.5, 1)
-        const int sh = m > 0.f ? 14 - e : 0;
+        const int sh = m > 0.f && (e > 14 || e < -2) ? 14 - e : 0;
         f16_on = f16cap != 0 && std::isfinite(m) && sh >= -60 && sh <= 60;
         xscale = std::ldexp(1.f, sh);
         dscale = -std::ldexp(1.f, 1 - 2 * sh);
