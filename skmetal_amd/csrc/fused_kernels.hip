@@ -522,6 +522,84 @@ __device__ __forceinline__ void split8(float4 u, float4 v, float sc, v8h& hi, v8
     lo = __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// The M-step wave of a k_fused16 pair: the per-cluster sums of each ready
+// tile as onehot^T x on v_mfma_f32_16x16x32_f16, x in the same two fp16
+// parts as the E-step (x 2^s = hi + lo up to 2^-22 |x 2^s|; the one-hot
+// operand is exact, so every product is exact in the fp32 accumulators).
+// A = onehot (16 clusters of block cb x 32 rows of K block kb: lane l holds
+// rows 32kb + 8(l/16) + j for cluster 16cb + l%16), B = x (the same rows x 16
+// features of block fb, read transposed from the LDS tile: lane l holds
+// feature 16fb + l%16), D lane l: clusters 16cb + 4(l/16) + i, feature 16fb +
+// l%16.  Progress is published per 16-feature block (all rows read).
+template <int CB, int NQ, int XS, int NFB, bool SC>
+__device__ __forceinline__ void msum_tiles(v4f (&S)[CB][NFB], int rounds, int lane, int* ready, int* prog,
+                                           const int* lab, const float* tile, float sc)
+{
+    const int h = lane >> 4, r16 = lane & 15;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+        for (int fb = 0; fb < NFB; ++fb) S[cb][fb] = v4f{0.f, 0.f, 0.f, 0.f};
+    }
+    const _Float16 one = (_Float16)1.0f, zero = (_Float16)0.0f;
+    for (int r = 0; r < rounds; ++r) {
+        wait_flag(ready, r + 1);
+        // one-hot operands of both K blocks (labels of past-the-end rows are -1)
+        v8h A[2][CB];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const int4 l0 = *reinterpret_cast<const int4*>(lab + 32 * kb + 8 * h);
+            const int4 l1 = *reinterpret_cast<const int4*>(lab + 32 * kb + 8 * h + 4);
+            const int lj[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                const int c = 16 * cb + r16;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) A[kb][cb][j] = lj[j] == c ? one : zero;
+            }
+        }
+        const float* col = tile + 8 * h * XS + r16;
+#pragma unroll
+        for (int fb = 0; fb < NFB; ++fb) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const float* src = col + 32 * kb * XS + 16 * fb;
+                const float4 u = make_float4(src[0], src[XS], src[2 * XS], src[3 * XS]);
+                const float4 v = make_float4(src[4 * XS], src[5 * XS], src[6 * XS], src[7 * XS]);
+                v8h bh, bl;
+                split8<SC>(u, v, sc, bh, bl);
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    S[cb][fb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[kb][cb], bh, S[cb][fb], 0, 0, 0);
+                    S[cb][fb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[kb][cb], bl, S[cb][fb], 0, 0, 0);
+                }
+            }
+            // columns of feature block fb read for every row (LDS keeps the
+            // order of the reads above and this flag)
+            set_flag(prog, r * NQ + (4 * fb + 4 < NQ ? 4 * fb + 4 : NQ));
+        }
+    }
+}
+
+// M-step sums into red = [4][CPC][ld] (unscaled), once every pair is done.
+template <int CB, int NFB>
+__device__ __forceinline__ void publish_msums(const v4f (&S)[CB][NFB], float* red, int ld, int pair, int lane,
+                                              float unscale)
+{
+    const int h = lane >> 4, r16 = lane & 15;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+        for (int fb = 0; fb < NFB; ++fb) {
+            const int f = 16 * fb + r16;
+            if (f < ld) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) red[(pair * 16 * CB + 16 * cb + 4 * h + i) * ld + f] = S[cb][fb][i] * unscale;
+            }
+        }
+    }
+}
+
 template <int CB, int NQ, bool SC>
 __global__ __launch_bounds__(512, 1) void k_fused16(FusedArgs a)
 {
@@ -540,13 +618,12 @@ __global__ __launch_bounds__(512, 1) void k_fused16(FusedArgs a)
     constexpr int QG = 2 * NK + (TAIL > 0 ? 1 : 0);  // float4s per lane per 16-row group
     constexpr int KP = 32 * NK + (TAIL > 0 ? 16 : 0);
     constexpr int CSTR = KP + 8;                 // halves per centre row: an odd number of 16-byte units
-    constexpr int WS = walk_steps<4 * CB - 3>();
     constexpr int XS = fused_stride(KP / 4);     // LDS row: >= KP floats (tail lanes write zeros past ld)
     static_assert(TAIL == 0 || TAIL == 4 || TAIL == 8 || TAIL == 16, "one 16-wide step covers the tail");
-    // LDS: zero row [XS] | 4 pair tiles [64 x XS] | centre hi parts [CPC x
-    // CSTR] halves | centre lo parts
+    // LDS: 4 pair tiles [64 x XS] | centre hi parts [CPC x CSTR] halves |
+    // centre lo parts
     extern __shared__ __attribute__((aligned(16))) float lds[];
-    __shared__ unsigned long long sMask[4][64];
+    __shared__ __attribute__((aligned(16))) int sLab[4][64];  // the tile's labels (-1: no row)
     __shared__ int sCnt[4][64];
     __shared__ __attribute__((aligned(16))) float sN[CPC];
     __shared__ int sReady[4];
@@ -559,13 +636,9 @@ __global__ __launch_bounds__(512, 1) void k_fused16(FusedArgs a)
     const int h = lane >> 4;    // this lane's K slice / centre quad in the MFMA layout
     const int r16 = lane & 15;  // this lane's row of a 16-row group / centre of a block
 
-    float* zrow = lds;
-    float* tiles = lds + XS;
+    float* tiles = lds;
     _Float16* sCH = reinterpret_cast<_Float16*>(tiles + 4 * 64 * XS);
     _Float16* sCL = sCH + CPC * CSTR;
-    const int zoff = 0;
-    const int toff = (XS + pair * 64 * XS) * 4;
-    const char* lbase = reinterpret_cast<const char*>(lds);
 
     const long ntiles = (n + 63) >> 6;
     const long P = (long)gridDim.x * 4;
@@ -711,9 +784,10 @@ __global__ __launch_bounds__(512, 1) void k_fused16(FusedArgs a)
             }
             __builtin_amdgcn_raw_buffer_store_b32(mylab, rl, lane * 4, 0, 0);
             changed += (int)__popcll(__ballot(valid && old != mylab));
-            // the tile's rows of each cluster
-            if (lane < CPC) sMask[pair][lane] = 0ull;
-            if (valid) atomicOr(&sMask[pair][mylab], 1ull << lane);
+            // the tile's labels for the M-step wave; the counts (integer
+            // adds: any order gives the same total)
+            sLab[pair][lane] = valid ? mylab : -1;
+            if (valid) atomicAdd(&sCnt[pair][mylab], 1);
             set_flag(&sReady[pair], r + 1);
         }
         if (lane == 0 && changed != 0) atomicAdd(a.changed, changed);
@@ -754,20 +828,21 @@ __global__ __launch_bounds__(512, 1) void k_fused16(FusedArgs a)
                 *reinterpret_cast<v4h*>(sCL + cl * CSTR + 4 * q) = lo;
             }
         }
-        for (int i = wt; i < XS; i += 256) zrow[i] = 0.f;
         if (wt < 4) {
             sReady[wt] = 0;
             sProg[wt] = 0;
         }
+        sCnt[wt >> 6][wt & 63] = 0;
         if (wave == 4) step_norms<CPC>(a, lane, sN, &sDone);
         __syncthreads();
         if (sDone != 0) return;
-        float4 S[NQ];
-        int cnt;
-        walk_tiles<CPC, WS, NQ, XS>(S, cnt, rounds, lane, &sReady[pair], &sProg[pair], sMask[pair], lbase, toff,
-                                    zoff);
+        // M-step wave
+        constexpr int NFB = KP / 16;
+        v4f S[CB][NFB];
+        msum_tiles<CB, NQ, XS, NFB, SC>(S, rounds, lane, &sReady[pair], &sProg[pair], sLab[pair],
+                                        tiles + pair * 64 * XS, sc);
         __syncthreads();  // every pair is done with its tile
-        publish_sums<CPC, NQ>(S, cnt, tiles, ld, pair, lane, sCnt);
+        publish_msums<CB, NFB>(S, tiles, ld, pair, lane, SC ? 1.f / sc : 1.f);
         __syncthreads();
     }
     combine_sums<CPC>(tiles, ld, k, a.psum, a.pcnt, sCnt, tid);
@@ -840,7 +915,7 @@ static size_t fused16_dyn_lds(int k, int ld)
     const int cpc = 16 * ((k + 15) / 16);
     const int nk = ld / 32;
     const int kp = 32 * nk + (ld > 32 * nk ? 16 : 0);
-    return (size_t)(1 + 4 * 64) * fused_stride(kp / 4) * sizeof(float) + (size_t)2 * cpc * (kp + 8) * sizeof(_Float16);
+    return (size_t)4 * 64 * fused_stride(kp / 4) * sizeof(float) + (size_t)2 * cpc * (kp + 8) * sizeof(_Float16);
 }
 
 int fused16_ready(int k, int ld)
