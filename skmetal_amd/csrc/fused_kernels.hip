@@ -558,25 +558,39 @@ __device__ __forceinline__ void msum_tiles(v4f (&S)[CB][NFB], int rounds, int la
                 for (int j = 0; j < 8; ++j) A[kb][cb][j] = lj[j] == c ? one : zero;
             }
         }
+        // the 16 values (2 K blocks x 8 rows) of feature block fb; the next
+        // block's reads are in flight while this block's MFMAs run
         const float* col = tile + 8 * h * XS + r16;
-#pragma unroll
-        for (int fb = 0; fb < NFB; ++fb) {
+        auto fetch = [&](float (&v)[16], int fb) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
-                const float* src = col + 32 * kb * XS + 16 * fb;
-                const float4 u = make_float4(src[0], src[XS], src[2 * XS], src[3 * XS]);
-                const float4 v = make_float4(src[4 * XS], src[5 * XS], src[6 * XS], src[7 * XS]);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[8 * kb + j] = col[(32 * kb + j) * XS + 16 * fb];
+            }
+        };
+        float cur[16], nxt[16];
+        fetch(cur, 0);
+#pragma unroll
+        for (int fb = 0; fb < NFB; ++fb) {
+            if (fb + 1 < NFB) fetch(nxt, fb + 1);
+            // columns of feature block fb have been read for every row (LDS
+            // performs this wave's reads above before this flag)
+            set_flag(prog, r * NQ + (4 * fb + 4 < NQ ? 4 * fb + 4 : NQ));
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
                 v8h bh, bl;
-                split8<SC>(u, v, sc, bh, bl);
+                split8<SC>(make_float4(cur[8 * kb], cur[8 * kb + 1], cur[8 * kb + 2], cur[8 * kb + 3]),
+                           make_float4(cur[8 * kb + 4], cur[8 * kb + 5], cur[8 * kb + 6], cur[8 * kb + 7]), sc, bh, bl);
 #pragma unroll
                 for (int cb = 0; cb < CB; ++cb) {
                     S[cb][fb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[kb][cb], bh, S[cb][fb], 0, 0, 0);
                     S[cb][fb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[kb][cb], bl, S[cb][fb], 0, 0, 0);
                 }
             }
-            // columns of feature block fb read for every row (LDS keeps the
-            // order of the reads above and this flag)
-            set_flag(prog, r * NQ + (4 * fb + 4 < NQ ? 4 * fb + 4 : NQ));
+            if (fb + 1 < NFB) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) cur[i] = nxt[i];
+            }
         }
     }
 }
