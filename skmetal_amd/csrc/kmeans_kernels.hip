@@ -654,7 +654,6 @@ constexpr int kFinUnroll = 8;  // partials in flight per thread
 
 __global__ __launch_bounds__(256) void k_finalize_cols(FinalizeArgs a)
 {
-    if (a.state->done != 0) return;
     const int j = blockIdx.x;
     const int cc = blockIdx.y;
     const int nch = gridDim.y;
@@ -668,8 +667,15 @@ __global__ __launch_bounds__(256) void k_finalize_cols(FinalizeArgs a)
     __shared__ double shd[2][4];
     __shared__ int shi[4];
 
-    // partials of cluster j: R of them at r*k + j, or its records
+    // block partials: the halt flag, the old centre, the counts and the
+    // partials are all requested before any of them is used (one memory
+    // round trip); records exist only for a step whose update ran, so that
+    // mode tests the flag first
     const bool recs = a.rec_off != nullptr;
+    const int done = a.state->done;
+    if (recs && done != 0) return;
+    const float c_old = tid < CW && col < a.d ? a.C_old[(long)j * a.ld + col] : 0.f;
+    // partials of cluster j: R of them at r*k + j, or its records
     const int R = recs ? a.rec_cnt[j] : a.R;
     const float* src = a.psum + (recs ? (long)a.rec_off[j] * a.ld : (long)j * a.ld) + col;
     const long step = recs ? (long)a.ld : (long)a.k * a.ld;
@@ -693,6 +699,7 @@ __global__ __launch_bounds__(256) void k_finalize_cols(FinalizeArgs a)
                 if (r0 + u * RS < R) s += (double)v[u];
         }
     }
+    if (done != 0) return;  // the loop has halted: nothing is written
     // lanes of one column inside a wave: xor offsets CW, 2CW, ... < 64
     for (int off = CW; off < 64; off <<= 1) s += __shfl_xor(s, off, 64);
     red[tid] = s;
@@ -707,7 +714,7 @@ __global__ __launch_bounds__(256) void k_finalize_cols(FinalizeArgs a)
         if (count > 0) {
             const float cn = (float)(tot / (double)count);
             a.C_new[(long)j * a.ld + col] = cn;
-            const double df = (double)cn - (double)a.C_old[(long)j * a.ld + col];
+            const double df = (double)cn - (double)c_old;
             sq = df * df;
             nrm = (double)cn * (double)cn;
         }
