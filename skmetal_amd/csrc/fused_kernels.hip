@@ -271,13 +271,13 @@ __device__ __forceinline__ void publish_sums(const float4 (&S)[NQ], int cnt, flo
     }
 }
 
-template <int CPC>
+template <int CPC, int NT = 512>
 __device__ __forceinline__ void combine_sums(const float* red, int ld, int k, float* psum, int* pcnt, int (*sCnt)[64],
                                              int tid)
 {
     const int kl = k * ld;
     float* out = psum + (long)blockIdx.x * kl;
-    for (int i = tid; i < kl; i += 512) {
+    for (int i = tid; i < kl; i += NT) {
         const int j = i / ld;
         const int col = i - j * ld;
         const float* p = red + j * ld + col;
@@ -595,6 +595,68 @@ __device__ __forceinline__ void msum_tiles(v4f (&S)[CB][NFB], int rounds, int la
     }
 }
 
+// The sums wave of SIMD m in k_fused16 serves E-step waves m and m + 4 (the
+// same SIMD), taking their 32-row tiles in turn: round r of wave m, then round
+// r of wave m + 4.  Per tile: A = one-hot (16 clusters x the tile's 32 rows:
+// lane l holds rows 8(l/16) + j for cluster 16cb + l%16), B = x (the 32 rows x
+// 16 features of block fb, read transposed from the LDS tile), both exact or
+// split as in the E-step; D lane l: clusters 16cb + 4(l/16) + i, feature 16fb +
+// l%16.  Progress is published per 16-feature block (all rows read).
+template <int CB, int NQ, int XS, int NFB, bool SC>
+__device__ __forceinline__ void msum_tiles2(v4f (&S)[CB][NFB], int rounds0, int rounds1, int* ready0, int* ready1,
+                                            int* prog0, int* prog1, const int* lab0, const int* lab1,
+                                            const float* tile0, const float* tile1, int lane, float sc)
+{
+    const int h = lane >> 4, r16 = lane & 15;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+        for (int fb = 0; fb < NFB; ++fb) S[cb][fb] = v4f{0.f, 0.f, 0.f, 0.f};
+    }
+    const _Float16 one = (_Float16)1.0f, zero = (_Float16)0.0f;
+    const int rmax = rounds0 > rounds1 ? rounds0 : rounds1;
+    for (int r = 0; r < rmax; ++r) {
+        for (int u = 0; u < 2; ++u) {
+            // (selects, not an indexed array: the pointers stay in registers)
+            if (r >= (u == 0 ? rounds0 : rounds1)) continue;
+            int* const ready = u == 0 ? ready0 : ready1;
+            int* const prog = u == 0 ? prog0 : prog1;
+            const int* const lab = u == 0 ? lab0 : lab1;
+            const float* const tile = u == 0 ? tile0 : tile1;
+            wait_flag(ready, r + 1);
+            v8h A[CB];
+            {
+                const int4 l0 = *reinterpret_cast<const int4*>(lab + 8 * h);
+                const int4 l1 = *reinterpret_cast<const int4*>(lab + 8 * h + 4);
+                const int lj[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    const int c = 16 * cb + r16;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) A[cb][j] = lj[j] == c ? one : zero;
+                }
+            }
+            const float* col = tile + 8 * h * XS + r16;
+#pragma unroll
+            for (int fb = 0; fb < NFB; ++fb) {
+                float cur[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) cur[j] = col[j * XS + 16 * fb];
+                // columns of feature block fb have been read for every row
+                set_flag(prog, r * NQ + (4 * fb + 4 < NQ ? 4 * fb + 4 : NQ));
+                v8h bh, bl;
+                split8<SC>(make_float4(cur[0], cur[1], cur[2], cur[3]), make_float4(cur[4], cur[5], cur[6], cur[7]), sc,
+                           bh, bl);
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    S[cb][fb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb], bh, S[cb][fb], 0, 0, 0);
+                    S[cb][fb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb], bl, S[cb][fb], 0, 0, 0);
+                }
+            }
+        }
+    }
+}
+
 // M-step sums into red = [4][CPC][ld] (unscaled), once every pair is done.
 template <int CB, int NFB>
 __device__ __forceinline__ void publish_msums(const v4f (&S)[CB][NFB], float* red, int ld, int pair, int lane,
@@ -615,7 +677,7 @@ __device__ __forceinline__ void publish_msums(const v4f (&S)[CB][NFB], float* re
 }
 
 template <int CB, int NQ, bool SC>
-__global__ __launch_bounds__(512, 1) void k_fused16(FusedArgs a)
+__global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
 {
     const float* __restrict__ X = a.X;
     const long n = a.n;
@@ -633,38 +695,50 @@ __global__ __launch_bounds__(512, 1) void k_fused16(FusedArgs a)
     constexpr int KP = 32 * NK + (TAIL > 0 ? 16 : 0);
     constexpr int CSTR = KP + 8;                 // halves per centre row: an odd number of 16-byte units
     constexpr int XS = fused_stride(KP / 4);     // LDS row: >= KP floats (tail lanes write zeros past ld)
+    constexpr int NFB = KP / 16;                 // 16-feature blocks of the sums
     static_assert(TAIL == 0 || TAIL == 4 || TAIL == 8 || TAIL == 16, "one 16-wide step covers the tail");
-    // LDS: 4 pair tiles [64 x XS] | centre hi parts [CPC x CSTR] halves |
+    // LDS: 8 wave tiles [32 x XS] | centre hi parts [CPC x CSTR] halves |
     // centre lo parts
     extern __shared__ __attribute__((aligned(16))) float lds[];
-    __shared__ __attribute__((aligned(16))) int sLab[4][64];  // the tile's labels (-1: no row)
-    __shared__ int sCnt[4][64];
+    __shared__ __attribute__((aligned(16))) int sLab[8][32];  // a tile's labels (-1: no row)
+    __shared__ int sCnt[4][64];                                // rows per cluster, per SIMD
     __shared__ __attribute__((aligned(16))) float sN[CPC];
-    __shared__ int sReady[4];
-    __shared__ int sProg[4];
-    __shared__ int sDone;
+    __shared__ int sReady[8];  // tiles E-step wave e has labelled
+    __shared__ int sProg[8];   // columns of e's tile the sums wave has read: tile * NQ + chunk
+    __shared__ int sDone;      // nonzero: the loop has halted, nothing to do
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int pair = wave & 3;
     const int h = lane >> 4;    // this lane's K slice / centre quad in the MFMA layout
     const int r16 = lane & 15;  // this lane's row of a 16-row group / centre of a block
 
     float* tiles = lds;
-    _Float16* sCH = reinterpret_cast<_Float16*>(tiles + 4 * 64 * XS);
+    _Float16* sCH = reinterpret_cast<_Float16*>(tiles + 8 * 32 * XS);
     _Float16* sCL = sCH + CPC * CSTR;
 
-    const long ntiles = (n + 63) >> 6;
-    const long P = (long)gridDim.x * 4;
-    const long t0 = (long)blockIdx.x * 4 + pair;
-    const int rounds = t0 < ntiles ? (int)((ntiles - t0 + P - 1) / P) : 0;
+    // 32-row tiles: E-step wave e of block b handles t = 8b + e + r*P
+    const long ntiles = (n + 31) >> 5;
+    const long P = (long)gridDim.x * 8;
+    auto rounds_of = [&](int e) {
+        const long t0 = (long)blockIdx.x * 8 + e;
+        return t0 < ntiles ? (int)((ntiles - t0 + P - 1) / P) : 0;
+    };
 
-    if (wave < 4) {
-        // MFMA wave.  xr[g] holds this lane's features of row 16g + l%16:
-        // K32 step s in xr[g][2s], xr[g][2s + 1] (features 32s + 8h + 0..7),
-        // the tail in xr[g][2NK] (features 32NK + 4h + 0..3; lanes past the
-        // row's last feature load nothing: zeros)
-        float4 xr[4][QG];
+    if (wave < 8) {
+        // E-step wave e (SIMD e % 4).  xr[g] holds this lane's features of
+        // row 16g + l%16 of the tile: K32 step s in xr[g][2s], xr[g][2s + 1]
+        // (features 32s + 8h + 0..7), the tail in xr[g][2NK] (features 32NK +
+        // 4h + 0..3; lanes past the row's last feature load nothing: zeros)
+        const int e = wave;
+        const long t0 = (long)blockIdx.x * 8 + e;
+        const int rounds = rounds_of(e);
+        float4 xr[2][QG];
+        auto rsrc32 = [&](long t) {
+            const long r0 = t * 32;
+            const long rows = n - r0 < 32 ? (n - r0 > 0 ? n - r0 : 0) : 32;
+            return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(X + (rows > 0 ? r0 * ld : 0)), (short)0,
+                                                     (int)(rows * ld * 4), 0x00020000);
+        };
         auto load_step = [&](__amdgpu_buffer_rsrc_t rs, int g, int s) {
             if (s < NK) {
                 const int o = ((16 * g + r16) * LDX + 32 * s + 8 * h) * 4;
@@ -676,147 +750,144 @@ __global__ __launch_bounds__(512, 1) void k_fused16(FusedArgs a)
             }
         };
         {
-            // in the order of the reloads in the rounds below
-            const __amdgpu_buffer_rsrc_t r0 = tile_rsrc(X, t0, n, ld);
+            // in the order of the reloads in the rounds below (the waits at
+            // the top of a round then count the same loads either way)
+            const __amdgpu_buffer_rsrc_t r0 = rsrc32(t0);
 #pragma unroll
-            for (int gp = 0; gp < 2; ++gp) {
-#pragma unroll
-                for (int s = 0; s < NS; ++s) {
-                    load_step(r0, 2 * gp, s);
-                    load_step(r0, 2 * gp + 1, s);
-                }
+            for (int s = 0; s < NS; ++s) {
+                load_step(r0, 0, s);
+                load_step(r0, 1, s);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-        __syncthreads();  // LDS set up by the walkers
+        __syncthreads();  // LDS set up by the sums waves
         if (sDone != 0) return;
         const float sc = a.xscale;
         const float f2 = a.dscale;  // -2 * 2^-2s
-        float* const trow = tiles + pair * 64 * XS + r16 * XS;  // group 0's row of this lane
+        float* const trow = tiles + e * 32 * XS + r16 * XS;  // group 0's row of this lane
+        // this lane's centre operands: one base address, the block, step and
+        // part as constant offsets (no per-block address registers)
+        const _Float16* const cbase = sCH + r16 * CSTR + 8 * h;
+        constexpr int CLO = CPC * CSTR;  // hi -> lo parts
         int changed = 0;
         for (int r = 0; r < rounds; ++r) {
             const long t = t0 + (long)r * P;
-            const long nrow = n - t * 64 < 64 ? n - t * 64 : 64;
+            const long nrow = n - t * 32 < 32 ? n - t * 32 : 32;
             const bool valid = lane < nrow;
             const __amdgpu_buffer_rsrc_t rl =
-                __builtin_amdgcn_make_buffer_rsrc(labels + t * 64, (short)0, (int)(nrow * 4), 0x00020000);
+                __builtin_amdgcn_make_buffer_rsrc(labels + t * 32, (short)0, (int)(nrow * 4), 0x00020000);
             const int old = __builtin_amdgcn_raw_buffer_load_b32(rl, lane * 4, 0, 0);
-            const __amdgpu_buffer_rsrc_t rn = tile_rsrc(X, t + P, n, ld);
-            int mylab = 0;
-            int seen = 0;  // walker progress last read
+            const __amdgpu_buffer_rsrc_t rn = rsrc32(t + P);
+            int seen = 0;  // sums-wave progress last read
+            v4f acc[2][CB];
 #pragma unroll
-            for (int gp = 0; gp < 2; ++gp) {
-                // groups 2gp and 2gp + 1
-                v4f acc[2][CB];
+            for (int g = 0; g < 2; ++g) {
 #pragma unroll
-                for (int e = 0; e < 2; ++e) {
+                for (int cb = 0; cb < CB; ++cb) acc[g][cb] = v4f{0.f, 0.f, 0.f, 0.f};
+            }
 #pragma unroll
-                    for (int cb = 0; cb < CB; ++cb) acc[e][cb] = v4f{0.f, 0.f, 0.f, 0.f};
+            for (int s = 0; s < NS; ++s) {
+                // the columns of step s are rewritten below once the sums
+                // wave has read them for tile t - P
+                if (r > 0) {
+                    const int need = (r - 1) * NQ + (s < NK ? min(NQ, 8 * s + 8) : NQ);
+                    if (seen < need) seen = wait_flag(&sProg[e], need);
                 }
+                if (s < NK) {
+                    v8h xh[2], xl[2];
 #pragma unroll
-                for (int s = 0; s < NS; ++s) {
-                    // the columns of step s are rewritten below once the
-                    // walker has read them for tile t - P
-                    if (gp == 0 && r > 0) {
-                        const int need = (r - 1) * NQ + (s < NK ? min(NQ, 8 * s + 8) : NQ);
-                        if (seen < need) seen = wait_flag(&sProg[pair], need);
+                    for (int g = 0; g < 2; ++g) {
+                        float* dst = trow + 16 * g * XS + 32 * s + 8 * h;
+                        *reinterpret_cast<float4*>(dst) = xr[g][2 * s];
+                        *reinterpret_cast<float4*>(dst + 4) = xr[g][2 * s + 1];
+                        split8<SC>(xr[g][2 * s], xr[g][2 * s + 1], sc, xh[g], xl[g]);
+                        load_step(rn, g, s);
                     }
-                    if (s < NK) {
-                        v8h xh[2], xl[2];
-#pragma unroll
-                        for (int e = 0; e < 2; ++e) {
-                            const int g = 2 * gp + e;
-                            float* dst = trow + 16 * g * XS + 32 * s + 8 * h;
-                            *reinterpret_cast<float4*>(dst) = xr[g][2 * s];
-                            *reinterpret_cast<float4*>(dst + 4) = xr[g][2 * s + 1];
-                            split8<SC>(xr[g][2 * s], xr[g][2 * s + 1], sc, xh[e], xl[e]);
-                            load_step(rn, g, s);
-                        }
-#pragma unroll
-                        for (int cb = 0; cb < CB; ++cb) {
-                            const int co = (16 * cb + r16) * CSTR + 32 * s + 8 * h;
-                            const v8h ah = *reinterpret_cast<const v8h*>(sCH + co);
-                            const v8h al = *reinterpret_cast<const v8h*>(sCL + co);
-#pragma unroll
-                            for (int e = 0; e < 2; ++e) {
-                                acc[e][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, xh[e], acc[e][cb], 0, 0, 0);
-                                acc[e][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, xh[e], acc[e][cb], 0, 0, 0);
-                                acc[e][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, xl[e], acc[e][cb], 0, 0, 0);
-                            }
-                        }
-                    } else {
-                        v4h xh[2], xl[2];
-#pragma unroll
-                        for (int e = 0; e < 2; ++e) {
-                            const int g = 2 * gp + e;
-                            *reinterpret_cast<float4*>(trow + 16 * g * XS + 32 * NK + 4 * h) = xr[g][2 * NK];
-                            split4<SC>(xr[g][2 * NK], sc, xh[e], xl[e]);
-                            load_step(rn, g, s);
-                        }
-#pragma unroll
-                        for (int cb = 0; cb < CB; ++cb) {
-                            const int co = (16 * cb + r16) * CSTR + 32 * NK + 4 * h;
-                            const v4h ah = *reinterpret_cast<const v4h*>(sCH + co);
-                            const v4h al = *reinterpret_cast<const v4h*>(sCL + co);
-#pragma unroll
-                            for (int e = 0; e < 2; ++e) {
-                                acc[e][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, xh[e], acc[e][cb], 0, 0, 0);
-                                acc[e][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(al, xh[e], acc[e][cb], 0, 0, 0);
-                                acc[e][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, xl[e], acc[e][cb], 0, 0, 0);
-                            }
-                        }
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-                // ||c||^2 - 2 x.c, first minimum wins (_k_means_lloyd.pyx:196-212)
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    float bd = INFINITY;
-                    int bi = 4 * h;
 #pragma unroll
                     for (int cb = 0; cb < CB; ++cb) {
-                        const float4 c4 = *reinterpret_cast<const float4*>(&sN[16 * cb + 4 * h]);
-                        const float cn[4] = {c4.x, c4.y, c4.z, c4.w};
+                        const _Float16* cp = cbase + 16 * cb * CSTR + 32 * s;
+                        const v8h ah = *reinterpret_cast<const v8h*>(cp);
+                        const v8h al = *reinterpret_cast<const v8h*>(cp + CLO);
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            // a NaN distance compares false: it never wins
-                            const float dd = fmaf(f2, acc[e][cb][i], cn[i]);
-                            const bool take = dd < bd;
-                            bd = take ? dd : bd;
-                            bi = take ? 16 * cb + 4 * h + i : bi;
+                        for (int g = 0; g < 2; ++g) {
+                            acc[g][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, xh[g], acc[g][cb], 0, 0, 0);
+                            acc[g][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, xh[g], acc[g][cb], 0, 0, 0);
+                            acc[g][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, xl[g], acc[g][cb], 0, 0, 0);
                         }
                     }
+                } else {
+                    v4h xh[2], xl[2];
 #pragma unroll
-                    for (int m = 16; m <= 32; m *= 2) {
-                        const float od = __shfl_xor(bd, m);
-                        const int oi = __shfl_xor(bi, m);
-                        const bool take = (od < bd) | ((od == bd) & (oi < bi));  // no branch
-                        bd = take ? od : bd;
-                        bi = take ? oi : bi;
+                    for (int g = 0; g < 2; ++g) {
+                        *reinterpret_cast<float4*>(trow + 16 * g * XS + 32 * NK + 4 * h) = xr[g][2 * NK];
+                        split4<SC>(xr[g][2 * NK], sc, xh[g], xl[g]);
+                        load_step(rn, g, s);
                     }
-                    if (h == 2 * gp + e) mylab = bi;
+#pragma unroll
+                    for (int cb = 0; cb < CB; ++cb) {
+                        const _Float16* cp = cbase - 4 * h + 16 * cb * CSTR + 32 * NK;
+                        const v4h ah = *reinterpret_cast<const v4h*>(cp);
+                        const v4h al = *reinterpret_cast<const v4h*>(cp + CLO);
+#pragma unroll
+                        for (int g = 0; g < 2; ++g) {
+                            acc[g][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, xh[g], acc[g][cb], 0, 0, 0);
+                            acc[g][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(al, xh[g], acc[g][cb], 0, 0, 0);
+                            acc[g][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, xl[g], acc[g][cb], 0, 0, 0);
+                        }
+                    }
                 }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            // ||c||^2 - 2 x.c, first minimum wins (_k_means_lloyd.pyx:196-212)
+            int mylab = 0;
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                float bd = INFINITY;
+                int bi = 4 * h;
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    const float4 c4 = *reinterpret_cast<const float4*>(&sN[16 * cb + 4 * h]);
+                    const float cn[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        // a NaN distance compares false: it never wins
+                        const float dd = fmaf(f2, acc[g][cb][i], cn[i]);
+                        const bool take = dd < bd;
+                        bd = take ? dd : bd;
+                        bi = take ? 16 * cb + 4 * h + i : bi;
+                    }
+                }
+#pragma unroll
+                for (int m = 16; m <= 32; m *= 2) {
+                    const float od = __shfl_xor(bd, m);
+                    const int oi = __shfl_xor(bi, m);
+                    const bool take = (od < bd) | ((od == bd) & (oi < bi));  // no branch
+                    bd = take ? od : bd;
+                    bi = take ? oi : bi;
+                }
+                if (h == g) mylab = bi;  // lanes 0..31: row = lane
             }
             __builtin_amdgcn_raw_buffer_store_b32(mylab, rl, lane * 4, 0, 0);
             changed += (int)__popcll(__ballot(valid && old != mylab));
-            // the tile's labels for the M-step wave; the counts (integer
-            // adds: any order gives the same total)
-            sLab[pair][lane] = valid ? mylab : -1;
-            if (valid) atomicAdd(&sCnt[pair][mylab], 1);
-            set_flag(&sReady[pair], r + 1);
+            // the tile's labels for the sums wave; the counts (integer adds:
+            // any order gives the same total)
+            if (lane < 32) sLab[e][lane] = valid ? mylab : -1;
+            if (valid) atomicAdd(&sCnt[e & 3][mylab], 1);
+            set_flag(&sReady[e], r + 1);
         }
         if (lane == 0 && changed != 0) atomicAdd(a.changed, changed);
-        __syncthreads();  // every pair's walker is done: the tile area is free
-        __syncthreads();  // the walkers' sums are in LDS
+        __syncthreads();  // every sums wave is done: the tile area is free
+        __syncthreads();  // the sums are in LDS
     } else {
-        // walker waves: the halt test, then the centres' scaled fp16 parts
-        // (rows >= k and columns >= ld zero), the zero row and ||c||^2
+        // sums waves 8..11: the halt test, then the centres' scaled fp16
+        // parts (rows >= k and columns >= ld zero) and ||c||^2
         const int prev = st->done;
         if (prev != 0) {
-            if (tid == 256) sDone = prev;
+            if (tid == 512) sDone = prev;
             __syncthreads();
             return;
         }
-        const int wt = tid - 256;
+        const int wt = tid - 512;
         constexpr int CQ = KP / 4;
         constexpr int NF = (CPC * CQ + 255) / 256;
         const float sc = a.xscale;
@@ -842,24 +913,25 @@ __global__ __launch_bounds__(512, 1) void k_fused16(FusedArgs a)
                 *reinterpret_cast<v4h*>(sCL + cl * CSTR + 4 * q) = lo;
             }
         }
-        if (wt < 4) {
+        if (wt < 8) {
             sReady[wt] = 0;
             sProg[wt] = 0;
         }
         sCnt[wt >> 6][wt & 63] = 0;
-        if (wave == 4) step_norms<CPC>(a, lane, sN, &sDone);
+        if (wave == 8) step_norms<CPC>(a, lane, sN, &sDone);
         __syncthreads();
         if (sDone != 0) return;
-        // M-step wave
-        constexpr int NFB = KP / 16;
+        // the sums wave of SIMD m serves E-step waves m and m + 4
+        const int m = wave - 8;
         v4f S[CB][NFB];
-        msum_tiles<CB, NQ, XS, NFB, SC>(S, rounds, lane, &sReady[pair], &sProg[pair], sLab[pair],
-                                        tiles + pair * 64 * XS, sc);
-        __syncthreads();  // every pair is done with its tile
-        publish_msums<CB, NFB>(S, tiles, ld, pair, lane, SC ? 1.f / sc : 1.f);
+        msum_tiles2<CB, NQ, XS, NFB, SC>(S, rounds_of(m), rounds_of(m + 4), &sReady[m], &sReady[m + 4], &sProg[m],
+                                         &sProg[m + 4], sLab[m], sLab[m + 4], tiles + m * 32 * XS,
+                                         tiles + (m + 4) * 32 * XS, lane, sc);
+        __syncthreads();  // every wave is done with its tile
+        publish_msums<CB, NFB>(S, tiles, ld, m, lane, SC ? 1.f / sc : 1.f);
         __syncthreads();
     }
-    combine_sums<CPC>(tiles, ld, k, a.psum, a.pcnt, sCnt, tid);
+    combine_sums<CPC, 768>(tiles, ld, k, a.psum, a.pcnt, sCnt, tid);
 }
 
 typedef void (*fused_fn)(FusedArgs);
@@ -929,7 +1001,7 @@ static size_t fused16_dyn_lds(int k, int ld)
     const int cpc = 16 * ((k + 15) / 16);
     const int nk = ld / 32;
     const int kp = 32 * nk + (ld > 32 * nk ? 16 : 0);
-    return (size_t)4 * 64 * fused_stride(kp / 4) * sizeof(float) + (size_t)2 * cpc * (kp + 8) * sizeof(_Float16);
+    return (size_t)8 * 32 * fused_stride(kp / 4) * sizeof(float) + (size_t)2 * cpc * (kp + 8) * sizeof(_Float16);
 }
 
 int fused16_ready(int k, int ld)
@@ -995,7 +1067,7 @@ hipError_t launch_fused(const FusedArgs& a, hipStream_t s)
     fused_fn f = a.f16 ? fused16_kernel(a.k, a.ld, a.xscale != 1.f) : fused_kernel(a.k, a.ld);
     if (f == nullptr || a.blocks < 1) return hipErrorInvalidValue;
     const size_t dyn = a.f16 ? fused16_dyn_lds(a.k, a.ld) : fused_dyn_lds(a.k, a.ld);
-    hipLaunchKernelGGL(f, dim3(a.blocks), dim3(512), dyn, s, a);
+    hipLaunchKernelGGL(f, dim3(a.blocks), dim3(a.f16 ? 768 : 512), dyn, s, a);
     return hipGetLastError();
 }
 
