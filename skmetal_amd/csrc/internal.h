@@ -145,13 +145,12 @@ hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t s, bool with_loop)
 // The loop decision alone (after a fused step whose successor is not enqueued).
 // nch: the chunk count the partials were written with (0: that of a.R).
 hipError_t launch_finalize_loop(const FinalizeArgs& a, hipStream_t s, int nch = 0);
-// A finalize block is 256 threads = cw columns x (256/cw) partial-sum lanes,
-// sized so that each thread reads at most about 8 of the R partials.
+// A finalize block is 256 threads = 8 float4 columns (32 columns) x 32
+// partial-sum lanes.
 inline int finalize_cols(int R)
 {
-    int rs = 1;
-    while (rs < 64 && rs * 8 < R) rs *= 2;
-    return 256 / rs;
+    (void)R;
+    return 32;
 }
 inline int finalize_col_chunks(int d, int R) { const int cw = finalize_cols(R); return (d + cw - 1) / cw; }
 

@@ -625,11 +625,12 @@ hipError_t launch_sorted_update(const SortArgs& a, const SortGeom& g, hipStream_
 // ---------------------------------------------------------------------------
 //
 // k_finalize_cols, block (j, cc): the R partial sums of cluster j, columns
-// [cc*CW, cc*CW + CW), reduced in a fixed order -- each of the RS lanes of a
-// column adds partials rs, rs+RS, ... in fp64, the lanes of a wave are
-// combined by an xor butterfly (every lane ends with bitwise the same value)
-// and the four waves in wave order -- then the new centre, and the chunk's
-// shift^2 and ||c||^2 partials.
+// [32 cc, 32 cc + 32), reduced in a fixed order -- thread (rs, q) adds the
+// float4 of columns 32 cc + 4q.. of partials rs, rs + 32, ... in fp64 (eight
+// threads read one 128-byte run of a partial), the eight rs lanes of a wave
+// are combined by an xor butterfly (every lane ends with bitwise the same
+// value) and the four waves in wave order -- then the new centre, and the
+// chunk's shift^2 and ||c||^2 partials.
 // k_finalize_loop, one block: folds each cluster's chunk partials in chunk
 // order and evaluates the loop's stopping rules (_kmeans.py:717-732).
 // The kernel boundary makes the first kernel's stores visible to the second;
@@ -658,26 +659,25 @@ __global__ __launch_bounds__(256) void k_finalize_cols(FinalizeArgs a)
     const int cc = blockIdx.y;
     const int nch = gridDim.y;
     const int tid = threadIdx.x;
-    const int CW = a.cw;            // columns per block (power of two)
-    const int RS = 256 / CW;        // partial-sum lanes per column
-    const int cl = tid % CW;
-    const int rs = tid / CW;
-    const int col = cc * CW + cl;
-    __shared__ double red[256];
+    const int q = tid & 7;          // float4 column of the block
+    const int rs = tid >> 3;        // partial lane, 0..31
+    const int c4 = cc * 32 + 4 * q; // first column of this thread
+    __shared__ double red[4][8][4];
     __shared__ double shd[2][4];
     __shared__ int shi[4];
 
-    // block partials: the halt flag, the old centre, the counts and the
+    // block partials: the halt flag, the old centres, the counts and the
     // partials are all requested before any of them is used (one memory
     // round trip); records exist only for a step whose update ran, so that
     // mode tests the flag first
     const bool recs = a.rec_off != nullptr;
     const int done = a.state->done;
     if (recs && done != 0) return;
-    const float c_old = tid < CW && col < a.d ? a.C_old[(long)j * a.ld + col] : 0.f;
+    const int ccol = cc * 32 + tid;  // threads 0..31: one column each for the centre update
+    const float c_old = tid < 32 && ccol < a.d ? a.C_old[(long)j * a.ld + ccol] : 0.f;
     // partials of cluster j: R of them at r*k + j, or its records
     const int R = recs ? a.rec_cnt[j] : a.R;
-    const float* src = a.psum + (recs ? (long)a.rec_off[j] * a.ld : (long)j * a.ld) + col;
+    const float* src = a.psum + (recs ? (long)a.rec_off[j] * a.ld : (long)j * a.ld) + c4;
     const long step = recs ? (long)a.ld : (long)a.k * a.ld;
     int cnt = 0;
     if (recs) {
@@ -685,35 +685,50 @@ __global__ __launch_bounds__(256) void k_finalize_cols(FinalizeArgs a)
     } else {
         for (int r = tid; r < a.R; r += 256) cnt += a.pcnt[(long)r * a.k + j];
     }
-    double s = 0.0;
-    if (col < a.d && R > 0) {
-        for (int r0 = rs; r0 < R; r0 += kFinUnroll * RS) {
-            float v[kFinUnroll];
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+    if (c4 < a.ld && R > 0) {  // ld is a multiple of 4: the float4 is in or out
+        for (int r0 = rs; r0 < R; r0 += kFinUnroll * 32) {
+            float4 v[kFinUnroll];
 #pragma unroll
             for (int u = 0; u < kFinUnroll; ++u) {
-                const int r = r0 + u * RS;
-                v[u] = src[(long)(r < R ? r : R - 1) * step];  // unconditional: all in flight
+                const int r = r0 + u * 32;
+                v[u] = *reinterpret_cast<const float4*>(src + (long)(r < R ? r : R - 1) * step);  // all in flight
             }
 #pragma unroll
-            for (int u = 0; u < kFinUnroll; ++u)
-                if (r0 + u * RS < R) s += (double)v[u];
+            for (int u = 0; u < kFinUnroll; ++u) {
+                if (r0 + u * 32 < R) {
+                    s0 += (double)v[u].x;
+                    s1 += (double)v[u].y;
+                    s2 += (double)v[u].z;
+                    s3 += (double)v[u].w;
+                }
+            }
         }
     }
     if (done != 0) return;  // the loop has halted: nothing is written
-    // lanes of one column inside a wave: xor offsets CW, 2CW, ... < 64
-    for (int off = CW; off < 64; off <<= 1) s += __shfl_xor(s, off, 64);
-    red[tid] = s;
+    // the eight partial lanes of a wave (lane bits 3..5), then the waves
+    for (int off = 8; off < 64; off <<= 1) {
+        s0 += __shfl_xor(s0, off, 64);
+        s1 += __shfl_xor(s1, off, 64);
+        s2 += __shfl_xor(s2, off, 64);
+        s3 += __shfl_xor(s3, off, 64);
+    }
+    if ((tid & 63) < 8) {
+        red[tid >> 6][q][0] = s0;
+        red[tid >> 6][q][1] = s1;
+        red[tid >> 6][q][2] = s2;
+        red[tid >> 6][q][3] = s3;
+    }
     const int count = block_sum(cnt, shi);  // its barrier also publishes red[]
 
     double sq = 0.0, nrm = 0.0;
-    if (tid < CW && col < a.d) {
-        const int stride = CW < 64 ? 64 : CW;
-        double tot = 0.0;
-        for (int t = cl; t < 256; t += stride) tot += red[t];
-        a.sums[(long)j * a.ld + col] = tot;
+    if (tid < 32 && ccol < a.d) {
+        const int qq = tid >> 2, e = tid & 3;
+        const double tot = ((red[0][qq][e] + red[1][qq][e]) + red[2][qq][e]) + red[3][qq][e];
+        a.sums[(long)j * a.ld + ccol] = tot;
         if (count > 0) {
             const float cn = (float)(tot / (double)count);
-            a.C_new[(long)j * a.ld + col] = cn;
+            a.C_new[(long)j * a.ld + ccol] = cn;
             const double df = (double)cn - (double)c_old;
             sq = df * df;
             nrm = (double)cn * (double)cn;
@@ -1041,19 +1056,55 @@ hipError_t launch_relocate(const RelocArgs& a, int E, hipStream_t s)
 // set-up kernels
 // ---------------------------------------------------------------------------
 
-constexpr long kColsumRows = 4096;
+constexpr long kColsumRows = 512;
 
 int colsum_grid(long n) { return (int)max(1L, (n + kColsumRows - 1) / kColsumRows); }
 
+// Block b sums rows [512 b, 512 b + 512) of every column in fp64: thread
+// (slot, q) adds the float4 of columns 4q.. (plus 128 per pass) of rows
+// slot, slot + 8, ... (eight slots, all loads of a batch in flight), then the
+// slots are added in slot order -- a fixed order, so the mean is bitwise
+// reproducible.
 __global__ __launch_bounds__(256) void k_colsum(const float* __restrict__ X, long n, int ld, int d,
                                                 double* __restrict__ part)
 {
     const long r0 = (long)blockIdx.x * kColsumRows;
     const long r1 = min(n, r0 + kColsumRows);
-    for (int c = threadIdx.x; c < d; c += blockDim.x) {
-        double s = 0.0;
-        for (long r = r0; r < r1; ++r) s += (double)X[r * ld + c];
-        part[(long)blockIdx.x * d + c] = s;
+    const int q = threadIdx.x & 31;
+    const int slot = threadIdx.x >> 5;
+    __shared__ double red[8][128];
+    for (int c0 = 0; c0 < ld; c0 += 128) {
+        const int c = c0 + 4 * q;
+        double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+        if (c < ld) {  // ld is a multiple of 4
+            for (long r = r0 + slot; r < r1; r += 8 * 8) {
+                float4 v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const long rr = r + 8 * u;
+                    v[u] = rr < r1 ? *reinterpret_cast<const float4*>(X + rr * ld + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    s0 += (double)v[u].x;
+                    s1 += (double)v[u].y;
+                    s2 += (double)v[u].z;
+                    s3 += (double)v[u].w;
+                }
+            }
+        }
+        red[slot][4 * q + 0] = s0;
+        red[slot][4 * q + 1] = s1;
+        red[slot][4 * q + 2] = s2;
+        red[slot][4 * q + 3] = s3;
+        __syncthreads();
+        if (threadIdx.x < 128 && c0 + (int)threadIdx.x < d) {
+            double t = 0.0;
+#pragma unroll
+            for (int k8 = 0; k8 < 8; ++k8) t += red[k8][threadIdx.x];
+            part[(long)blockIdx.x * d + c0 + threadIdx.x] = t;
+        }
+        __syncthreads();
     }
 }
 
@@ -1063,18 +1114,22 @@ hipError_t launch_colsum(const float* X, long n, int ld, int d, double* part, in
     return hipGetLastError();
 }
 
-__global__ void k_colmean(const double* __restrict__ part, int nblk, long n, int d, float* __restrict__ mean)
+// Block c: column c's mean from the nblk block sums -- thread t adds sums t,
+// t + 256, ... and the block adds its threads in a fixed order.
+__global__ __launch_bounds__(256) void k_colmean(const double* __restrict__ part, int nblk, long n, int d,
+                                                 float* __restrict__ mean)
 {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= d) return;
+    __shared__ double sh[4];
+    const int c = blockIdx.x;
     double s = 0.0;
-    for (int b = 0; b < nblk; ++b) s += part[(long)b * d + c];
-    mean[c] = (float)(s / (double)n);
+    for (int b = threadIdx.x; b < nblk; b += 256) s += part[(long)b * d + c];
+    s = block_sum(s, sh);
+    if (threadIdx.x == 0) mean[c] = (float)(s / (double)n);
 }
 
 hipError_t launch_colmean(const double* part, int nblk, long n, int d, float* mean, hipStream_t s)
 {
-    hipLaunchKernelGGL(k_colmean, dim3((d + 255) / 256), dim3(256), 0, s, part, nblk, n, d, mean);
+    hipLaunchKernelGGL(k_colmean, dim3(d), dim3(256), 0, s, part, nblk, n, d, mean);
     return hipGetLastError();
 }
 
@@ -1104,20 +1159,31 @@ __global__ __launch_bounds__(256) void k_absmax(const float* __restrict__ X, lon
 {
     float m = 0.f;
     const long stride = (long)gridDim.x * 256;
-    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < count; i += stride) {
+    const long c4 = count >> 2;  // 16-byte loads over the multiple-of-4 part
+    const float4* X4 = reinterpret_cast<const float4*>(X);
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < c4; i += stride) {
+        const float4 v4 = X4[i];
+        const float e[4] = {fabsf(v4.x), fabsf(v4.y), fabsf(v4.z), fabsf(v4.w)};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) m = e[u] != e[u] ? INFINITY : fmaxf(m, e[u]);
+    }
+    for (long i = 4 * c4 + (long)blockIdx.x * 256 + threadIdx.x; i < count; i += stride) {
         const float v = fabsf(X[i]);
         m = v != v ? INFINITY : fmaxf(m, v);
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    if ((threadIdx.x & 63) == 0) atomicMax(out, __float_as_uint(m));
+    __shared__ float wm[4];
+    if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) atomicMax(out, __float_as_uint(fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]))));
 }
 
 hipError_t launch_absmax(const float* X, long count, unsigned* out, hipStream_t s)
 {
     const hipError_t e = hipMemsetAsync(out, 0, sizeof(unsigned), s);
     if (e != hipSuccess) return e;
-    long blocks = (count + 255) / 256;
+    long blocks = (count / 4 + 255) / 256;
     if (blocks > 1024) blocks = 1024;
     if (blocks < 1) blocks = 1;
     hipLaunchKernelGGL(k_absmax, dim3((unsigned)blocks), dim3(256), 0, s, X, count, out);
