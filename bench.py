@@ -33,6 +33,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_FP16_MFMA_TFLOPS = 2500.0
 PEAK_HBM_GBPS = 8000.0
 
 
@@ -142,8 +143,8 @@ def main():
     it_s = 1.0 / step_s
     flops = 2.0 * n * k * d
     assign_s = ms_assign / 1e3
-    fused, f16 = mode["fused"], mode["f16"]
-    kname = "k_fused16" if f16 else "k_fused" if fused else "k_assign"
+    fused, f16, a16 = mode["fused"], mode["f16"], mode["a16"]
+    kname = "k_fused16" if f16 else "k_fused" if fused else "k_assign16" if a16 else "k_assign"
     traffic = _traffic_from_profile(f"{kname}_{args.workload}_pmc.txt")
     if f16:
         # HBM roofline: the bytes one launch must move -- X once, the labels
@@ -158,6 +159,22 @@ def main():
             "frac": round(nbytes / assign_s / 1e9 / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
             "algorithmic_bytes": nbytes,
+            "fp32_equiv_tflops": round(flops / assign_s / 1e12, 2),
+        }
+    elif a16:
+        # MFMA roofline of the fp16 split: three fp16 products per x.c term,
+        # over the padded centres (multiples of 16 per pass) and features (32)
+        kp = -(-k // (16 * (4 if k <= 64 else 8 if k <= 128 else 16))) * (16 * (4 if k <= 64 else 8 if k <= 128 else 16))
+        dp = -(-d // 32) * 32
+        mflops = 3.0 * 2.0 * n * kp * dp
+        roofline = {
+            "kernel": "k_assign16: ||c||^2 - 2 x.c on fp16x2-split MFMA (v_mfma_f32_16x16x32_f16) + argmin",
+            "bound": "mfma",
+            "achieved": round(mflops / assign_s / 1e12, 1),
+            "peak": PEAK_FP16_MFMA_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(mflops / assign_s / 1e12 / PEAK_FP16_MFMA_TFLOPS, 4),
+            "traffic": traffic,
             "fp32_equiv_tflops": round(flops / assign_s / 1e12, 2),
         }
     else:
@@ -195,12 +212,12 @@ def main():
         "wall_s_timed": round(wall, 4),
         "h2d_s": round(h2d_s, 4),
         "step_mode": (f"fused: {kname} (E-step + per-cluster sums) + k_finalize" if fused
-                      else "k_assign + k_update + k_finalize"),
+                      else f"{kname} + sorted update + k_finalize"),
         "e_step": ("fp16x2 split (x, c scaled by 2^s; hi/lo parts), v_mfma_f32_16x16x32_f16, fp32 accumulate"
-                   if f16 else "fp32 MFMA (v_mfma_f32_4x4x1_16b_f32)"),
+                   if (f16 or (a16 and not fused)) else "fp32 MFMA (v_mfma_f32_4x4x1_16b_f32)"),
         "partials": mode["partials"],
         "kernels_ms": ({kname: round(ms_assign, 5), "k_finalize": round(ms_final, 5)} if fused
-                       else {"k_assign": round(ms_assign, 5), "update": round(ms_update, 5),
+                       else {kname: round(ms_assign, 5), "update": round(ms_update, 5),
                              "k_finalize": round(ms_final, 5)}),
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -130,11 +130,12 @@ SKMETAL_API int skmetal_hip_lloyd_iterate(skmetal_hip_lloyd* h, size_t iters, fl
  * including the final E-step and inertia. */
 SKMETAL_API int skmetal_hip_lloyd_run(skmetal_hip_lloyd* h, size_t max_iter, double tol, int flags,
                           int32_t* n_iter_out, double* inertia_out);
-/* *fused = 0 when a step runs as separate E-step and update kernels, 1 when
- * as one fused E-step + sums kernel with the E-step on fp32 MFMA (k <= 64,
- * d <= 100), 2 when that kernel's E-step runs on fp16 MFMA with x and c split
- * in two scaled fp16 parts (d >= 17 and finite data); *partials = per-step
- * partial sums the finalize reduces. */
+/* *fused & 3 = 0 when a step runs as separate E-step and update kernels, 1
+ * when as one fused E-step + sums kernel with the E-step on fp32 MFMA
+ * (k <= 64, d <= 100), 2 when that kernel's E-step runs on fp16 MFMA with x
+ * and c split in two scaled fp16 parts (d >= 17 and finite data); *fused & 4
+ * = the separate E-step kernel (generic path, final E-step, assign) uses the
+ * same fp16 split; *partials = per-step partial sums the finalize reduces. */
 SKMETAL_API int skmetal_hip_lloyd_info(skmetal_hip_lloyd* h, int* fused, int* partials);
 SKMETAL_API int skmetal_hip_lloyd_get_centers(skmetal_hip_lloyd* h, float* C);
 SKMETAL_API int skmetal_hip_lloyd_get_labels(skmetal_hip_lloyd* h, int32_t* labels);

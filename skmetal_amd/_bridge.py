@@ -279,7 +279,8 @@ class LloydHandle:
         partials = ctypes.c_int(0)
         _check(_lib.skmetal_hip_lloyd_info(self._h, ctypes.byref(fused), ctypes.byref(partials)),
                "skmetal_hip_lloyd_info")
-        return dict(fused=bool(fused.value), f16=fused.value == 2, partials=int(partials.value))
+        mode = int(fused.value)
+        return dict(fused=bool(mode & 3), f16=(mode & 3) == 2, a16=bool(mode & 4), partials=int(partials.value))
 
     def centers(self):
         out = np.empty((self.k, self.d), np.float32)

@@ -934,6 +934,205 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
     combine_sums<CPC, 768>(tiles, ld, k, a.psum, a.pcnt, sCnt, tid);
 }
 
+// ---------------------------------------------------------------------------
+// k_assign16: the E-step for any k (the generic path and the assign entry
+// point) on fp16 MFMA with the same two-part split and operand layout as
+// k_fused16.  A block of 8 waves owns 256 rows (32 per wave: two 16-row
+// groups); it takes the centres in passes of 16*CB (A operands from LDS, hi
+// and lo parts staged per 128-feature segment by the whole block) and keeps
+// per lane the first minimum over its centres 16cb + 4(l/16) + i, in
+// ascending order across passes; the four lanes of a row are combined after
+// the last pass.  X is read once per pass (k/(16 CB) times), the centres once
+// per 256 rows.
+template <int CB, bool SC>
+__global__ __launch_bounds__(512, 1) void k_assign16(const float* __restrict__ X, long n, int ld,
+                                                    const float* __restrict__ C, const float* __restrict__ cnorm,
+                                                    int k, int* __restrict__ labels, LoopState* st, int* changed,
+                                                    float sc, float f2)
+{
+    if (st != nullptr && st->done != 0) return;
+    constexpr int CPC = 16 * CB;       // centres per pass
+    constexpr int SEG = 128;           // features per staged segment (4 K32 steps)
+    constexpr int CSTR = SEG + 8;      // halves per centre row: an odd number of 16-byte units
+    constexpr int CLO = CPC * CSTR;    // hi -> lo parts
+    extern __shared__ __attribute__((aligned(16))) _Float16 cs[];  // [2][CPC][CSTR]
+    __shared__ __attribute__((aligned(16))) float sN[CPC];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 4, r16 = lane & 15;
+    const int npass = (k + CPC - 1) / CPC;
+    const int nseg = (ld + SEG - 1) / SEG;
+    const _Float16* const cbase = cs + r16 * CSTR + 8 * h;
+
+    for (long base = (long)blockIdx.x * 256; base < n; base += (long)gridDim.x * 256) {
+        const long wrow = base + 32 * wave;  // this wave's first row
+        const long nrow = n - wrow < 32 ? (n - wrow > 0 ? n - wrow : 0) : 32;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(X + (nrow > 0 ? wrow * ld : 0)), (short)0, (int)(nrow * ld * 4), 0x00020000);
+        float bd[2] = {INFINITY, INFINITY};
+        int bi[2] = {0, 0};
+        for (int p = 0; p < npass; ++p) {
+            v4f acc[2][CB];
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) acc[g][cb] = v4f{0.f, 0.f, 0.f, 0.f};
+            }
+            for (int sg = 0; sg < nseg; ++sg) {
+                const int f0 = sg * SEG;
+                __syncthreads();  // the previous segment's operands are consumed
+                // stage centres p*CPC.. x features f0..f0+127 as scaled fp16
+                // parts (centres >= k and features >= ld zero)
+                // (CPC * 32 float4s over 512 threads: CB each, in batches of
+                // up to 8 loads in flight before the first conversion)
+                constexpr int SB = CB < 8 ? CB : 8;
+#pragma unroll
+                for (int u0 = 0; u0 < CB; u0 += SB) {
+                    float4 v[SB];
+#pragma unroll
+                    for (int u = 0; u < SB; ++u) {
+                        const int idx = tid + 512 * (u0 + u);
+                        const int cl = idx >> 5;
+                        const int j = p * CPC + cl;
+                        const int f = f0 + 4 * (idx & 31);
+                        v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+                        if (j < k && f < ld) v[u] = *reinterpret_cast<const float4*>(C + (long)j * ld + f);
+                    }
+#pragma unroll
+                    for (int u = 0; u < SB; ++u) {
+                        const int idx = tid + 512 * (u0 + u);
+                        const int cl = idx >> 5;
+                        const int q = idx & 31;
+                        v4h hi, lo;
+                        split4<SC>(v[u], sc, hi, lo);
+                        *reinterpret_cast<v4h*>(cs + cl * CSTR + 4 * q) = hi;
+                        *reinterpret_cast<v4h*>(cs + CLO + cl * CSTR + 4 * q) = lo;
+                    }
+                }
+                if (sg == 0) {
+                    for (int i = tid; i < CPC; i += 512) {
+                        const int j = p * CPC + i;
+                        sN[i] = j < k ? cnorm[j] : INFINITY;  // padding centres never win
+                    }
+                }
+                __syncthreads();
+                const int nks = min(4, (ld - f0 + 31) / 32);
+                for (int ks = 0; ks < nks; ++ks) {
+                    // rows 16g + l%16, features f0 + 32ks + 8h..: past the
+                    // row's end the next row's (finite) values meet zero
+                    // centre parts; past the last row the loads return 0
+                    v8h xh[2], xl[2];
+#pragma unroll
+                    for (int g = 0; g < 2; ++g) {
+                        const int o = ((16 * g + r16) * ld + f0 + 32 * ks + 8 * h) * 4;
+                        split8<SC>(load_quad(rs, o), load_quad(rs, o + 16), sc, xh[g], xl[g]);
+                    }
+#pragma unroll
+                    for (int cb = 0; cb < CB; ++cb) {
+                        const _Float16* cp = cbase + 16 * cb * CSTR + 32 * ks;
+                        const v8h ah = *reinterpret_cast<const v8h*>(cp);
+                        const v8h al = *reinterpret_cast<const v8h*>(cp + CLO);
+#pragma unroll
+                        for (int g = 0; g < 2; ++g) {
+                            acc[g][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, xh[g], acc[g][cb], 0, 0, 0);
+                            acc[g][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, xh[g], acc[g][cb], 0, 0, 0);
+                            acc[g][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, xl[g], acc[g][cb], 0, 0, 0);
+                        }
+                    }
+                }
+            }
+            // ||c||^2 - 2 x.c, first minimum wins (_k_means_lloyd.pyx:196-212);
+            // the lane's centres come in ascending order, passes too
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    const float4 c4 = *reinterpret_cast<const float4*>(&sN[16 * cb + 4 * h]);
+                    const float cn[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float dd = fmaf(f2, acc[g][cb][i], cn[i]);  // NaN compares false
+                        const bool take = dd < bd[g];
+                        bd[g] = take ? dd : bd[g];
+                        bi[g] = take ? p * CPC + 16 * cb + 4 * h + i : bi[g];
+                    }
+                }
+            }
+        }
+        int mylab = 0;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            float d0 = bd[g];
+            int i0 = bi[g];
+#pragma unroll
+            for (int m = 16; m <= 32; m *= 2) {
+                const float od = __shfl_xor(d0, m);
+                const int oi = __shfl_xor(i0, m);
+                const bool take = (od < d0) | ((od == d0) & (oi < i0));
+                d0 = take ? od : d0;
+                i0 = take ? oi : i0;
+            }
+            if (h == g) mylab = i0;  // lanes 0..31: row = lane
+        }
+        const bool valid = lane < nrow;
+        const long row = wrow + lane;
+        int moved = 0;
+        if (valid) {
+            if (changed != nullptr) moved = labels[row] != mylab;
+            labels[row] = mylab;
+        }
+        if (changed != nullptr) {
+            const unsigned long long mm = __ballot(moved);
+            if (lane == 0 && mm != 0ull) atomicAdd(changed, (int)__popcll(mm));
+        }
+    }
+}
+
+typedef void (*assign16_fn)(const float*, long, int, const float*, const float*, int, int*, LoopState*, int*, float,
+                            float);
+
+static assign16_fn assign16_kernel(int k, bool scaled)
+{
+    const int cb = k <= 64 ? 4 : k <= 128 ? 8 : 16;
+    if (cb == 4) return scaled ? &k_assign16<4, true> : &k_assign16<4, false>;
+    if (cb == 8) return scaled ? &k_assign16<8, true> : &k_assign16<8, false>;
+    return scaled ? &k_assign16<16, true> : &k_assign16<16, false>;
+}
+
+static size_t assign16_lds(int k)
+{
+    const int cb = k <= 64 ? 4 : k <= 128 ? 8 : 16;
+    return (size_t)2 * 16 * cb * (128 + 8) * sizeof(_Float16);
+}
+
+int assign16_ready(int d, int k)
+{
+    const char* env = getenv("SKMETAL_HIP_F16");
+    if (env != nullptr && env[0] == '0') return 0;
+    if (d < 17 || k < 1) return 0;
+    for (const bool scaled : {false, true}) {
+        assign16_fn f = assign16_kernel(k, scaled);
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(f), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)assign16_lds(k)) != hipSuccess) {
+            (void)hipGetLastError();
+            return 0;
+        }
+    }
+    return 1;
+}
+
+hipError_t launch_assign16(const AssignArgs& a, float xscale, float dscale, int num_cu, hipStream_t s)
+{
+    if (a.n <= 0) return hipSuccess;
+    assign16_fn f = assign16_kernel(a.k, xscale != 1.f);
+    long blocks = (a.n + 255) / 256;
+    if (blocks > num_cu) blocks = num_cu;
+    hipLaunchKernelGGL(f, dim3((unsigned)blocks), dim3(512), assign16_lds(a.k), s, a.X, a.n, a.ld, a.C, a.cnorm, a.k,
+                       a.labels, a.state, a.changed, xscale, dscale);
+    return hipGetLastError();
+}
+
 typedef void (*fused_fn)(FusedArgs);
 
 template <int NQ, int... KGs>

@@ -46,6 +46,11 @@ struct AssignArgs {
     int* changed;          // nullable: compare with previous labels, add the changes here
 };
 hipError_t launch_assign(const AssignArgs& a, int num_cu, hipStream_t s);
+// The same E-step on fp16 MFMA with x and c split in two scaled fp16 parts
+// (xscale = 2^s, dscale = -2 * 2^-2s); assign16_ready(d, k) = 1 when it
+// applies to the shape (sets its LDS attribute).
+int assign16_ready(int d, int k);
+hipError_t launch_assign16(const AssignArgs& a, float xscale, float dscale, int num_cu, hipStream_t s);
 
 // Fused E-step + per-cluster sums (k <= 64, d <= 100).
 struct FusedArgs {

@@ -282,6 +282,8 @@ struct Lloyd {
     // coordinates
     int f16cap = 0;
     bool f16_on = false;
+    int a16cap = 0;         // the fp16-split E-step of the separate assign kernel
+    bool a16_on = false;
     float xmax = 0.f, cmax = 0.f, xscale = 1.f, dscale = -2.f;
     unsigned* absmax = nullptr;
     int cur = 0;            // index of the current centres in cen[]
@@ -308,6 +310,7 @@ struct Lloyd {
         ug = update_geometry(n, d, k, C->num_cu);
         fblocks = lf > 0 ? fused_blocks(n, ld, k, C->num_cu) : 0;
         f16cap = fblocks > 0 ? fused16_ready(k, ld) : 0;
+        a16cap = assign16_ready(d, k);
         if (fblocks == 0) sg = sort_geometry(n, d, ld, k);
         const int Rmax = sg.on ? 1 : std::max(ug.R, fblocks);
         const int chunks = std::max({finalize_col_chunks(d, ug.R), fblocks > 0 ? finalize_col_chunks(d, fblocks) : 0,
@@ -379,7 +382,7 @@ struct Lloyd {
             std::fill(h_mean.begin(), h_mean.end(), 0.f);
             HIP_TRY(hipMemsetAsync(mean, 0, size_t(ld) * sizeof(float), s), "hipMemsetAsync");
         }
-        if (f16cap) {
+        if (f16cap || a16cap) {
             unsigned bits = 0;
             HIP_TRY(launch_absmax(X, n * (long)ld, absmax, s), "absmax launch");
             TRY(download_bytes(*C, absmax, sizeof(unsigned), &bits, s));
@@ -403,7 +406,9 @@ struct Lloyd {
         int e = 0;
         if (m > 0.f && std::isfinite(m)) std::frexp(m, &e);  // m = f 2^e, f in [0.5, 1)
         const int sh = m > 0.f && (e > 14 || e < -2) ? 14 - e : 0;
-        f16_on = f16cap != 0 && std::isfinite(m) && sh >= -60 && sh <= 60;
+        const bool ok = std::isfinite(m) && sh >= -60 && sh <= 60;
+        f16_on = f16cap != 0 && ok;
+        a16_on = a16cap != 0 && ok;
         xscale = std::ldexp(1.f, sh);
         dscale = -std::ldexp(1.f, 1 - 2 * sh);
     }
@@ -411,7 +416,7 @@ struct Lloyd {
     // Centres given in caller coordinates -> device (centred like X).
     int set_centers(const float* host)
     {
-        if (f16cap) {
+        if (f16cap || a16cap) {
             double m = 0.0;
             for (int j = 0; j < k; ++j)
                 for (int c = 0; c < d; ++c) {
@@ -455,7 +460,10 @@ struct Lloyd {
     int assign(const float* cents, LoopState* state, int* changed)
     {
         AssignArgs a{X, n, ld, cents, cnorm, k, labels, state, changed};
-        HIP_TRY(launch_assign(a, C->num_cu, s), "assign launch");
+        if (a16_on)
+            HIP_TRY(launch_assign16(a, xscale, dscale, C->num_cu, s), "assign launch");
+        else
+            HIP_TRY(launch_assign(a, C->num_cu, s), "assign launch");
         return 0;
     }
 
@@ -1032,7 +1040,7 @@ int skmetal_hip_lloyd_run(skmetal_hip_lloyd* h, size_t max_iter, double tol, int
 int skmetal_hip_lloyd_info(skmetal_hip_lloyd* h, int* fused, int* partials)
 {
     if (!h) return fail(SKMETAL_EINVAL, "null pointer argument");
-    if (fused) *fused = h->L.fblocks > 0 ? (h->L.f16_on ? 2 : 1) : 0;
+    if (fused) *fused = (h->L.fblocks > 0 ? (h->L.f16_on ? 2 : 1) : 0) | (h->L.a16_on ? 4 : 0);
     if (partials) *partials = h->L.fblocks > 0 ? h->L.fblocks : h->L.sg.on ? (int)h->L.sg.nchunks : h->L.ug.R;
     return 0;
 }

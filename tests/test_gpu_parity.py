@@ -59,7 +59,7 @@ def test_known_answer_assign(bridge):
 ASSIGN_SHAPES = [
     (1, 1, 1), (2, 3, 2), (63, 7, 5), (64, 4, 4), (65, 33, 9), (257, 2, 64), (1000, 32, 8),
     (3001, 100, 50), (2048, 16, 65), (999, 20, 200), (4096, 129, 17), (1500, 300, 70),
-    (700, 5, 1024), (513, 768, 96),
+    (700, 5, 1024), (513, 768, 96), (3000, 257, 530), (1000, 1000, 300),
 ]
 
 
@@ -184,13 +184,24 @@ def test_f16_switched_off_by_env(bridge, monkeypatch):
     _lockstep_gpu(bridge, X, C0, 2, what="fp32 E-step")
 
 
+@pytest.mark.parametrize("n,d,k", [(5000, 40, 100), (3000, 130, 300)])
+def test_a16_generic_path_lockstep(bridge, n, d, k):
+    """k > 64: the separate E-step on fp16 MFMA (several centre passes and
+    feature segments) with the sorted update, step by step against the oracle."""
+    _say(f"a16 lockstep n={n} d={d} k={k}")
+    X, C0 = _blob_problem(n, d, k, seed=n + k)
+    info = _f16_engaged(bridge, X, C0)
+    assert not info["fused"] and info["a16"], info
+    _lockstep_gpu(bridge, X, C0, 2, what=f"a16 {n}x{d} k={k}")
+
+
 def test_f16_off_for_non_finite_data(bridge):
     X, C0 = _blob_problem(3000, 40, 8, seed=3)
     X[17, 5] = np.inf
     with bridge.LloydHandle(3000, 40, 8) as h:
         h.load(X, center=False)
         h.set_centers(C0)
-        assert not h.info()["f16"]
+        assert not h.info()["f16"] and not h.info()["a16"]
 
 
 def _golden_names():
