@@ -1,15 +1,22 @@
 // fused_kernels.hip -- one-pass Lloyd step for small k*d on gfx950 (MI355X):
 // the E-step (sklearn/cluster/_k_means_lloyd.pyx:196-212) and the
 // per-cluster sums and counts of the M-step (:214-218) in one kernel that
-// reads X from HBM once per step.
+// reads X from HBM once per step, plus the fp16-split E-step for any k.
 //
-// Used when k <= 64 and d <= 100; X's row stride ld is then padded (with
-// zeros) to 4*NQ floats for one of the compiled NQ, so the kernel's loops over
-// the row's float4s have no bounds.  The separate assign / update kernels
-// cover every other shape.
+//   k_fused16   E-step on fp16 MFMA (x and c split in two scaled fp16 parts),
+//               per-cluster sums on fp16 MFMA (one-hot x the same parts);
+//               12 waves per block (d >= 17).
+//   k_fused     E-step on fp32 MFMA, per-cluster sums by a VALU walker; 8
+//               waves per block (d <= 16, non-finite data, or the fp32 switch).
+//   k_assign16  E-step alone for any k on fp16 MFMA (the generic path).
 //
-// Built without -amdgpu-mfma-vgpr-form: the MFMA accumulators live in AGPRs,
-// next to the VGPRs that hold the tile's rows.
+// The fused kernels are used when k <= 64 and d <= 100; X's row stride ld is
+// then padded (with zeros) to 4*NQ floats for one of the compiled NQ, so the
+// kernels' loops over the row's float4s have no bounds.  The separate assign
+// / update kernels cover every other shape.
+//
+// Built without -amdgpu-mfma-vgpr-form (the register allocator places the
+// MFMA accumulators).
 #include <math.h>
 #include <stdlib.h>
 
@@ -522,86 +529,16 @@ __device__ __forceinline__ void split8(float4 u, float4 v, float sc, v8h& hi, v8
     lo = __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-// The M-step wave of a k_fused16 pair: the per-cluster sums of each ready
-// tile as onehot^T x on v_mfma_f32_16x16x32_f16, x in the same two fp16
-// parts as the E-step (x 2^s = hi + lo up to 2^-22 |x 2^s|; the one-hot
-// operand is exact, so every product is exact in the fp32 accumulators).
-// A = onehot (16 clusters of block cb x 32 rows of K block kb: lane l holds
-// rows 32kb + 8(l/16) + j for cluster 16cb + l%16), B = x (the same rows x 16
-// features of block fb, read transposed from the LDS tile: lane l holds
-// feature 16fb + l%16), D lane l: clusters 16cb + 4(l/16) + i, feature 16fb +
-// l%16.  Progress is published per 16-feature block (all rows read).
-template <int CB, int NQ, int XS, int NFB, bool SC>
-__device__ __forceinline__ void msum_tiles(v4f (&S)[CB][NFB], int rounds, int lane, int* ready, int* prog,
-                                           const int* lab, const float* tile, float sc)
-{
-    const int h = lane >> 4, r16 = lane & 15;
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-#pragma unroll
-        for (int fb = 0; fb < NFB; ++fb) S[cb][fb] = v4f{0.f, 0.f, 0.f, 0.f};
-    }
-    const _Float16 one = (_Float16)1.0f, zero = (_Float16)0.0f;
-    for (int r = 0; r < rounds; ++r) {
-        wait_flag(ready, r + 1);
-        // one-hot operands of both K blocks (labels of past-the-end rows are -1)
-        v8h A[2][CB];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            const int4 l0 = *reinterpret_cast<const int4*>(lab + 32 * kb + 8 * h);
-            const int4 l1 = *reinterpret_cast<const int4*>(lab + 32 * kb + 8 * h + 4);
-            const int lj[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
-#pragma unroll
-            for (int cb = 0; cb < CB; ++cb) {
-                const int c = 16 * cb + r16;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) A[kb][cb][j] = lj[j] == c ? one : zero;
-            }
-        }
-        // the 16 values (2 K blocks x 8 rows) of feature block fb; the next
-        // block's reads are in flight while this block's MFMAs run
-        const float* col = tile + 8 * h * XS + r16;
-        auto fetch = [&](float (&v)[16], int fb) {
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) v[8 * kb + j] = col[(32 * kb + j) * XS + 16 * fb];
-            }
-        };
-        float cur[16], nxt[16];
-        fetch(cur, 0);
-#pragma unroll
-        for (int fb = 0; fb < NFB; ++fb) {
-            if (fb + 1 < NFB) fetch(nxt, fb + 1);
-            // columns of feature block fb have been read for every row (LDS
-            // performs this wave's reads above before this flag)
-            set_flag(prog, r * NQ + (4 * fb + 4 < NQ ? 4 * fb + 4 : NQ));
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                v8h bh, bl;
-                split8<SC>(make_float4(cur[8 * kb], cur[8 * kb + 1], cur[8 * kb + 2], cur[8 * kb + 3]),
-                           make_float4(cur[8 * kb + 4], cur[8 * kb + 5], cur[8 * kb + 6], cur[8 * kb + 7]), sc, bh, bl);
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb) {
-                    S[cb][fb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[kb][cb], bh, S[cb][fb], 0, 0, 0);
-                    S[cb][fb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[kb][cb], bl, S[cb][fb], 0, 0, 0);
-                }
-            }
-            if (fb + 1 < NFB) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) cur[i] = nxt[i];
-            }
-        }
-    }
-}
-
 // The sums wave of SIMD m in k_fused16 serves E-step waves m and m + 4 (the
 // same SIMD), taking their 32-row tiles in turn: round r of wave m, then round
-// r of wave m + 4.  Per tile: A = one-hot (16 clusters x the tile's 32 rows:
-// lane l holds rows 8(l/16) + j for cluster 16cb + l%16), B = x (the 32 rows x
-// 16 features of block fb, read transposed from the LDS tile), both exact or
-// split as in the E-step; D lane l: clusters 16cb + 4(l/16) + i, feature 16fb +
-// l%16.  Progress is published per 16-feature block (all rows read).
+// r of wave m + 4.  The per-cluster sums of a tile are onehot^T x on
+// v_mfma_f32_16x16x32_f16 with x in the E-step's two fp16 parts (x 2^s = hi +
+// lo up to 2^-22 |x 2^s|); the one-hot operand is exact, so every product is
+// exact in the fp32 accumulators.  A = one-hot (16 clusters x the tile's 32
+// rows: lane l holds rows 8(l/16) + j for cluster 16cb + l%16), B = x (the 32
+// rows x 16 features of block fb, read transposed from the LDS tile); D lane
+// l: clusters 16cb + 4(l/16) + i, feature 16fb + l%16.  Progress is published
+// per 16-feature block (all rows read).
 template <int CB, int NQ, int XS, int NFB, bool SC>
 __device__ __forceinline__ void msum_tiles2(v4f (&S)[CB][NFB], int rounds0, int rounds1, int* ready0, int* ready1,
                                             int* prog0, int* prog1, const int* lab0, const int* lab1,
