@@ -173,7 +173,7 @@ __device__ __forceinline__ void step_norms(const FusedArgs& a, int lane, float* 
             done = 3;
         else if ((a.flags & kStopStrict) && chg == 0)
             done = 1;
-        else if (a.tol > 0.0 && tot <= a.tol)
+        else if (a.tol >= 0.0 && tot <= a.tol)  // tol < 0: no shift rule (fixed iterations)
             done = 2;
         if (blockIdx.x == 0) {
             LoopState* st = a.state;

@@ -778,7 +778,7 @@ __global__ __launch_bounds__(256) void k_finalize_loop(FinalizeArgs a, int nch)
             done = 3;
         else if ((a.flags & kStopStrict) && changed == 0)
             done = 1;
-        else if (a.tol > 0.0 && tot <= a.tol)
+        else if (a.tol >= 0.0 && tot <= a.tol)  // tol < 0: no shift rule (fixed iterations)
             done = 2;
         if (done != 0) st->halt_iter = a.iter;
         st->done = done;

@@ -645,7 +645,7 @@ struct Lloyd {
         int done = 0;
         if ((flags & kStopStrict) && hs.last_changed == 0)
             done = 1;
-        else if (tol > 0.0 && shift_tot <= tol)
+        else if (tol >= 0.0 && shift_tot <= tol)
             done = 2;
         hs.done = done;
         hs.n_iter = t + 1;
@@ -663,7 +663,7 @@ struct Lloyd {
     {
         if (fixed) {
             flags &= ~kStopStrict;
-            tol = 0.0;
+            tol = -1.0;  // no shift rule: sklearn's `shift <= tol` stops at tol = 0 on a zero shift
         }
         LoopState hs{};
         TRY(write_state(hs));

@@ -166,6 +166,24 @@ def test_f16_estep_lockstep(bridge, n, d, k):
     _lockstep_gpu(bridge, X, C0, 3, what=f"f16 {n}x{d} k={k}")
 
 
+@pytest.mark.parametrize("n,k", [(1, 1), (5, 3), (31, 4), (33, 7), (100, 20), (257, 64)])
+def test_f16_tiny_problems(bridge, n, k):
+    """Partial 32-row tiles and waves with no tile at all (most of the grid)."""
+    _say(f"f16 tiny n={n} k={k}")
+    rng = np.random.default_rng(n * 7 + k)
+    X = (rng.standard_normal((n, 40)) * 3).astype(np.float32)
+    C0 = X[np.sort(rng.choice(n, k, replace=False))].copy()
+    info = _f16_engaged(bridge, X, C0)
+    assert info["fused"] and info["f16"], info
+    _lockstep_gpu(bridge, X, C0, 2, what=f"f16 tiny {n} k={k}")
+    C = C0.copy()
+    lab = np.empty(n, np.int32)
+    n_iter, _ = bridge.kmeans_fit(X, C, lab, 50, 0.0, strict=True)
+    out = oracle.lloyd(X, C0, 50)
+    assert n_iter == out["n_iter"]
+    parity.check_centers(C, out["centers"], what=f"tiny fit n={n} k={k}")
+
+
 @pytest.mark.parametrize("scale", [1e-15, 1e-3, 1e4, 1e15])
 def test_f16_estep_scaled_data(bridge, scale):
     """The 2^s scaling keeps the fp16 parts in range for any data magnitude."""
