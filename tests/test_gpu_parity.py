@@ -184,6 +184,30 @@ def test_f16_tiny_problems(bridge, n, k):
     parity.check_centers(C, out["centers"], what=f"tiny fit n={n} k={k}")
 
 
+def test_f16_assign_duplicate_centres_lowest_index(bridge):
+    """Identical centres give identical fp16-split distances: the lowest index wins."""
+    rng = np.random.default_rng(11)
+    X = rng.standard_normal((3000, 40)).astype(np.float32)
+    base = rng.standard_normal((7, 40)).astype(np.float32)
+    C = np.concatenate([base, base, base])
+    out = np.empty(3000, np.int32)
+    bridge.kmeans_assign(X, C, out, 3000, 40, 21)
+    ref, best, second = oracle.assign(X, C, return_gap=True)
+    assert out.max() < 7
+    parity.check_labels(out, ref, best, second, X, what="f16 duplicate centres")
+
+
+@pytest.mark.parametrize("n,d,k", [(3000, 101, 10), (40, 20, 40), (2000, 17, 64)])
+def test_f16_edge_shapes_lockstep(bridge, n, d, k):
+    """d just past the fused limit (generic path with k <= 64), k = n, the
+    smallest fp16 row stride with 64 centres."""
+    _say(f"f16 edge n={n} d={d} k={k}")
+    X, C0 = _blob_problem(n, d, k, seed=3 * n + d)
+    info = _f16_engaged(bridge, X, C0)
+    assert info["f16"] or info["a16"], info
+    _lockstep_gpu(bridge, X, C0, 2, what=f"f16 edge {n}x{d} k={k}")
+
+
 @pytest.mark.parametrize("scale", [1e-15, 1e-3, 1e4, 1e15])
 def test_f16_estep_scaled_data(bridge, scale):
     """The 2^s scaling keeps the fp16 parts in range for any data magnitude."""
