@@ -75,7 +75,8 @@ def build(verbose: bool = False) -> Path:
                                "-o", obj], verbose))
         for p in procs:
             _finish(p, verbose)
-        _finish(_run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)], verbose), verbose)
+        _finish(_run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", *objs, "-o", str(tmp)], verbose),
+                verbose)
     os.replace(tmp, LIB)
     return LIB
 

@@ -21,6 +21,7 @@
 #include <mutex>
 #include <numeric>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "skmetal_hip.h"
@@ -165,6 +166,39 @@ Context& ctx()
 
 // Host -> device copy of `rows` rows of `cols` floats into rows of stride
 // `ld` floats (pad columns zeroed), through the two pinned staging buffers.
+// Host rows [0, m) of `cols` floats into the pinned staging buffer with
+// stride ld (pad columns zeroed), split over up to 8 host threads for large
+// chunks: one thread's memcpy runs at a fraction of the host's memory
+// bandwidth, which would otherwise bound the upload.
+static void stage_rows(float* p, const float* src, long m, int cols, int ld)
+{
+    auto part = [&](long r0, long r1) {
+        if (ld == cols) {
+            std::memcpy(p + r0 * ld, src + r0 * cols, size_t(r1 - r0) * size_t(ld) * sizeof(float));
+        } else {
+            for (long i = r0; i < r1; ++i) {
+                std::memcpy(p + i * ld, src + i * cols, size_t(cols) * sizeof(float));
+                std::memset(p + i * ld + cols, 0, size_t(ld - cols) * sizeof(float));
+            }
+        }
+    };
+    const size_t bytes = size_t(m) * size_t(ld) * sizeof(float);
+    unsigned nt = std::thread::hardware_concurrency();
+    nt = nt < 1 ? 1 : nt > 8 ? 8 : nt;
+    if (bytes < (size_t(4) << 20) || nt == 1) {
+        part(0, m);
+        return;
+    }
+    std::vector<std::thread> th;
+    const long per = (m + nt - 1) / nt;
+    for (unsigned t = 1; t < nt; ++t) {
+        const long r0 = t * per, r1 = std::min<long>(m, r0 + per);
+        if (r0 < r1) th.emplace_back(part, r0, r1);
+    }
+    part(0, std::min<long>(m, per));
+    for (auto& x : th) x.join();
+}
+
 int upload_rows(Context& C, const float* src, long rows, int cols, int ld, float* dst, hipStream_t s)
 {
     const size_t row_bytes = size_t(ld) * sizeof(float);
@@ -175,14 +209,7 @@ int upload_rows(Context& C, const float* src, long rows, int cols, int ld, float
         const long m = std::min(chunk, rows - r);
         HIP_TRY(hipEventSynchronize(C.pin_ev[b]), "hipEventSynchronize(staging)");
         float* p = static_cast<float*>(C.pin[b]);
-        if (ld == cols) {
-            std::memcpy(p, src + r * cols, size_t(m) * row_bytes);
-        } else {
-            for (long i = 0; i < m; ++i) {
-                std::memcpy(p + i * ld, src + (r + i) * cols, size_t(cols) * sizeof(float));
-                std::memset(p + i * ld + cols, 0, size_t(ld - cols) * sizeof(float));
-            }
-        }
+        stage_rows(p, src + r * cols, m, cols, ld);
         HIP_TRY(hipMemcpyAsync(dst + r * ld, p, size_t(m) * row_bytes, hipMemcpyHostToDevice, s), "hipMemcpyAsync(H2D)");
         HIP_TRY(hipEventRecord(C.pin_ev[b], s), "hipEventRecord");
     }
