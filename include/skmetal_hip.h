@@ -130,6 +130,25 @@ SKMETAL_API int skmetal_hip_lloyd_iterate(skmetal_hip_lloyd* h, size_t iters, fl
  * including the final E-step and inertia. */
 SKMETAL_API int skmetal_hip_lloyd_run(skmetal_hip_lloyd* h, size_t max_iter, double tol, int flags,
                           int32_t* n_iter_out, double* inertia_out);
+/* Greedy k-means++ seeding of the handle's centres from the loaded X
+ * (centred if it was loaded with center != 0, as scikit-learn's fit seeds on
+ * centred X): scikit-learn's _kmeans_plusplus with unit sample weights
+ * (sklearn/cluster/_kmeans.py:174-260), the random numbers drawn by the
+ * caller in scikit-learn's order: first_index = the first centre's row
+ * (RandomState.choice(n, p=w / w.sum()), :230), uniforms = the
+ * (k - 1) x n_local_trials values of the k - 1 calls
+ * RandomState.uniform(size=n_local_trials) (:243), row-major.  The k chosen
+ * rows become the current centres and their indices go to indices_out [k].
+ * n_local_trials in [1, 64]; scikit-learn's default is 2 + int(ln k).
+ * No counterpart in the reference (skmetal seeded with k-means|| on the host,
+ * skmetal/estimators/cluster.py:70-116); this replaces the scikit-learn
+ * seeding the estimator would otherwise run on the CPU. */
+SKMETAL_API int skmetal_hip_lloyd_plusplus(skmetal_hip_lloyd* h, size_t n_local_trials, int64_t first_index,
+                                           const double* uniforms, int64_t* indices_out);
+/* The same seeding on X [n x d] as given (no centring), like
+ * sklearn.cluster.kmeans_plusplus: indices_out [k] receives the chosen rows. */
+SKMETAL_API int skmetal_hip_kmeans_plusplus(const float* X, size_t n, size_t d, size_t k, size_t n_local_trials,
+                                            int64_t first_index, const double* uniforms, int64_t* indices_out);
 /* *fused & 3 = 0 when a step runs as separate E-step and update kernels, 1
  * when as one fused E-step + sums kernel with the E-step on fp32 MFMA
  * (k <= 64, d <= 100), 2 when that kernel's E-step runs on fp16 MFMA with x

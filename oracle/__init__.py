@@ -255,3 +255,62 @@ def numpy_lloyd(X, C_init, max_iter: int, tol_abs: float = 0.0):
         labels = np.argmin(D, axis=1).astype(np.int32)
     inert = float(((Xd - Cd[labels]) ** 2).sum())
     return dict(centers=(C + mean).astype(np.float32), labels=labels, inertia=inert, n_iter=n_iter)
+
+
+def _upcast_sqdist(Xc, rows, X64=None, xx=None):
+    """sklearn/metrics/pairwise.py:391-446,582-640 (_euclidean_distances with
+    fp32 data -> _euclidean_distances_upcast): fp64 -2 c.x + ||c||^2 + ||x||^2 of
+    the candidate rows against every row, cast to fp32, negatives set to 0."""
+    if X64 is None:
+        X64 = Xc.astype(np.float64)
+        xx = np.einsum("ij,ij->i", X64, X64)
+    C64 = X64[rows]
+    cc = xx[rows]
+    d = -2.0 * (C64 @ X64.T)
+    d += cc[:, None]
+    d += xx[None, :]
+    d = d.astype(np.float32)
+    np.maximum(d, 0, out=d)
+    return d
+
+
+def kmeans_plusplus(X, k: int, first: int, uniforms, n_local_trials: int, trace: bool = False):
+    """Greedy k-means++ with the random draws given: sklearn/cluster/_kmeans.py:174-263
+    (_kmeans_plusplus), unit sample weights.
+
+    first    -- the first centre's row (random_state.choice, :225)
+    uniforms -- [(k-1) x n_local_trials] values of random_state.uniform (:243)
+
+    Reductions are exact in fp64 (sequential cumsum as stable_cumsum, :244-246;
+    potentials as fp64 sums of the fp32 minima, where scikit-learn uses an fp32
+    BLAS dot product, :236,257), and the potential enters the draws rounded to
+    fp32 as scikit-learn's fp32 current_pot does (:243).  Returns the k row
+    indices (and, with trace, each centre's candidate rows and potentials)."""
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    n = X.shape[0]
+    T = int(n_local_trials)
+    U = np.asarray(uniforms, dtype=np.float64).reshape(max(k - 1, 0), T)
+    idx = np.empty(k, np.int64)
+    idx[0] = first
+    X64 = X.astype(np.float64)
+    xx = np.einsum("ij,ij->i", X64, X64)
+    closest = _upcast_sqdist(X, np.array([first]), X64, xx)[0]         # :234-236
+    pot = float(np.sum(closest.astype(np.float64)))                    # :237
+    cands, pots = [np.array([first])], [np.array([pot])]
+    for c in range(1, k):
+        r = U[c - 1] * float(np.float32(pot))                          # :243
+        cum = np.cumsum(closest, dtype=np.float64)                     # :244-246 stable_cumsum
+        cid = np.searchsorted(cum, r)                                  # side='left'
+        np.clip(cid, None, n - 1, out=cid)                             # :248
+        dist = _upcast_sqdist(X, cid, X64, xx)                         # :251-253
+        np.minimum(closest[None, :], dist, out=dist)                   # :256
+        cpot = dist.astype(np.float64).sum(axis=1)                     # :257
+        b = int(np.argmin(cpot))                                       # :260 first minimum
+        pot = float(cpot[b])
+        closest = dist[b]
+        idx[c] = cid[b]
+        cands.append(cid)
+        pots.append(cpot)
+    if trace:
+        return idx, cands, pots
+    return idx

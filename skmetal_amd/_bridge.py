@@ -61,6 +61,8 @@ _REGISTRY = [
     ("skmetal_hip_lloyd_get_centers", ctypes.c_int, _vp, _vp),
     ("skmetal_hip_lloyd_get_labels", ctypes.c_int, _vp, _vp),
     ("skmetal_hip_lloyd_inertia", ctypes.c_int, _vp, ctypes.POINTER(ctypes.c_double)),
+    ("skmetal_hip_lloyd_plusplus", ctypes.c_int, _vp, _c_size, ctypes.c_int64, _vp, _vp),
+    ("skmetal_hip_kmeans_plusplus", ctypes.c_int, _vp, _c_size, _c_size, _c_size, _c_size, ctypes.c_int64, _vp, _vp),
 ]
 
 SKMETAL_FIT_STRICT = 1
@@ -217,6 +219,34 @@ def kmeans_fit(X, centroids, labels, max_iter, tol_abs, strict=True):
     return int(n_iter.value), float(inertia.value)
 
 
+def plusplus_draws(random_state, n: int, k: int, n_local_trials: int | None = None, dtype=np.float32):
+    """The random numbers scikit-learn's k-means++ takes from `random_state`, in its
+    order (sklearn/cluster/_kmeans.py:225-243, unit sample weights of X's dtype):
+    the first centre's row, ``choice(n, p=w / w.sum())``, then
+    ``uniform(size=n_local_trials)`` for each further centre.  Drawing the k - 1
+    uniform vectors at once consumes the generator exactly as k - 1 separate
+    calls do.  Returns (n_local_trials, first_index, uniforms [(k-1) x T] float64)."""
+    if n_local_trials is None:
+        n_local_trials = 2 + int(np.log(k))
+    w = np.ones(n, dtype=dtype)
+    first = int(random_state.choice(n, p=w / w.sum()))
+    u = np.ascontiguousarray(random_state.uniform(size=(k - 1) * n_local_trials), dtype=np.float64)
+    return int(n_local_trials), first, u.reshape(k - 1, n_local_trials)
+
+
+def kmeans_plusplus(X, n_clusters: int, random_state, n_local_trials: int | None = None):
+    """k-means++ seeding of X (as given) on the GPU with scikit-learn's draws:
+    returns (centers, indices) like sklearn.cluster.kmeans_plusplus (unit weights)."""
+    _f32c(X, "X")
+    ensure_warmed_up()
+    n, d = X.shape
+    T, first, u = plusplus_draws(random_state, n, n_clusters, n_local_trials, X.dtype)
+    idx = np.empty(n_clusters, np.int64)
+    _check(_lib.skmetal_hip_kmeans_plusplus(X.ctypes.data, n, d, n_clusters, T, first, u.ctypes.data,
+                                            idx.ctypes.data), "skmetal_hip_kmeans_plusplus")
+    return X[idx], idx
+
+
 class LloydHandle:
     """Device-resident Lloyd problem (X uploaded once, kept in HBM)."""
 
@@ -273,6 +303,21 @@ class LloydHandle:
                                           SKMETAL_FIT_STRICT if strict else 0, ctypes.byref(n_iter),
                                           ctypes.byref(inertia)), "skmetal_hip_lloyd_run")
         return int(n_iter.value), float(inertia.value)
+
+    def plusplus(self, random_state, n_local_trials: int | None = None):
+        """Seed the centres with k-means++ on the loaded X, drawing from
+        `random_state` as scikit-learn does; returns the chosen row indices."""
+        T, first, u = plusplus_draws(random_state, self.n, self.k, n_local_trials)
+        return self.plusplus_with(T, first, u)
+
+    def plusplus_with(self, n_local_trials: int, first: int, uniforms):
+        """k-means++ with given draws (first row, (k-1) x n_local_trials uniforms)."""
+        u = np.ascontiguousarray(uniforms, dtype=np.float64)
+        assert u.size == (self.k - 1) * n_local_trials
+        idx = np.empty(self.k, np.int64)
+        _check(_lib.skmetal_hip_lloyd_plusplus(self._h, int(n_local_trials), int(first), u.ctypes.data,
+                                               idx.ctypes.data), "skmetal_hip_lloyd_plusplus")
+        return idx
 
     def info(self):
         fused = ctypes.c_int(0)

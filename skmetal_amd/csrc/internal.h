@@ -190,6 +190,32 @@ struct RelocArgs {
 // E = number of empty clusters (1 <= E <= kMaxReloc).
 hipError_t launch_relocate(const RelocArgs& a, int E, hipStream_t s);
 
+// Greedy k-means++ seeding (plusplus_kernels.hip): sklearn's _kmeans_plusplus
+// with unit weights and the random draws made by the caller.
+constexpr int kPPRows = 256;        // rows per k_pp_dist block (one per thread)
+constexpr int kPPMaxTrials = 64;    // largest n_local_trials
+struct PPArgs {
+    const float* X; long n; int ld;
+    int k;
+    int T;                 // n_local_trials (candidates per centre after the first)
+    int nb;                // k_pp_dist blocks = ceil(n / kPPRows)
+    double* xx;            // [n] fp64 ||x_i||^2
+    float* D[2];           // [T x n] min(closest, distance to candidate t), by centre parity
+    double* P[2];          // [T x nb] per-block fp64 sums of D[.][t]
+    double* pfx;           // [nb] inclusive prefix of the chosen candidate's block sums
+    long* cand;            // [T] candidate rows of the centre being drawn (cand[0] = first row at start)
+    long* idx;             // [k] chosen rows
+    int* best;             // [k] chosen candidate of each centre
+    double* pot;           // [k] potential after each centre (fp64 total)
+    const double* U;       // [(k - 1) x T] uniforms in [0, 1), in sklearn's draw order
+    float* centers;        // [k x ld] the chosen rows of X
+};
+hipError_t launch_pp_norms(const PPArgs& a, hipStream_t s);
+// Candidate distances of centre c (c = 0: the first row alone).
+hipError_t launch_pp_dist(const PPArgs& a, int c, hipStream_t s);
+// Pick centre c - 1 among its candidates; for c < k draw centre c's candidates.
+hipError_t launch_pp_select(const PPArgs& a, int c, hipStream_t s);
+
 hipError_t launch_colsum(const float* X, long n, int ld, int d, double* part, int nblk, hipStream_t s);
 int colsum_grid(long n);
 hipError_t launch_colmean(const double* part, int nblk, long n, int d, float* mean, hipStream_t s);

@@ -391,6 +391,7 @@ struct Lloyd {
         if (s) hipStreamSynchronize(s);
         for (void* p : owned) C->release(p);
         owned.clear();
+        pp_release();
         for (hipEvent_t e : kev) hipEventDestroy(e);
         kev.clear();
     }
@@ -746,6 +747,75 @@ struct Lloyd {
         return 0;
     }
 
+    // Greedy k-means++ on the resident X (sklearn's _kmeans_plusplus,
+    // _kmeans.py:174-260, unit weights): T candidates per centre after the
+    // first, first = the first centre's row, U = the (k - 1) x T uniforms in
+    // draw order.  The chosen rows become the current centres; idx_out
+    // receives their row indices.  Buffers are kept for further calls.
+    PPArgs pp{};
+    std::vector<void*> pp_owned;
+    int pp_T = 0;
+
+    int pp_grab(void** p, size_t bytes)
+    {
+        TRY(C->alloc(p, bytes));
+        pp_owned.push_back(*p);
+        return 0;
+    }
+
+    void pp_release()
+    {
+        for (void* p : pp_owned) C->release(p);
+        pp_owned.clear();
+        pp_T = 0;
+    }
+
+    int plusplus(int T, long first, const double* U, long* idx_out)
+    {
+        if (T < 1 || T > kPPMaxTrials) return fail(SKMETAL_ERANGE, "n_local_trials=%d not in [1, %d]", T, kPPMaxTrials);
+        if (first < 0 || first >= n) return fail(SKMETAL_EINVAL, "first index %ld not in [0, %ld)", first, n);
+        if (k > 1 && U == nullptr) return fail(SKMETAL_EINVAL, "null uniforms");
+        const int nb = (int)((n + kPPRows - 1) / kPPRows);
+        if (T != pp_T) {
+            pp_release();
+            TRY(pp_grab((void**)&pp.xx, size_t(n) * sizeof(double)));
+            for (int i = 0; i < 2; ++i) {
+                TRY(pp_grab((void**)&pp.D[i], size_t(T) * n * sizeof(float)));
+                TRY(pp_grab((void**)&pp.P[i], size_t(T) * nb * sizeof(double)));
+            }
+            TRY(pp_grab((void**)&pp.pfx, size_t(nb) * sizeof(double)));
+            TRY(pp_grab((void**)&pp.cand, size_t(T) * sizeof(long)));
+            TRY(pp_grab((void**)&pp.idx, size_t(k) * sizeof(long)));
+            TRY(pp_grab((void**)&pp.best, size_t(k) * sizeof(int)));
+            TRY(pp_grab((void**)&pp.pot, size_t(k) * sizeof(double)));
+            TRY(pp_grab((void**)&pp.U, std::max<size_t>(1, size_t(k - 1) * T) * sizeof(double)));
+            pp_T = T;
+        }
+        pp.X = X;
+        pp.n = n;
+        pp.ld = ld;
+        pp.k = k;
+        pp.T = T;
+        pp.nb = nb;
+        pp.centers = cen[cur];
+        TRY(upload_bytes(*C, &first, sizeof(long), pp.cand, s));
+        if (k > 1) TRY(upload_bytes(*C, U, size_t(k - 1) * T * sizeof(double), const_cast<double*>(pp.U), s));
+        HIP_TRY(launch_pp_norms(pp, s), "pp norms launch");
+        HIP_TRY(launch_pp_dist(pp, 0, s), "pp dist launch");
+        for (int c = 1; c < k; ++c) {
+            HIP_TRY(launch_pp_select(pp, c, s), "pp select launch");
+            HIP_TRY(launch_pp_dist(pp, c, s), "pp dist launch");
+        }
+        HIP_TRY(launch_pp_select(pp, k, s), "pp select launch");
+        HIP_TRY(launch_cnorm(cen[cur], k, ld, cnorm, s), "cnorm launch");
+        if (f16cap || a16cap) {
+            cmax = xmax;  // the centres are rows of X
+            update_scale();
+        }
+        TRY(download_bytes(*C, pp.idx, size_t(k) * sizeof(long), idx_out, s));
+        return 0;
+    }
+
     // Full sklearn fit from the current centres: loop, final E-step, inertia.
     int fit(long max_iter, double tol, int flags, int* n_iter_out, double* inertia_out)
     {
@@ -1061,6 +1131,37 @@ int skmetal_hip_lloyd_run(skmetal_hip_lloyd* h, size_t max_iter, double tol, int
     TRY(h->L.fit((long)max_iter, tol, flags & SKMETAL_FIT_STRICT ? kStopStrict : 0, &it, &in));
     if (n_iter_out) *n_iter_out = it;
     if (inertia_out) *inertia_out = in;
+    return 0;
+}
+
+int skmetal_hip_lloyd_plusplus(skmetal_hip_lloyd* h, size_t n_local_trials, int64_t first_index,
+                               const double* uniforms, int64_t* indices_out)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!h || !indices_out) return fail(SKMETAL_EINVAL, "null pointer argument");
+    static_assert(sizeof(long) == sizeof(int64_t), "64-bit long expected");
+    TRY(h->L.plusplus((int)std::min<size_t>(n_local_trials, size_t(kPPMaxTrials) + 1), (long)first_index, uniforms,
+                      reinterpret_cast<long*>(indices_out)));
+    HIP_TRY(hipStreamSynchronize(h->L.s), "hipStreamSynchronize");
+    return 0;
+}
+
+int skmetal_hip_kmeans_plusplus(const float* X, size_t n, size_t d, size_t k, size_t n_local_trials,
+                                int64_t first_index, const double* uniforms, int64_t* indices_out)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!X || !indices_out) return fail(SKMETAL_EINVAL, "null pointer argument");
+    TRY(check_sizes(n, d, k));
+    if (k > n) return fail(SKMETAL_EINVAL, "n_samples=%zu should be >= n_clusters=%zu", n, k);
+    TRY(c.init());
+    Scoped sc;
+    Lloyd& L = sc.L;
+    TRY(L.create(&c, (long)n, (int)d, (int)k));
+    TRY(L.load_X(X, false));
+    TRY(L.plusplus((int)std::min<size_t>(n_local_trials, size_t(kPPMaxTrials) + 1), (long)first_index, uniforms,
+                   reinterpret_cast<long*>(indices_out)));
     return 0;
 }
 

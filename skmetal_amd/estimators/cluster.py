@@ -8,7 +8,10 @@ implementation.  It follows scikit-learn's ``KMeans.fit``
 
 * ``init`` may be an array (used as given, ``n_init`` forced to 1),
   ``"k-means++"``, ``"random"`` or a callable, drawn from the estimator's
-  ``random_state`` in the same order scikit-learn draws them;
+  ``random_state`` in the same order scikit-learn draws them; k-means++
+  (sklearn/cluster/_kmeans.py:174-260) runs on the GPU on the centred X that
+  is already resident for the Lloyd loop, with scikit-learn's random draws;
+* X is uploaded once for all ``n_init`` runs;
 * ``tol`` is scaled by the mean feature variance (``_tolerance``,
   _kmeans.py:279-287) and the loop stops on strict label convergence;
 * for ``n_init > 1`` the run with the lowest inertia that is not the same
@@ -23,7 +26,6 @@ from __future__ import annotations
 import warnings
 
 import numpy as np
-from sklearn.cluster import kmeans_plusplus
 from sklearn.exceptions import ConvergenceWarning
 from sklearn.utils.validation import check_array, check_random_state
 
@@ -76,12 +78,12 @@ class HipKMeans(BaseGPUEstimator):
         return int(n_init)
 
     def _initial_centers(self, X, init, k, random_state):
-        """sklearn/cluster/_kmeans.py:958-1029 (_init_centroids), unit weights."""
+        """sklearn/cluster/_kmeans.py:958-1029 (_init_centroids), unit weights,
+        for the inits other than k-means++ (seeded on the device)."""
         n = X.shape[0]
-        if isinstance(init, str) and init == "k-means++":
-            centers, _ = kmeans_plusplus(X, k, random_state=random_state)
-        elif isinstance(init, str) and init == "random":
-            seeds = random_state.choice(n, size=k, replace=False, p=np.full(n, 1.0 / n))
+        if isinstance(init, str) and init == "random":
+            w = np.ones(n, dtype=X.dtype)  # _check_sample_weight(None, X, dtype=X.dtype)
+            seeds = random_state.choice(n, size=k, replace=False, p=w / w.sum())
             centers = X[seeds]
         elif callable(init):
             centers = init(X, k, random_state=random_state)
@@ -115,12 +117,18 @@ class HipKMeans(BaseGPUEstimator):
         random_state = check_random_state(est.random_state)
 
         best = None
-        for _ in range(n_init):
-            centers = self._initial_centers(X, init, k, random_state)
-            labels = np.empty(n, dtype=np.int32)
-            n_iter, inertia = _bridge.kmeans_fit(X, centers, labels, est.max_iter, tol_abs, strict=True)
-            if best is None or (inertia < best[2] and not _same_clustering(labels, best[1], k)):
-                best = (centers, labels, inertia, n_iter)
+        plusplus = isinstance(init, str) and init == "k-means++"
+        with _bridge.LloydHandle(n, d, k) as h:
+            h.load(X, center=True)
+            for _ in range(n_init):
+                if plusplus:
+                    h.plusplus(random_state)
+                else:
+                    h.set_centers(self._initial_centers(X, init, k, random_state))
+                n_iter, inertia = h.run(est.max_iter, tol_abs, strict=True)
+                labels = h.labels()
+                if best is None or (inertia < best[2] and not _same_clustering(labels, best[1], k)):
+                    best = (h.centers(), labels, inertia, n_iter)
 
         centers, labels, inertia, n_iter = best
         if len(np.unique(labels)) < k:
