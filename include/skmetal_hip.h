@@ -135,7 +135,7 @@ SKMETAL_API int skmetal_hip_lloyd_run(skmetal_hip_lloyd* h, size_t max_iter, dou
  * centred X): scikit-learn's _kmeans_plusplus with unit sample weights
  * (sklearn/cluster/_kmeans.py:174-260), the random numbers drawn by the
  * caller in scikit-learn's order: first_index = the first centre's row
- * (RandomState.choice(n, p=w / w.sum()), :230), uniforms = the
+ * (RandomState.choice(n, p=w / w.sum()), :225), uniforms = the
  * (k - 1) x n_local_trials values of the k - 1 calls
  * RandomState.uniform(size=n_local_trials) (:243), row-major.  The k chosen
  * rows become the current centres and their indices go to indices_out [k].
@@ -149,6 +149,15 @@ SKMETAL_API int skmetal_hip_lloyd_plusplus(skmetal_hip_lloyd* h, size_t n_local_
  * sklearn.cluster.kmeans_plusplus: indices_out [k] receives the chosen rows. */
 SKMETAL_API int skmetal_hip_kmeans_plusplus(const float* X, size_t n, size_t d, size_t k, size_t n_local_trials,
                                             int64_t first_index, const double* uniforms, int64_t* indices_out);
+/* KMeans.transform: out[i * k + j] = ||x_i - c_j|| (float32, [n x k]) as
+ * scikit-learn computes it for float32 data (euclidean_distances,
+ * sklearn/cluster/_kmeans.py:1124-1148; sklearn/metrics/pairwise.py:582-652):
+ * the fp64 expanded distance cast to fp32, negatives set to 0, fp32 square
+ * root.  Replaces the reference's transform through skmetal_gemm
+ * (skmetal/estimators/cluster.py:135-146; _bridge.py:499-563), which formed
+ * the same expression in fp32. */
+SKMETAL_API int skmetal_hip_kmeans_transform(const float* X, const float* centroids, float* out, size_t n, size_t d,
+                                             size_t k);
 /* *fused & 3 = 0 when a step runs as separate E-step and update kernels, 1
  * when as one fused E-step + sums kernel with the E-step on fp32 MFMA
  * (k <= 64, d <= 100), 2 when that kernel's E-step runs on fp16 MFMA with x

@@ -314,3 +314,18 @@ def kmeans_plusplus(X, k: int, first: int, uniforms, n_local_trials: int, trace:
     if trace:
         return idx, cands, pots
     return idx
+
+
+def transform(X, C):
+    """sklearn/cluster/_kmeans.py:1124-1148 (KMeans.transform = euclidean_distances(X,
+    cluster_centers_)) for fp32 data: sklearn/metrics/pairwise.py:582-652 upcast
+    chunks, d = (-2 x.c + ||x||^2) + ||c||^2 in fp64, cast to fp32, negatives to 0
+    (:428-431), np.sqrt in fp32 (:441)."""
+    X64 = np.asarray(X, dtype=np.float32).astype(np.float64)
+    C64 = np.asarray(C, dtype=np.float32).astype(np.float64)
+    d = -2.0 * (X64 @ C64.T)
+    d += np.einsum("ij,ij->i", X64, X64)[:, None]
+    d += np.einsum("ij,ij->i", C64, C64)[None, :]
+    d = d.astype(np.float32)
+    np.maximum(d, 0, out=d)
+    return np.sqrt(d)

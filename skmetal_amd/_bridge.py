@@ -63,6 +63,7 @@ _REGISTRY = [
     ("skmetal_hip_lloyd_inertia", ctypes.c_int, _vp, ctypes.POINTER(ctypes.c_double)),
     ("skmetal_hip_lloyd_plusplus", ctypes.c_int, _vp, _c_size, ctypes.c_int64, _vp, _vp),
     ("skmetal_hip_kmeans_plusplus", ctypes.c_int, _vp, _c_size, _c_size, _c_size, _c_size, ctypes.c_int64, _vp, _vp),
+    ("skmetal_hip_kmeans_transform", ctypes.c_int, _vp, _vp, _vp, _c_size, _c_size, _c_size),
 ]
 
 SKMETAL_FIT_STRICT = 1
@@ -245,6 +246,21 @@ def kmeans_plusplus(X, n_clusters: int, random_state, n_local_trials: int | None
     _check(_lib.skmetal_hip_kmeans_plusplus(X.ctypes.data, n, d, n_clusters, T, first, u.ctypes.data,
                                             idx.ctypes.data), "skmetal_hip_kmeans_plusplus")
     return X[idx], idx
+
+
+def kmeans_transform(X, centroids):
+    """Distances of every row of X to every centroid, [n x k] float32, as
+    scikit-learn's KMeans.transform computes them (GPU)."""
+    _f32c(X, "X"), _f32c(centroids, "centroids")
+    ensure_warmed_up()
+    n, d = X.shape
+    k = centroids.shape[0]
+    if centroids.shape[1] != d:
+        raise ValueError(f"X has {d} features, centroids have {centroids.shape[1]}")
+    out = np.empty((n, k), np.float32)
+    _check(_lib.skmetal_hip_kmeans_transform(X.ctypes.data, centroids.ctypes.data, out.ctypes.data, n, d, k),
+           "skmetal_hip_kmeans_transform")
+    return out
 
 
 class LloydHandle:

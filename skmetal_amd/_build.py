@@ -37,6 +37,7 @@ SOURCES = [
     ("kmeans_kernels.hip", VGPR_FORM),
     ("fused_kernels.hip", []),
     ("plusplus_kernels.hip", []),
+    ("transform_kernels.hip", []),
     ("skmetal_hip.hip", VGPR_FORM),
 ]
 

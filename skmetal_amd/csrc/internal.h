@@ -199,7 +199,6 @@ struct PPArgs {
     int k;
     int T;                 // n_local_trials (candidates per centre after the first)
     int nb;                // k_pp_dist blocks = ceil(n / kPPRows)
-    double* xx;            // [n] fp64 ||x_i||^2
     float* D[2];           // [T x n] min(closest, distance to candidate t), by centre parity
     double* P[2];          // [T x nb] per-block fp64 sums of D[.][t]
     double* pfx;           // [nb] inclusive prefix of the chosen candidate's block sums
@@ -210,11 +209,20 @@ struct PPArgs {
     const double* U;       // [(k - 1) x T] uniforms in [0, 1), in sklearn's draw order
     float* centers;        // [k x ld] the chosen rows of X
 };
-hipError_t launch_pp_norms(const PPArgs& a, hipStream_t s);
 // Candidate distances of centre c (c = 0: the first row alone).
 hipError_t launch_pp_dist(const PPArgs& a, int c, hipStream_t s);
 // Pick centre c - 1 among its candidates; for c < k draw centre c's candidates.
 hipError_t launch_pp_select(const PPArgs& a, int c, hipStream_t s);
+
+// KMeans.transform (transform_kernels.hip): out[i, j] = ||x_i - c_j|| in
+// scikit-learn's fp32 form (fp64 expanded distance, fp32 cast, clamp, sqrt).
+struct TransformArgs {
+    const float* X; long n; int ld;    // rows, stride ld (pad columns 0)
+    const float* C; int k;             // centres [k x ld]
+    double* cc;                        // [k] fp64 ||c||^2 (written first)
+    float* out;                        // [n x k]
+};
+hipError_t launch_transform(const TransformArgs& a, hipStream_t s);
 
 hipError_t launch_colsum(const float* X, long n, int ld, int d, double* part, int nblk, hipStream_t s);
 int colsum_grid(long n);

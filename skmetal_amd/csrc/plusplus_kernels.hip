@@ -14,7 +14,8 @@
 //                   fp32 dot product), candidate_t = the first row whose
 //                   running sum of closest distances reaches r_t (searchsorted
 //                   over stable_cumsum, :247-250), clipped to n - 1;
-//   k_pp_dist(c)    one thread per row: the distance to each candidate in
+//   k_pp_dist(c)    one thread per row (rows staged through LDS in
+//                   coalesced 128-byte runs): the distance to each candidate in
 //                   sklearn's form for fp32 data (_euclidean_distances_upcast:
 //                   fp64 -2 x.c + ||c||^2 + ||x||^2, cast to fp32, negatives
 //                   to 0), min with the row's closest distance so far, and
@@ -32,47 +33,52 @@ namespace skm {
 
 namespace {
 
-constexpr int kFS = 256;  // features staged in LDS per segment
+constexpr int kFS = 32;         // features per LDS segment (one 128-byte run per row)
+constexpr int kXS = kFS + 4;    // LDS row stride (floats): 144 bytes keeps 8 lanes' float4 reads on distinct banks
 
-__global__ __launch_bounds__(256) void k_pp_norms(PPArgs a)
-{
-    const long row = (long)blockIdx.x * 256 + threadIdx.x;
-    if (row >= a.n) return;
-    const float* x = a.X + row * a.ld;
-    double acc = 0.0;
-    for (int f = 0; f < a.ld; f += 4) {
-        const float4 v = *reinterpret_cast<const float4*>(x + f);
-        acc = fma((double)v.x, (double)v.x, acc);
-        acc = fma((double)v.y, (double)v.y, acc);
-        acc = fma((double)v.z, (double)v.z, acc);
-        acc = fma((double)v.w, (double)v.w, acc);
-    }
-    a.xx[row] = acc;
-}
-
-// Centre c's candidate distances, TP candidates per pass (Tc in all).
+// Centre c's candidate distances, TP candidates per pass (Tc in all).  The
+// block's 256 rows go through LDS one 32-feature segment at a time: eight
+// lanes load one row's 128-byte run (coalesced), then thread r works on row r.
+// ||x||^2 and the candidates' ||c||^2 come from the same staged values.
 template <int TP>
 __global__ __launch_bounds__(256) void k_pp_dist(PPArgs a, int c, int Tc)
 {
+    __shared__ float4 xs4[kPPRows * kXS / 4];
     __shared__ double cs[TP][kFS];
+    __shared__ double ccs[TP];
     __shared__ double red[4][TP];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const long row = (long)blockIdx.x * kPPRows + tid;
+    const long r0 = (long)blockIdx.x * kPPRows;
+    const long row = r0 + tid;
     const bool live = row < a.n;
     const int p = c & 1;
     float closest = INFINITY;
     if (c > 0 && live) closest = a.D[p ^ 1][(long)a.best[c - 1] * a.n + row];
-    const float* x = a.X + (live ? row : 0L) * a.ld;
-    const double xx = live ? a.xx[row] : 0.0;
 
     for (int t0 = 0; t0 < Tc; t0 += TP) {
         const int tn = min(TP, Tc - t0);
         double acc[TP];
 #pragma unroll
         for (int t = 0; t < TP; ++t) acc[t] = 0.0;
+        double xx = 0.0, cc = 0.0;
+        // segment f0's runs: lane group tid >> 3 loads rows (tid >> 3) + 32 i
+        const int q = tid & 7;
+        float4 pre[8];
+        auto load_seg = [&](int f0) {
+            const int fl = min(kFS, a.ld - f0);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int lr = (tid >> 3) + 32 * i;
+                pre[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (4 * q < fl && r0 + lr < a.n) pre[i] = *reinterpret_cast<const float4*>(a.X + (r0 + lr) * a.ld + f0 + 4 * q);
+            }
+        };
+        load_seg(0);
         for (int f0 = 0; f0 < a.ld; f0 += kFS) {
             const int fl = min(kFS, a.ld - f0);  // a multiple of 4 (ld is)
             __syncthreads();
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xs4[(((tid >> 3) + 32 * i) * kXS) / 4 + q] = pre[i];
             for (int e = tid; e < TP * kFS; e += 256) {
                 const int t = e / kFS, f = e % kFS;
                 double v = 0.0;
@@ -80,22 +86,32 @@ __global__ __launch_bounds__(256) void k_pp_dist(PPArgs a, int c, int Tc)
                 cs[t][f] = v;
             }
             __syncthreads();
-            if (live) {
-                for (int f = 0; f < fl; f += 4) {
-                    const float4 xv = *reinterpret_cast<const float4*>(x + f0 + f);
+            if (f0 + kFS < a.ld) load_seg(f0 + kFS);  // in flight during this segment's work
+            if (tid < TP)
+                for (int f = 0; f < kFS; ++f) cc = fma(cs[tid][f], cs[tid][f], cc);
+#pragma unroll
+            for (int j = 0; j < kFS / 4; ++j) {
+                if (4 * j < fl) {
+                    const float4 xv = xs4[(tid * kXS) / 4 + j];
                     const double x0 = xv.x, x1 = xv.y, x2 = xv.z, x3 = xv.w;
+                    xx = fma(x0, x0, xx);
+                    xx = fma(x1, x1, xx);
+                    xx = fma(x2, x2, xx);
+                    xx = fma(x3, x3, xx);
 #pragma unroll
                     for (int t = 0; t < TP; ++t) {
                         double v = acc[t];
-                        v = fma(x0, cs[t][f], v);
-                        v = fma(x1, cs[t][f + 1], v);
-                        v = fma(x2, cs[t][f + 2], v);
-                        v = fma(x3, cs[t][f + 3], v);
+                        v = fma(x0, cs[t][4 * j], v);
+                        v = fma(x1, cs[t][4 * j + 1], v);
+                        v = fma(x2, cs[t][4 * j + 2], v);
+                        v = fma(x3, cs[t][4 * j + 3], v);
                         acc[t] = v;
                     }
                 }
             }
         }
+        if (tid < TP) ccs[tid] = cc;
+        __syncthreads();
         // distances, minima with the closest so far, block sums
 #pragma unroll
         for (int t = 0; t < TP; ++t) {
@@ -103,8 +119,7 @@ __global__ __launch_bounds__(256) void k_pp_dist(PPArgs a, int c, int Tc)
             if (t < tn) {
                 float m = 0.f;
                 if (live) {
-                    const double cc = a.xx[a.cand[t0 + t]];
-                    float d32 = (float)((-2.0 * acc[t] + cc) + xx);
+                    float d32 = (float)((-2.0 * acc[t] + ccs[t]) + xx);
                     if (d32 < 0.f) d32 = 0.f;
                     m = d32 < closest ? d32 : closest;
                     a.D[p][(long)(t0 + t) * a.n + row] = m;
@@ -132,7 +147,7 @@ __device__ __forceinline__ double wave_scan(double v, int lane)
 
 __global__ __launch_bounds__(1024) void k_pp_select(PPArgs a, int c)
 {
-    __shared__ double red[1024];
+    __shared__ double wpot[16][kPPMaxTrials];
     __shared__ double wsum[16];
     __shared__ double rv[kPPMaxTrials];
     __shared__ int found[kPPMaxTrials];
@@ -140,25 +155,29 @@ __global__ __launch_bounds__(1024) void k_pp_select(PPArgs a, int c)
     const int q = (c - 1) & 1;
     const int Tq = c == 1 ? 1 : a.T;
 
-    // centre c - 1: the candidate of least potential (first one on ties)
-    double bestpot = 0.0;
-    int best = 0;
+    // centre c - 1: the candidate of least potential (first one on ties);
+    // each potential is a fixed-order sum of the block partials
     for (int t = 0; t < Tq; ++t) {
         double v = 0.0;
         for (int b = tid; b < a.nb; b += 1024) v += a.P[q][(long)t * a.nb + b];
-        red[tid] = v;
-        __syncthreads();
-        for (int w = 512; w > 0; w >>= 1) {
-            if (tid < w) red[tid] += red[tid + w];
-            __syncthreads();
-        }
-        const double pt = red[0];
-        if (t == 0 || pt < bestpot) {
-            bestpot = pt;
+        v = wave_sum(v);
+        if (lane == 0) wpot[wv][t] = v;
+    }
+    __syncthreads();
+    if (tid < Tq) {
+        double v = 0.0;
+        for (int w = 0; w < 16; ++w) v += wpot[w][tid];
+        rv[tid] = v;
+    }
+    __syncthreads();
+    double bestpot = rv[0];
+    int best = 0;
+    for (int t = 1; t < Tq; ++t)
+        if (rv[t] < bestpot) {
+            bestpot = rv[t];
             best = t;
         }
-        __syncthreads();
-    }
+    __syncthreads();
     const long crow = a.cand[best];
     if (tid == 0) {
         a.idx[c - 1] = crow;
@@ -221,12 +240,6 @@ __global__ __launch_bounds__(1024) void k_pp_select(PPArgs a, int c)
 }
 
 }  // namespace
-
-hipError_t launch_pp_norms(const PPArgs& a, hipStream_t s)
-{
-    hipLaunchKernelGGL(k_pp_norms, dim3((unsigned)((a.n + 255) / 256)), dim3(256), 0, s, a);
-    return hipGetLastError();
-}
 
 hipError_t launch_pp_dist(const PPArgs& a, int c, hipStream_t s)
 {

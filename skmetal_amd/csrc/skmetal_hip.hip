@@ -778,7 +778,6 @@ struct Lloyd {
         const int nb = (int)((n + kPPRows - 1) / kPPRows);
         if (T != pp_T) {
             pp_release();
-            TRY(pp_grab((void**)&pp.xx, size_t(n) * sizeof(double)));
             for (int i = 0; i < 2; ++i) {
                 TRY(pp_grab((void**)&pp.D[i], size_t(T) * n * sizeof(float)));
                 TRY(pp_grab((void**)&pp.P[i], size_t(T) * nb * sizeof(double)));
@@ -800,7 +799,6 @@ struct Lloyd {
         pp.centers = cen[cur];
         TRY(upload_bytes(*C, &first, sizeof(long), pp.cand, s));
         if (k > 1) TRY(upload_bytes(*C, U, size_t(k - 1) * T * sizeof(double), const_cast<double*>(pp.U), s));
-        HIP_TRY(launch_pp_norms(pp, s), "pp norms launch");
         HIP_TRY(launch_pp_dist(pp, 0, s), "pp dist launch");
         for (int c = 1; c < k; ++c) {
             HIP_TRY(launch_pp_select(pp, c, s), "pp select launch");
@@ -1162,6 +1160,46 @@ int skmetal_hip_kmeans_plusplus(const float* X, size_t n, size_t d, size_t k, si
     TRY(L.load_X(X, false));
     TRY(L.plusplus((int)std::min<size_t>(n_local_trials, size_t(kPPMaxTrials) + 1), (long)first_index, uniforms,
                    reinterpret_cast<long*>(indices_out)));
+    return 0;
+}
+
+int skmetal_hip_kmeans_transform(const float* X, const float* centroids, float* out, size_t n, size_t d, size_t k)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!X || !centroids || !out) return fail(SKMETAL_EINVAL, "null pointer argument");
+    TRY(check_sizes(n, d, k));
+    TRY(c.init());
+    const int ld = ((int)d + 3) & ~3;
+    // rows per pass: the pass's X rows and distances stay under ~512 MB
+    const size_t row_bytes = size_t(ld + k) * sizeof(float);
+    long rows = (long)std::max<size_t>(64, (size_t(512) << 20) / row_bytes) & ~63L;
+    rows = std::min<long>(rows, ((long)n + 63) & ~63L);
+    struct Bufs {
+        Context& c;
+        std::vector<void*> p;
+        ~Bufs() { for (void* q : p) c.release(q); }
+        int get(void** out, size_t bytes)
+        {
+            TRY(c.alloc(out, bytes));
+            p.push_back(*out);
+            return 0;
+        }
+    } b{c, {}};
+    float *dX = nullptr, *dC = nullptr, *dO = nullptr;
+    double* dcc = nullptr;
+    TRY(b.get((void**)&dX, size_t(rows) * ld * sizeof(float)));
+    TRY(b.get((void**)&dC, k * size_t(ld) * sizeof(float)));
+    TRY(b.get((void**)&dcc, k * sizeof(double)));
+    TRY(b.get((void**)&dO, size_t(rows) * k * sizeof(float)));
+    TRY(upload_rows(c, centroids, (long)k, (int)d, ld, dC, c.stream));
+    for (long r = 0; r < (long)n; r += rows) {
+        const long m = std::min<long>(rows, (long)n - r);
+        TRY(upload_rows(c, X + size_t(r) * d, m, (int)d, ld, dX, c.stream));
+        TransformArgs a{dX, m, ld, dC, (int)k, dcc, dO};
+        HIP_TRY(launch_transform(a, c.stream), "transform launch");
+        TRY(download_bytes(c, dO, size_t(m) * k * sizeof(float), out + size_t(r) * k, c.stream));
+    }
     return 0;
 }
 

@@ -161,6 +161,14 @@ class HipKMeans(BaseGPUEstimator):
         _bridge.kmeans_assign(X, C, out, n, d, C.shape[0])
         return out
 
+    def transform(self, X):
+        """Distances to the centres (sklearn/cluster/_kmeans.py:1124-1148) on the GPU."""
+        X, _ = self._validate_data(X)
+        if not self._gpu_ready(X):
+            return self._fallback_transform(X)
+        C = np.ascontiguousarray(self._estimator.cluster_centers_, dtype=np.float32)
+        return _bridge.kmeans_transform(X, C)
+
     def fit_predict(self, X, y=None, sample_weight=None):
         return self.fit(X, y, sample_weight=sample_weight)._estimator.labels_
 
