@@ -136,6 +136,14 @@ def main():
         h.set_centers(C0)
         _, (ms_assign, ms_update, ms_final) = h.iterate(args.steps, kernel_times=True)
         mode = h.info()
+        # k-means++ seeding of the same resident X on the device with
+        # scikit-learn's draws for random_state=0 (reported beside the metric:
+        # KMeans(init="k-means++") runs it once per fit)
+        T, first, u = _bridge.plusplus_draws(np.random.RandomState(0), n, k)
+        h.plusplus_with(T, first, u)
+        t = time.perf_counter()
+        h.plusplus_with(T, first, u)
+        pp_ms = (time.perf_counter() - t) * 1e3
     if args.calib_copy:
         copy_probe(args.calib_copy)
 
@@ -220,6 +228,7 @@ def main():
                        else {kname: round(ms_assign, 5), "update": round(ms_update, 5),
                              "k_finalize": round(ms_final, 5)}),
         "roofline": roofline,
+        "kmeans_plusplus_ms": round(pp_ms, 3),
         "cpu_baseline": cpu,
     }
     if cpu:
