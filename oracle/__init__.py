@@ -28,6 +28,12 @@ Parity status per function (what pins it, see tests/test_oracle.py):
 * ``inertia``     -- closed form (sum of squares about the mean for k=1),
                      sklearn golden inertia.
 * ``mean_f32``    -- bit-exact against numpy's float32 X.mean(axis=0).
+* ``kmeans_plusplus`` -- scikit-learn's kmeans_plusplus picks on 9 golden inputs
+                     (tests/golden/plusplus.npz, make_plusplus_fixtures.py) and its
+                     docstring vector; planted mistakes (tests/test_plusplus_oracle.py).
+* ``transform``   -- scikit-learn's KMeans.transform bit for bit on 4 golden inputs
+                     (tests/golden/transform.npz), closed forms, planted mistakes
+                     (tests/test_transform_oracle.py).
 """
 
 from __future__ import annotations
