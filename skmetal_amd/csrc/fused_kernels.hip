@@ -511,23 +511,34 @@ __global__ __launch_bounds__(512, 1) void k_fused(FusedArgs a)
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
+// m1 must be -1.0f from a runtime value (see neg_one): fma(hi, m1, x) is then
+// one v_fma_mix_f32 reading the fp16 hi; with a literal -1 the compiler turns
+// it back into a conversion and a subtraction
 template <bool SC>
-__device__ __forceinline__ void split4(float4 v, float sc, v4h& hi, v4h& lo)
+__device__ __forceinline__ void split4(float4 v, float sc, float m1, v4h& hi, v4h& lo)
 {
     const v4f x = SC ? v4f{v.x * sc, v.y * sc, v.z * sc, v.w * sc} : v4f{v.x, v.y, v.z, v.w};
     hi = __builtin_convertvector(x, v4h);
-    lo = __builtin_convertvector(x - __builtin_convertvector(hi, v4f), v4h);
+    // x - hi is exact in fp32 (hi is x rounded to 11 bits), so fma(hi, -1, x)
+    // gives the same lo
+    const v4f r = {__builtin_fmaf((float)hi[0], m1, x[0]), __builtin_fmaf((float)hi[1], m1, x[1]),
+                   __builtin_fmaf((float)hi[2], m1, x[2]), __builtin_fmaf((float)hi[3], m1, x[3])};
+    lo = __builtin_convertvector(r, v4h);
 }
 
 template <bool SC>
-__device__ __forceinline__ void split8(float4 u, float4 v, float sc, v8h& hi, v8h& lo)
+__device__ __forceinline__ void split8(float4 u, float4 v, float sc, float m1, v8h& hi, v8h& lo)
 {
     v4h h0, l0, h1, l1;
-    split4<SC>(u, sc, h0, l0);
-    split4<SC>(v, sc, h1, l1);
+    split4<SC>(u, sc, m1, h0, l0);
+    split4<SC>(v, sc, m1, h1, l1);
     hi = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
     lo = __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7);
 }
+
+// -1.0f from the kernel's scale arguments, sc = 2^s and f2 = -2 * 2^-2s:
+// (f2 / 2) * sc^2 = -2^-2s * 2^2s, exact for the |s| <= 60 the host allows.
+__device__ __forceinline__ float neg_one(float sc, float f2) { return (0.5f * f2) * (sc * sc); }
 
 // The sums wave of SIMD m in k_fused16 serves E-step waves m and m + 4 (the
 // same SIMD), taking their 32-row tiles in turn: round r of wave m, then round
@@ -542,7 +553,7 @@ __device__ __forceinline__ void split8(float4 u, float4 v, float sc, v8h& hi, v8
 template <int CB, int NQ, int XS, int NFB, bool SC>
 __device__ __forceinline__ void msum_tiles2(v4f (&S)[CB][NFB], int rounds0, int rounds1, int* ready0, int* ready1,
                                             int* prog0, int* prog1, const int* lab0, const int* lab1,
-                                            const float* tile0, const float* tile1, int lane, float sc)
+                                            const float* tile0, const float* tile1, int lane, float sc, float m1)
 {
     const int h = lane >> 4, r16 = lane & 15;
 #pragma unroll
@@ -573,7 +584,7 @@ __device__ __forceinline__ void msum_tiles2(v4f (&S)[CB][NFB], int rounds0, int 
                     for (int j = 0; j < 8; ++j) A[cb][j] = lj[j] == c ? one : zero;
                 }
             }
-            const float* col = tile + 8 * h * XS + r16;
+            const float* col = tile + 8 * h * XS + 16 * h + r16;  // rows 8h .. 8h + 7 sit 16 h floats further
 #pragma unroll
             for (int fb = 0; fb < NFB; ++fb) {
                 float cur[8];
@@ -583,7 +594,7 @@ __device__ __forceinline__ void msum_tiles2(v4f (&S)[CB][NFB], int rounds0, int 
                 set_flag(prog, r * NQ + (4 * fb + 4 < NQ ? 4 * fb + 4 : NQ));
                 v8h bh, bl;
                 split8<SC>(make_float4(cur[0], cur[1], cur[2], cur[3]), make_float4(cur[4], cur[5], cur[6], cur[7]), sc,
-                           bh, bl);
+                           m1, bh, bl);
 #pragma unroll
                 for (int cb = 0; cb < CB; ++cb) {
                     S[cb][fb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb], bh, S[cb][fb], 0, 0, 0);
@@ -633,8 +644,14 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
     constexpr int CSTR = KP + 8;                 // halves per centre row: an odd number of 16-byte units
     constexpr int XS = fused_stride(KP / 4);     // LDS row: >= KP floats (tail lanes write zeros past ld)
     constexpr int NFB = KP / 16;                 // 16-feature blocks of the sums
+    // a wave's tile: row rho at rho * XS + 16 (rho >> 3).  XS is 4 x odd, so
+    // 8 XS = 32 (mod 64): without the shift the sums wave's column reads of
+    // rows 8h + j (lanes h = 0..3) fall on the same banks in pairs; with it
+    // the four h start 48 h (mod 64) apart, distinct in every 32-lane pass.
+    // The shift only grows down the tile, so rows never overlap (XS >= KP).
+    constexpr int TS = 32 * XS + 48;
     static_assert(TAIL == 0 || TAIL == 4 || TAIL == 8 || TAIL == 16, "one 16-wide step covers the tail");
-    // LDS: 8 wave tiles [32 x XS] | centre hi parts [CPC x CSTR] halves |
+    // LDS: 8 wave tiles [TS floats] | centre hi parts [CPC x CSTR] halves |
     // centre lo parts
     extern __shared__ __attribute__((aligned(16))) float lds[];
     __shared__ __attribute__((aligned(16))) int sLab[8][32];  // a tile's labels (-1: no row)
@@ -650,7 +667,7 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
     const int r16 = lane & 15;  // this lane's row of a 16-row group / centre of a block
 
     float* tiles = lds;
-    _Float16* sCH = reinterpret_cast<_Float16*>(tiles + 8 * 32 * XS);
+    _Float16* sCH = reinterpret_cast<_Float16*>(tiles + 8 * TS);
     _Float16* sCL = sCH + CPC * CSTR;
 
     // 32-row tiles: E-step wave e of block b handles t = 8b + e + r*P
@@ -701,7 +718,9 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
         if (sDone != 0) return;
         const float sc = a.xscale;
         const float f2 = a.dscale;  // -2 * 2^-2s
-        float* const trow = tiles + e * 32 * XS + r16 * XS;  // group 0's row of this lane
+        const float m1 = neg_one(sc, f2);
+        float* const trow = tiles + e * TS + r16 * XS + 16 * (r16 >> 3);  // group 0's row; group g's: + g * GS
+        constexpr int GS = 16 * XS + 32;
         // this lane's centre operands: one base address, the block, step and
         // part as constant offsets (no per-block address registers)
         const _Float16* const cbase = sCH + r16 * CSTR + 8 * h;
@@ -734,10 +753,10 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
                     v8h xh[2], xl[2];
 #pragma unroll
                     for (int g = 0; g < 2; ++g) {
-                        float* dst = trow + 16 * g * XS + 32 * s + 8 * h;
+                        float* dst = trow + g * GS + 32 * s + 8 * h;
                         *reinterpret_cast<float4*>(dst) = xr[g][2 * s];
                         *reinterpret_cast<float4*>(dst + 4) = xr[g][2 * s + 1];
-                        split8<SC>(xr[g][2 * s], xr[g][2 * s + 1], sc, xh[g], xl[g]);
+                        split8<SC>(xr[g][2 * s], xr[g][2 * s + 1], sc, m1, xh[g], xl[g]);
                         load_step(rn, g, s);
                     }
 #pragma unroll
@@ -756,8 +775,8 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
                     v4h xh[2], xl[2];
 #pragma unroll
                     for (int g = 0; g < 2; ++g) {
-                        *reinterpret_cast<float4*>(trow + 16 * g * XS + 32 * NK + 4 * h) = xr[g][2 * NK];
-                        split4<SC>(xr[g][2 * NK], sc, xh[g], xl[g]);
+                        *reinterpret_cast<float4*>(trow + g * GS + 32 * NK + 4 * h) = xr[g][2 * NK];
+                        split4<SC>(xr[g][2 * NK], sc, m1, xh[g], xl[g]);
                         load_step(rn, g, s);
                     }
 #pragma unroll
@@ -845,7 +864,7 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
             const int q = idx - cl * CQ;
             if (idx < CPC * CQ) {
                 v4h hi, lo;
-                split4<SC>(cf[u], sc, hi, lo);
+                split4<SC>(cf[u], sc, neg_one(sc, a.dscale), hi, lo);
                 *reinterpret_cast<v4h*>(sCH + cl * CSTR + 4 * q) = hi;
                 *reinterpret_cast<v4h*>(sCL + cl * CSTR + 4 * q) = lo;
             }
@@ -862,8 +881,8 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
         const int m = wave - 8;
         v4f S[CB][NFB];
         msum_tiles2<CB, NQ, XS, NFB, SC>(S, rounds_of(m), rounds_of(m + 4), &sReady[m], &sReady[m + 4], &sProg[m],
-                                         &sProg[m + 4], sLab[m], sLab[m + 4], tiles + m * 32 * XS,
-                                         tiles + (m + 4) * 32 * XS, lane, sc);
+                                         &sProg[m + 4], sLab[m], sLab[m + 4], tiles + m * TS,
+                                         tiles + (m + 4) * TS, lane, sc, neg_one(sc, a.dscale));
         __syncthreads();  // every wave is done with its tile
         publish_msums<CB, NFB>(S, tiles, ld, m, lane, SC ? 1.f / sc : 1.f);
         __syncthreads();
@@ -942,7 +961,7 @@ __global__ __launch_bounds__(512, 1) void k_assign16(const float* __restrict__ X
                         const int cl = idx >> 5;
                         const int q = idx & 31;
                         v4h hi, lo;
-                        split4<SC>(v[u], sc, hi, lo);
+                        split4<SC>(v[u], sc, neg_one(sc, f2), hi, lo);
                         *reinterpret_cast<v4h*>(cs + cl * CSTR + 4 * q) = hi;
                         *reinterpret_cast<v4h*>(cs + CLO + cl * CSTR + 4 * q) = lo;
                     }
@@ -963,7 +982,7 @@ __global__ __launch_bounds__(512, 1) void k_assign16(const float* __restrict__ X
 #pragma unroll
                     for (int g = 0; g < 2; ++g) {
                         const int o = ((16 * g + r16) * ld + f0 + 32 * ks + 8 * h) * 4;
-                        split8<SC>(load_quad(rs, o), load_quad(rs, o + 16), sc, xh[g], xl[g]);
+                        split8<SC>(load_quad(rs, o), load_quad(rs, o + 16), sc, neg_one(sc, f2), xh[g], xl[g]);
                     }
 #pragma unroll
                     for (int cb = 0; cb < CB; ++cb) {
@@ -1137,7 +1156,7 @@ static size_t fused16_dyn_lds(int k, int ld)
     const int cpc = 16 * ((k + 15) / 16);
     const int nk = ld / 32;
     const int kp = 32 * nk + (ld > 32 * nk ? 16 : 0);
-    return (size_t)8 * 32 * fused_stride(kp / 4) * sizeof(float) + (size_t)2 * cpc * (kp + 8) * sizeof(_Float16);
+    return (size_t)8 * (32 * fused_stride(kp / 4) + 48) * sizeof(float) + (size_t)2 * cpc * (kp + 8) * sizeof(_Float16);
 }
 
 int fused16_ready(int k, int ld)
