@@ -920,6 +920,9 @@ __global__ __launch_bounds__(512, 1) void k_assign16(const float* __restrict__ X
     const int npass = (k + CPC - 1) / CPC;
     const int nseg = (ld + SEG - 1) / SEG;
     const _Float16* const cbase = cs + r16 * CSTR + 8 * h;
+    // one pass of one segment (k <= 16 CB, ld <= 128): the staged operands
+    // are the same for every row block, so they are staged once
+    const bool once = npass == 1 && nseg == 1;
 
     for (long base = (long)blockIdx.x * 256; base < n; base += (long)gridDim.x * 256) {
         const long wrow = base + 32 * wave;  // this wave's first row
@@ -937,6 +940,7 @@ __global__ __launch_bounds__(512, 1) void k_assign16(const float* __restrict__ X
             }
             for (int sg = 0; sg < nseg; ++sg) {
                 const int f0 = sg * SEG;
+                if (!once || base == (long)blockIdx.x * 256) {  // (uniform across the block)
                 __syncthreads();  // the previous segment's operands are consumed
                 // stage centres p*CPC.. x features f0..f0+127 as scaled fp16
                 // parts (centres >= k and features >= ld zero)
@@ -973,6 +977,7 @@ __global__ __launch_bounds__(512, 1) void k_assign16(const float* __restrict__ X
                     }
                 }
                 __syncthreads();
+                }
                 const int nks = min(4, (ld - f0 + 31) / 32);
                 for (int ks = 0; ks < nks; ++ks) {
                     // rows 16g + l%16, features f0 + 32ks + 8h..: past the
