@@ -520,7 +520,7 @@ template <int CPT>
 __global__ __launch_bounds__(256) void k_segsum(SortArgs a, int B, int G)
 {
     if (a.state->done != 0) return;
-    constexpr int U = 8;  // sorted rows in flight
+    constexpr int U = 16;  // sorted rows in flight
     const int groups = 256 / G;
     const int grp = threadIdx.x / G;
     const int t = threadIdx.x - grp * G;
@@ -549,23 +549,35 @@ __global__ __launch_bounds__(256) void k_segsum(SortArgs a, int B, int G)
             acc[i] = 0.f;
         }
     };
-    for (long p = p0; p < p1; p += U) {
-        int lab[U];
-        float v[U][CPT];
+    // the labels and row ids of a batch are loaded one batch ahead, so a
+    // batch's X rows and the next batch's ids are in flight together
+    int lab[U], rid[U];
+    auto load_ids = [&](long p) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const long q = p + u < p1 ? p + u : p1 - 1;
-            lab[u] = p + u < p1 ? a.slab[q] : cur;
-            const float* row = a.X + (long)a.perm[q] * a.ld;
+            lab[u] = a.slab[q];
+            rid[u] = a.perm[q];
+        }
+    };
+    load_ids(p0);
+    for (long p = p0; p < p1; p += U) {
+        float v[U][CPT];
+        int lb[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            lb[u] = lab[u];
+            const float* row = a.X + (long)rid[u] * a.ld;
 #pragma unroll
             for (int i = 0; i < CPT; ++i) v[u][i] = on[i] ? row[cols[i]] : 0.f;
         }
+        if (p + U < p1) load_ids(p + U);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (p + u >= p1) break;
-            if (lab[u] != cur) {
+            if (lb[u] != cur) {
                 flush(cur);
-                cur = lab[u];
+                cur = lb[u];
             }
 #pragma unroll
             for (int i = 0; i < CPT; ++i) acc[i] += v[u][i];
