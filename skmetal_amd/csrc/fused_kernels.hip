@@ -640,6 +640,7 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
     constexpr int TAIL = LDX - 32 * NK;          // features of the last, 16-wide step (0: none)
     constexpr int NS = NK + (TAIL > 0 ? 1 : 0);  // K steps
     constexpr int QG = 2 * NK + (TAIL > 0 ? 1 : 0);  // float4s per lane per 16-row group
+    constexpr int TQ = TAIL > 0 ? 2 * NK : 0;        // the tail's float4 (its code is dead without a tail)
     constexpr int KP = 32 * NK + (TAIL > 0 ? 16 : 0);
     constexpr int CSTR = KP + 8;                 // halves per centre row: an odd number of 16-byte units
     constexpr int XS = fused_stride(KP / 4);     // LDS row: >= KP floats (tail lanes write zeros past ld)
@@ -700,7 +701,7 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
                 xr[g][2 * s + 1] = load_quad(rs, o + 16);
             } else {
                 const int o = ((16 * g + r16) * LDX + 32 * NK + 4 * h) * 4;
-                xr[g][2 * NK] = load_quad(rs, 4 * h < TAIL ? o : 0x40000000);
+                xr[g][TQ] = load_quad(rs, 4 * h < TAIL ? o : 0x40000000);
             }
         };
         {
@@ -775,8 +776,8 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
                     v4h xh[2], xl[2];
 #pragma unroll
                     for (int g = 0; g < 2; ++g) {
-                        *reinterpret_cast<float4*>(trow + g * GS + 32 * NK + 4 * h) = xr[g][2 * NK];
-                        split4<SC>(xr[g][2 * NK], sc, m1, xh[g], xl[g]);
+                        *reinterpret_cast<float4*>(trow + g * GS + 32 * NK + 4 * h) = xr[g][TQ];
+                        split4<SC>(xr[g][TQ], sc, m1, xh[g], xl[g]);
                         load_step(rn, g, s);
                     }
 #pragma unroll

@@ -130,7 +130,7 @@ struct Context {
         hipError_t e = hipMalloc(&p, bytes);
         if (e != hipSuccess) {
             // drop the cache and retry once
-            hipGetLastError();
+            (void)hipGetLastError();  // clear the failed allocation's error
             release_cache();
             e = hipMalloc(&p, bytes);
             if (e != hipSuccess) return hip_fail(e, "hipMalloc");
@@ -152,7 +152,7 @@ struct Context {
     {
         for (auto& kv : free_blocks) {
             sizes.erase(kv.second);
-            hipFree(kv.second);
+            (void)hipFree(kv.second);
         }
         free_blocks.clear();
     }
@@ -388,11 +388,11 @@ struct Lloyd {
 
     void destroy()
     {
-        if (s) hipStreamSynchronize(s);
+        if (s) (void)hipStreamSynchronize(s);  // teardown: nothing to report to
         for (void* p : owned) C->release(p);
         owned.clear();
         pp_release();
-        for (hipEvent_t e : kev) hipEventDestroy(e);
+        for (hipEvent_t e : kev) (void)hipEventDestroy(e);
         kev.clear();
     }
 
@@ -775,6 +775,7 @@ struct Lloyd {
         if (T < 1 || T > kPPMaxTrials) return fail(SKMETAL_ERANGE, "n_local_trials=%d not in [1, %d]", T, kPPMaxTrials);
         if (first < 0 || first >= n) return fail(SKMETAL_EINVAL, "first index %ld not in [0, %ld)", first, n);
         if (k > 1 && U == nullptr) return fail(SKMETAL_EINVAL, "null uniforms");
+        if (n >= (1L << 31)) return fail(SKMETAL_ERANGE, "k-means++ seeding supports n < 2^31 rows (n=%ld)", n);
         const int nb = (int)((n + kPPRows - 1) / kPPRows);
         if (T != pp_T) {
             pp_release();
@@ -909,7 +910,7 @@ int skmetal_hip_release_cache(void)
     Context& c = ctx();
     Guard g(c);
     if (c.ready) {
-        hipStreamSynchronize(c.stream);
+        HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
         c.release_cache();
     }
     return 0;
@@ -1091,14 +1092,19 @@ int skmetal_hip_lloyd_iterate(skmetal_hip_lloyd* h, size_t iters, float* ms_out,
     rc = L.write_state(hs);
     if (rc == 0) {
         L.kev_base = kernel_ms ? 0 : -1;
-        hipEventRecord(e0, L.s);
+        hipError_t er = hipEventRecord(e0, L.s);
+        if (er != hipSuccess) rc = hip_fail(er, "hipEventRecord");
         int n_iter = 0, done = 0;
-        rc = L.run_loop((long)iters, 0.0, 0, true, &n_iter, &done);
-        hipEventRecord(e1, L.s);
+        if (rc == 0) rc = L.run_loop((long)iters, 0.0, 0, true, &n_iter, &done);
+        er = hipEventRecord(e1, L.s);
+        if (rc == 0 && er != hipSuccess) rc = hip_fail(er, "hipEventRecord");
         L.kev_base = -1;
         hipError_t e = hipEventSynchronize(e1);
         if (rc == 0 && e != hipSuccess) rc = hip_fail(e, "hipEventSynchronize");
-        if (rc == 0 && ms_out) hipEventElapsedTime(ms_out, e0, e1);
+        if (rc == 0 && ms_out) {
+            e = hipEventElapsedTime(ms_out, e0, e1);
+            if (e != hipSuccess) rc = hip_fail(e, "hipEventElapsedTime");
+        }
         if (rc == 0 && kernel_ms) {
             // averages over the steps: main kernel, update kernels, finalize
             double sum[3] = {0.0, 0.0, 0.0};
@@ -1113,8 +1119,8 @@ int skmetal_hip_lloyd_iterate(skmetal_hip_lloyd* h, size_t iters, float* ms_out,
             for (int j = 0; j < 3; ++j) kernel_ms[j] = iters ? float(sum[j] / double(iters)) : 0.f;
         }
     }
-    hipEventDestroy(e0);
-    hipEventDestroy(e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
     return rc;
 }
 
