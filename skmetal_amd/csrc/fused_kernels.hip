@@ -552,8 +552,9 @@ __device__ __forceinline__ float neg_one(float sc, float f2) { return (0.5f * f2
 // per 16-feature block (all rows read).
 template <int CB, int NQ, int XS, int NFB, bool SC>
 __device__ __forceinline__ void msum_tiles2(v4f (&S)[CB][NFB], int rounds0, int rounds1, int* ready0, int* ready1,
-                                            int* prog0, int* prog1, const int* lab0, const int* lab1,
-                                            const float* tile0, const float* tile1, int lane, float sc, float m1)
+                                            int* prog0, int* prog1, unsigned* mask0, unsigned* mask1,
+                                            const v8h* onehot, const float* tile0, const float* tile1, int lane,
+                                            float sc, float m1)
 {
     const int h = lane >> 4, r16 = lane & 15;
 #pragma unroll
@@ -561,7 +562,6 @@ __device__ __forceinline__ void msum_tiles2(v4f (&S)[CB][NFB], int rounds0, int 
 #pragma unroll
         for (int fb = 0; fb < NFB; ++fb) S[cb][fb] = v4f{0.f, 0.f, 0.f, 0.f};
     }
-    const _Float16 one = (_Float16)1.0f, zero = (_Float16)0.0f;
     const int rmax = rounds0 > rounds1 ? rounds0 : rounds1;
     for (int r = 0; r < rmax; ++r) {
         for (int u = 0; u < 2; ++u) {
@@ -569,19 +569,23 @@ __device__ __forceinline__ void msum_tiles2(v4f (&S)[CB][NFB], int rounds0, int 
             if (r >= (u == 0 ? rounds0 : rounds1)) continue;
             int* const ready = u == 0 ? ready0 : ready1;
             int* const prog = u == 0 ? prog0 : prog1;
-            const int* const lab = u == 0 ? lab0 : lab1;
+            unsigned* const mask = u == 0 ? mask0 : mask1;
             const float* const tile = u == 0 ? tile0 : tile1;
             wait_flag(ready, r + 1);
+            // A[cb][j] = 1 when row 8h + j has label 16 cb + r16: byte h of that
+            // cluster's row mask, through the one-hot table; then the masks
+            // are cleared for the next round (the E-step wave sets the next
+            // bits only after this tile's progress flags, which follow)
             v8h A[CB];
             {
-                const int4 l0 = *reinterpret_cast<const int4*>(lab + 8 * h);
-                const int4 l1 = *reinterpret_cast<const int4*>(lab + 8 * h + 4);
-                const int lj[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+                unsigned mw[CB];
 #pragma unroll
-                for (int cb = 0; cb < CB; ++cb) {
-                    const int c = 16 * cb + r16;
+                for (int cb = 0; cb < CB; ++cb) mw[cb] = mask[16 * cb + r16];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) A[cb][j] = lj[j] == c ? one : zero;
+                for (int cb = 0; cb < CB; ++cb) A[cb] = onehot[(mw[cb] >> (8 * h)) & 0xffu];
+                if (h == 0) {
+#pragma unroll
+                    for (int cb = 0; cb < CB; ++cb) mask[16 * cb + r16] = 0u;
                 }
             }
             const float* col = tile + 8 * h * XS + 16 * h + r16;  // rows 8h .. 8h + 7 sit 16 h floats further
@@ -655,7 +659,8 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
     // LDS: 8 wave tiles [TS floats] | centre hi parts [CPC x CSTR] halves |
     // centre lo parts
     extern __shared__ __attribute__((aligned(16))) float lds[];
-    __shared__ __attribute__((aligned(16))) int sLab[8][32];  // a tile's labels (-1: no row)
+    __shared__ unsigned sMask[8][64];                          // a tile's rows of each cluster (bit = row)
+    __shared__ __attribute__((aligned(16))) v8h sOneHot[256];  // byte b -> its 8 bits as fp16 0 / 1
     __shared__ int sCnt[4][64];                                // rows per cluster, per SIMD
     __shared__ __attribute__((aligned(16))) float sN[CPC];
     __shared__ int sReady[8];  // tiles E-step wave e has labelled
@@ -826,9 +831,9 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
             }
             __builtin_amdgcn_raw_buffer_store_b32(mylab, rl, lane * 4, 0, 0);
             changed += (int)__popcll(__ballot(valid && old != mylab));
-            // the tile's labels for the sums wave; the counts (integer adds:
-            // any order gives the same total)
-            if (lane < 32) sLab[e][lane] = valid ? mylab : -1;
+            // the tile's rows per cluster for the sums wave (an OR of bits:
+            // any order gives the same mask); the counts (integer adds)
+            if (valid) atomicOr(&sMask[e][mylab], 1u << lane);
             if (valid) atomicAdd(&sCnt[e & 3][mylab], 1);
             set_flag(&sReady[e], r + 1);
         }
@@ -879,6 +884,14 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
             sProg[wt] = 0;
         }
         sCnt[wt >> 6][wt & 63] = 0;
+        sMask[wt >> 6][wt & 63] = 0u;
+        sMask[4 + (wt >> 6)][wt & 63] = 0u;
+        {
+            v8h oh;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) oh[j] = (wt >> j) & 1 ? (_Float16)1.0f : (_Float16)0.0f;
+            sOneHot[wt] = oh;
+        }
         if (wave == 8) step_norms<CPC>(a, lane, sN, &sDone);
         __syncthreads();
         if (sDone != 0) return;
@@ -886,7 +899,7 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
         const int m = wave - 8;
         v4f S[CB][NFB];
         msum_tiles2<CB, NQ, XS, NFB, SC>(S, rounds_of(m), rounds_of(m + 4), &sReady[m], &sReady[m + 4], &sProg[m],
-                                         &sProg[m + 4], sLab[m], sLab[m + 4], tiles + m * TS,
+                                         &sProg[m + 4], sMask[m], sMask[m + 4], sOneHot, tiles + m * TS,
                                          tiles + (m + 4) * TS, lane, sc, neg_one(sc, a.dscale));
         __syncthreads();  // every wave is done with its tile
         publish_msums<CB, NFB>(S, tiles, ld, m, lane, SC ? 1.f / sc : 1.f);
@@ -1175,7 +1188,8 @@ int fused16_ready(int k, int ld)
     const char* env = getenv("SKMETAL_HIP_F16");
     if (env != nullptr && env[0] == '0') return 0;
     const size_t dyn = fused16_dyn_lds(k, ld);
-    const size_t stat = 4 * 64 * (sizeof(unsigned long long) + sizeof(int)) + 64 * sizeof(float) + 64;
+    // sMask, sOneHot, sCnt, sN, flags
+    const size_t stat = 8 * 64 * sizeof(unsigned) + 256 * 16 + 4 * 64 * sizeof(int) + 64 * sizeof(float) + 128;
     if (dyn + stat > 160 * 1024) return 0;
     for (const bool scaled : {false, true}) {
         fused_fn f = fused16_kernel(k, ld, scaled);
