@@ -960,32 +960,39 @@ __global__ __launch_bounds__(512, 1) void k_assign16(const float* __restrict__ X
                 const int f0 = sg * SEG;
                 if (!once || base == (long)blockIdx.x * 256) {  // (uniform across the block)
                 __syncthreads();  // the previous segment's operands are consumed
-                // stage centres p*CPC.. x features f0..f0+127 as scaled fp16
-                // parts (centres >= k and features >= ld zero)
-                // (CPC * 32 float4s over 512 threads: CB each, in batches of
-                // up to 8 loads in flight before the first conversion)
-                constexpr int SB = CB < 8 ? CB : 8;
+                // stage centres p*CPC.. x the features f0.. of the K steps this
+                // segment has (32 each; centres >= k and features >= ld zero),
+                // as scaled fp16 parts: eight threads per (centre, K step), two
+                // K steps' loads in flight before the first conversion
+                constexpr int UPK = CPC * 8 / 512;  // float4s per thread per K step
+                const int nks_s = min(4, (ld - f0 + 31) / 32);
+                for (int ks0 = 0; ks0 < nks_s; ks0 += 2) {
+                    float4 v[2][UPK];
 #pragma unroll
-                for (int u0 = 0; u0 < CB; u0 += SB) {
-                    float4 v[SB];
+                    for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
-                    for (int u = 0; u < SB; ++u) {
-                        const int idx = tid + 512 * (u0 + u);
-                        const int cl = idx >> 5;
-                        const int j = p * CPC + cl;
-                        const int f = f0 + 4 * (idx & 31);
-                        v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-                        if (j < k && f < ld) v[u] = *reinterpret_cast<const float4*>(C + (long)j * ld + f);
+                        for (int u = 0; u < UPK; ++u) {
+                            const int idx = tid + 512 * u;
+                            const int j = p * CPC + (idx >> 3);
+                            const int f = f0 + 4 * (8 * (ks0 + kk) + (idx & 7));
+                            v[kk][u] = make_float4(0.f, 0.f, 0.f, 0.f);
+                            if (ks0 + kk < nks_s && j < k && f < ld)
+                                v[kk][u] = *reinterpret_cast<const float4*>(C + (long)j * ld + f);
+                        }
                     }
 #pragma unroll
-                    for (int u = 0; u < SB; ++u) {
-                        const int idx = tid + 512 * (u0 + u);
-                        const int cl = idx >> 5;
-                        const int q = idx & 31;
-                        v4h hi, lo;
-                        split4<SC>(v[u], sc, neg_one(sc, f2), hi, lo);
-                        *reinterpret_cast<v4h*>(cs + cl * CSTR + 4 * q) = hi;
-                        *reinterpret_cast<v4h*>(cs + CLO + cl * CSTR + 4 * q) = lo;
+                    for (int kk = 0; kk < 2; ++kk) {
+                        if (ks0 + kk >= nks_s) break;
+#pragma unroll
+                        for (int u = 0; u < UPK; ++u) {
+                            const int idx = tid + 512 * u;
+                            const int cl = idx >> 3;
+                            const int q = 8 * (ks0 + kk) + (idx & 7);
+                            v4h hi, lo;
+                            split4<SC>(v[kk][u], sc, neg_one(sc, f2), hi, lo);
+                            *reinterpret_cast<v4h*>(cs + cl * CSTR + 4 * q) = hi;
+                            *reinterpret_cast<v4h*>(cs + CLO + cl * CSTR + 4 * q) = lo;
+                        }
                     }
                 }
                 if (sg == 0) {
