@@ -158,6 +158,13 @@ SKMETAL_API int skmetal_hip_kmeans_plusplus(const float* X, size_t n, size_t d, 
  * the same expression in fp32. */
 SKMETAL_API int skmetal_hip_kmeans_transform(const float* X, const float* centroids, float* out, size_t n, size_t d,
                                              size_t k);
+/* out[d] = numpy's float32 np.var(X, axis=0) of a C-ordered X [n x d], bit for
+ * bit: the column variances scikit-learn's _tolerance averages
+ * (sklearn/cluster/_kmeans.py:279-287).  Host threads run numpy's row-order
+ * fp32 chains over column ranges, two passes over X without temporaries
+ * (numpy's own np.var makes four, and a copy of X).  Needs no device.  No
+ * counterpart in the reference. */
+SKMETAL_API int skmetal_hip_column_variance(const float* X, size_t n, size_t d, float* out);
 /* *fused & 3 = 0 when a step runs as separate E-step and update kernels, 1
  * when as one fused E-step + sums kernel with the E-step on fp32 MFMA
  * (k <= 64, d <= 100), 2 when that kernel's E-step runs on fp16 MFMA with x

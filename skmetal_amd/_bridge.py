@@ -64,6 +64,7 @@ _REGISTRY = [
     ("skmetal_hip_lloyd_plusplus", ctypes.c_int, _vp, _c_size, ctypes.c_int64, _vp, _vp),
     ("skmetal_hip_kmeans_plusplus", ctypes.c_int, _vp, _c_size, _c_size, _c_size, _c_size, ctypes.c_int64, _vp, _vp),
     ("skmetal_hip_kmeans_transform", ctypes.c_int, _vp, _vp, _vp, _c_size, _c_size, _c_size),
+    ("skmetal_hip_column_variance", ctypes.c_int, _vp, _c_size, _c_size, _vp),
 ]
 
 SKMETAL_FIT_STRICT = 1
@@ -246,6 +247,18 @@ def kmeans_plusplus(X, n_clusters: int, random_state, n_local_trials: int | None
     _check(_lib.skmetal_hip_kmeans_plusplus(X.ctypes.data, n, d, n_clusters, T, first, u.ctypes.data,
                                             idx.ctypes.data), "skmetal_hip_kmeans_plusplus")
     return X[idx], idx
+
+
+def column_variance(X):
+    """numpy's float32 np.var(X, axis=0) bit for bit, in host threads (the
+    library's; no device needed)."""
+    _f32c(X, "X")
+    if _lib is None:
+        raise RuntimeError(f"{LIB_NAME} not loaded: {_load_error}")
+    n, d = X.shape
+    out = np.empty(d, np.float32)
+    _check(_lib.skmetal_hip_column_variance(X.ctypes.data, n, d, out.ctypes.data), "skmetal_hip_column_variance")
+    return out
 
 
 def kmeans_transform(X, centroids):

@@ -199,6 +199,49 @@ static void stage_rows(float* p, const float* src, long m, int cols, int ld)
     for (auto& x : th) x.join();
 }
 
+// numpy's float32 np.var(X, axis=0) of a C-ordered X [n x d] (numpy
+// _core/_methods.py _var, ddof 0), the variances scikit-learn's _tolerance
+// averages (sklearn/cluster/_kmeans.py:279-287).  numpy reduces axis 0 row by
+// row, so each column's sum and sum of squared deviations are fp32 chains in
+// row order, and both divisions by the count run in fp64 (an intp count) and
+// round to fp32.  Host threads take contiguous column ranges and run those
+// chains: two passes over X, no temporary arrays, numpy's bits.
+static void column_variance_f32(const float* X, long n, int d, float* out)
+{
+    auto work = [X, n, d, out](int c0, int c1) {
+#pragma clang fp contract(off)
+        const int w = c1 - c0;
+        std::vector<float> s(static_cast<size_t>(w), 0.f), s2(static_cast<size_t>(w), 0.f),
+            mean(static_cast<size_t>(w));
+        for (long r = 0; r < n; ++r) {
+            const float* row = X + r * d + c0;
+            for (int c = 0; c < w; ++c) s[size_t(c)] = s[size_t(c)] + row[c];
+        }
+        for (int c = 0; c < w; ++c) mean[size_t(c)] = (float)((double)s[size_t(c)] / (double)n);
+        for (long r = 0; r < n; ++r) {
+            const float* row = X + r * d + c0;
+            for (int c = 0; c < w; ++c) {
+                const float t = row[c] - mean[size_t(c)];
+                const float t2 = t * t;
+                s2[size_t(c)] = s2[size_t(c)] + t2;
+            }
+        }
+        for (int c = 0; c < w; ++c) out[c0 + c] = (float)((double)s2[size_t(c)] / (double)n);
+    };
+    unsigned nt = std::thread::hardware_concurrency();
+    const unsigned by_cols = unsigned((d + 7) / 8);  // at least 8 columns (32 bytes of a row) per thread
+    nt = std::max(1u, std::min({nt, 16u, by_cols}));
+    if (size_t(n) * size_t(d) < (size_t(1) << 20)) nt = 1;
+    std::vector<std::thread> th;
+    const int per = (d + int(nt) - 1) / int(nt);
+    for (unsigned t = 1; t < nt; ++t) {
+        const int c0 = int(t) * per, c1 = std::min(d, c0 + per);
+        if (c0 < c1) th.emplace_back(work, c0, c1);
+    }
+    work(0, std::min(d, per));
+    for (auto& x : th) x.join();
+}
+
 int upload_rows(Context& C, const float* src, long rows, int cols, int ld, float* dst, hipStream_t s)
 {
     const size_t row_bytes = size_t(ld) * sizeof(float);
@@ -1206,6 +1249,15 @@ int skmetal_hip_kmeans_transform(const float* X, const float* centroids, float* 
         HIP_TRY(launch_transform(a, c.stream), "transform launch");
         TRY(download_bytes(c, dO, size_t(m) * k * sizeof(float), out + size_t(r) * k, c.stream));
     }
+    return 0;
+}
+
+int skmetal_hip_column_variance(const float* X, size_t n, size_t d, float* out)
+{
+    if (!X || !out) return fail(SKMETAL_EINVAL, "null pointer argument");
+    if (n == 0 || d == 0) return fail(SKMETAL_EINVAL, "n and d must be positive (n=%zu d=%zu)", n, d);
+    if (d > (size_t(1) << 30) || n > (size_t(1) << 40)) return fail(SKMETAL_ERANGE, "n=%zu or d=%zu too large", n, d);
+    column_variance_f32(X, (long)n, (int)d, out);
     return 0;
 }
 

@@ -35,10 +35,13 @@ from ._base import BaseGPUEstimator
 
 
 def _tolerance(X: np.ndarray, tol: float) -> float:
-    """sklearn/cluster/_kmeans.py:279-287 for dense X."""
+    """sklearn/cluster/_kmeans.py:279-287 for dense float32 X: np.mean of
+    np.var(X, axis=0), times tol.  The column variances come from the library
+    (numpy's float32 np.var bit for bit, in host threads: numpy's own np.var
+    is most of a fit's time on large X)."""
     if tol == 0:
         return 0.0
-    return float(np.mean(np.var(X, axis=0)) * tol)
+    return float(np.mean(_bridge.column_variance(X)) * tol)
 
 
 def _same_clustering(a: np.ndarray, b: np.ndarray, k: int) -> bool:

@@ -192,6 +192,17 @@ def test_config_api_validation_and_context():
     assert get_config().device == "gpu"
 
 
+@pytest.mark.parametrize("n,d", [(1, 1), (2, 3), (17, 5), (1000, 100), (4099, 130), (20000, 9), (65, 768)])
+def test_column_variance_is_numpys(n, d):
+    """The library's host column variances are numpy's float32 np.var(X, axis=0)
+    bit for bit (row-order fp32 chains, fp64 divisions)."""
+    from skmetal_amd import _bridge
+
+    rng = np.random.default_rng(n + d)
+    X = (rng.standard_normal((n, d)) * rng.uniform(0.01, 100, d) + rng.uniform(-1e3, 1e3, d)).astype(np.float32)
+    np.testing.assert_array_equal(_bridge.column_variance(X), np.var(X, axis=0))
+
+
 def test_tolerance_matches_sklearn():
     from sklearn.cluster._kmeans import _tolerance as sk_tolerance
 
@@ -200,7 +211,7 @@ def test_tolerance_matches_sklearn():
     rng = np.random.default_rng(2)
     X = (rng.standard_normal((500, 7)) * rng.uniform(0.1, 5, 7)).astype(np.float32)
     for tol in (0.0, 1e-4, 0.3):
-        assert _tolerance(X, tol) == pytest.approx(sk_tolerance(X, tol), rel=1e-6, abs=0)
+        assert _tolerance(X, tol) == sk_tolerance(X, tol)  # the same bits
 
 
 def test_same_clustering_is_permutation_invariant():
