@@ -165,6 +165,11 @@ SKMETAL_API int skmetal_hip_kmeans_transform(const float* X, const float* centro
  * (numpy's own np.var makes four, and a copy of X).  Needs no device.  No
  * counterpart in the reference. */
 SKMETAL_API int skmetal_hip_column_variance(const float* X, size_t n, size_t d, float* out);
+/* Largest |x| of the loaded X (after the centring, if any), NaN counted as
+ * +inf: a finite value means X holds no NaN or infinity, so a caller can skip
+ * its own pass over X.  A non-finite value can also come from a centring
+ * that overflowed, so the caller then checks X itself. */
+SKMETAL_API int skmetal_hip_lloyd_max_abs(skmetal_hip_lloyd* h, float* out);
 /* *fused & 3 = 0 when a step runs as separate E-step and update kernels, 1
  * when as one fused E-step + sums kernel with the E-step on fp32 MFMA
  * (k <= 64, d <= 100), 2 when that kernel's E-step runs on fp16 MFMA with x

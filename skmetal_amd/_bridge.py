@@ -65,6 +65,7 @@ _REGISTRY = [
     ("skmetal_hip_kmeans_plusplus", ctypes.c_int, _vp, _c_size, _c_size, _c_size, _c_size, ctypes.c_int64, _vp, _vp),
     ("skmetal_hip_kmeans_transform", ctypes.c_int, _vp, _vp, _vp, _c_size, _c_size, _c_size),
     ("skmetal_hip_column_variance", ctypes.c_int, _vp, _c_size, _c_size, _vp),
+    ("skmetal_hip_lloyd_max_abs", ctypes.c_int, _vp, ctypes.POINTER(ctypes.c_float)),
 ]
 
 SKMETAL_FIT_STRICT = 1
@@ -347,6 +348,12 @@ class LloydHandle:
         _check(_lib.skmetal_hip_lloyd_plusplus(self._h, int(n_local_trials), int(first), u.ctypes.data,
                                                idx.ctypes.data), "skmetal_hip_lloyd_plusplus")
         return idx
+
+    def max_abs(self) -> float:
+        """Largest |x| of the loaded X (NaN as +inf), measured on the device."""
+        v = ctypes.c_float(0.0)
+        _check(_lib.skmetal_hip_lloyd_max_abs(self._h, ctypes.byref(v)), "skmetal_hip_lloyd_max_abs")
+        return float(v.value)
 
     def info(self):
         fused = ctypes.c_int(0)

@@ -453,13 +453,23 @@ struct Lloyd {
             std::fill(h_mean.begin(), h_mean.end(), 0.f);
             HIP_TRY(hipMemsetAsync(mean, 0, size_t(ld) * sizeof(float), s), "hipMemsetAsync");
         }
+        xmax_known = false;
         if (f16cap || a16cap) {
-            unsigned bits = 0;
-            HIP_TRY(launch_absmax(X, n * (long)ld, absmax, s), "absmax launch");
-            TRY(download_bytes(*C, absmax, sizeof(unsigned), &bits, s));
-            std::memcpy(&xmax, &bits, sizeof(float));
+            TRY(measure_xmax());
             update_scale();
         }
+        return 0;
+    }
+
+    // max |x| of the loaded X (NaN counted as +inf) into xmax
+    bool xmax_known = false;
+    int measure_xmax()
+    {
+        unsigned bits = 0;
+        HIP_TRY(launch_absmax(X, n * (long)ld, absmax, s), "absmax launch");
+        TRY(download_bytes(*C, absmax, sizeof(unsigned), &bits, s));
+        std::memcpy(&xmax, &bits, sizeof(float));
+        xmax_known = true;
         return 0;
     }
 
@@ -1258,6 +1268,16 @@ int skmetal_hip_column_variance(const float* X, size_t n, size_t d, float* out)
     if (n == 0 || d == 0) return fail(SKMETAL_EINVAL, "n and d must be positive (n=%zu d=%zu)", n, d);
     if (d > (size_t(1) << 30) || n > (size_t(1) << 40)) return fail(SKMETAL_ERANGE, "n=%zu or d=%zu too large", n, d);
     column_variance_f32(X, (long)n, (int)d, out);
+    return 0;
+}
+
+int skmetal_hip_lloyd_max_abs(skmetal_hip_lloyd* h, float* out)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!h || !out) return fail(SKMETAL_EINVAL, "null pointer argument");
+    if (!h->L.xmax_known) TRY(h->L.measure_xmax());
+    *out = h->L.xmax;
     return 0;
 }
 

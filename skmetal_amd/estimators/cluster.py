@@ -27,7 +27,7 @@ import warnings
 
 import numpy as np
 from sklearn.exceptions import ConvergenceWarning
-from sklearn.utils.validation import check_array, check_random_state
+from sklearn.utils.validation import _assert_all_finite, check_array, check_random_state
 
 from .. import _bridge
 from .._config import get_config
@@ -101,7 +101,9 @@ class HipKMeans(BaseGPUEstimator):
         return np.ascontiguousarray(centers, dtype=np.float32)
 
     def fit(self, X, y=None, sample_weight=None):
-        X, _ = self._validate_data(X)
+        # the finiteness check is done on the device once X is resident
+        # (scikit-learn's own check is a sum over X on the host)
+        X = check_array(X, dtype=np.float32, order="C", ensure_min_samples=2, ensure_all_finite=False)
         if sample_weight is not None:
             if get_config().verbose:
                 print("[skmetal_amd] HipKMeans: device=cpu (sample_weight is not supported on the GPU path)")
@@ -123,6 +125,10 @@ class HipKMeans(BaseGPUEstimator):
         plusplus = isinstance(init, str) and init == "k-means++"
         with _bridge.LloydHandle(n, d, k) as h:
             h.load(X, center=True)
+            if not np.isfinite(h.max_abs()):
+                # NaN or infinity in X (or a centring that overflowed): scikit-learn's
+                # check raises its own error for the first two and passes the last
+                _assert_all_finite(X, input_name="X", estimator_name=type(est).__name__)
             for _ in range(n_init):
                 if plusplus:
                     h.plusplus(random_state)

@@ -504,3 +504,41 @@ def test_accelerate_kmeans_plusplus_same_draws_as_sklearn(bridge):
     ref = KMeans(**kw).fit(X)
     parity.check_centers(model.cluster_centers_, ref.cluster_centers_, what="k-means++ centres")
     assert model.n_iter_ == ref.n_iter_
+
+
+@pytest.mark.parametrize("bad,msg", [(np.nan, "NaN"), (np.inf, "infinity"), (-np.inf, "infinity")])
+def test_fit_rejects_non_finite_like_sklearn(bridge, bad, msg):
+    """fit checks finiteness on the device (max |x| of the resident X) and then
+    raises scikit-learn's own error."""
+    from sklearn.cluster import KMeans
+
+    import skmetal_amd
+    from skmetal_amd.estimators.cluster import HipKMeans
+
+    X, _ = _separated_blobs(3000, 12, 4, 5)
+    X[17, 3] = bad
+    model = skmetal_amd.accelerate(KMeans(n_clusters=4, n_init=1, random_state=0))
+    assert isinstance(model, HipKMeans) and model._should_use_gpu(X)  # the GPU path, not the CPU fallback
+    with pytest.raises(ValueError, match=msg):
+        model.fit(X)
+    with pytest.raises(ValueError, match=msg):
+        KMeans(n_clusters=4, n_init=1, random_state=0).fit(X)
+
+
+def test_fit_extreme_finite_values(bridge):
+    """Finite values whose centring overflows fp32 pass the check (scikit-learn
+    accepts them) and the fit still returns finite labels."""
+    from sklearn.cluster import KMeans
+
+    import skmetal_amd
+
+    X = np.zeros((2000, 12), np.float32)
+    X[:1000, 0] = 3.0e38
+    X[1000:, 0] = -3.0e38
+    X[:, 1:] = np.random.default_rng(1).standard_normal((2000, 11)).astype(np.float32)
+    model = skmetal_amd.accelerate(KMeans(n_clusters=2, n_init=1, random_state=0))
+    assert model._should_use_gpu(X)
+    with np.errstate(over="ignore", invalid="ignore"):
+        model.fit(X)
+    assert model.labels_.shape == (2000,)
+    assert model.labels_.min() >= 0 and model.labels_.max() < 2
