@@ -24,6 +24,7 @@ Estimator attributes set after ``fit``: ``cluster_centers_``, ``labels_``
 from __future__ import annotations
 
 import warnings
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 from sklearn.exceptions import ConvergenceWarning
@@ -118,22 +119,30 @@ class HipKMeans(BaseGPUEstimator):
             raise ValueError(f"n_samples={n} should be >= n_clusters={k}.")
         init = est.init
         n_init = self._resolve_n_init(init)
-        tol_abs = _tolerance(X, est.tol)
         random_state = check_random_state(est.random_state)
 
         best = None
         plusplus = isinstance(init, str) and init == "k-means++"
-        with _bridge.LloydHandle(n, d, k) as h:
+        # The tolerance's column variances (host threads, no device) and the first
+        # seeding's random draws run while X is uploaded and centred.  Nothing else
+        # draws from random_state in between, so the draws are those of the serial order.
+        with ThreadPoolExecutor(max_workers=2) as pool, _bridge.LloydHandle(n, d, k) as h:
+            tol_f = pool.submit(_tolerance, X, est.tol)
+            draws_f = pool.submit(_bridge.plusplus_draws, random_state, n, k) if plusplus else None
             h.load(X, center=True)
             if not np.isfinite(h.max_abs()):
                 # NaN or infinity in X (or a centring that overflowed): scikit-learn's
                 # check raises its own error for the first two and passes the last
                 _assert_all_finite(X, input_name="X", estimator_name=type(est).__name__)
-            for _ in range(n_init):
+            tol_abs = None
+            for i in range(n_init):
                 if plusplus:
-                    h.plusplus(random_state)
+                    T, first, u = draws_f.result() if i == 0 else _bridge.plusplus_draws(random_state, n, k)
+                    h.plusplus_with(T, first, u)
                 else:
                     h.set_centers(self._initial_centers(X, init, k, random_state))
+                if tol_abs is None:
+                    tol_abs = tol_f.result()
                 n_iter, inertia = h.run(est.max_iter, tol_abs, strict=True)
                 labels = h.labels()
                 if best is None or (inertia < best[2] and not _same_clustering(labels, best[1], k)):
