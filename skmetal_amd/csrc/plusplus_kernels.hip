@@ -73,20 +73,42 @@ __global__ __launch_bounds__(256) void k_pp_dist(PPArgs a, int c, int Tc)
                 if (4 * q < fl && r0 + lr < a.n) pre[i] = *reinterpret_cast<const float4*>(a.X + (r0 + lr) * a.ld + f0 + 4 * q);
             }
         };
+        // the candidates' values of a segment: element e = tid + 256 j is
+        // feature e % kFS (= tid % kFS) of candidate e / kFS; they are loaded
+        // with the segment's rows, so no dependent load waits between barriers
+        constexpr int CE = (TP * kFS + 255) / 256;
+        long coff[CE];
+        float cpre[CE];
+#pragma unroll
+        for (int j = 0; j < CE; ++j) {
+            const int t = (tid + 256 * j) / kFS;
+            coff[j] = t < tn ? a.cand[t0 + t] * a.ld : -1;
+        }
+        auto load_cand = [&](int f0) {
+            const int f = tid % kFS;
+#pragma unroll
+            for (int j = 0; j < CE; ++j) {
+                cpre[j] = 0.f;
+                if (coff[j] >= 0 && f < a.ld - f0) cpre[j] = a.X[coff[j] + f0 + f];
+            }
+        };
         load_seg(0);
+        load_cand(0);
         for (int f0 = 0; f0 < a.ld; f0 += kFS) {
             const int fl = min(kFS, a.ld - f0);  // a multiple of 4 (ld is)
             __syncthreads();
 #pragma unroll
             for (int i = 0; i < 8; ++i) xs4[(((tid >> 3) + 32 * i) * kXS) / 4 + q] = pre[i];
-            for (int e = tid; e < TP * kFS; e += 256) {
-                const int t = e / kFS, f = e % kFS;
-                double v = 0.0;
-                if (t < tn && f < fl) v = (double)a.X[a.cand[t0 + t] * a.ld + f0 + f];
-                cs[t][f] = v;
+#pragma unroll
+            for (int j = 0; j < CE; ++j) {
+                const int e = tid + 256 * j;
+                if (e < TP * kFS) (&cs[0][0])[e] = (double)cpre[j];
             }
             __syncthreads();
-            if (f0 + kFS < a.ld) load_seg(f0 + kFS);  // in flight during this segment's work
+            if (f0 + kFS < a.ld) {  // in flight during this segment's work
+                load_seg(f0 + kFS);
+                load_cand(f0 + kFS);
+            }
             if (tid < TP)
                 for (int f = 0; f < kFS; ++f) cc = fma(cs[tid][f], cs[tid][f], cc);
 #pragma unroll
@@ -147,29 +169,42 @@ __device__ __forceinline__ double wave_scan(double v, int lane)
 
 __global__ __launch_bounds__(1024) void k_pp_select(PPArgs a, int c)
 {
-    __shared__ double wpot[16][kPPMaxTrials];
+    static_assert(kPPRows == 4 * 64, "the row search gives each lane 4 rows");
+    constexpr int TB = 8;  // candidates whose partials are summed together
     __shared__ double wsum[16];
+    __shared__ double wpot[16][TB];
     __shared__ double rv[kPPMaxTrials];
     __shared__ int found[kPPMaxTrials];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int q = (c - 1) & 1;
     const int Tq = c == 1 ? 1 : a.T;
 
-    // centre c - 1: the candidate of least potential (first one on ties);
-    // each potential is a fixed-order sum of the block partials
-    for (int t = 0; t < Tq; ++t) {
-        double v = 0.0;
-        for (int b = tid; b < a.nb; b += 1024) v += a.P[q][(long)t * a.nb + b];
-        v = wave_sum(v);
-        if (lane == 0) wpot[wv][t] = v;
+    // centre c - 1: the candidate of least potential (first one on ties).
+    // Each potential is a fixed-order sum of the block partials: thread i adds
+    // blocks i, i + 1024, ... (the loads of TB candidates in flight together),
+    // then a butterfly per wave, then the 16 waves in order.
+    for (int t0 = 0; t0 < Tq; t0 += TB) {
+        double v[TB];
+#pragma unroll
+        for (int t = 0; t < TB; ++t) v[t] = 0.0;
+        for (int b = tid; b < a.nb; b += 1024) {
+#pragma unroll
+            for (int t = 0; t < TB; ++t)
+                if (t0 + t < Tq) v[t] += a.P[q][(long)(t0 + t) * a.nb + b];
+        }
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+            const double w = wave_sum(v[t]);
+            if (lane == 0) wpot[wv][t] = w;
+        }
+        __syncthreads();
+        if (tid < TB && t0 + tid < Tq) {
+            double w = 0.0;
+            for (int i = 0; i < 16; ++i) w += wpot[i][tid];
+            rv[t0 + tid] = w;
+        }
+        __syncthreads();
     }
-    __syncthreads();
-    if (tid < Tq) {
-        double v = 0.0;
-        for (int w = 0; w < 16; ++w) v += wpot[w][tid];
-        rv[tid] = v;
-    }
-    __syncthreads();
     double bestpot = rv[0];
     int best = 0;
     for (int t = 1; t < Tq; ++t)
@@ -193,46 +228,80 @@ __global__ __launch_bounds__(1024) void k_pp_select(PPArgs a, int c)
         rv[t] = a.U[(long)(c - 1) * a.T + t] * pot32;
         found[t] = INT_MAX;
     }
+
+    // running sum over the blocks' sums in one pass: thread i owns blocks
+    // [m i, m i + m); its start is the scan of the thread totals before it.
+    // found[t] = the first block whose running sum reaches r_t.
+    const double* S = a.P[q] + (long)best * a.nb;
+    const int m = (a.nb + 1023) / 1024;
+    const int b0 = m * tid, b1 = min(a.nb, b0 + m);
+    double own = 0.0;
+    for (int b = b0; b < b1; ++b) own += S[b];
+    const double incl = wave_scan(own, lane);
+    if (lane == 63) wsum[wv] = incl;
+    double excl = __shfl_up(incl, 1, 64);
+    if (lane == 0) excl = 0.0;
+    __syncthreads();  // wsum, rv and found
+    double run0 = 0.0;
+    for (int w = 0; w < wv; ++w) run0 += wsum[w];
+    run0 += excl;
+    double run = run0;
+    for (int b = b0; b < b1; ++b) {
+        run += S[b];
+        a.pfx[b] = run;
+    }
+    // a thread's running sum only grows, so the first lane of a wave whose last
+    // value reaches r_t holds the wave's first such block: it alone finds it
+    // (the same additions again) and posts it
+    for (int t = 0; t < a.T; ++t) {
+        const unsigned long long msk = __ballot(b0 < b1 && run >= rv[t]);
+        if (msk != 0ull && lane == __ffsll((long long)msk) - 1) {
+            double r = run0;
+            int bf = b1 - 1;
+            for (int b = b0; b < b1; ++b) {
+                r += S[b];
+                if (r >= rv[t]) {
+                    bf = b;
+                    break;
+                }
+            }
+            atomicMin(&found[t], bf);
+        }
+    }
     __syncthreads();
 
-    // running sum over the blocks' sums; found[t] = first block reaching r_t
-    const double* S = a.P[q] + (long)best * a.nb;
-    double carry = 0.0;
-    for (int b0 = 0; b0 < a.nb; b0 += 1024) {
-        const int b = b0 + tid;
-        const double v = wave_scan(b < a.nb ? S[b] : 0.0, lane);
-        if (lane == 63) wsum[wv] = v;
-        __syncthreads();
-        double off = carry;
-        for (int w = 0; w < wv; ++w) off += wsum[w];
-        const double incl = off + v;
-        if (b < a.nb) {
-            a.pfx[b] = incl;
-            for (int t = 0; t < a.T; ++t)
-                if (incl >= rv[t]) atomicMin(&found[t], b);
-        }
-        for (int w = 0; w < 16; ++w) carry += wsum[w];
-        __syncthreads();
-    }
-
-    // within that block: the first row whose running sum reaches r_t
+    // within that block: the first row whose running sum reaches r_t; lane l
+    // holds rows 4l .. 4l + 3 of the block, all loaded at once
     const float* Dq = a.D[q] + (long)best * a.n;
     for (int t = wv; t < a.T; t += 16) {
         const int b = found[t];
         long pick = a.n - 1;
         if (b != INT_MAX) {
-            double base = b > 0 ? a.pfx[b - 1] : 0.0;
+            const double base = b > 0 ? a.pfx[b - 1] : 0.0;
             const long r0 = (long)b * kPPRows, r1 = min(a.n, r0 + (long)kPPRows);
+            const long i0 = r0 + 4 * lane;
+            float dv[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dv[j] = i0 + j < r1 ? Dq[i0 + j] : 0.f;
+            double sj[4], acc = 0.0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc += (double)dv[j];
+                sj[j] = acc;
+            }
+            const double inc = wave_scan(acc, lane);
+            double ex = __shfl_up(inc, 1, 64);
+            if (lane == 0) ex = 0.0;
+            const double lb = base + ex;
+            int jf = 4;
+#pragma unroll
+            for (int j = 3; j >= 0; --j)
+                if (i0 + j < r1 && lb + sj[j] >= rv[t]) jf = j;
+            const unsigned long long msk = __ballot(jf < 4);
             pick = r1 - 1;
-            for (long r = r0; r < r1; r += 64) {
-                const long i = r + lane;
-                const double v = wave_scan(i < r1 ? (double)Dq[i] : 0.0, lane);
-                const unsigned long long m = __ballot(i < r1 && base + v >= rv[t]);
-                if (m != 0ull) {
-                    pick = r + __ffsll((long long)m) - 1;
-                    break;
-                }
-                base += __shfl(v, 63, 64);
+            if (msk != 0ull) {
+                const int L = __ffsll((long long)msk) - 1;
+                pick = r0 + 4 * L + __shfl(jf, L, 64);
             }
         }
         if (lane == 0) a.cand[t] = pick;
@@ -244,14 +313,22 @@ __global__ __launch_bounds__(1024) void k_pp_select(PPArgs a, int c)
 hipError_t launch_pp_dist(const PPArgs& a, int c, hipStream_t s)
 {
     const dim3 grid((unsigned)a.nb), block(256);
-    if (c == 0)
-        hipLaunchKernelGGL(k_pp_dist<1>, grid, block, 0, s, a, 0, 1);
-    else if (a.T <= 4)
-        hipLaunchKernelGGL(k_pp_dist<4>, grid, block, 0, s, a, c, a.T);
-    else if (a.T <= 8)
-        hipLaunchKernelGGL(k_pp_dist<8>, grid, block, 0, s, a, c, a.T);
-    else
-        hipLaunchKernelGGL(k_pp_dist<16>, grid, block, 0, s, a, c, a.T);
+    // one pass over X for T <= 16 (the candidate count exactly for T <= 8,
+    // the usual 2 + ln k), passes of 16 beyond
+    const int T = c == 0 ? 1 : a.T;
+    switch (T) {
+    case 1: hipLaunchKernelGGL(k_pp_dist<1>, grid, block, 0, s, a, c, T); break;
+    case 2: hipLaunchKernelGGL(k_pp_dist<2>, grid, block, 0, s, a, c, T); break;
+    case 3: hipLaunchKernelGGL(k_pp_dist<3>, grid, block, 0, s, a, c, T); break;
+    case 4: hipLaunchKernelGGL(k_pp_dist<4>, grid, block, 0, s, a, c, T); break;
+    case 5: hipLaunchKernelGGL(k_pp_dist<5>, grid, block, 0, s, a, c, T); break;
+    case 6: hipLaunchKernelGGL(k_pp_dist<6>, grid, block, 0, s, a, c, T); break;
+    case 7: hipLaunchKernelGGL(k_pp_dist<7>, grid, block, 0, s, a, c, T); break;
+    case 8: hipLaunchKernelGGL(k_pp_dist<8>, grid, block, 0, s, a, c, T); break;
+    default:
+        if (T <= 12) hipLaunchKernelGGL(k_pp_dist<12>, grid, block, 0, s, a, c, T);
+        else hipLaunchKernelGGL(k_pp_dist<16>, grid, block, 0, s, a, c, T);
+    }
     return hipGetLastError();
 }
 
