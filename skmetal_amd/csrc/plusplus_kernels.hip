@@ -37,16 +37,18 @@ constexpr int kFS = 32;         // features per LDS segment (one 128-byte run pe
 constexpr int kXS = kFS + 4;    // LDS row stride (floats): 144 bytes keeps 8 lanes' float4 reads on distinct banks
 
 // Centre c's candidate distances, TP candidates per pass (Tc in all).  The
-// block's 256 rows go through LDS one 32-feature segment at a time: eight
+// block's kPPRows rows go through LDS one 32-feature segment at a time: eight
 // lanes load one row's 128-byte run (coalesced), then thread r works on row r.
 // ||x||^2 and the candidates' ||c||^2 come from the same staged values.
 template <int TP>
-__global__ __launch_bounds__(256) void k_pp_dist(PPArgs a, int c, int Tc)
+__global__ __launch_bounds__(kPPRows) void k_pp_dist(PPArgs a, int c, int Tc)
 {
     __shared__ float4 xs4[kPPRows * kXS / 4];
     __shared__ double cs[TP][kFS];
     __shared__ double ccs[TP];
-    __shared__ double red[4][TP];
+    constexpr int NW = kPPRows / 64;  // waves
+    constexpr int RG = kPPRows / 8;   // rows loaded per instruction (8 lanes a row)
+    __shared__ double red[NW][TP];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const long r0 = (long)blockIdx.x * kPPRows;
     const long row = r0 + tid;
@@ -61,27 +63,27 @@ __global__ __launch_bounds__(256) void k_pp_dist(PPArgs a, int c, int Tc)
 #pragma unroll
         for (int t = 0; t < TP; ++t) acc[t] = 0.0;
         double xx = 0.0, cc = 0.0;
-        // segment f0's runs: lane group tid >> 3 loads rows (tid >> 3) + 32 i
+        // segment f0's runs: lane group tid >> 3 loads rows (tid >> 3) + RG i
         const int q = tid & 7;
         float4 pre[8];
         auto load_seg = [&](int f0) {
             const int fl = min(kFS, a.ld - f0);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const int lr = (tid >> 3) + 32 * i;
+                const int lr = (tid >> 3) + RG * i;
                 pre[i] = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (4 * q < fl && r0 + lr < a.n) pre[i] = *reinterpret_cast<const float4*>(a.X + (r0 + lr) * a.ld + f0 + 4 * q);
             }
         };
-        // the candidates' values of a segment: element e = tid + 256 j is
+        // the candidates' values of a segment: element e = tid + kPPRows j is
         // feature e % kFS (= tid % kFS) of candidate e / kFS; they are loaded
         // with the segment's rows, so no dependent load waits between barriers
-        constexpr int CE = (TP * kFS + 255) / 256;
+        constexpr int CE = (TP * kFS + kPPRows - 1) / kPPRows;
         long coff[CE];
         float cpre[CE];
 #pragma unroll
         for (int j = 0; j < CE; ++j) {
-            const int t = (tid + 256 * j) / kFS;
+            const int t = (tid + kPPRows * j) / kFS;
             coff[j] = t < tn ? a.cand[t0 + t] * a.ld : -1;
         }
         auto load_cand = [&](int f0) {
@@ -98,10 +100,10 @@ __global__ __launch_bounds__(256) void k_pp_dist(PPArgs a, int c, int Tc)
             const int fl = min(kFS, a.ld - f0);  // a multiple of 4 (ld is)
             __syncthreads();
 #pragma unroll
-            for (int i = 0; i < 8; ++i) xs4[(((tid >> 3) + 32 * i) * kXS) / 4 + q] = pre[i];
+            for (int i = 0; i < 8; ++i) xs4[(((tid >> 3) + RG * i) * kXS) / 4 + q] = pre[i];
 #pragma unroll
             for (int j = 0; j < CE; ++j) {
-                const int e = tid + 256 * j;
+                const int e = tid + kPPRows * j;
                 if (e < TP * kFS) (&cs[0][0])[e] = (double)cpre[j];
             }
             __syncthreads();
@@ -152,7 +154,12 @@ __global__ __launch_bounds__(256) void k_pp_dist(PPArgs a, int c, int Tc)
         }
         __syncthreads();
         if (tid < tn)
-            a.P[p][(long)(t0 + tid) * a.nb + blockIdx.x] = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+        {
+            double v = red[0][tid];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) v += red[w][tid];
+            a.P[p][(long)(t0 + tid) * a.nb + blockIdx.x] = v;
+        }
     }
 }
 
@@ -169,7 +176,8 @@ __device__ __forceinline__ double wave_scan(double v, int lane)
 
 __global__ __launch_bounds__(1024) void k_pp_select(PPArgs a, int c)
 {
-    static_assert(kPPRows == 4 * 64, "the row search gives each lane 4 rows");
+    constexpr int RPL = kPPRows / 64;  // rows per lane in the row search
+    static_assert(kPPRows % 64 == 0, "the row search gives each lane whole rows");
     constexpr int TB = 8;  // candidates whose partials are summed together
     __shared__ double wsum[16];
     __shared__ double wpot[16][TB];
@@ -271,7 +279,7 @@ __global__ __launch_bounds__(1024) void k_pp_select(PPArgs a, int c)
     __syncthreads();
 
     // within that block: the first row whose running sum reaches r_t; lane l
-    // holds rows 4l .. 4l + 3 of the block, all loaded at once
+    // holds rows RPL l .. RPL l + RPL - 1 of the block, all loaded at once
     const float* Dq = a.D[q] + (long)best * a.n;
     for (int t = wv; t < a.T; t += 16) {
         const int b = found[t];
@@ -279,13 +287,13 @@ __global__ __launch_bounds__(1024) void k_pp_select(PPArgs a, int c)
         if (b != INT_MAX) {
             const double base = b > 0 ? a.pfx[b - 1] : 0.0;
             const long r0 = (long)b * kPPRows, r1 = min(a.n, r0 + (long)kPPRows);
-            const long i0 = r0 + 4 * lane;
-            float dv[4];
+            const long i0 = r0 + RPL * lane;
+            float dv[RPL];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) dv[j] = i0 + j < r1 ? Dq[i0 + j] : 0.f;
-            double sj[4], acc = 0.0;
+            for (int j = 0; j < RPL; ++j) dv[j] = i0 + j < r1 ? Dq[i0 + j] : 0.f;
+            double sj[RPL], acc = 0.0;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < RPL; ++j) {
                 acc += (double)dv[j];
                 sj[j] = acc;
             }
@@ -293,15 +301,15 @@ __global__ __launch_bounds__(1024) void k_pp_select(PPArgs a, int c)
             double ex = __shfl_up(inc, 1, 64);
             if (lane == 0) ex = 0.0;
             const double lb = base + ex;
-            int jf = 4;
+            int jf = RPL;
 #pragma unroll
-            for (int j = 3; j >= 0; --j)
+            for (int j = RPL - 1; j >= 0; --j)
                 if (i0 + j < r1 && lb + sj[j] >= rv[t]) jf = j;
-            const unsigned long long msk = __ballot(jf < 4);
+            const unsigned long long msk = __ballot(jf < RPL);
             pick = r1 - 1;
             if (msk != 0ull) {
                 const int L = __ffsll((long long)msk) - 1;
-                pick = r0 + 4 * L + __shfl(jf, L, 64);
+                pick = r0 + RPL * L + __shfl(jf, L, 64);
             }
         }
         if (lane == 0) a.cand[t] = pick;
@@ -312,7 +320,7 @@ __global__ __launch_bounds__(1024) void k_pp_select(PPArgs a, int c)
 
 hipError_t launch_pp_dist(const PPArgs& a, int c, hipStream_t s)
 {
-    const dim3 grid((unsigned)a.nb), block(256);
+    const dim3 grid((unsigned)a.nb), block(kPPRows);
     // one pass over X for T <= 16 (the candidate count exactly for T <= 8,
     // the usual 2 + ln k), passes of 16 beyond
     const int T = c == 0 ? 1 : a.T;
