@@ -170,6 +170,18 @@ SKMETAL_API int skmetal_hip_column_variance(const float* X, size_t n, size_t d, 
  * its own pass over X.  A non-finite value can also come from a centring
  * that overflowed, so the caller then checks X itself. */
 SKMETAL_API int skmetal_hip_lloyd_max_abs(skmetal_hip_lloyd* h, float* out);
+/* One k-means|| round on the loaded X: the squared distance of every row to
+ * its nearest candidate so far, kept on the device and lowered with the m new
+ * candidate rows (indices into X); reset = 1 starts from +inf (required on the
+ * first call).  dists_out [n] (nullable) receives the result.  Replaces the
+ * per-round skmetal_kmeans_assign + skmetal_compute_mindists pair of
+ * MetalKMeans._kmeans_parallel_init (skmetal/estimators/cluster.py:92-93),
+ * each of which uploads X again; the distance to the assigned candidate is the
+ * minimum over the candidates.  Distances are scikit-learn's fp32 form (fp64
+ * expanded distance, cast to fp32, negatives to 0), as in the k-means++ entry
+ * points. */
+SKMETAL_API int skmetal_hip_lloyd_mindists(skmetal_hip_lloyd* h, const int64_t* rows, size_t m, int reset,
+                                           float* dists_out);
 /* *fused & 3 = 0 when a step runs as separate E-step and update kernels, 1
  * when as one fused E-step + sums kernel with the E-step on fp32 MFMA
  * (k <= 64, d <= 100), 2 when that kernel's E-step runs on fp16 MFMA with x

@@ -34,6 +34,14 @@ Parity status per function (what pins it, see tests/test_oracle.py):
 * ``transform``   -- scikit-learn's KMeans.transform bit for bit on 4 golden inputs
                      (tests/golden/transform.npz), closed forms, planted mistakes
                      (tests/test_transform_oracle.py).
+* ``kmeans_parallel_init`` (skmetal's k-means||) -- its distances against
+                     scikit-learn's euclidean_distances(squared=True) and brute
+                     force; the first draw, the round count, the {0} taken-set
+                     rule and the cyclic fill by properties
+                     (tests/test_kpar_oracle.py).  The sampling loop itself is
+                     parity unpinned: the reference runs it over its Metal
+                     kernels, which cannot run here, and its tests hold no
+                     vectors for it.
 """
 
 from __future__ import annotations
@@ -320,6 +328,68 @@ def kmeans_plusplus(X, k: int, first: int, uniforms, n_local_trials: int, trace:
     if trace:
         return idx, cands, pots
     return idx
+
+
+def parallel_mindists(X):
+    """The k-means|| rounds' distances on the CPU: returns mindists(rows, reset),
+    the fp32 squared distance of every row of X to its nearest candidate so far
+    (_upcast_sqdist of each candidate row, min), lowered with `rows`; reset
+    starts from +inf."""
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    X64 = X.astype(np.float64)
+    xx = np.einsum("ij,ij->i", X64, X64)
+    state = {}
+
+    def mindists(rows, reset):
+        if reset:
+            state["c"] = np.full(X.shape[0], np.inf, dtype=np.float32)
+        if len(rows):
+            np.minimum(state["c"], _upcast_sqdist(X, np.asarray(rows, dtype=np.int64), X64, xx).min(axis=0),
+                       out=state["c"])
+        return state["c"].copy()
+
+    return mindists
+
+
+def kmeans_parallel_init(X, k: int, rng, mindists=None, trace: bool = False):
+    """skmetal's k-means|| seeding, MetalKMeans._kmeans_parallel_init
+    (skmetal/estimators/cluster.py:70-116), with `rng` a numpy RandomState:
+    first row rng.randint(n) (:77); max(1, int(2 + ln k)) rounds (:83); each
+    round the squared distance of every row to its assigned candidate, i.e. the
+    nearest one (:91-93; here _upcast_sqdist, min over the candidates), floored
+    at 1e-30 and normalised in fp32 (:94-95), then rng.choice(n, min(k, n),
+    p, replace=False) (:97-98); new indices join in draw order, the taken set
+    starting as {0} as the reference's does (:85,99-102); more than k
+    candidates are pruned by one scikit-learn KMeans iteration from the first
+    k (:112-116), fewer are repeated cyclically (:105-110).
+    mindists(rows, reset) may replace the CPU distances (the device's, for a
+    cross-check).  Returns the k centroids (and, with trace, the candidate rows)."""
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    n, d = X.shape
+    if mindists is None:
+        mindists = parallel_mindists(X)
+    first = int(rng.randint(n))
+    rows, taken, new = [first], {0}, [first]
+    for r in range(max(1, int(2 + np.log(k)))):
+        dists = np.maximum(mindists(new, r == 0), 1e-30)
+        probs = dists / dists.sum()
+        new = []
+        for i in rng.choice(n, size=min(k, n), p=probs, replace=False):
+            if i not in taken:
+                taken.add(i)
+                rows.append(int(i))
+                new.append(int(i))
+    cand = X[np.asarray(rows, dtype=np.int64)]
+    if cand.shape[0] <= k:
+        out = np.empty((k, d), dtype=np.float32)
+        for i in range(k):
+            out[i] = cand[i % cand.shape[0]]
+    else:
+        from sklearn.cluster import KMeans
+
+        out = KMeans(n_clusters=k, init=cand[:k], n_init=1, max_iter=1, random_state=rng).fit(cand)
+        out = out.cluster_centers_.astype(np.float32)
+    return (out, rows) if trace else out
 
 
 def transform(X, C):

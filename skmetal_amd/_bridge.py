@@ -66,6 +66,7 @@ _REGISTRY = [
     ("skmetal_hip_kmeans_transform", ctypes.c_int, _vp, _vp, _vp, _c_size, _c_size, _c_size),
     ("skmetal_hip_column_variance", ctypes.c_int, _vp, _c_size, _c_size, _vp),
     ("skmetal_hip_lloyd_max_abs", ctypes.c_int, _vp, ctypes.POINTER(ctypes.c_float)),
+    ("skmetal_hip_lloyd_mindists", ctypes.c_int, _vp, _vp, _c_size, ctypes.c_int, _vp),
 ]
 
 SKMETAL_FIT_STRICT = 1
@@ -354,6 +355,16 @@ class LloydHandle:
         v = ctypes.c_float(0.0)
         _check(_lib.skmetal_hip_lloyd_max_abs(self._h, ctypes.byref(v)), "skmetal_hip_lloyd_max_abs")
         return float(v.value)
+
+    def mindists(self, rows, reset: bool = False):
+        """k-means|| round: squared distance of every loaded row to its nearest
+        candidate so far, lowered with the candidate rows `rows` (indices into X);
+        reset starts from +inf.  Returns float32 [n]."""
+        r = np.ascontiguousarray(rows, dtype=np.int64).reshape(-1)
+        out = np.empty(self.n, np.float32)
+        _check(_lib.skmetal_hip_lloyd_mindists(self._h, r.ctypes.data if r.size else None, r.size, int(bool(reset)),
+                                               out.ctypes.data), "skmetal_hip_lloyd_mindists")
+        return out
 
     def info(self):
         fused = ctypes.c_int(0)

@@ -208,9 +208,14 @@ struct PPArgs {
     double* pot;           // [k] potential after each centre (fp64 total)
     const double* U;       // [(k - 1) x T] uniforms in [0, 1), in sklearn's draw order
     float* centers;        // [k x ld] the chosen rows of X
+    float* mind;           // [n] k-means||: running minimum distance over the candidates so far
+    int mind_reset;        // k-means||: 1 = start the minimum from +inf
 };
 // Candidate distances of centre c (c = 0: the first row alone).
 hipError_t launch_pp_dist(const PPArgs& a, int c, hipStream_t s);
+// k-means||: mind[row] = min(mind[row] (or +inf with mind_reset), distance to
+// each of the m candidate rows cand[0 .. m-1]), distances in the same form.
+hipError_t launch_pp_mindist(const PPArgs& a, int m, hipStream_t s);
 // Pick centre c - 1 among its candidates; for c < k draw centre c's candidates.
 hipError_t launch_pp_select(const PPArgs& a, int c, hipStream_t s);
 

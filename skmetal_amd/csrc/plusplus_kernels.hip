@@ -40,7 +40,11 @@ constexpr int kXS = kFS + 4;    // LDS row stride (floats): 144 bytes keeps 8 la
 // block's kPPRows rows go through LDS one 32-feature segment at a time: eight
 // lanes load one row's 128-byte run (coalesced), then thread r works on row r.
 // ||x||^2 and the candidates' ||c||^2 come from the same staged values.
-template <int TP>
+//
+// MIN = true (k-means||): the row's running minimum over every candidate so
+// far, a.mind[row], is updated with the Tc candidates (started from +inf when
+// a.mind_reset); no per-candidate minima or block sums are written.
+template <int TP, bool MIN = false>
 __global__ __launch_bounds__(kPPRows) void k_pp_dist(PPArgs a, int c, int Tc)
 {
     __shared__ float4 xs4[kPPRows * kXS / 4];
@@ -55,7 +59,11 @@ __global__ __launch_bounds__(kPPRows) void k_pp_dist(PPArgs a, int c, int Tc)
     const bool live = row < a.n;
     const int p = c & 1;
     float closest = INFINITY;
-    if (c > 0 && live) closest = a.D[p ^ 1][(long)a.best[c - 1] * a.n + row];
+    if (MIN) {
+        if (!a.mind_reset && live) closest = a.mind[row];
+    } else if (c > 0 && live) {
+        closest = a.D[p ^ 1][(long)a.best[c - 1] * a.n + row];
+    }
 
     for (int t0 = 0; t0 < Tc; t0 += TP) {
         const int tn = min(TP, Tc - t0);
@@ -136,6 +144,17 @@ __global__ __launch_bounds__(kPPRows) void k_pp_dist(PPArgs a, int c, int Tc)
         }
         if (tid < TP) ccs[tid] = cc;
         __syncthreads();
+        if (MIN) {
+            // the next pass rewrites ccs only after its first segment barrier
+#pragma unroll
+            for (int t = 0; t < TP; ++t)
+                if (t < tn && live) {
+                    float d32 = (float)((-2.0 * acc[t] + ccs[t]) + xx);
+                    if (d32 < 0.f) d32 = 0.f;
+                    closest = d32 < closest ? d32 : closest;
+                }
+            continue;
+        }
         // distances, minima with the closest so far, block sums
 #pragma unroll
         for (int t = 0; t < TP; ++t) {
@@ -161,6 +180,7 @@ __global__ __launch_bounds__(kPPRows) void k_pp_dist(PPArgs a, int c, int Tc)
             a.P[p][(long)(t0 + tid) * a.nb + blockIdx.x] = v;
         }
     }
+    if (MIN && live) a.mind[row] = closest;
 }
 
 // Inclusive scan over the 64 lanes of a wave (fixed order).
@@ -337,6 +357,16 @@ hipError_t launch_pp_dist(const PPArgs& a, int c, hipStream_t s)
         if (T <= 12) hipLaunchKernelGGL(k_pp_dist<12>, grid, block, 0, s, a, c, T);
         else hipLaunchKernelGGL(k_pp_dist<16>, grid, block, 0, s, a, c, T);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_pp_mindist(const PPArgs& a, int m, hipStream_t s)
+{
+    const dim3 grid((unsigned)a.nb), block(kPPRows);
+    if (m <= 8)
+        hipLaunchKernelGGL((k_pp_dist<8, true>), grid, block, 0, s, a, 0, m);
+    else
+        hipLaunchKernelGGL((k_pp_dist<16, true>), grid, block, 0, s, a, 0, m);
     return hipGetLastError();
 }
 

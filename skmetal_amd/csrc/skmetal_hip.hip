@@ -868,6 +868,51 @@ struct Lloyd {
         return 0;
     }
 
+    // k-means|| rounds (skmetal's MetalKMeans._kmeans_parallel_init): the
+    // squared distance of every row to its nearest candidate so far, kept on
+    // the device and lowered with each round's new candidate rows (reset
+    // starts it from +inf).  Distances are sklearn's fp32 form, as k-means++'s.
+    float* kp_mind = nullptr;
+    long* kp_cand = nullptr;
+    long kp_cap = 0;
+    bool kp_valid = false;
+
+    int mindists(const long* rows, long m, int reset, float* out)
+    {
+        if (n >= (1L << 31)) return fail(SKMETAL_ERANGE, "k-means|| rounds support n < 2^31 rows (n=%ld)", n);
+        if (m < 0 || m > (1L << 30)) return fail(SKMETAL_ERANGE, "m=%ld candidate rows out of range", m);
+        if (m > 0 && rows == nullptr) return fail(SKMETAL_EINVAL, "null candidate rows");
+        if (!reset && !kp_valid) return fail(SKMETAL_EINVAL, "the first k-means|| round must reset the distances");
+        for (long i = 0; i < m; ++i)
+            if (rows[i] < 0 || rows[i] >= n) return fail(SKMETAL_EINVAL, "candidate row %ld not in [0, %ld)", rows[i], n);
+        if (kp_mind == nullptr) TRY(grab((void**)&kp_mind, size_t(n) * sizeof(float)));
+        if (m > kp_cap) {
+            const long cap = std::max<long>(m, 2 * kp_cap);
+            if (kp_cand != nullptr) {
+                C->release(kp_cand);
+                owned.erase(std::find(owned.begin(), owned.end(), (void*)kp_cand));
+                kp_cand = nullptr;
+            }
+            TRY(grab((void**)&kp_cand, size_t(cap) * sizeof(long)));
+            kp_cap = cap;
+        }
+        if (m > 0 || reset) {
+            PPArgs a{};
+            a.X = X;
+            a.n = n;
+            a.ld = ld;
+            a.nb = (int)((n + kPPRows - 1) / kPPRows);
+            a.cand = kp_cand;
+            a.mind = kp_mind;
+            a.mind_reset = reset ? 1 : 0;
+            if (m > 0) TRY(upload_bytes(*C, rows, size_t(m) * sizeof(long), kp_cand, s));
+            HIP_TRY(launch_pp_mindist(a, (int)m, s), "mindist launch");
+        }
+        kp_valid = true;
+        if (out != nullptr) TRY(download_bytes(*C, kp_mind, size_t(n) * sizeof(float), out, s));
+        return 0;
+    }
+
     // Full sklearn fit from the current centres: loop, final E-step, inertia.
     int fit(long max_iter, double tol, int flags, int* n_iter_out, double* inertia_out)
     {
@@ -1200,6 +1245,17 @@ int skmetal_hip_lloyd_plusplus(skmetal_hip_lloyd* h, size_t n_local_trials, int6
     static_assert(sizeof(long) == sizeof(int64_t), "64-bit long expected");
     TRY(h->L.plusplus((int)std::min<size_t>(n_local_trials, size_t(kPPMaxTrials) + 1), (long)first_index, uniforms,
                       reinterpret_cast<long*>(indices_out)));
+    HIP_TRY(hipStreamSynchronize(h->L.s), "hipStreamSynchronize");
+    return 0;
+}
+
+int skmetal_hip_lloyd_mindists(skmetal_hip_lloyd* h, const int64_t* rows, size_t m, int reset, float* dists_out)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!h) return fail(SKMETAL_EINVAL, "null pointer argument");
+    if (m > (size_t(1) << 30)) return fail(SKMETAL_ERANGE, "m=%zu candidate rows out of range", m);
+    TRY(h->L.mindists(reinterpret_cast<const long*>(rows), (long)m, reset, dists_out));
     HIP_TRY(hipStreamSynchronize(h->L.s), "hipStreamSynchronize");
     return 0;
 }

@@ -207,5 +207,113 @@ class HipKMeans(BaseGPUEstimator):
         return -float(v)
 
 
-# name kept for code written against skmetal
-MetalKMeans = HipKMeans
+def kmeans_parallel_init(X: np.ndarray, k: int, rng, handle) -> np.ndarray:
+    """skmetal's k-means|| seeding, MetalKMeans._kmeans_parallel_init
+    (skmetal/estimators/cluster.py:70-116), with its distance rounds on the
+    device: `handle` holds X (uploaded once) and keeps every row's squared
+    distance to its nearest candidate, lowered with each round's new rows
+    (skmetal_hip_lloyd_mindists).  The distance to the assigned candidate that
+    the reference's kmeans_assign + compute_mindists pair gives is that
+    minimum.  Sampling and pruning are the reference's, on the host: rounds =
+    max(1, int(2 + ln k)); min(k, n) rows drawn without replacement with
+    probability proportional to max(dist, 1e-30); the set of taken indices
+    starts as {0}, as the reference's does; more than k candidates are pruned
+    by one scikit-learn KMeans iteration from the first k."""
+    n, d = X.shape
+    first = int(rng.randint(n))
+    n_rounds = max(1, int(2 + np.log(k)))
+    rows = [first]
+    taken = {0}
+    new = [first]
+    for r in range(n_rounds):
+        dists = handle.mindists(new, reset=(r == 0))
+        dists = np.maximum(dists, 1e-30)
+        probs = dists / dists.sum()
+        idx = rng.choice(n, size=min(k, n), p=probs, replace=False)
+        new = []
+        for i in idx:
+            if i not in taken:
+                taken.add(i)
+                rows.append(int(i))
+                new.append(int(i))
+    cand = X[np.asarray(rows, dtype=np.int64)]
+    if cand.shape[0] <= k:
+        centroids = np.empty((k, d), dtype=np.float32)
+        centroids[: cand.shape[0]] = cand
+        for i in range(cand.shape[0], k):
+            centroids[i] = cand[i % cand.shape[0]]
+        return centroids
+    from sklearn.cluster import KMeans as SklearnKMeans
+
+    km = SklearnKMeans(n_clusters=k, init=cand[:k], n_init=1, max_iter=1, random_state=rng)
+    km.fit(cand)
+    return km.cluster_centers_.astype(np.float32)
+
+
+class MetalKMeans(BaseGPUEstimator):
+    """skmetal's MetalKMeans (skmetal/estimators/cluster.py:18-146) on the MI355X,
+    for code that wants its behaviour rather than scikit-learn's: k-means||
+    seeding per init attempt (distance rounds on the device, X uploaded once
+    for all attempts), then the reference's call sequence per attempt,
+    kmeans_batch_fused with the estimator's tol as given and kmeans_inertia,
+    keeping the attempt of lowest inertia.  n_iter_ is the last attempt's, as in
+    the reference.  HipKMeans is the registered KMeans (scikit-learn's fit)."""
+
+    def fit(self, X, y=None, **kwargs):
+        X, _ = self._validate_data(X, y)
+        if not self._should_use_gpu(X):
+            return self._fallback_fit(X, y, **kwargs)
+        est = self._estimator
+        n, d = X.shape
+        k = int(est.n_clusters)
+        if n < k:
+            raise ValueError(f"n_samples={n} should be >= n_clusters={k}.")
+        max_iter = est.max_iter
+        tol = est.tol
+        n_init = est.n_init
+        if n_init == "auto":
+            init = getattr(est, "init", "k-means++")
+            n_init = 1 if isinstance(init, str) and init == "k-means++" else (10 if n > 10000 else 5)
+        rng = check_random_state(est.random_state)
+        num_groups = max(1, (n + 255) // 256)
+
+        best_inertia, best_centroids, best_assignments = np.inf, None, None
+        actual_iters = 0
+        with _bridge.LloydHandle(n, d, k) as h:
+            h.load(X, center=False)
+            for _ in range(int(n_init)):
+                centroids = np.ascontiguousarray(kmeans_parallel_init(X, k, rng, h), dtype=np.float32)
+                assignments = np.empty(n, dtype=np.int32)
+                actual_iters = _bridge.kmeans_batch_fused(X, centroids, assignments, n, d, k, num_groups,
+                                                          max_iter, tol)
+                inertia = _bridge.kmeans_inertia(X, centroids, assignments, n, d, k)
+                if inertia < best_inertia:
+                    best_inertia = inertia
+                    best_centroids = centroids.copy()
+                    best_assignments = assignments.copy()
+        if best_centroids is None:
+            raise RuntimeError("MetalKMeans: no init attempt gave a valid inertia")
+        est.cluster_centers_ = best_centroids
+        est.labels_ = best_assignments.astype(np.int32)
+        est.inertia_ = float(best_inertia)
+        est.n_iter_ = int(actual_iters)
+        est.n_features_in_ = d
+        est._n_features_out = k
+        self._fitted = True
+        return self
+
+    def predict(self, X):
+        X, _ = self._validate_data(X)
+        if not self._fitted or not self._should_use_gpu(X):
+            return self._fallback_predict(X)
+        C = np.ascontiguousarray(self._estimator.cluster_centers_, dtype=np.float32)
+        out = np.empty(X.shape[0], dtype=np.int32)
+        _bridge.kmeans_assign(X, C, out, X.shape[0], X.shape[1], C.shape[0])
+        return out
+
+    def transform(self, X):
+        X, _ = self._validate_data(X)
+        if not self._fitted or not self._should_use_gpu(X):
+            return self._fallback_transform(X)
+        C = np.ascontiguousarray(self._estimator.cluster_centers_, dtype=np.float32)
+        return _bridge.kmeans_transform(X, C)

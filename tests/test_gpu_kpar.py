@@ -1,0 +1,132 @@
+"""GPU parity of skmetal's k-means|| seeding with its distance rounds on the
+device (skmetal_hip_lloyd_mindists; MetalKMeans._kmeans_parallel_init,
+skmetal/estimators/cluster.py:70-116) against the oracle, and of the
+MetalKMeans mirror's fit."""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def bridge():
+    from skmetal_amd import _bridge
+
+    if not _bridge.HIP_AVAILABLE:
+        pytest.fail(f"GPU path unavailable on a GPU run: {_bridge.last_error()}")
+    return _bridge
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _blobs(n, d, k, seed):
+    rng = np.random.default_rng(seed)
+    C = rng.normal(0, 10, (k, d))
+    return (C[rng.integers(0, k, n)] + rng.normal(0, 1, (n, d))).astype(np.float32)
+
+
+def _check(got, ref, X, rows, what):
+    """Both are the fp32 cast of the fp64 expanded distance; the fp64 sums
+    differ in order, so values agree to 1 ulp plus that rounding."""
+    X64 = X.astype(np.float64)
+    xx = np.einsum("ij,ij->i", X64, X64)
+    cc = xx[np.asarray(rows)].max()
+    eps = 2.0 * X.shape[1] * 2.0**-53 * (xx + cc)
+    r = ref.astype(np.float64)
+    tol = np.spacing(ref).astype(np.float64) + np.minimum(np.sqrt(eps), eps / (2.0 * np.maximum(r, 1e-300)))
+    bad = np.abs(got.astype(np.float64) - r) > tol
+    assert not bad.any(), f"{what}: {int(bad.sum())} distances off, e.g. {got[bad][:4]} vs {ref[bad][:4]}"
+    # at a candidate's own row (x = c) the device's sums cancel exactly, where the
+    # oracle's BLAS product leaves fp64 noise; elsewhere the casts agree
+    own = np.zeros(X.shape[0], dtype=bool)
+    own[np.asarray(rows)] = True
+    assert np.all(got[own] == 0.0), f"{what}: x = c not exactly 0"
+    exact = float(np.mean(got[~own] == ref[~own]))
+    assert exact >= 0.99, f"{what}: only {exact:.5f} bit-exact"
+
+
+@pytest.mark.parametrize("n,d,m", [(1000, 5, 1), (4097, 33, 20), (3001, 100, 70), (777, 1, 9)])
+def test_mindists_match_oracle(bridge, n, d, m):
+    _say(f"k-means|| mindists n={n} d={d} m={m}")
+    X = _blobs(n, d, 6, n + m)
+    rng = np.random.default_rng(m)
+    a = rng.choice(n, m, replace=False)
+    b = rng.choice(n, 5, replace=False)
+    f = oracle.parallel_mindists(X)
+    with bridge.LloydHandle(n, d, 2) as h:
+        h.load(X, center=False)
+        _check(h.mindists(a, reset=True), f(a, True), X, a, "first round")
+        _check(h.mindists(b), f(b, False), X, np.concatenate([a, b]), "second round")
+        _check(h.mindists([]), f([], False), X, np.concatenate([a, b]), "no new rows")
+        _check(h.mindists(b[:2], reset=True), f(b[:2], True), X, b[:2], "reset")
+
+
+def test_mindists_errors(bridge):
+    X = _blobs(500, 4, 3, 0)
+    with bridge.LloydHandle(500, 4, 2) as h:
+        h.load(X, center=False)
+        with pytest.raises(RuntimeError):
+            h.mindists([1, 2])            # the first round must reset
+        with pytest.raises(RuntimeError):
+            h.mindists([1, 500], reset=True)
+        with pytest.raises(RuntimeError):
+            h.mindists([-1], reset=True)
+        assert np.isfinite(h.mindists([7], reset=True)).all()
+
+
+@pytest.mark.parametrize("n,d,k,seed", [(20000, 20, 8, 0), (5000, 100, 50, 1), (3000, 7, 3, 2)])
+def test_parallel_init_matches_oracle(bridge, n, d, k, seed):
+    from skmetal_amd.estimators.cluster import kmeans_parallel_init
+
+    _say(f"k-means|| init n={n} d={d} k={k} seed={seed}")
+    X = _blobs(n, d, k, seed + 10)
+    with bridge.LloydHandle(n, d, k) as h:
+        h.load(X, center=False)
+        got = kmeans_parallel_init(X, k, np.random.RandomState(seed), h)
+    ref = oracle.kmeans_parallel_init(X, k, np.random.RandomState(seed))
+    assert got.shape == (k, d) and got.dtype == np.float32
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_metal_kmeans_fit(bridge):
+    from sklearn.cluster import KMeans
+
+    from skmetal_amd.estimators.cluster import MetalKMeans
+
+    X = _blobs(30000, 24, 10, 4)
+    m = MetalKMeans(KMeans(n_clusters=10, n_init=2, random_state=0))
+    assert m._should_use_gpu(X)
+    m.fit(X)
+    est = m._estimator
+    assert est.labels_.shape == (30000,) and est.labels_.min() >= 0 and est.labels_.max() < 10
+    assert est.cluster_centers_.shape == (10, 24) and est.n_iter_ >= 1
+    # the reference's fit sequence (cluster.py:20-67) with the oracle's k-means||:
+    # per attempt kmeans_batch_fused with tol as given, kmeans_inertia, the
+    # lowest inertia kept (its k-means|| prune can end above scikit-learn's fit)
+    rng = np.random.RandomState(0)
+    best = (np.inf, None, None)
+    for _ in range(2):
+        C = oracle.kmeans_parallel_init(X, 10, rng)
+        a = np.empty(30000, np.int32)
+        bridge.kmeans_batch_fused(X, C, a, 30000, 24, 10, 118, 300, 1e-4)
+        inertia = bridge.kmeans_inertia(X, C, a, 30000, 24, 10)
+        if inertia < best[0]:
+            best = (inertia, C.copy(), a.copy())
+    assert est.inertia_ == best[0]
+    np.testing.assert_array_equal(est.cluster_centers_, best[1])
+    np.testing.assert_array_equal(est.labels_, best[2])
+    # labels_ come from the fit's final E-step on the centred X, predict works on
+    # X as given: the two can differ at near-ties only
+    assert np.mean(m.predict(X) == est.labels_) >= 0.999
+    D = m.transform(X[:1000])
+    assert D.shape == (1000, 10) and np.mean(np.argmin(D, axis=1) == est.labels_[:1000]) >= 0.99
