@@ -302,6 +302,14 @@ class MetalKMeans(BaseGPUEstimator):
         self._fitted = True
         return self
 
+    def fit_predict(self, X, y=None, **kwargs):
+        # defined here so that attribute delegation to the wrapped estimator
+        # does not run scikit-learn's own fit on the CPU
+        return self.fit(X, y, **kwargs)._estimator.labels_
+
+    def fit_transform(self, X, y=None, **kwargs):
+        return self.fit(X, y, **kwargs).transform(X)
+
     def predict(self, X):
         X, _ = self._validate_data(X)
         if not self._fitted or not self._should_use_gpu(X):

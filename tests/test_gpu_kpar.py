@@ -128,5 +128,7 @@ def test_metal_kmeans_fit(bridge):
     # labels_ come from the fit's final E-step on the centred X, predict works on
     # X as given: the two can differ at near-ties only
     assert np.mean(m.predict(X) == est.labels_) >= 0.999
+    m2 = MetalKMeans(KMeans(n_clusters=10, n_init=2, random_state=0))
+    np.testing.assert_array_equal(m2.fit_predict(X), est.labels_)   # the device fit, not sklearn's
     D = m.transform(X[:1000])
     assert D.shape == (1000, 10) and np.mean(np.argmin(D, axis=1) == est.labels_[:1000]) >= 0.99
