@@ -889,8 +889,9 @@ struct Lloyd {
         if (m > kp_cap) {
             const long cap = std::max<long>(m, 2 * kp_cap);
             if (kp_cand != nullptr) {
+                const auto it = std::find(owned.begin(), owned.end(), (void*)kp_cand);
+                if (it != owned.end()) owned.erase(it);
                 C->release(kp_cand);
-                owned.erase(std::find(owned.begin(), owned.end(), (void*)kp_cand));
                 kp_cand = nullptr;
             }
             TRY(grab((void**)&kp_cand, size_t(cap) * sizeof(long)));

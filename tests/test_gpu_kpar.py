@@ -132,3 +132,17 @@ def test_metal_kmeans_fit(bridge):
     np.testing.assert_array_equal(m2.fit_predict(X), est.labels_)   # the device fit, not sklearn's
     D = m.transform(X[:1000])
     assert D.shape == (1000, 10) and np.mean(np.argmin(D, axis=1) == est.labels_[:1000]) >= 0.99
+
+
+def test_mindists_candidate_buffer_growth(bridge):
+    # rounds with more new rows than any before regrow the device candidate list
+    X = _blobs(5000, 12, 4, 9)
+    f = oracle.parallel_mindists(X)
+    rng = np.random.default_rng(3)
+    seen = []
+    with bridge.LloydHandle(5000, 12, 4) as h:
+        h.load(X, center=False)
+        for i, m in enumerate((3, 40, 150, 2)):
+            rows = rng.choice(5000, m, replace=False)
+            seen.extend(rows.tolist())
+            _check(h.mindists(rows, reset=(i == 0)), f(rows, i == 0), X, seen, f"round {i} (m={m})")
