@@ -10,10 +10,10 @@
 // The fp32 square root is taken as the fp64 root rounded to fp32, which is the
 // correctly rounded fp32 root (53 >= 2 * 24 + 2 bits).
 //
-// A block owns a 64-row x 64-centre tile: thread (rg, cg) accumulates rows
-// rg, rg + 32 against centres cg + 8 j (j < 8) in fp64 registers, the rows
-// and centres staged through LDS 32 features at a time (coalesced 128-byte
-// row runs).  The reference computed ||x||^2 + ||c||^2 - 2 x.c in fp32 around
+// A block owns a 128-row x 64-centre tile: thread (rg, cg) accumulates rows
+// rg + 32 i (i < 4) against centres cg + 8 j (j < 8) in fp64 registers, the
+// rows and centres staged through LDS (as fp64) 32 features at a time
+// (coalesced 128-byte row runs).  The reference computed ||x||^2 + ||c||^2 - 2 x.c in fp32 around
 // skmetal_gemm (skmetal/estimators/cluster.py:135-146).
 #include "device.h"
 
@@ -21,7 +21,7 @@ namespace skm {
 
 namespace {
 
-constexpr int kTR = 64;   // rows per tile
+constexpr int kTR = 128;  // rows per tile (4 per thread)
 constexpr int kTC = 64;   // centres per tile
 constexpr int kTF = 32;   // features per LDS segment
 
@@ -31,30 +31,43 @@ __global__ __launch_bounds__(256) void k_cnorm64(TransformArgs a)
     if (j >= a.k) return;
     const float* c = a.C + (long)j * a.ld;
     double acc = 0.0;
-    for (int f = 0; f < a.ld; ++f) acc = fma((double)c[f], (double)c[f], acc);
+    // the loads of 8 features in flight at once, the sum in feature order
+    int f = 0;
+    for (; f + 8 <= a.ld; f += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = c[f + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = fma((double)v[u], (double)v[u], acc);
+    }
+    for (; f < a.ld; ++f) acc = fma((double)c[f], (double)c[f], acc);
     a.cc[j] = acc;
 }
 
 __global__ __launch_bounds__(256) void k_transform(TransformArgs a)
 {
-    __shared__ float xs[kTR][kTF + 1];
+    // x is staged as fp64 (converted once, not at every use)
+    __shared__ double xs[kTR][kTF + 1];
     __shared__ double cs[kTC][kTF + 1];
+    constexpr int RI = kTR / 32;  // rows per thread
     const int tid = threadIdx.x;
     const int rg = tid >> 3, cg = tid & 7;
     const long r0 = (long)blockIdx.x * kTR;
     const int c0 = blockIdx.y * kTC;
-    double acc[2][8];
+    double acc[RI][8];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < RI; ++i)
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[i][j] = 0.0;
-    double xx0 = 0.0, xx1 = 0.0;
+    double xx[RI];
+#pragma unroll
+    for (int i = 0; i < RI; ++i) xx[i] = 0.0;
 
     for (int f0 = 0; f0 < a.ld; f0 += kTF) {
         const int fl = min(kTF, a.ld - f0);  // a multiple of 4 (ld is)
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < kTR * kTF / 4 / 256; ++i) {
             const int e = tid + 256 * i;
             const int r = e >> 3, q = e & 7;
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -63,6 +76,11 @@ __global__ __launch_bounds__(256) void k_transform(TransformArgs a)
             xs[r][4 * q + 1] = v.y;
             xs[r][4 * q + 2] = v.z;
             xs[r][4 * q + 3] = v.w;
+        }
+#pragma unroll
+        for (int i = 0; i < kTC * kTF / 4 / 256; ++i) {
+            const int e = tid + 256 * i;
+            const int r = e >> 3, q = e & 7;
             float4 w = make_float4(0.f, 0.f, 0.f, 0.f);
             if (4 * q < fl && c0 + r < a.k) w = *reinterpret_cast<const float4*>(a.C + (long)(c0 + r) * a.ld + f0 + 4 * q);
             cs[r][4 * q] = w.x;
@@ -72,27 +90,29 @@ __global__ __launch_bounds__(256) void k_transform(TransformArgs a)
         }
         __syncthreads();
         for (int f = 0; f < fl; ++f) {
-            const double x0 = xs[rg][f], x1 = xs[rg + 32][f];
-            xx0 = fma(x0, x0, xx0);
-            xx1 = fma(x1, x1, xx1);
+            double x[RI];
+#pragma unroll
+            for (int i = 0; i < RI; ++i) {
+                x[i] = xs[rg + 32 * i][f];
+                xx[i] = fma(x[i], x[i], xx[i]);
+            }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const double c = cs[cg + 8 * j][f];
-                acc[0][j] = fma(x0, c, acc[0][j]);
-                acc[1][j] = fma(x1, c, acc[1][j]);
+#pragma unroll
+                for (int i = 0; i < RI; ++i) acc[i][j] = fma(x[i], c, acc[i][j]);
             }
         }
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < RI; ++i) {
         const long row = r0 + rg + 32 * i;
         if (row >= a.n) continue;
-        const double xx = i == 0 ? xx0 : xx1;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int col = c0 + cg + 8 * j;
             if (col < a.k) {
-                float d32 = (float)((-2.0 * acc[i][j] + xx) + a.cc[col]);
+                float d32 = (float)((-2.0 * acc[i][j] + xx[i]) + a.cc[col]);
                 if (d32 < 0.f) d32 = 0.f;
                 a.out[row * a.k + col] = (float)sqrt((double)d32);
             }
