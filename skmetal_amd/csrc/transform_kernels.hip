@@ -47,8 +47,9 @@ __global__ __launch_bounds__(256) void k_cnorm64(TransformArgs a)
 __global__ __launch_bounds__(256) void k_transform(TransformArgs a)
 {
     // x is staged as fp64 (converted once, not at every use)
-    __shared__ double xs[kTR][kTF + 1];
-    __shared__ double cs[kTC][kTF + 1];
+    // rows of kTF + 2 doubles: 16-byte aligned for the two-feature reads
+    __shared__ __attribute__((aligned(16))) double xs[kTR][kTF + 2];
+    __shared__ __attribute__((aligned(16))) double cs[kTC][kTF + 2];
     constexpr int RI = kTR / 32;  // rows per thread
     const int tid = threadIdx.x;
     const int rg = tid >> 3, cg = tid & 7;
@@ -89,18 +90,22 @@ __global__ __launch_bounds__(256) void k_transform(TransformArgs a)
             cs[r][4 * q + 3] = w.w;
         }
         __syncthreads();
-        for (int f = 0; f < fl; ++f) {
-            double x[RI];
+        for (int f = 0; f < fl; f += 2) {  // fl is even: features f, f + 1 per read
+            double2 x[RI];
 #pragma unroll
             for (int i = 0; i < RI; ++i) {
-                x[i] = xs[rg + 32 * i][f];
-                xx[i] = fma(x[i], x[i], xx[i]);
+                x[i] = *reinterpret_cast<const double2*>(&xs[rg + 32 * i][f]);
+                xx[i] = fma(x[i].x, x[i].x, xx[i]);
+                xx[i] = fma(x[i].y, x[i].y, xx[i]);
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const double c = cs[cg + 8 * j][f];
+                const double2 c = *reinterpret_cast<const double2*>(&cs[cg + 8 * j][f]);
 #pragma unroll
-                for (int i = 0; i < RI; ++i) acc[i][j] = fma(x[i], c, acc[i][j]);
+                for (int i = 0; i < RI; ++i) {
+                    acc[i][j] = fma(x[i].x, c.x, acc[i][j]);
+                    acc[i][j] = fma(x[i].y, c.y, acc[i][j]);
+                }
             }
         }
     }
