@@ -2,9 +2,14 @@
 
 Workload: 500,000 x 100 fp32 from 50 isotropic Gaussian blobs (centres
 ~U[-10,10]^100, sigma 1), k = 50, seeded random-row init -- the shape of
-skmetal's README headline.  A "step" is one Lloyd iteration (fused E-step on
-fp16x2-split MFMA, per-cluster sums, finalize) over all 500,000 rows, with X already
-resident in HBM.  The steps are timed with HIP events on the library's stream
+skmetal's README headline.  A "step" is one Lloyd iteration (fused E-step and
+per-cluster sums, finalize) over all 500,000 rows, with X already resident in
+HBM.  The arithmetic is fp32-equivalent: x and c enter as an exact three-part
+bf16 split (x = hi + mid + lo, every fp32 value represented exactly), the
+products of the parts are exact in the fp32 accumulators of the bf16 MFMAs,
+the sums use all three parts and the E-step 6 of the 9 part products (the
+three left out total at most 2^-23 |x_i c_i| per feature).  The same steps on
+the fp32-MFMA kernel are timed beside it.  The steps are timed with HIP events on the library's stream
 (skmetal_hip_lloyd_iterate).  The same steps are then run again from the same
 initial centres with each step's kernels bracketed by HIP events on that
 stream: the dominant kernel's average launch time over those steps gives its
@@ -33,7 +38,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_FP32_MFMA_TFLOPS = 157.3
-PEAK_FP16_MFMA_TFLOPS = 2500.0
+PEAK_BF16_MFMA_TFLOPS = 2500.0
 PEAK_HBM_GBPS = 8000.0
 
 
@@ -136,6 +141,22 @@ def main():
         h.set_centers(C0)
         _, (ms_assign, ms_update, ms_final) = h.iterate(args.steps, kernel_times=True)
         mode = h.info()
+    # the same fixed-iteration run on the fp32-MFMA kernel (v_mfma_f32_4x4x1,
+    # per-cluster sums by a VALU walker), reported beside the metric
+    os.environ["SKMETAL_HIP_SPLIT"] = "0"
+    try:
+        with _bridge.LloydHandle(n, d, k) as h32:
+            h32.load(X, center=True)
+            h32.set_centers(C0)
+            h32.iterate(args.warmup)
+            h32.set_centers(C0)
+            ms32 = h32.iterate(args.steps)
+            fp32_mode = h32.info()
+    finally:
+        del os.environ["SKMETAL_HIP_SPLIT"]
+    with _bridge.LloydHandle(n, d, k) as h:
+        h.load(X, center=True)
+        h.set_centers(C0)
         # k-means++ seeding of the same resident X on the device with
         # scikit-learn's draws for random_state=0 (reported beside the metric:
         # KMeans(init="k-means++") runs it once per fit)
@@ -165,15 +186,21 @@ def main():
     it_s = 1.0 / step_s
     flops = 2.0 * n * k * d
     assign_s = ms_assign / 1e3
-    fused, f16, a16 = mode["fused"], mode["f16"], mode["a16"]
-    kname = "k_fused16" if f16 else "k_fused" if fused else "k_assign16" if a16 else "k_assign"
+    fused, split, asplit = mode["fused"], mode["split"], mode["asplit"]
+    kname = "k_fused3" if split else "k_fused" if fused else "k_assign3" if asplit else "k_assign"
     traffic = _traffic_from_profile(f"{kname}_{args.workload}_pmc.txt")
-    if f16:
-        # HBM roofline: the bytes one launch must move -- X once, the labels
-        # read and written, the per-block partial sums and counts written
-        nbytes = 4.0 * n * d + 8.0 * n + 4.0 * mode["partials"] * k * (d + 1)
+    if split:
+        # HBM roofline with the assign bytes per step: X once, the labels
+        # written, the centres read (4nd + 4n + 4kd).  The kernel's MFMA work
+        # over the padded shapes (64 centres, 112 features) is reported beside
+        # it: 6 part products in the E-step, 3 in the sums.
+        nbytes = 4.0 * n * d + 4.0 * n + 4.0 * k * d
+        kp = -(-k // 16) * 16
+        dp = -(-d // 32) * 32 if d % 32 == 0 or d % 32 > 16 else (d // 32) * 32 + 16
+        bf16_flops = (6.0 + 3.0) * 2.0 * n * kp * dp
         roofline = {
-            "kernel": "k_fused16: E-step (||c||^2 - 2 x.c, fp16x2-split MFMA) + argmin + per-cluster sums",
+            "kernel": ("k_fused3: E-step (||c||^2 - 2 x.c) + argmin + per-cluster sums, bf16 MFMAs over the exact "
+                       "three-part split, fp32 accumulation"),
             "bound": "hbm",
             "achieved": round(nbytes / assign_s / 1e9, 1),
             "peak": PEAK_HBM_GBPS,
@@ -182,20 +209,23 @@ def main():
             "traffic": traffic,
             "algorithmic_bytes": nbytes,
             "fp32_equiv_tflops": round(flops / assign_s / 1e12, 2),
+            "fp32_mfma_frac": round(flops / assign_s / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
+            "bf16_mfma_tflops": round(bf16_flops / assign_s / 1e12, 1),
+            "bf16_mfma_frac": round(bf16_flops / assign_s / 1e12 / PEAK_BF16_MFMA_TFLOPS, 4),
         }
-    elif a16:
-        # MFMA roofline of the fp16 split: three fp16 products per x.c term,
+    elif asplit:
+        # MFMA roofline of the split E-step: six bf16 products per x.c term,
         # over the padded centres (multiples of 16 per pass) and features (32)
         kp = -(-k // (16 * (4 if k <= 64 else 8 if k <= 128 else 16))) * (16 * (4 if k <= 64 else 8 if k <= 128 else 16))
         dp = -(-d // 32) * 32
-        mflops = 3.0 * 2.0 * n * kp * dp
+        mflops = 6.0 * 2.0 * n * kp * dp
         roofline = {
-            "kernel": "k_assign16: ||c||^2 - 2 x.c on fp16x2-split MFMA (v_mfma_f32_16x16x32_f16) + argmin",
+            "kernel": "k_assign3: ||c||^2 - 2 x.c on bf16 MFMAs over the exact three-part split + argmin",
             "bound": "mfma",
             "achieved": round(mflops / assign_s / 1e12, 1),
-            "peak": PEAK_FP16_MFMA_TFLOPS,
+            "peak": PEAK_BF16_MFMA_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": round(mflops / assign_s / 1e12 / PEAK_FP16_MFMA_TFLOPS, 4),
+            "frac": round(mflops / assign_s / 1e12 / PEAK_BF16_MFMA_TFLOPS, 4),
             "traffic": traffic,
             "fp32_equiv_tflops": round(flops / assign_s / 1e12, 2),
         }
@@ -235,8 +265,15 @@ def main():
         "h2d_s": round(h2d_s, 4),
         "step_mode": (f"fused: {kname} (E-step + per-cluster sums) + k_finalize" if fused
                       else f"{kname} + sorted update + k_finalize"),
-        "e_step": ("fp16x2 split (x, c scaled by 2^s; hi/lo parts), v_mfma_f32_16x16x32_f16, fp32 accumulate"
-                   if (f16 or (a16 and not fused)) else "fp32 MFMA (v_mfma_f32_4x4x1_16b_f32)"),
+        "e_step": ("fp32-equivalent: exact three-part bf16 split of x and c (x = hi + mid + lo), 6 of 9 part "
+                   "products on v_mfma_f32_16x16x32_bf16, fp32 accumulation; the 3 left out total <= 2^-23 |x_i c_i|"
+                   if (split or (asplit and not fused)) else "fp32 MFMA (v_mfma_f32_4x4x1_16b_f32)"),
+        "m_step": ("fp32: one-hot x each of the three exact bf16 parts on v_mfma_f32_16x16x32_bf16, fp32 "
+                   "accumulation per block, fp64 across blocks" if split
+                   else "fp32 VALU sums per block, fp64 across blocks"),
+        "fp32_mfma_path": {"value": round(args.steps / (ms32 / 1e3), 2), "unit": "Lloyd iters/s",
+                           "ms_per_step": round(ms32 / args.steps, 5),
+                           "kernel": "k_fused" if fp32_mode["fused"] else "k_assign"},
         "partials": mode["partials"],
         "kernels_ms": ({kname: round(ms_assign, 5), "k_finalize": round(ms_final, 5)} if fused
                        else {kname: round(ms_assign, 5), "update": round(ms_update, 5),

@@ -184,10 +184,11 @@ SKMETAL_API int skmetal_hip_lloyd_mindists(skmetal_hip_lloyd* h, const int64_t* 
                                            float* dists_out);
 /* *fused & 3 = 0 when a step runs as separate E-step and update kernels, 1
  * when as one fused E-step + sums kernel with the E-step on fp32 MFMA
- * (k <= 64, d <= 100), 2 when that kernel's E-step runs on fp16 MFMA with x
- * and c split in two scaled fp16 parts (d >= 17 and finite data); *fused & 4
- * = the separate E-step kernel (generic path, final E-step, assign) uses the
- * same fp16 split; *partials = per-step partial sums the finalize reduces. */
+ * (k <= 64, d <= 100), 2 when that kernel's E-step and sums run on bf16 MFMAs
+ * over an exact three-part bf16 split of x and c with fp32 accumulation
+ * (d >= 17, finite data with max |x| 0 or in [2^-50, 2^60]); *fused & 4 = the
+ * separate E-step kernel (generic path, final E-step, assign) uses the same
+ * split; *partials = per-step partial sums the finalize reduces. */
 SKMETAL_API int skmetal_hip_lloyd_info(skmetal_hip_lloyd* h, int* fused, int* partials);
 SKMETAL_API int skmetal_hip_lloyd_get_centers(skmetal_hip_lloyd* h, float* C);
 SKMETAL_API int skmetal_hip_lloyd_get_labels(skmetal_hip_lloyd* h, int32_t* labels);

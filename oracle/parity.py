@@ -6,9 +6,14 @@ outputs in the golden fixtures):
 * labels  -- identical, except rows whose oracle best-vs-second squared
              distance gap is below ``LABEL_GAP_REL * ||x||^2`` (x in the
              coordinates the distances were evaluated in);
-* centres -- per centre row j: max_c |a_jc - b_jc| <= CENTER_RTOL * max_c |b_jc|
-             (relative to the row's own magnitude, so coordinates that happen
-             to sit near zero do not make the test ill-conditioned);
+* centres -- three checks, each at CENTER_RTOL:
+             per centre row j: max_c |a_jc - b_jc| / max_c |b_jc|;
+             per column c: max_j |a_jc - b_jc| / max_j |b_jc| (a column whose
+             values are far smaller than the others' is held to its own scale);
+             per element, in a lockstep step: |a_jc - b_jc| / mean |x_ic| over
+             the rows i of cluster j (the scale an fp32 sum of those rows works
+             at, so a cluster whose values in a column are far smaller than
+             other clusters' is held to its own scale too);
 * inertia -- |a - b| <= INERTIA_RTOL * |b| against an fp64 recomputation.
 """
 
@@ -19,6 +24,10 @@ import numpy as np
 LABEL_GAP_REL = 1e-5
 CENTER_RTOL = 1e-4
 INERTIA_RTOL = 1e-5
+# per-element centre error, relative to the cluster's own mean |x|, that fp32
+# sums over chains of up to a few hundred rows stay within (used where the
+# arithmetic itself is under test: columns and clusters of mixed scales)
+FP32_ELEM_RTOL = 1e-5
 
 
 def label_mismatches(labels, ref_labels, best, second, X, gap_rel=LABEL_GAP_REL):
@@ -52,10 +61,50 @@ def center_rel_err(C, C_ref):
     return float((num / den).max())
 
 
+def center_col_err(C, C_ref):
+    """max over columns c of max_j |C_jc - R_jc| / max_j |R_jc|."""
+    C = np.asarray(C, dtype=np.float64)
+    R = np.asarray(C_ref, dtype=np.float64)
+    floor = max(float(np.abs(R).max(initial=0.0)) * 1e-30, 1e-300)
+    num = np.abs(C - R).max(axis=0)
+    den = np.maximum(np.abs(R).max(axis=0), floor)
+    return float((num / den).max())
+
+
+def center_member_err(C, C_ref, X, labels):
+    """max over (j, c) of |C_jc - R_jc| / mean_{i in cluster j} |x_ic|, over the
+    clusters that have rows in `labels`."""
+    C = np.asarray(C, dtype=np.float64)
+    R = np.asarray(C_ref, dtype=np.float64)
+    X = np.asarray(X)
+    lab = np.asarray(labels, dtype=np.int64)
+    k = R.shape[0]
+    cnt = np.bincount(lab, minlength=k).astype(np.float64)
+    absum = np.zeros_like(R)
+    order = np.argsort(lab, kind="stable")
+    xmax = 0.0
+    step = 1 << 17
+    for s0 in range(0, len(order), step):
+        idx = order[s0:s0 + step]
+        lb = lab[idx]
+        blk = np.abs(X[idx].astype(np.float64))
+        xmax = max(xmax, float(blk.max(initial=0.0)))
+        starts = np.flatnonzero(np.r_[True, lb[1:] != lb[:-1]])
+        absum[lb[starts]] += np.add.reduceat(blk, starts, axis=0)
+    has = cnt > 0
+    if not has.any():
+        return 0.0
+    scale = absum[has] / cnt[has, None]
+    floor = max(xmax * 1e-30, 1e-300)
+    return float((np.abs(C[has] - R[has]) / np.maximum(scale, floor)).max())
+
+
 def check_centers(C, C_ref, rtol=CENTER_RTOL, what="centers"):
     err = center_rel_err(C, C_ref)
     assert err <= rtol, f"{what}: max row-relative error {err:.3e} > {rtol:.1e}"
-    return err
+    col = center_col_err(C, C_ref)
+    assert col <= rtol, f"{what}: max per-column error {col:.3e} > {rtol:.1e}"
+    return max(err, col)
 
 
 def centring_floor(X) -> float:
@@ -85,7 +134,7 @@ def near_ties(best, second, X, gap_rel=LABEL_GAP_REL):
 
 
 def _match_relocated(C, C_ref, rows):
-    """Row-relative error after best-matching the given rows of C to those of C_ref."""
+    """C with the given rows best-matched (greedily) to those of C_ref."""
     C = np.asarray(C, dtype=np.float64).copy()
     R = np.asarray(C_ref, dtype=np.float64)
     rows = list(rows)
@@ -94,10 +143,10 @@ def _match_relocated(C, C_ref, rows):
         errs = [np.abs(C[f] - R[r]).max() for f in free]
         f = free.pop(int(np.argmin(errs)))
         C[r], C[f] = C[f].copy(), C[r].copy()
-    return center_rel_err(C, R)
+    return C
 
 
-def check_lockstep(X, C_prev, C_next_ref, labels_ref, rtol=CENTER_RTOL, what="step"):
+def check_lockstep(X, C_prev, C_next_ref, labels_ref, rtol=CENTER_RTOL, what="step", elem_rtol=None):
     """One Lloyd step from C_prev checked against a reference step.
 
     X and C_prev are in the coordinates the step runs in; labels_ref and
@@ -106,16 +155,24 @@ def check_lockstep(X, C_prev, C_next_ref, labels_ref, rtol=CENTER_RTOL, what="st
     oracle's M-step applied to labels_ref must reproduce C_next_ref.  When
     three or more clusters were empty, the reference may hand the relocated
     points to the empty clusters in a different order, so those rows are
-    compared as a set.  Returns the number of label mismatches.
+    compared as a set.  elem_rtol (default rtol) bounds the per-element error
+    at the cluster's own scale.  Returns the number of label mismatches.
     """
     import oracle
 
     labels, best, second = oracle.assign(X, C_prev, return_gap=True)
     n_m = check_labels(labels_ref, labels, best, second, X, what=f"{what} labels")
     C_new, _, n_empty = oracle.mstep(X, labels_ref, C_prev)
-    err = center_rel_err(C_new, C_next_ref)
+    C_got = np.asarray(C_next_ref, dtype=np.float64)
+    err = center_rel_err(C_new, C_got)
     if err > rtol and n_empty >= 3:
         counts = np.bincount(np.asarray(labels_ref, dtype=np.int64), minlength=len(C_prev))
-        err = _match_relocated(C_new, C_next_ref, np.flatnonzero(counts == 0))
+        C_got = _match_relocated(C_got, C_new, np.flatnonzero(counts == 0))
+        err = center_rel_err(C_new, C_got)
     assert err <= rtol, f"{what}: centres row-relative error {err:.3e} > {rtol:.1e}"
+    col = center_col_err(C_got, C_new)
+    assert col <= rtol, f"{what}: centres per-column error {col:.3e} > {rtol:.1e}"
+    mem = center_member_err(C_got, C_new, X, labels_ref)
+    er = rtol if elem_rtol is None else elem_rtol
+    assert mem <= er, f"{what}: centres per-element error (cluster scale) {mem:.3e} > {er:.1e}"
     return n_m

@@ -372,7 +372,7 @@ class LloydHandle:
         _check(_lib.skmetal_hip_lloyd_info(self._h, ctypes.byref(fused), ctypes.byref(partials)),
                "skmetal_hip_lloyd_info")
         mode = int(fused.value)
-        return dict(fused=bool(mode & 3), f16=(mode & 3) == 2, a16=bool(mode & 4), partials=int(partials.value))
+        return dict(fused=bool(mode & 3), split=(mode & 3) == 2, asplit=bool(mode & 4), partials=int(partials.value))
 
     def centers(self):
         out = np.empty((self.k, self.d), np.float32)

@@ -1,14 +1,15 @@
 // fused_kernels.hip -- one-pass Lloyd step for small k*d on gfx950 (MI355X):
 // the E-step (sklearn/cluster/_k_means_lloyd.pyx:196-212) and the
 // per-cluster sums and counts of the M-step (:214-218) in one kernel that
-// reads X from HBM once per step, plus the fp16-split E-step for any k.
+// reads X from HBM once per step, plus the split E-step for any k.
 //
-//   k_fused16   E-step on fp16 MFMA (x and c split in two scaled fp16 parts),
-//               per-cluster sums on fp16 MFMA (one-hot x the same parts);
+//   k_fused3    E-step and per-cluster sums on bf16 MFMAs over an exact
+//               three-part bf16 split of x and c (fp32 accumulation);
 //               12 waves per block (d >= 17).
 //   k_fused     E-step on fp32 MFMA, per-cluster sums by a VALU walker; 8
-//               waves per block (d <= 16, non-finite data, or the fp32 switch).
-//   k_assign16  E-step alone for any k on fp16 MFMA (the generic path).
+//               waves per block (d <= 16, data outside the split's range, or
+//               the fp32 switch).
+//   k_assign3   E-step alone for any k over the same split (the generic path).
 //
 // The fused kernels are used when k <= 64 and d <= 100; X's row stride ld is
 // then padded (with zeros) to 4*NQ floats for one of the compiled NQ, so the
@@ -481,80 +482,133 @@ __global__ __launch_bounds__(512, 1) void k_fused(FusedArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// k_fused16: the same step (same pairs, walker, LDS hand-over and sums) with
-// the E-step on v_mfma_f32_16x16x32_f16 (v_mfma_f32_16x16x16_f16 for a last
-// 4-, 8- or 16-feature slice).  x and c are scaled by 2^s (s from the largest
-// |x| and |c|, so scaled values stay below 2^14) and split in two fp16
-// parts, hi = fp16(v 2^s) and lo = fp16(v 2^s - hi), both rounded to
-// nearest: v 2^s = hi + lo + e with |e| <= 2^-22 |v 2^s|.  Then
-//   x.c = 2^-2s (xh.ch + xl.ch + xh.cl) + O(3 * 2^-22 sum_i |x_i c_i|),
-// the dropped xl.cl and the residuals being of the order of fp32's own
-// rounding in a dot product of d terms; the products are exact in the fp32
-// accumulators.
+// Three-part bf16 split.  bf16 keeps fp32's exponent range with 8 significant
+// bits, so every finite fp32 v with |v| >= 2^-103 is the exact sum of three
+// bf16 values, each rounded to nearest:
+//   hi = bf16(v),  mid = bf16(v - hi),  lo = (v - hi) - mid.
+// v - hi is a multiple of v's fp32 ulp no larger than 2^16 of them, so the fp32
+// subtraction is exact; likewise (v - hi) - mid, which is at most 2^8 ulps and
+// therefore exactly a bf16.  |mid| <= 2^-8 |v|, |lo| <= 2^-16 |v|.
+// A product of two bf16 values is exact in fp32, and the MFMAs accumulate in
+// fp32, so
+//  - the per-cluster sums (one-hot x hi, x mid, x lo) add every x exactly as
+//    given, in fp32 (the one-hot operand is exact);
+//  - the E-step takes 6 of the 9 part products of x.c (hh, hm, mh, hl, lh, mm):
+//    the three left out (ml, lm, ll) total at most (2^-23 + 2^-32) |x_i c_i|
+//    per feature, two units of fp32 roundoff, against the one unit by which an
+//    fp32 product of x_i and c_i is itself rounded.
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+// (a, b) rounded to nearest even bf16, a in the low half: v_cvt_pk_bf16_f32
+__device__ __forceinline__ unsigned pack_bf16(float a, float b)
+{
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(v2f{a, b}, v2bf));
+}
+__device__ __forceinline__ float bf16_lo(unsigned p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf16_hi(unsigned p) { return __uint_as_float(p & 0xffff0000u); }
+
+// The parts of a and b, as bf16 pairs (a's part in the low half).
+__device__ __forceinline__ void split3(float a, float b, unsigned& hi, unsigned& mid, unsigned& lo)
+{
+    hi = pack_bf16(a, b);
+    const float ra = a - bf16_lo(hi), rb = b - bf16_hi(hi);  // exact
+    mid = pack_bf16(ra, rb);
+    lo = pack_bf16(ra - bf16_lo(mid), rb - bf16_hi(mid));   // exact, and exactly bf16
+}
+
+struct Parts8 {
+    v8bf h, m, l;
+};
+struct Parts4 {
+    v4s h, m, l;  // 16x16x16 bf16 operands are passed as shorts
+};
+
+__device__ __forceinline__ Parts8 split8(float4 u, float4 v)
+{
+    unsigned h0, h1, h2, h3, m0, m1, m2, m3, l0, l1, l2, l3;
+    split3(u.x, u.y, h0, m0, l0);
+    split3(u.z, u.w, h1, m1, l1);
+    split3(v.x, v.y, h2, m2, l2);
+    split3(v.z, v.w, h3, m3, l3);
+    return Parts8{__builtin_bit_cast(v8bf, v4u{h0, h1, h2, h3}), __builtin_bit_cast(v8bf, v4u{m0, m1, m2, m3}),
+                  __builtin_bit_cast(v8bf, v4u{l0, l1, l2, l3})};
+}
+
+__device__ __forceinline__ Parts4 split4(float4 u)
+{
+    unsigned h0, h1, m0, m1, l0, l1;
+    split3(u.x, u.y, h0, m0, l0);
+    split3(u.z, u.w, h1, m1, l1);
+    return Parts4{__builtin_bit_cast(v4s, v2u{h0, h1}), __builtin_bit_cast(v4s, v2u{m0, m1}),
+                  __builtin_bit_cast(v4s, v2u{l0, l1})};
+}
+
+// D += A B on bf16: 16x16x32 (8 values per lane) and 16x16x16 (4)
+__device__ __forceinline__ v4f mfma_bf16(v8bf a, v8bf b, v4f c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v4f mfma_bf16(v4s a, v4s b, v4f c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// acc += the six kept part products of a.b (smaller terms first)
+template <typename P>
+__device__ __forceinline__ v4f dot6(const P& a, const P& b, v4f acc)
+{
+    acc = mfma_bf16(a.m, b.m, acc);
+    acc = mfma_bf16(a.l, b.h, acc);
+    acc = mfma_bf16(a.h, b.l, acc);
+    acc = mfma_bf16(a.m, b.h, acc);
+    acc = mfma_bf16(a.h, b.m, acc);
+    return mfma_bf16(a.h, b.h, acc);
+}
+
+// ---------------------------------------------------------------------------
+// k_fused3: the fused step with the E-step and the per-cluster sums on bf16
+// MFMAs over the three-part split (v_mfma_f32_16x16x32_bf16, and
+// v_mfma_f32_16x16x16_bf16 for a last 4-, 8- or 16-feature slice).
 //
 // MFMA operand layout (16x16x32, checked on the device): lane l holds A[m =
 // l%16][kk = 8(l/16) + j] and B[kk = 8(l/16) + j][n = l%16], j < 8, and
 // receives D[m = 4(l/16) + i][n = l%16], i < 4; 16x16x16 the same with 4
-// values per lane.  Here A = 16 centres (block cb, hi/lo parts from LDS) and
-// B = 16 rows of the tile (group g, from registers), so lane l ends with the
-// distances of row 16g + l%16 to centres 16cb + 4(l/16) + i: the first
-// minimum over the lane's 4 CB centres, then over the four lanes l%16 + 16h
-// (lower index wins ties: the first minimum over all centres), and lane 16g +
-// r keeps row 16g + r's label -- lane = row again for the labels, masks and
-// walker.
+// values per lane.  In the E-step A = 16 centres (block cb, parts from LDS)
+// and B = 16 rows of the tile (group g, from registers), so lane l ends with
+// the x.c of row 16g + l%16 and centres 16cb + 4(l/16) + i: the first minimum
+// over the lane's 4 CB centres, then over the four lanes l%16 + 16h (lower
+// index wins ties: the first minimum over all centres), and lane 16g + r
+// keeps row 16g + r's label -- lane = row for the labels and counts.
 //
-// Each lane loads its 8 (K32 step) or 4 (tail) features of its rows straight
-// from HBM into registers (one 128-byte piece of each of 16 rows per pair of
-// loads), writes them to the pair's LDS tile for the walker and reloads them
-// with tile t + P; the walker is k_fused's.
+// A block is 12 waves, three per SIMD.  E-step waves e = 0..7 (two per SIMD)
+// each work on their own 32-row tiles t = 8b + e + r P, with their own LDS
+// tile; sums wave 8 + m serves the two E-step waves m and m + 4 of its SIMD,
+// taking their tiles in turn.  Each lane loads its 8 (K32 step) or 4 (tail)
+// features of its rows straight from HBM into registers, writes them to the
+// wave's LDS tile for the sums wave and reloads them with tile t + P once the
+// sums wave has read those columns of the previous tile.  The waves hand over
+// work through LDS flags; there is no block barrier until the end.
 
-typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-
-// m1 must be -1.0f from a runtime value (see neg_one): fma(hi, m1, x) is then
-// one v_fma_mix_f32 reading the fp16 hi; with a literal -1 the compiler turns
-// it back into a conversion and a subtraction
-template <bool SC>
-__device__ __forceinline__ void split4(float4 v, float sc, float m1, v4h& hi, v4h& lo)
-{
-    const v4f x = SC ? v4f{v.x * sc, v.y * sc, v.z * sc, v.w * sc} : v4f{v.x, v.y, v.z, v.w};
-    hi = __builtin_convertvector(x, v4h);
-    // x - hi is exact in fp32 (hi is x rounded to 11 bits), so fma(hi, -1, x)
-    // gives the same lo
-    const v4f r = {__builtin_fmaf((float)hi[0], m1, x[0]), __builtin_fmaf((float)hi[1], m1, x[1]),
-                   __builtin_fmaf((float)hi[2], m1, x[2]), __builtin_fmaf((float)hi[3], m1, x[3])};
-    lo = __builtin_convertvector(r, v4h);
-}
-
-template <bool SC>
-__device__ __forceinline__ void split8(float4 u, float4 v, float sc, float m1, v8h& hi, v8h& lo)
-{
-    v4h h0, l0, h1, l1;
-    split4<SC>(u, sc, m1, h0, l0);
-    split4<SC>(v, sc, m1, h1, l1);
-    hi = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
-    lo = __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7);
-}
-
-// -1.0f from the kernel's scale arguments, sc = 2^s and f2 = -2 * 2^-2s:
-// (f2 / 2) * sc^2 = -2^-2s * 2^2s, exact for the |s| <= 60 the host allows.
-__device__ __forceinline__ float neg_one(float sc, float f2) { return (0.5f * f2) * (sc * sc); }
-
-// The sums wave of SIMD m in k_fused16 serves E-step waves m and m + 4 (the
-// same SIMD), taking their 32-row tiles in turn: round r of wave m, then round
-// r of wave m + 4.  The per-cluster sums of a tile are onehot^T x on
-// v_mfma_f32_16x16x32_f16 with x in the E-step's two fp16 parts (x 2^s = hi +
-// lo up to 2^-22 |x 2^s|); the one-hot operand is exact, so every product is
-// exact in the fp32 accumulators.  A = one-hot (16 clusters x the tile's 32
-// rows: lane l holds rows 8(l/16) + j for cluster 16cb + l%16), B = x (the 32
-// rows x 16 features of block fb, read transposed from the LDS tile); D lane
-// l: clusters 16cb + 4(l/16) + i, feature 16fb + l%16.  Progress is published
-// per 16-feature block (all rows read).
-template <int CB, int NQ, int XS, int NFB, bool SC>
-__device__ __forceinline__ void msum_tiles2(v4f (&S)[CB][NFB], int rounds0, int rounds1, int* ready0, int* ready1,
+// The sums wave of SIMD m serves E-step waves m and m + 4 (the same SIMD),
+// taking their 32-row tiles in turn: round r of wave m, then round r of wave
+// m + 4.  The per-cluster sums of a tile are onehot^T x on
+// v_mfma_f32_16x16x32_bf16, once for each part of x.  A = one-hot (16
+// clusters x the tile's 32 rows: lane l holds rows 8(l/16) + j for cluster
+// 16cb + l%16), B = a part of x (the 32 rows x 16 features of block fb, read
+// transposed from the LDS tile); D lane l: clusters 16cb + 4(l/16) + i,
+// feature 16fb + l%16.  Progress is published per 16-feature block (all rows
+// read).  Columns at and past ld hold whatever the LDS has there (the next
+// row's values, never-written padding): their sums are never published.
+template <int CB, int NQ, int XS, int NFB>
+__device__ __forceinline__ void msum_tiles3(v4f (&S)[CB][NFB], int rounds0, int rounds1, int* ready0, int* ready1,
                                             int* prog0, int* prog1, unsigned* mask0, unsigned* mask1,
-                                            const v8h* onehot, const float* tile0, const float* tile1, int lane,
-                                            float sc, float m1)
+                                            const v8bf* onehot, const float* tile0, const float* tile1, int lane)
 {
     const int h = lane >> 4, r16 = lane & 15;
 #pragma unroll
@@ -576,7 +630,7 @@ __device__ __forceinline__ void msum_tiles2(v4f (&S)[CB][NFB], int rounds0, int 
             // cluster's row mask, through the one-hot table; then the masks
             // are cleared for the next round (the E-step wave sets the next
             // bits only after this tile's progress flags, which follow)
-            v8h A[CB];
+            v8bf A[CB];
             {
                 unsigned mw[CB];
 #pragma unroll
@@ -596,23 +650,22 @@ __device__ __forceinline__ void msum_tiles2(v4f (&S)[CB][NFB], int rounds0, int 
                 for (int j = 0; j < 8; ++j) cur[j] = col[j * XS + 16 * fb];
                 // columns of feature block fb have been read for every row
                 set_flag(prog, r * NQ + (4 * fb + 4 < NQ ? 4 * fb + 4 : NQ));
-                v8h bh, bl;
-                split8<SC>(make_float4(cur[0], cur[1], cur[2], cur[3]), make_float4(cur[4], cur[5], cur[6], cur[7]), sc,
-                           m1, bh, bl);
+                const Parts8 b = split8(make_float4(cur[0], cur[1], cur[2], cur[3]),
+                                        make_float4(cur[4], cur[5], cur[6], cur[7]));
 #pragma unroll
                 for (int cb = 0; cb < CB; ++cb) {
-                    S[cb][fb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb], bh, S[cb][fb], 0, 0, 0);
-                    S[cb][fb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[cb], bl, S[cb][fb], 0, 0, 0);
+                    S[cb][fb] = mfma_bf16(A[cb], b.l, S[cb][fb]);
+                    S[cb][fb] = mfma_bf16(A[cb], b.m, S[cb][fb]);
+                    S[cb][fb] = mfma_bf16(A[cb], b.h, S[cb][fb]);
                 }
             }
         }
     }
 }
 
-// M-step sums into red = [4][CPC][ld] (unscaled), once every pair is done.
+// M-step sums into red = [4][CPC][ld], once every pair is done.
 template <int CB, int NFB>
-__device__ __forceinline__ void publish_msums(const v4f (&S)[CB][NFB], float* red, int ld, int pair, int lane,
-                                              float unscale)
+__device__ __forceinline__ void publish_msums(const v4f (&S)[CB][NFB], float* red, int ld, int pair, int lane)
 {
     const int h = lane >> 4, r16 = lane & 15;
 #pragma unroll
@@ -622,15 +675,40 @@ __device__ __forceinline__ void publish_msums(const v4f (&S)[CB][NFB], float* re
             const int f = 16 * fb + r16;
             if (f < ld) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) red[(pair * 16 * CB + 16 * cb + 4 * h + i) * ld + f] = S[cb][fb][i] * unscale;
+                for (int i = 0; i < 4; ++i) red[(pair * 16 * CB + 16 * cb + 4 * h + i) * ld + f] = S[cb][fb][i];
             }
         }
     }
 }
 
-template <int CB, int NQ, bool SC>
-__global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
+// Geometry of k_fused3 for a row of NQ float4s.
+template <int NQ>
+struct Fused3Geom {
+    static constexpr int LDX = 4 * NQ;                       // == ld
+    static constexpr int NK = LDX / 32;                      // 32-feature K steps
+    static constexpr int TAIL = LDX - 32 * NK;               // features of the last, 16-wide step (0: none)
+    static constexpr int NS = NK + (TAIL > 0 ? 1 : 0);       // K steps
+    static constexpr int QG = 2 * NK + (TAIL > 0 ? 1 : 0);   // float4s per lane per 16-row group
+    static constexpr int TQ = TAIL > 0 ? 2 * NK : 0;         // the tail's float4 (dead code without a tail)
+    static constexpr int KP = 32 * NK + (TAIL > 0 ? 16 : 0); // features the MFMAs cover
+    static constexpr int CSTR = KP + 8;                      // bf16 per centre row: an odd number of 16-byte units
+    static constexpr int XS = fused_stride(NQ);              // LDS row: >= ld floats
+    static constexpr int NFB = KP / 16;                      // 16-feature blocks of the sums
+    // a wave's tile: row rho at rho * XS + 16 (rho >> 3).  XS is 4 x odd, so
+    // 8 XS = 32 (mod 64): without the shift the sums wave's column reads of
+    // rows 8h + j (lanes h = 0..3) fall on the same banks in pairs; with it
+    // the four h start 48 h (mod 64) apart, distinct in every 32-lane pass.
+    // The sums wave reads KP columns of every row: rows past XS floats run
+    // into the next row (KP - XS floats of padding after the last one).
+    static constexpr int TS = 32 * XS + 48 + (KP > XS ? KP - XS : 0);
+    static_assert(TAIL == 0 || TAIL == 4 || TAIL == 8 || TAIL == 16, "one 16-wide step covers the tail");
+    static_assert(TS % 4 == 0, "16-byte aligned tiles");
+};
+
+template <int CB, int NQ>
+__global__ __launch_bounds__(768, 1) void k_fused3(FusedArgs a)
 {
+    using G = Fused3Geom<NQ>;
     const float* __restrict__ X = a.X;
     const long n = a.n;
     const int ld = a.ld;
@@ -638,30 +716,15 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
     const int k = a.k;
     int* __restrict__ labels = a.labels;
     LoopState* st = a.state;
-    constexpr int CPC = 16 * CB;                 // clusters padded to 16-centre blocks
-    constexpr int LDX = 4 * NQ;                  // == ld
-    constexpr int NK = LDX / 32;                 // 32-feature K steps
-    constexpr int TAIL = LDX - 32 * NK;          // features of the last, 16-wide step (0: none)
-    constexpr int NS = NK + (TAIL > 0 ? 1 : 0);  // K steps
-    constexpr int QG = 2 * NK + (TAIL > 0 ? 1 : 0);  // float4s per lane per 16-row group
-    constexpr int TQ = TAIL > 0 ? 2 * NK : 0;        // the tail's float4 (its code is dead without a tail)
-    constexpr int KP = 32 * NK + (TAIL > 0 ? 16 : 0);
-    constexpr int CSTR = KP + 8;                 // halves per centre row: an odd number of 16-byte units
-    constexpr int XS = fused_stride(KP / 4);     // LDS row: >= KP floats (tail lanes write zeros past ld)
-    constexpr int NFB = KP / 16;                 // 16-feature blocks of the sums
-    // a wave's tile: row rho at rho * XS + 16 (rho >> 3).  XS is 4 x odd, so
-    // 8 XS = 32 (mod 64): without the shift the sums wave's column reads of
-    // rows 8h + j (lanes h = 0..3) fall on the same banks in pairs; with it
-    // the four h start 48 h (mod 64) apart, distinct in every 32-lane pass.
-    // The shift only grows down the tile, so rows never overlap (XS >= KP).
-    constexpr int TS = 32 * XS + 48;
-    static_assert(TAIL == 0 || TAIL == 4 || TAIL == 8 || TAIL == 16, "one 16-wide step covers the tail");
-    // LDS: 8 wave tiles [TS floats] | centre hi parts [CPC x CSTR] halves |
-    // centre lo parts
+    constexpr int CPC = 16 * CB;  // clusters padded to 16-centre blocks
+    constexpr int LDX = G::LDX, NK = G::NK, TAIL = G::TAIL, NS = G::NS, QG = G::QG, TQ = G::TQ, KP = G::KP;
+    constexpr int CSTR = G::CSTR, XS = G::XS, NFB = G::NFB, TS = G::TS;
+    constexpr int CPART = CPC * CSTR;  // bf16 from one centre part to the next
+    // LDS: 8 wave tiles [TS floats] | centre parts hi, mid, lo [CPC x CSTR] bf16
     extern __shared__ __attribute__((aligned(16))) float lds[];
-    __shared__ unsigned sMask[8][64];                          // a tile's rows of each cluster (bit = row)
-    __shared__ __attribute__((aligned(16))) v8h sOneHot[256];  // byte b -> its 8 bits as fp16 0 / 1
-    __shared__ int sCnt[4][64];                                // rows per cluster, per SIMD
+    __shared__ unsigned sMask[8][64];                           // a tile's rows of each cluster (bit = row)
+    __shared__ __attribute__((aligned(16))) v8bf sOneHot[256];  // byte b -> its 8 bits as bf16 0 / 1
+    __shared__ int sCnt[4][64];                                 // rows per cluster, per SIMD
     __shared__ __attribute__((aligned(16))) float sN[CPC];
     __shared__ int sReady[8];  // tiles E-step wave e has labelled
     __shared__ int sProg[8];   // columns of e's tile the sums wave has read: tile * NQ + chunk
@@ -673,8 +736,7 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
     const int r16 = lane & 15;  // this lane's row of a 16-row group / centre of a block
 
     float* tiles = lds;
-    _Float16* sCH = reinterpret_cast<_Float16*>(tiles + 8 * TS);
-    _Float16* sCL = sCH + CPC * CSTR;
+    __bf16* sCP = reinterpret_cast<__bf16*>(tiles + 8 * TS);
 
     // 32-row tiles: E-step wave e of block b handles t = 8b + e + r*P
     const long ntiles = (n + 31) >> 5;
@@ -722,15 +784,11 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
         }
         __syncthreads();  // LDS set up by the sums waves
         if (sDone != 0) return;
-        const float sc = a.xscale;
-        const float f2 = a.dscale;  // -2 * 2^-2s
-        const float m1 = neg_one(sc, f2);
         float* const trow = tiles + e * TS + r16 * XS + 16 * (r16 >> 3);  // group 0's row; group g's: + g * GS
         constexpr int GS = 16 * XS + 32;
         // this lane's centre operands: one base address, the block, step and
         // part as constant offsets (no per-block address registers)
-        const _Float16* const cbase = sCH + r16 * CSTR + 8 * h;
-        constexpr int CLO = CPC * CSTR;  // hi -> lo parts
+        const __bf16* const cbase = sCP + r16 * CSTR + 8 * h;
         int changed = 0;
         for (int r = 0; r < rounds; ++r) {
             const long t = t0 + (long)r * P;
@@ -756,46 +814,43 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
                     if (seen < need) seen = wait_flag(&sProg[e], need);
                 }
                 if (s < NK) {
-                    v8h xh[2], xl[2];
+                    Parts8 xp[2];
 #pragma unroll
                     for (int g = 0; g < 2; ++g) {
                         float* dst = trow + g * GS + 32 * s + 8 * h;
                         *reinterpret_cast<float4*>(dst) = xr[g][2 * s];
                         *reinterpret_cast<float4*>(dst + 4) = xr[g][2 * s + 1];
-                        split8<SC>(xr[g][2 * s], xr[g][2 * s + 1], sc, m1, xh[g], xl[g]);
+                        xp[g] = split8(xr[g][2 * s], xr[g][2 * s + 1]);
                         load_step(rn, g, s);
                     }
 #pragma unroll
                     for (int cb = 0; cb < CB; ++cb) {
-                        const _Float16* cp = cbase + 16 * cb * CSTR + 32 * s;
-                        const v8h ah = *reinterpret_cast<const v8h*>(cp);
-                        const v8h al = *reinterpret_cast<const v8h*>(cp + CLO);
+                        const __bf16* cp = cbase + 16 * cb * CSTR + 32 * s;
+                        const Parts8 cpt{*reinterpret_cast<const v8bf*>(cp),
+                                         *reinterpret_cast<const v8bf*>(cp + CPART),
+                                         *reinterpret_cast<const v8bf*>(cp + 2 * CPART)};
 #pragma unroll
-                        for (int g = 0; g < 2; ++g) {
-                            acc[g][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, xh[g], acc[g][cb], 0, 0, 0);
-                            acc[g][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, xh[g], acc[g][cb], 0, 0, 0);
-                            acc[g][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, xl[g], acc[g][cb], 0, 0, 0);
-                        }
+                        for (int g = 0; g < 2; ++g) acc[g][cb] = dot6(cpt, xp[g], acc[g][cb]);
                     }
                 } else {
-                    v4h xh[2], xl[2];
+                    Parts4 xp[2];
 #pragma unroll
                     for (int g = 0; g < 2; ++g) {
-                        *reinterpret_cast<float4*>(trow + g * GS + 32 * NK + 4 * h) = xr[g][TQ];
-                        split4<SC>(xr[g][TQ], sc, m1, xh[g], xl[g]);
+                        // lanes past the row's last feature hold zeros and
+                        // store nothing: the LDS row may be shorter than KP
+                        if (4 * h < TAIL)
+                            *reinterpret_cast<float4*>(trow + g * GS + 32 * NK + 4 * h) = xr[g][TQ];
+                        xp[g] = split4(xr[g][TQ]);
                         load_step(rn, g, s);
                     }
 #pragma unroll
                     for (int cb = 0; cb < CB; ++cb) {
-                        const _Float16* cp = cbase - 4 * h + 16 * cb * CSTR + 32 * NK;
-                        const v4h ah = *reinterpret_cast<const v4h*>(cp);
-                        const v4h al = *reinterpret_cast<const v4h*>(cp + CLO);
+                        const __bf16* cp = cbase - 4 * h + 16 * cb * CSTR + 32 * NK;  // features 32 NK + 4h ..
+                        const Parts4 cpt{*reinterpret_cast<const v4s*>(cp),
+                                         *reinterpret_cast<const v4s*>(cp + CPART),
+                                         *reinterpret_cast<const v4s*>(cp + 2 * CPART)};
 #pragma unroll
-                        for (int g = 0; g < 2; ++g) {
-                            acc[g][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, xh[g], acc[g][cb], 0, 0, 0);
-                            acc[g][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(al, xh[g], acc[g][cb], 0, 0, 0);
-                            acc[g][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, xl[g], acc[g][cb], 0, 0, 0);
-                        }
+                        for (int g = 0; g < 2; ++g) acc[g][cb] = dot6(cpt, xp[g], acc[g][cb]);
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
@@ -813,7 +868,7 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         // a NaN distance compares false: it never wins
-                        const float dd = fmaf(f2, acc[g][cb][i], cn[i]);
+                        const float dd = fmaf(-2.0f, acc[g][cb][i], cn[i]);
                         const bool take = dd < bd;
                         bd = take ? dd : bd;
                         bi = take ? 16 * cb + 4 * h + i : bi;
@@ -842,11 +897,10 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
         __syncthreads();  // the sums are in LDS
     } else {
         // the E-step waves wait on the sums wave's progress before rewriting
-        // their tile: issue priority for the sums wave (measured +2% on the
-        // 500k x 100 k=50 step; raising the E-step waves instead changed nothing)
+        // their tile: issue priority for the sums wave
         __builtin_amdgcn_s_setprio(2);
-        // sums waves 8..11: the halt test, then the centres' scaled fp16
-        // parts (rows >= k and columns >= ld zero) and ||c||^2
+        // sums waves 8..11: the halt test, then the centres' three parts
+        // (rows >= k and columns >= ld zero) and ||c||^2
         const int prev = st->done;
         if (prev != 0) {
             if (tid == 512) sDone = prev;
@@ -856,7 +910,6 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
         const int wt = tid - 512;
         constexpr int CQ = KP / 4;
         constexpr int NF = (CPC * CQ + 255) / 256;
-        const float sc = a.xscale;
         float4 cf[NF];
 #pragma unroll
         for (int u = 0; u < NF; ++u) {
@@ -873,10 +926,11 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
             const int cl = idx / CQ;
             const int q = idx - cl * CQ;
             if (idx < CPC * CQ) {
-                v4h hi, lo;
-                split4<SC>(cf[u], sc, neg_one(sc, a.dscale), hi, lo);
-                *reinterpret_cast<v4h*>(sCH + cl * CSTR + 4 * q) = hi;
-                *reinterpret_cast<v4h*>(sCL + cl * CSTR + 4 * q) = lo;
+                const Parts4 p = split4(cf[u]);
+                __bf16* dst = sCP + cl * CSTR + 4 * q;
+                *reinterpret_cast<v4s*>(dst) = p.h;
+                *reinterpret_cast<v4s*>(dst + CPART) = p.m;
+                *reinterpret_cast<v4s*>(dst + 2 * CPART) = p.l;
             }
         }
         if (wt < 8) {
@@ -887,10 +941,11 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
         sMask[wt >> 6][wt & 63] = 0u;
         sMask[4 + (wt >> 6)][wt & 63] = 0u;
         {
-            v8h oh;
+            unsigned w[4];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) oh[j] = (wt >> j) & 1 ? (_Float16)1.0f : (_Float16)0.0f;
-            sOneHot[wt] = oh;
+            for (int j = 0; j < 4; ++j)
+                w[j] = ((wt >> (2 * j)) & 1 ? 0x3f80u : 0u) | ((wt >> (2 * j + 1)) & 1 ? 0x3f800000u : 0u);
+            sOneHot[wt] = __builtin_bit_cast(v8bf, v4u{w[0], w[1], w[2], w[3]});
         }
         if (wave == 8) step_norms<CPC>(a, lane, sN, &sDone);
         __syncthreads();
@@ -898,38 +953,44 @@ __global__ __launch_bounds__(768, 1) void k_fused16(FusedArgs a)
         // the sums wave of SIMD m serves E-step waves m and m + 4
         const int m = wave - 8;
         v4f S[CB][NFB];
-        msum_tiles2<CB, NQ, XS, NFB, SC>(S, rounds_of(m), rounds_of(m + 4), &sReady[m], &sReady[m + 4], &sProg[m],
-                                         &sProg[m + 4], sMask[m], sMask[m + 4], sOneHot, tiles + m * TS,
-                                         tiles + (m + 4) * TS, lane, sc, neg_one(sc, a.dscale));
+        msum_tiles3<CB, NQ, XS, NFB>(S, rounds_of(m), rounds_of(m + 4), &sReady[m], &sReady[m + 4], &sProg[m],
+                                     &sProg[m + 4], sMask[m], sMask[m + 4], sOneHot, tiles + m * TS,
+                                     tiles + (m + 4) * TS, lane);
         __syncthreads();  // every wave is done with its tile
-        publish_msums<CB, NFB>(S, tiles, ld, m, lane, SC ? 1.f / sc : 1.f);
+        publish_msums<CB, NFB>(S, tiles, ld, m, lane);
         __syncthreads();
     }
     combine_sums<CPC, 768>(tiles, ld, k, a.psum, a.pcnt, sCnt, tid);
 }
 
 // ---------------------------------------------------------------------------
-// k_assign16: the E-step for any k (the generic path and the assign entry
-// point) on fp16 MFMA with the same two-part split and operand layout as
-// k_fused16.  A block of 8 waves owns 256 rows (32 per wave: two 16-row
-// groups); it takes the centres in passes of 16*CB (A operands from LDS, hi
-// and lo parts staged per 128-feature segment by the whole block) and keeps
-// per lane the first minimum over its centres 16cb + 4(l/16) + i, in
-// ascending order across passes; the four lanes of a row are combined after
-// the last pass.  X is read once per pass (k/(16 CB) times), the centres once
-// per 256 rows.
-template <int CB, bool SC>
-__global__ __launch_bounds__(512, 1) void k_assign16(const float* __restrict__ X, long n, int ld,
-                                                    const float* __restrict__ C, const float* __restrict__ cnorm,
-                                                    int k, int* __restrict__ labels, LoopState* st, int* changed,
-                                                    float sc, float f2)
+// k_assign3: the E-step for any k (the generic path and the assign entry
+// point) on bf16 MFMA over the three-part split, with k_fused3's operand
+// layout.  A block of 8 waves owns 256 rows (32 per wave: two 16-row groups);
+// it takes the centres in passes of 16*CB (A operands from LDS, the three
+// parts staged per SEG-feature segment by the whole block) and keeps per lane
+// the first minimum over its centres 16cb + 4(l/16) + i, in ascending order
+// across passes; the four lanes of a row are combined after the last pass.
+// X is read once per pass (k/(16 CB) times), the centres once per 256 rows.
+template <int CB>
+struct Assign3Geom {
+    static constexpr int CPC = 16 * CB;               // centres per pass
+    static constexpr int SEG = CB >= 16 ? 64 : 128;   // features per staged segment
+    static constexpr int NKS = SEG / 32;              // K32 steps per segment
+    static constexpr int CSTR = SEG + 8;              // bf16 per centre row: an odd number of 16-byte units
+    static constexpr int CPART = CPC * CSTR;          // bf16 from one part to the next
+    static constexpr size_t LDS = size_t(3) * CPART * sizeof(__bf16);
+};
+
+template <int CB>
+__global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X, long n, int ld,
+                                                   const float* __restrict__ C, const float* __restrict__ cnorm,
+                                                   int k, int* __restrict__ labels, LoopState* st, int* changed)
 {
     if (st != nullptr && st->done != 0) return;
-    constexpr int CPC = 16 * CB;       // centres per pass
-    constexpr int SEG = 128;           // features per staged segment (4 K32 steps)
-    constexpr int CSTR = SEG + 8;      // halves per centre row: an odd number of 16-byte units
-    constexpr int CLO = CPC * CSTR;    // hi -> lo parts
-    extern __shared__ __attribute__((aligned(16))) _Float16 cs[];  // [2][CPC][CSTR]
+    using G = Assign3Geom<CB>;
+    constexpr int CPC = G::CPC, SEG = G::SEG, NKS = G::NKS, CSTR = G::CSTR, CPART = G::CPART;
+    extern __shared__ __attribute__((aligned(16))) __bf16 cs[];  // [3][CPC][CSTR]
     __shared__ __attribute__((aligned(16))) float sN[CPC];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -937,8 +998,8 @@ __global__ __launch_bounds__(512, 1) void k_assign16(const float* __restrict__ X
     const int h = lane >> 4, r16 = lane & 15;
     const int npass = (k + CPC - 1) / CPC;
     const int nseg = (ld + SEG - 1) / SEG;
-    const _Float16* const cbase = cs + r16 * CSTR + 8 * h;
-    // one pass of one segment (k <= 16 CB, ld <= 128): the staged operands
+    const __bf16* const cbase = cs + r16 * CSTR + 8 * h;
+    // one pass of one segment (k <= 16 CB, ld <= SEG): the staged operands
     // are the same for every row block, so they are staged once
     const bool once = npass == 1 && nseg == 1;
 
@@ -962,10 +1023,10 @@ __global__ __launch_bounds__(512, 1) void k_assign16(const float* __restrict__ X
                 __syncthreads();  // the previous segment's operands are consumed
                 // stage centres p*CPC.. x the features f0.. of the K steps this
                 // segment has (32 each; centres >= k and features >= ld zero),
-                // as scaled fp16 parts: eight threads per (centre, K step), two
-                // K steps' loads in flight before the first conversion
+                // as the three bf16 parts: eight threads per (centre, K step),
+                // two K steps' loads in flight before the first split
                 constexpr int UPK = CPC * 8 / 512;  // float4s per thread per K step
-                const int nks_s = min(4, (ld - f0 + 31) / 32);
+                const int nks_s = min(NKS, (ld - f0 + 31) / 32);
                 for (int ks0 = 0; ks0 < nks_s; ks0 += 2) {
                     float4 v[2][UPK];
 #pragma unroll
@@ -988,10 +1049,11 @@ __global__ __launch_bounds__(512, 1) void k_assign16(const float* __restrict__ X
                             const int idx = tid + 512 * u;
                             const int cl = idx >> 3;
                             const int q = 8 * (ks0 + kk) + (idx & 7);
-                            v4h hi, lo;
-                            split4<SC>(v[kk][u], sc, neg_one(sc, f2), hi, lo);
-                            *reinterpret_cast<v4h*>(cs + cl * CSTR + 4 * q) = hi;
-                            *reinterpret_cast<v4h*>(cs + CLO + cl * CSTR + 4 * q) = lo;
+                            const Parts4 pt = split4(v[kk][u]);
+                            __bf16* dst = cs + cl * CSTR + 4 * q;
+                            *reinterpret_cast<v4s*>(dst) = pt.h;
+                            *reinterpret_cast<v4s*>(dst + CPART) = pt.m;
+                            *reinterpret_cast<v4s*>(dst + 2 * CPART) = pt.l;
                         }
                     }
                 }
@@ -1003,28 +1065,25 @@ __global__ __launch_bounds__(512, 1) void k_assign16(const float* __restrict__ X
                 }
                 __syncthreads();
                 }
-                const int nks = min(4, (ld - f0 + 31) / 32);
+                const int nks = min(NKS, (ld - f0 + 31) / 32);
                 for (int ks = 0; ks < nks; ++ks) {
                     // rows 16g + l%16, features f0 + 32ks + 8h..: past the
                     // row's end the next row's (finite) values meet zero
                     // centre parts; past the last row the loads return 0
-                    v8h xh[2], xl[2];
+                    Parts8 xp[2];
 #pragma unroll
                     for (int g = 0; g < 2; ++g) {
                         const int o = ((16 * g + r16) * ld + f0 + 32 * ks + 8 * h) * 4;
-                        split8<SC>(load_quad(rs, o), load_quad(rs, o + 16), sc, neg_one(sc, f2), xh[g], xl[g]);
+                        xp[g] = split8(load_quad(rs, o), load_quad(rs, o + 16));
                     }
 #pragma unroll
                     for (int cb = 0; cb < CB; ++cb) {
-                        const _Float16* cp = cbase + 16 * cb * CSTR + 32 * ks;
-                        const v8h ah = *reinterpret_cast<const v8h*>(cp);
-                        const v8h al = *reinterpret_cast<const v8h*>(cp + CLO);
+                        const __bf16* cp = cbase + 16 * cb * CSTR + 32 * ks;
+                        const Parts8 cpt{*reinterpret_cast<const v8bf*>(cp),
+                                         *reinterpret_cast<const v8bf*>(cp + CPART),
+                                         *reinterpret_cast<const v8bf*>(cp + 2 * CPART)};
 #pragma unroll
-                        for (int g = 0; g < 2; ++g) {
-                            acc[g][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, xh[g], acc[g][cb], 0, 0, 0);
-                            acc[g][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, xh[g], acc[g][cb], 0, 0, 0);
-                            acc[g][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, xl[g], acc[g][cb], 0, 0, 0);
-                        }
+                        for (int g = 0; g < 2; ++g) acc[g][cb] = dot6(cpt, xp[g], acc[g][cb]);
                     }
                 }
             }
@@ -1038,7 +1097,7 @@ __global__ __launch_bounds__(512, 1) void k_assign16(const float* __restrict__ X
                     const float cn[4] = {c4.x, c4.y, c4.z, c4.w};
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const float dd = fmaf(f2, acc[g][cb][i], cn[i]);  // NaN compares false
+                        const float dd = fmaf(-2.0f, acc[g][cb][i], cn[i]);  // NaN compares false
                         const bool take = dd < bd[g];
                         bd[g] = take ? dd : bd[g];
                         bi[g] = take ? p * CPC + 16 * cb + 4 * h + i : bi[g];
@@ -1075,32 +1134,36 @@ __global__ __launch_bounds__(512, 1) void k_assign16(const float* __restrict__ X
     }
 }
 
-typedef void (*assign16_fn)(const float*, long, int, const float*, const float*, int, int*, LoopState*, int*, float,
-                            float);
+typedef void (*assign3_fn)(const float*, long, int, const float*, const float*, int, int*, LoopState*, int*);
 
-static assign16_fn assign16_kernel(int k, bool scaled)
+static int assign3_cb(int k) { return k <= 64 ? 4 : k <= 128 ? 8 : 16; }
+
+static assign3_fn assign3_kernel(int k)
 {
-    const int cb = k <= 64 ? 4 : k <= 128 ? 8 : 16;
-    if (cb == 4) return scaled ? &k_assign16<4, true> : &k_assign16<4, false>;
-    if (cb == 8) return scaled ? &k_assign16<8, true> : &k_assign16<8, false>;
-    return scaled ? &k_assign16<16, true> : &k_assign16<16, false>;
+    const int cb = assign3_cb(k);
+    return cb == 4 ? &k_assign3<4> : cb == 8 ? &k_assign3<8> : &k_assign3<16>;
 }
 
-static size_t assign16_lds(int k)
+static size_t assign3_lds(int k)
 {
-    const int cb = k <= 64 ? 4 : k <= 128 ? 8 : 16;
-    return (size_t)2 * 16 * cb * (128 + 8) * sizeof(_Float16);
+    const int cb = assign3_cb(k);
+    return cb == 4 ? Assign3Geom<4>::LDS : cb == 8 ? Assign3Geom<8>::LDS : Assign3Geom<16>::LDS;
 }
 
-int assign16_ready(int d, int k)
+// SKMETAL_HIP_SPLIT=0 keeps the fp32 MFMA E-step for every shape
+static bool split_disabled()
 {
-    const char* env = getenv("SKMETAL_HIP_F16");
-    if (env != nullptr && env[0] == '0') return 0;
-    if (d < 17 || k < 1) return 0;
-    for (const bool scaled : {false, true}) {
-        assign16_fn f = assign16_kernel(k, scaled);
+    const char* env = getenv("SKMETAL_HIP_SPLIT");
+    return env != nullptr && env[0] == '0';
+}
+
+int assign3_ready(int d, int k)
+{
+    if (split_disabled() || d < 17 || k < 1) return 0;
+    for (const int kk : {64, 128, 129}) {
+        assign3_fn f = assign3_kernel(kk);
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(f), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)assign16_lds(k)) != hipSuccess) {
+                                (int)assign3_lds(kk)) != hipSuccess) {
             (void)hipGetLastError();
             return 0;
         }
@@ -1108,14 +1171,13 @@ int assign16_ready(int d, int k)
     return 1;
 }
 
-hipError_t launch_assign16(const AssignArgs& a, float xscale, float dscale, int num_cu, hipStream_t s)
+hipError_t launch_assign3(const AssignArgs& a, int num_cu, hipStream_t s)
 {
     if (a.n <= 0) return hipSuccess;
-    assign16_fn f = assign16_kernel(a.k, xscale != 1.f);
     long blocks = (a.n + 255) / 256;
     if (blocks > num_cu) blocks = num_cu;
-    hipLaunchKernelGGL(f, dim3((unsigned)blocks), dim3(512), assign16_lds(a.k), s, a.X, a.n, a.ld, a.C, a.cnorm, a.k,
-                       a.labels, a.state, a.changed, xscale, dscale);
+    hipLaunchKernelGGL(assign3_kernel(a.k), dim3((unsigned)blocks), dim3(512), assign3_lds(a.k), s, a.X, a.n, a.ld,
+                       a.C, a.cnorm, a.k, a.labels, a.state, a.changed);
     return hipGetLastError();
 }
 
@@ -1156,56 +1218,48 @@ static fused_fn fused_kernel(int k, int ld)
 }
 
 template <int NQ, int... CBs>
-struct Fused16Table {
-    static fused_fn get(int cb, bool scaled)
+struct Fused3Table {
+    static fused_fn get(int cb)
     {
         fused_fn f = nullptr;
-        ((cb == CBs ? (f = scaled ? &k_fused16<CBs, NQ, true> : &k_fused16<CBs, NQ, false>, 0) : 0), ...);
+        ((cb == CBs ? (f = &k_fused3<CBs, NQ>, 0) : 0), ...);
         return f;
+    }
+    static size_t dyn_lds(int cb)
+    {
+        using G = Fused3Geom<NQ>;
+        return (size_t)8 * G::TS * sizeof(float) + (size_t)3 * 16 * cb * G::CSTR * sizeof(__bf16);
     }
 };
 
-// The fp16-split kernel for row strides of 32 floats and more (below that
-// the K steps would be mostly padding).
-static fused_fn fused16_kernel(int k, int ld, bool scaled)
+// The split kernel for row strides of 32 floats and more (below that the K
+// steps would be mostly padding).
+static fused_fn fused3_kernel(int k, int ld, size_t* dyn)
 {
     if (k < 1 || k > 64) return nullptr;
     const int cb = (k + 15) / 16;
     switch (ld) {
-    case 32: return Fused16Table<8, 1, 2, 3, 4>::get(cb, scaled);
-    case 48: return Fused16Table<12, 1, 2, 3, 4>::get(cb, scaled);
-    case 64: return Fused16Table<16, 1, 2, 3, 4>::get(cb, scaled);
-    case 80: return Fused16Table<20, 1, 2, 3, 4>::get(cb, scaled);
-    case 100: return Fused16Table<25, 1, 2, 3, 4>::get(cb, scaled);
+    case 32: *dyn = Fused3Table<8, 1, 2, 3, 4>::dyn_lds(cb); return Fused3Table<8, 1, 2, 3, 4>::get(cb);
+    case 48: *dyn = Fused3Table<12, 1, 2, 3, 4>::dyn_lds(cb); return Fused3Table<12, 1, 2, 3, 4>::get(cb);
+    case 64: *dyn = Fused3Table<16, 1, 2, 3, 4>::dyn_lds(cb); return Fused3Table<16, 1, 2, 3, 4>::get(cb);
+    case 80: *dyn = Fused3Table<20, 1, 2, 3, 4>::dyn_lds(cb); return Fused3Table<20, 1, 2, 3, 4>::get(cb);
+    case 100: *dyn = Fused3Table<25, 1, 2, 3, 4>::dyn_lds(cb); return Fused3Table<25, 1, 2, 3, 4>::get(cb);
     default: return nullptr;
     }
 }
 
-static size_t fused16_dyn_lds(int k, int ld)
+int fused3_ready(int k, int ld)
 {
-    const int cpc = 16 * ((k + 15) / 16);
-    const int nk = ld / 32;
-    const int kp = 32 * nk + (ld > 32 * nk ? 16 : 0);
-    return (size_t)8 * (32 * fused_stride(kp / 4) + 48) * sizeof(float) + (size_t)2 * cpc * (kp + 8) * sizeof(_Float16);
-}
-
-int fused16_ready(int k, int ld)
-{
-    // SKMETAL_HIP_F16=0 keeps the fp32 MFMA E-step for every shape
-    const char* env = getenv("SKMETAL_HIP_F16");
-    if (env != nullptr && env[0] == '0') return 0;
-    const size_t dyn = fused16_dyn_lds(k, ld);
+    if (split_disabled()) return 0;
+    size_t dyn = 0;
+    fused_fn f = fused3_kernel(k, ld, &dyn);
     // sMask, sOneHot, sCnt, sN, flags
     const size_t stat = 8 * 64 * sizeof(unsigned) + 256 * 16 + 4 * 64 * sizeof(int) + 64 * sizeof(float) + 128;
-    if (dyn + stat > 160 * 1024) return 0;
-    for (const bool scaled : {false, true}) {
-        fused_fn f = fused16_kernel(k, ld, scaled);
-        if (f == nullptr) return 0;
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(f), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)dyn) != hipSuccess) {
-            (void)hipGetLastError();
-            return 0;
-        }
+    if (f == nullptr || dyn + stat > 160 * 1024) return 0;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(f), hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) !=
+        hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
     }
     return 1;
 }
@@ -1250,10 +1304,11 @@ int fused_blocks(long n, int ld, int k, int num_cu)
 
 hipError_t launch_fused(const FusedArgs& a, hipStream_t s)
 {
-    fused_fn f = a.f16 ? fused16_kernel(a.k, a.ld, a.xscale != 1.f) : fused_kernel(a.k, a.ld);
+    size_t dyn = 0;
+    fused_fn f = a.split ? fused3_kernel(a.k, a.ld, &dyn) : fused_kernel(a.k, a.ld);
+    if (!a.split) dyn = fused_dyn_lds(a.k, a.ld);
     if (f == nullptr || a.blocks < 1) return hipErrorInvalidValue;
-    const size_t dyn = a.f16 ? fused16_dyn_lds(a.k, a.ld) : fused_dyn_lds(a.k, a.ld);
-    hipLaunchKernelGGL(f, dim3(a.blocks), dim3(a.f16 ? 768 : 512), dyn, s, a);
+    hipLaunchKernelGGL(f, dim3(a.blocks), dim3(a.split ? 768 : 512), dyn, s, a);
     return hipGetLastError();
 }
 

@@ -46,11 +46,16 @@ struct AssignArgs {
     int* changed;          // nullable: compare with previous labels, add the changes here
 };
 hipError_t launch_assign(const AssignArgs& a, int num_cu, hipStream_t s);
-// The same E-step on fp16 MFMA with x and c split in two scaled fp16 parts
-// (xscale = 2^s, dscale = -2 * 2^-2s); assign16_ready(d, k) = 1 when it
-// applies to the shape (sets its LDS attribute).
-int assign16_ready(int d, int k);
-hipError_t launch_assign16(const AssignArgs& a, float xscale, float dscale, int num_cu, hipStream_t s);
+// The same E-step on bf16 MFMAs over the exact three-part bf16 split of x
+// and c (k_assign3); assign3_ready(d, k) = 1 when it applies to the shape
+// (sets its LDS attributes).  The data must be in the split's range
+// (split_range_ok).
+int assign3_ready(int d, int k);
+hipError_t launch_assign3(const AssignArgs& a, int num_cu, hipStream_t s);
+// The three-part bf16 split is exact for finite values of magnitude >= 2^-103,
+// and the E-step's smallest kept part products stay normal fp32 numbers when
+// the data's largest magnitude is 0 or at least 2^-50.
+inline bool split_range_ok(float absmax) { return absmax == 0.f || (absmax >= 0x1p-50f && absmax <= 0x1p+60f); }
 
 // Fused E-step + per-cluster sums (k <= 64, d <= 100).
 struct FusedArgs {
@@ -69,18 +74,18 @@ struct FusedArgs {
     int decide; int iter; double tol; int flags;
     const double* part; int nch; const int* counts; const int* prev_changed;
     float* cnorm_out; float* shift_sq;
-    // f16 = 1: the E-step on fp16 MFMAs with x and c split in two scaled
-    // parts (xscale = 2^s, dscale = -2 * 2^-2s); see fused16_ready
-    int f16 = 0; float xscale = 1.f; float dscale = -2.f;
+    // split = 1: k_fused3 (E-step and sums on bf16 MFMAs over the exact
+    // three-part split); see fused3_ready
+    int split = 0;
 };
 // Row stride (floats) X must have for the fused kernel, or 0 when (d, k) does
 // not qualify; the pad columns are zero.
 int fused_ld(int d, int k);
 // Number of blocks (= partials) of the fused kernel for n rows of stride ld.
 int fused_blocks(long n, int ld, int k, int num_cu);
-// 1 when the fp16-split fused kernel exists for (k, ld) and fits in LDS (sets
-// its LDS attribute); the caller still needs a valid scale for the data.
-int fused16_ready(int k, int ld);
+// 1 when the split fused kernel exists for (k, ld) and fits in LDS (sets its
+// LDS attribute); the data must still be in the split's range.
+int fused3_ready(int k, int ld);
 hipError_t launch_fused(const FusedArgs& a, hipStream_t s);
 
 struct UpdateArgs {

@@ -346,15 +346,14 @@ struct Lloyd {
     int* s_slab = nullptr;
     float* s_rec = nullptr;
     int fblocks = 0;        // > 0: fused E-step + sums kernel with this many partials
-    // fp16-split E-step of the fused kernel: available for this shape
-    // (f16cap) and used while the data's scale allows it (f16_on); xmax/cmax
-    // are the largest |x| of X and of the centres last set, in device
-    // coordinates
-    int f16cap = 0;
-    bool f16_on = false;
-    int a16cap = 0;         // the fp16-split E-step of the separate assign kernel
-    bool a16_on = false;
-    float xmax = 0.f, cmax = 0.f, xscale = 1.f, dscale = -2.f;
+    // kernels over the exact three-part bf16 split: the fused one (f3cap) and
+    // the separate E-step (a3cap) exist for this shape; they run while X is
+    // in the split's range (split_on, from xmax = the largest |x| of the
+    // loaded X, NaN counted as +inf)
+    int f3cap = 0;
+    int a3cap = 0;
+    bool split_on = false;
+    float xmax = 0.f;
     unsigned* absmax = nullptr;
     int cur = 0;            // index of the current centres in cen[]
     bool centred = false;
@@ -379,8 +378,8 @@ struct Lloyd {
         s = C->stream;
         ug = update_geometry(n, d, k, C->num_cu);
         fblocks = lf > 0 ? fused_blocks(n, ld, k, C->num_cu) : 0;
-        f16cap = fblocks > 0 ? fused16_ready(k, ld) : 0;
-        a16cap = assign16_ready(d, k);
+        f3cap = fblocks > 0 ? fused3_ready(k, ld) : 0;
+        a3cap = assign3_ready(d, k);
         if (fblocks == 0) sg = sort_geometry(n, d, ld, k);
         const int Rmax = sg.on ? 1 : std::max(ug.R, fblocks);
         const int chunks = std::max({finalize_col_chunks(d, ug.R), fblocks > 0 ? finalize_col_chunks(d, fblocks) : 0,
@@ -454,9 +453,10 @@ struct Lloyd {
             HIP_TRY(hipMemsetAsync(mean, 0, size_t(ld) * sizeof(float), s), "hipMemsetAsync");
         }
         xmax_known = false;
-        if (f16cap || a16cap) {
+        split_on = false;
+        if (f3cap || a3cap) {
             TRY(measure_xmax());
-            update_scale();
+            split_on = split_range_ok(xmax);
         }
         return 0;
     }
@@ -473,40 +473,9 @@ struct Lloyd {
         return 0;
     }
 
-    // x and c are scaled by 2^s for the fp16 split so that the largest |x|,
-    // |c| (m) stays below 2^14, far from fp16's overflow (65504), and above
-    // 2^-3: a split part that falls below fp16's smallest normal (2^-14) then
-    // errs by at most 2^-25 absolute, under 2^-22 m, the same order as the
-    // relative error of the split.  s = 0 whenever m is already in
-    // [2^-3, 2^14) (no scaling multiply in the kernel), else m lands in
-    // [2^13, 2^14).  Non-finite data, or a scale whose 2^(1-2s) would leave
-    // fp32's normal range, keep the fp32 E-step.
-    void update_scale()
-    {
-        const float m = std::max(xmax, cmax);
-        int e = 0;
-        if (m > 0.f && std::isfinite(m)) std::frexp(m, &e);  // m = f 2^e, f in [0.5, 1)
-        const int sh = m > 0.f && (e > 14 || e < -2) ? 14 - e : 0;
-        const bool ok = std::isfinite(m) && sh >= -60 && sh <= 60;
-        f16_on = f16cap != 0 && ok;
-        a16_on = a16cap != 0 && ok;
-        xscale = std::ldexp(1.f, sh);
-        dscale = -std::ldexp(1.f, 1 - 2 * sh);
-    }
-
     // Centres given in caller coordinates -> device (centred like X).
     int set_centers(const float* host)
     {
-        if (f16cap || a16cap) {
-            double m = 0.0;
-            for (int j = 0; j < k; ++j)
-                for (int c = 0; c < d; ++c) {
-                    const double v = std::fabs(double(host[size_t(j) * d + c]) - (centred ? double(h_mean[c]) : 0.0));
-                    m = v != v ? INFINITY : std::max(m, v);
-                }
-            cmax = float(m * (1.0 + 1e-6));
-            update_scale();
-        }
         TRY(upload_rows(*C, host, k, d, ld, cen[cur], s));
         if (centred) HIP_TRY(launch_center(cen[cur], k, ld, d, mean, s), "center launch");
         HIP_TRY(launch_cnorm(cen[cur], k, ld, cnorm, s), "cnorm launch");
@@ -541,8 +510,8 @@ struct Lloyd {
     int assign(const float* cents, LoopState* state, int* changed)
     {
         AssignArgs a{X, n, ld, cents, cnorm, k, labels, state, changed};
-        if (a16_on)
-            HIP_TRY(launch_assign16(a, xscale, dscale, C->num_cu, s), "assign launch");
+        if (split_on && a3cap)
+            HIP_TRY(launch_assign3(a, C->num_cu, s), "assign launch");
         else
             HIP_TRY(launch_assign(a, C->num_cu, s), "assign launch");
         return 0;
@@ -568,9 +537,7 @@ struct Lloyd {
         FusedArgs a{X, n, ld, cen[cur], cnorm, k, labels, psum, pcnt, st, fblocks, &st->chg[iter & 1],
                     decide ? 1 : 0, iter, tol, flags, part, finalize_col_chunks(d, fblocks), counts,
                     &st->chg[(iter + 1) & 1], cnorm, shift_sq};
-        a.f16 = f16_on ? 1 : 0;
-        a.xscale = xscale;
-        a.dscale = dscale;
+        a.split = split_on && f3cap ? 1 : 0;
         HIP_TRY(launch_fused(a, s), "fused launch");
         return 0;
     }
@@ -860,10 +827,6 @@ struct Lloyd {
         }
         HIP_TRY(launch_pp_select(pp, k, s), "pp select launch");
         HIP_TRY(launch_cnorm(cen[cur], k, ld, cnorm, s), "cnorm launch");
-        if (f16cap || a16cap) {
-            cmax = xmax;  // the centres are rows of X
-            update_scale();
-        }
         TRY(download_bytes(*C, pp.idx, size_t(k) * sizeof(long), idx_out, s));
         return 0;
     }
@@ -1341,7 +1304,8 @@ int skmetal_hip_lloyd_max_abs(skmetal_hip_lloyd* h, float* out)
 int skmetal_hip_lloyd_info(skmetal_hip_lloyd* h, int* fused, int* partials)
 {
     if (!h) return fail(SKMETAL_EINVAL, "null pointer argument");
-    if (fused) *fused = (h->L.fblocks > 0 ? (h->L.f16_on ? 2 : 1) : 0) | (h->L.a16_on ? 4 : 0);
+    const Lloyd& L = h->L;
+    if (fused) *fused = (L.fblocks > 0 ? (L.split_on && L.f3cap ? 2 : 1) : 0) | (L.split_on && L.a3cap ? 4 : 0);
     if (partials) *partials = h->L.fblocks > 0 ? h->L.fblocks : h->L.sg.on ? (int)h->L.sg.nchunks : h->L.ug.R;
     return 0;
 }

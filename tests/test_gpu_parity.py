@@ -18,6 +18,7 @@ import pytest
 
 import oracle
 from oracle import parity
+from problems import mixed_scale_problem
 
 pytestmark = pytest.mark.gpu
 
@@ -114,29 +115,33 @@ def test_mindists_and_inertia_vs_oracle(bridge):
     parity.check_inertia(v, oracle.inertia(X, C, lab), what="kmeans_inertia")
 
 
-def _lockstep_gpu(bridge, X, C0, steps, what):
-    """Run `steps` single GPU steps from C0, checking each against the oracle."""
+def _lockstep_gpu(bridge, X, C0, steps, what, center=True, elem_rtol=None):
+    """Run `steps` single GPU steps from C0, checking each against the oracle
+    (in the coordinates the device runs in: X centred on its fp32 column mean,
+    as scikit-learn's fit does, or X as given)."""
     n, d = X.shape
     k = C0.shape[0]
-    mean = X.mean(axis=0)
+    mean = X.mean(axis=0) if center else np.zeros(d, np.float32)
     Xc = X - mean
     prev = C0
     n_mism = 0
     with bridge.LloydHandle(n, d, k) as h:
-        h.load(X, center=True)
+        h.load(X, center=center)
         for m in range(steps):
             h.set_centers(prev)
             h.iterate(1)
             lab = h.labels()
             Cn = h.centers()
-            n_mism += parity.check_lockstep(Xc, prev - mean, Cn - mean, lab, what=f"{what} step {m + 1}")
+            n_mism += parity.check_lockstep(Xc, prev - mean, Cn - mean, lab, what=f"{what} step {m + 1}",
+                                            elem_rtol=elem_rtol)
             prev = Cn
     return n_mism
 
 
-# (n, d, k) covering every row stride of the fp16x2-split E-step (with and
-# without a 16-wide K tail, pad columns) and 1..4 blocks of 16 centres
-F16_SHAPES = [(3000, 17, 5), (4100, 33, 16), (5000, 64, 17), (6000, 80, 48), (20000, 97, 50), (7000, 100, 64)]
+# (n, d, k) covering every row stride of the split kernel (with and without a
+# 16-wide K tail, pad columns; d = 100 has an LDS row shorter than its MFMA
+# span) and 1..4 blocks of 16 centres
+SPLIT_SHAPES = [(3000, 17, 5), (4100, 33, 16), (5000, 64, 17), (6000, 80, 48), (20000, 97, 50), (7000, 100, 64)]
 
 
 def _blob_problem(n, d, k, seed, scale=1.0):
@@ -147,7 +152,7 @@ def _blob_problem(n, d, k, seed, scale=1.0):
     return X, C0
 
 
-def _f16_engaged(bridge, X, C0):
+def _split_engaged(bridge, X, C0):
     n, d = X.shape
     with bridge.LloydHandle(n, d, C0.shape[0]) as h:
         h.load(X, center=True)
@@ -155,27 +160,27 @@ def _f16_engaged(bridge, X, C0):
         return h.info()
 
 
-@pytest.mark.parametrize("n,d,k", F16_SHAPES)
-def test_f16_estep_lockstep(bridge, n, d, k):
-    """Fused steps with the E-step on fp16 MFMA (x, c split in two scaled
-    fp16 parts) against the oracle, step by step."""
-    _say(f"f16 lockstep n={n} d={d} k={k}")
+@pytest.mark.parametrize("n,d,k", SPLIT_SHAPES)
+def test_split_estep_lockstep(bridge, n, d, k):
+    """Fused steps with the E-step and sums on bf16 MFMAs over the exact
+    three-part split, against the oracle step by step."""
+    _say(f"split lockstep n={n} d={d} k={k}")
     X, C0 = _blob_problem(n, d, k, seed=n + d + k)
-    info = _f16_engaged(bridge, X, C0)
-    assert info["fused"] and info["f16"], info
-    _lockstep_gpu(bridge, X, C0, 3, what=f"f16 {n}x{d} k={k}")
+    info = _split_engaged(bridge, X, C0)
+    assert info["fused"] and info["split"], info
+    _lockstep_gpu(bridge, X, C0, 3, what=f"split {n}x{d} k={k}")
 
 
 @pytest.mark.parametrize("n,k", [(1, 1), (5, 3), (31, 4), (33, 7), (100, 20), (257, 64)])
-def test_f16_tiny_problems(bridge, n, k):
+def test_split_tiny_problems(bridge, n, k):
     """Partial 32-row tiles and waves with no tile at all (most of the grid)."""
-    _say(f"f16 tiny n={n} k={k}")
+    _say(f"split tiny n={n} k={k}")
     rng = np.random.default_rng(n * 7 + k)
     X = (rng.standard_normal((n, 40)) * 3).astype(np.float32)
     C0 = X[np.sort(rng.choice(n, k, replace=False))].copy()
-    info = _f16_engaged(bridge, X, C0)
-    assert info["fused"] and info["f16"], info
-    _lockstep_gpu(bridge, X, C0, 2, what=f"f16 tiny {n} k={k}")
+    info = _split_engaged(bridge, X, C0)
+    assert info["fused"] and info["split"], info
+    _lockstep_gpu(bridge, X, C0, 2, what=f"split tiny {n} k={k}")
     C = C0.copy()
     lab = np.empty(n, np.int32)
     n_iter, _ = bridge.kmeans_fit(X, C, lab, 50, 0.0, strict=True)
@@ -184,8 +189,8 @@ def test_f16_tiny_problems(bridge, n, k):
     parity.check_centers(C, out["centers"], what=f"tiny fit n={n} k={k}")
 
 
-def test_f16_assign_duplicate_centres_lowest_index(bridge):
-    """Identical centres give identical fp16-split distances: the lowest index wins."""
+def test_split_assign_duplicate_centres_lowest_index(bridge):
+    """Identical centres give identical split distances: the lowest index wins."""
     rng = np.random.default_rng(11)
     X = rng.standard_normal((3000, 40)).astype(np.float32)
     base = rng.standard_normal((7, 40)).astype(np.float32)
@@ -194,56 +199,95 @@ def test_f16_assign_duplicate_centres_lowest_index(bridge):
     bridge.kmeans_assign(X, C, out, 3000, 40, 21)
     ref, best, second = oracle.assign(X, C, return_gap=True)
     assert out.max() < 7
-    parity.check_labels(out, ref, best, second, X, what="f16 duplicate centres")
+    parity.check_labels(out, ref, best, second, X, what="split duplicate centres")
 
 
 @pytest.mark.parametrize("n,d,k", [(3000, 101, 10), (40, 20, 40), (2000, 17, 64)])
-def test_f16_edge_shapes_lockstep(bridge, n, d, k):
+def test_split_edge_shapes_lockstep(bridge, n, d, k):
     """d just past the fused limit (generic path with k <= 64), k = n, the
-    smallest fp16 row stride with 64 centres."""
-    _say(f"f16 edge n={n} d={d} k={k}")
+    smallest split row stride with 64 centres."""
+    _say(f"split edge n={n} d={d} k={k}")
     X, C0 = _blob_problem(n, d, k, seed=3 * n + d)
-    info = _f16_engaged(bridge, X, C0)
-    assert info["f16"] or info["a16"], info
-    _lockstep_gpu(bridge, X, C0, 2, what=f"f16 edge {n}x{d} k={k}")
+    info = _split_engaged(bridge, X, C0)
+    assert info["split"] or info["asplit"], info
+    _lockstep_gpu(bridge, X, C0, 2, what=f"split edge {n}x{d} k={k}")
 
 
 @pytest.mark.parametrize("scale", [1e-15, 1e-3, 1e4, 1e15])
-def test_f16_estep_scaled_data(bridge, scale):
-    """The 2^s scaling keeps the fp16 parts in range for any data magnitude."""
-    _say(f"f16 scale {scale}")
+def test_split_estep_scaled_data(bridge, scale):
+    """The bf16 parts share fp32's exponent range: no scaling for any data
+    magnitude within the split's range."""
+    _say(f"split scale {scale}")
     X, C0 = _blob_problem(6000, 40, 30, seed=5, scale=scale)
-    assert _f16_engaged(bridge, X, C0)["f16"]
-    _lockstep_gpu(bridge, X, C0, 2, what=f"f16 scale {scale}")
+    assert _split_engaged(bridge, X, C0)["split"]
+    _lockstep_gpu(bridge, X, C0, 2, what=f"split scale {scale}")
 
 
-def test_f16_switched_off_by_env(bridge, monkeypatch):
-    """SKMETAL_HIP_F16=0 keeps the fp32 MFMA E-step; both agree with the oracle."""
-    monkeypatch.setenv("SKMETAL_HIP_F16", "0")
+@pytest.mark.parametrize("kind", ["quantised", "1e6", "cluster"])
+@pytest.mark.parametrize("n,d,k", [(20000, 100, 50), (6000, 40, 13), (8000, 48, 150)])
+def test_split_mixed_scale_columns(bridge, n, d, k, kind):
+    """Per-element fp32 accuracy of the split path: columns (or clusters) whose
+    values are 10^5..10^8 times smaller than the rest keep their own relative
+    accuracy -- every lockstep step checks centres per row, per column and per
+    element at the scale of the cluster's own values, the last at the fp32
+    level (FP32_ELEM_RTOL)."""
+    _say(f"split mixed scale {kind} n={n} d={d} k={k}")
+    X, C0 = mixed_scale_problem(n, d, k, seed=n + d + k, kind=kind)
+    info = _split_engaged(bridge, X, C0)
+    assert info["split"] or info["asplit"], info
+    # "cluster" runs on X as given: centring would move the small clusters'
+    # values to the scale of the column mean
+    _lockstep_gpu(bridge, X, C0, 3, what=f"mixed scale {kind} {n}x{d} k={k}", center=kind != "cluster",
+                  elem_rtol=parity.FP32_ELEM_RTOL)
+
+
+@pytest.mark.parametrize("kind", ["quantised", "cluster"])
+def test_split_mixed_scale_assign(bridge, kind):
+    """The separate E-step (assign entry point) on mixed-scale columns."""
+    X, C0 = mixed_scale_problem(5000, 100, 200, seed=21, kind=kind)
+    out = np.empty(len(X), np.int32)
+    bridge.kmeans_assign(X, C0, out, X.shape[0], X.shape[1], C0.shape[0])
+    ref, best, second = oracle.assign(X, C0, return_gap=True)
+    parity.check_labels(out, ref, best, second, X, what=f"mixed scale assign {kind}")
+
+
+def test_split_switched_off_by_env(bridge, monkeypatch):
+    """SKMETAL_HIP_SPLIT=0 keeps the fp32 MFMA E-step; both agree with the oracle."""
+    monkeypatch.setenv("SKMETAL_HIP_SPLIT", "0")
     X, C0 = _blob_problem(8000, 100, 50, seed=9)
-    info = _f16_engaged(bridge, X, C0)
-    assert info["fused"] and not info["f16"], info
+    info = _split_engaged(bridge, X, C0)
+    assert info["fused"] and not info["split"], info
     _lockstep_gpu(bridge, X, C0, 2, what="fp32 E-step")
 
 
 @pytest.mark.parametrize("n,d,k", [(5000, 40, 100), (3000, 130, 300)])
-def test_a16_generic_path_lockstep(bridge, n, d, k):
-    """k > 64: the separate E-step on fp16 MFMA (several centre passes and
+def test_asplit_generic_path_lockstep(bridge, n, d, k):
+    """k > 64: the separate E-step over the split (several centre passes and
     feature segments) with the sorted update, step by step against the oracle."""
-    _say(f"a16 lockstep n={n} d={d} k={k}")
+    _say(f"asplit lockstep n={n} d={d} k={k}")
     X, C0 = _blob_problem(n, d, k, seed=n + k)
-    info = _f16_engaged(bridge, X, C0)
-    assert not info["fused"] and info["a16"], info
-    _lockstep_gpu(bridge, X, C0, 2, what=f"a16 {n}x{d} k={k}")
+    info = _split_engaged(bridge, X, C0)
+    assert not info["fused"] and info["asplit"], info
+    _lockstep_gpu(bridge, X, C0, 2, what=f"asplit {n}x{d} k={k}")
 
 
-def test_f16_off_for_non_finite_data(bridge):
+def test_split_off_for_non_finite_data(bridge):
     X, C0 = _blob_problem(3000, 40, 8, seed=3)
     X[17, 5] = np.inf
     with bridge.LloydHandle(3000, 40, 8) as h:
         h.load(X, center=False)
         h.set_centers(C0)
-        assert not h.info()["f16"] and not h.info()["a16"]
+        assert not h.info()["split"] and not h.info()["asplit"]
+
+
+def test_split_off_below_its_range(bridge):
+    """Data whose largest magnitude is below 2^-50 keeps the fp32 E-step."""
+    X, C0 = _blob_problem(3000, 40, 8, seed=4, scale=1e-17)
+    with bridge.LloydHandle(3000, 40, 8) as h:
+        h.load(X, center=False)
+        h.set_centers(C0)
+        assert h.info()["fused"] and not h.info()["split"]
+    _lockstep_gpu(bridge, X, C0, 2, what="fp32 E-step for 1e-17 data")
 
 
 def _golden_names():
@@ -431,11 +475,17 @@ def _sampled_steps(bridge, X, C0, steps, sample, seed, what):
             ref, best, second = oracle.assign(Xc[idx], prev - mean, return_gap=True)
             parity.check_labels(lab[idx], ref, best, second, Xc[idx], what=f"{what} step {m + 1} sampled labels")
             C_ref, _, n_empty = oracle.mstep(Xc, lab, prev - mean)
-            err = parity.center_rel_err(C_ref, Cn - mean)
+            C_got = (Cn - mean).astype(np.float64)
+            err = parity.center_rel_err(C_ref, C_got)
             if err > parity.CENTER_RTOL and n_empty >= 3:
                 counts = np.bincount(lab, minlength=k)
-                err = parity._match_relocated(C_ref, Cn - mean, np.flatnonzero(counts == 0))
+                C_got = parity._match_relocated(C_got, C_ref, np.flatnonzero(counts == 0))
+                err = parity.center_rel_err(C_ref, C_got)
             assert err <= parity.CENTER_RTOL, f"{what} step {m + 1}: centres error {err:.3e}"
+            col = parity.center_col_err(C_got, C_ref)
+            assert col <= parity.CENTER_RTOL, f"{what} step {m + 1}: per-column centres error {col:.3e}"
+            mem = parity.center_member_err(C_got, C_ref, Xc, lab)
+            assert mem <= parity.CENTER_RTOL, f"{what} step {m + 1}: per-element centres error {mem:.3e}"
             prev = Cn
 
 
