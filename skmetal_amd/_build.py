@@ -36,6 +36,7 @@ VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 SOURCES = [
     ("kmeans_kernels.hip", VGPR_FORM),
     ("fused_kernels.hip", []),
+    ("split_kernels.hip", []),
     ("plusplus_kernels.hip", []),
     ("transform_kernels.hip", []),
     ("skmetal_hip.hip", VGPR_FORM),

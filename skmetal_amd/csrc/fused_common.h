@@ -1,0 +1,125 @@
+// fused_common.h -- device helpers shared by the fused Lloyd-step kernels
+// (fused_kernels.hip: k_fused; split_kernels.hip: k_fused3, k_assign3).
+#pragma once
+
+#include <math.h>
+
+#include "device.h"
+
+namespace skm {
+
+// Floats per LDS row for a row of NQ float4s: an odd number of float4s, so
+// 16-byte accesses of different rows at the same column fall in different
+// bank groups.
+__host__ __device__ constexpr int fused_stride(int nq) { return 4 * (nq | 1); }
+
+__device__ __forceinline__ float4 load_quad(__amdgpu_buffer_rsrc_t rs, int off)
+{
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+    return *reinterpret_cast<const float4*>(&v);
+}
+
+// Waits (polling LDS) until *flag >= v and returns the value seen.  Flags are
+// written by the other wave of the pair; LDS operations of one wave are
+// performed in issue order, so a wave that sees a flag value also sees the
+// LDS writes issued before it, and LDS reads issued before it are done.
+__device__ __forceinline__ int wait_flag(int* flag, int v)
+{
+    int seen;
+    while ((seen = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < v)
+        __builtin_amdgcn_s_sleep(1);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // no LDS access moves above the wait
+    return seen;
+}
+
+__device__ __forceinline__ void set_flag(int* flag, int v)
+{
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // every LDS access above stays above
+    __hip_atomic_store(flag, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Wave 4 of every block: the previous step's stopping rules when a.decide
+// (evaluated identically by every block: same loads, same order as
+// k_finalize_loop for k <= 64; block 0 records the decision), else nothing
+// to decide.  Writes ||c||^2 of this step's centres to sN (padding clusters
+// j >= k get +inf: their distance never wins) and the decision to *sDone.
+template <int CPC>
+__device__ __forceinline__ void step_norms(const FusedArgs& a, int lane, float* sN, int* sDone)
+{
+    const int k = a.k;
+    const int j = lane;
+    if (a.decide) {
+        double tsq = 0.0, tnr = 0.0;
+        int count = 1;
+        if (j < k) {
+            // all chunk partials in flight at once (the sum order is the
+            // finalize's: chunk 0, 1, ...)
+            const double* pj = a.part + (long)j * a.nch * 2;
+            constexpr int NB = 16;
+            for (int c0 = 0; c0 < a.nch; c0 += NB) {
+                double v[2 * NB];
+#pragma unroll
+                for (int u = 0; u < NB; ++u) {
+                    const int c = min(c0 + u, a.nch - 1);
+                    v[2 * u] = pj[2 * c];
+                    v[2 * u + 1] = pj[2 * c + 1];
+                }
+#pragma unroll
+                for (int u = 0; u < NB; ++u) {
+                    if (c0 + u < a.nch) {
+                        tsq += v[2 * u];
+                        tnr += v[2 * u + 1];
+                    }
+                }
+            }
+            count = a.counts[j];
+        }
+        const int n_empty = wave_sum(j < k && count == 0 ? 1 : 0);
+        const double tot = wave_sum(j < k ? (double)(float)tsq : 0.0);
+        const int chg = *a.prev_changed;
+        int done = 0;
+        if (n_empty > 0)
+            done = 3;
+        else if ((a.flags & kStopStrict) && chg == 0)
+            done = 1;
+        else if (a.tol >= 0.0 && tot <= a.tol)  // tol < 0: no shift rule (fixed iterations)
+            done = 2;
+        if (blockIdx.x == 0) {
+            LoopState* st = a.state;
+            if (j < k) {
+                a.shift_sq[j] = (float)tsq;
+                if (count > 0) a.cnorm_out[j] = (float)tnr;
+            }
+            if (lane == 0) {
+                st->n_empty = n_empty;
+                st->shift_tot = tot;
+                st->last_changed = chg;
+                st->n_iter = a.iter;
+                if (done != 0) st->halt_iter = a.iter - 1;
+                st->done = done;
+            }
+        }
+        if (j < CPC) sN[j] = j < k ? (float)tnr : INFINITY;
+        if (lane == 0) *sDone = done;
+    } else {
+        if (j < CPC) sN[j] = j < k ? a.cnorm[j] : INFINITY;
+        if (lane == 0) *sDone = 0;
+    }
+}
+
+template <int CPC, int NT = 512>
+__device__ __forceinline__ void combine_sums(const float* red, int ld, int k, float* psum, int* pcnt, int (*sCnt)[64],
+                                             int tid)
+{
+    const int kl = k * ld;
+    float* out = psum + (long)blockIdx.x * kl;
+    for (int i = tid; i < kl; i += NT) {
+        const int j = i / ld;
+        const int col = i - j * ld;
+        const float* p = red + j * ld + col;
+        out[i] = ((p[0] + p[CPC * ld]) + p[2 * CPC * ld]) + p[3 * CPC * ld];
+    }
+    if (tid < k) pcnt[(long)blockIdx.x * k + tid] = ((sCnt[0][tid] + sCnt[1][tid]) + sCnt[2][tid]) + sCnt[3][tid];
+}
+
+}  // namespace skm

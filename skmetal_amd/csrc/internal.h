@@ -86,6 +86,7 @@ int fused_blocks(long n, int ld, int k, int num_cu);
 // 1 when the split fused kernel exists for (k, ld) and fits in LDS (sets its
 // LDS attribute); the data must still be in the split's range.
 int fused3_ready(int k, int ld);
+hipError_t launch_fused3(const FusedArgs& a, hipStream_t s);
 hipError_t launch_fused(const FusedArgs& a, hipStream_t s);
 
 struct UpdateArgs {
