@@ -202,6 +202,29 @@ def test_split_assign_duplicate_centres_lowest_index(bridge):
     parity.check_labels(out, ref, best, second, X, what="split duplicate centres")
 
 
+@pytest.mark.parametrize("d,reps", [(100, 3), (40, 2), (64, 4)])
+def test_split_fused_duplicate_centres_lowest_index(bridge, d, reps):
+    """Every row is an exact tie between copies of its centre, so every
+    16-row group takes the E-step's second pass: the lowest index must win,
+    exactly as scikit-learn's strict '<' scan picks it."""
+    rng = np.random.default_rng(d + reps)
+    n = 9000
+    base = rng.uniform(-5, 5, (16, d)).astype(np.float32)
+    X = (base[rng.integers(0, 16, n)] + rng.standard_normal((n, d))).astype(np.float32)
+    C = np.concatenate([base] * reps)[:64]
+    k = C.shape[0]
+    mean = X.mean(axis=0)
+    with bridge.LloydHandle(n, d, k) as h:
+        h.load(X, center=True)
+        h.set_centers(C)
+        assert h.info()["split"]
+        h.iterate(1)
+        lab = h.labels()
+    ref = oracle.assign(X - mean, C - mean)
+    np.testing.assert_array_equal(lab, ref)
+    assert lab.max() < 16
+
+
 @pytest.mark.parametrize("n,d,k", [(3000, 101, 10), (40, 20, 40), (2000, 17, 64)])
 def test_split_edge_shapes_lockstep(bridge, n, d, k):
     """d just past the fused limit (generic path with k <= 64), k = n, the
