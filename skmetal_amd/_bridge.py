@@ -159,17 +159,33 @@ def _i32c(a, name):
     return a
 
 
+def _check_sizes(n, d, k, X, centroids, assignments, dists=None):
+    """The arrays hold exactly the n x d, k x d and n elements the library
+    will read or write through their pointers."""
+    n, d, k = int(n), int(d), int(k)
+    if X.size != n * d:
+        raise ValueError(f"X has {X.size} elements, expected n * d = {n} * {d}")
+    if centroids.size != k * d:
+        raise ValueError(f"centroids has {centroids.size} elements, expected k * d = {k} * {d}")
+    if assignments.size != n:
+        raise ValueError(f"assignments has {assignments.size} elements, expected n = {n}")
+    if dists is not None and dists.size != n:
+        raise ValueError(f"dists has {dists.size} elements, expected n = {n}")
+
+
 # ---- the reference's KMeans wrappers (skmetal/_bridge.py:576-639) ----
 
 def kmeans_assign(X, centroids, assignments, n, d, k) -> None:
     """E-step: assignments[i] = nearest centroid of X[i]."""
     _f32c(X, "X"), _f32c(centroids, "centroids"), _i32c(assignments, "assignments")
+    _check_sizes(n, d, k, X, centroids, assignments)
     _bridge_call(_lib.skmetal_kmeans_assign, X, centroids, assignments, n, d, k)
 
 
 def kmeans_batch_fused(X, centroids, assignments, n, d, k, num_groups, max_iter, tol) -> int:
     """Lloyd fit on the GPU (centroids in/out); returns n_iter."""
     _f32c(X, "X"), _f32c(centroids, "centroids"), _i32c(assignments, "assignments")
+    _check_sizes(n, d, k, X, centroids, assignments)
     n_iter_out = ctypes.c_int32(0)
     _bridge_call(_lib.skmetal_kmeans_batch_fused, X, centroids, assignments, n, d, k, num_groups, max_iter,
                  ctypes.c_float(tol), ctypes.byref(n_iter_out))
@@ -179,11 +195,14 @@ def kmeans_batch_fused(X, centroids, assignments, n, d, k, num_groups, max_iter,
 def compute_mindists(X, centroids, assignments, dists, n, d, k) -> None:
     """dists[i] = ||X[i] - centroids[assignments[i]]||^2."""
     _f32c(X, "X"), _f32c(centroids, "centroids"), _i32c(assignments, "assignments"), _f32c(dists, "dists")
+    _check_sizes(n, d, k, X, centroids, assignments, dists)
     _bridge_call(_lib.skmetal_compute_mindists, X, centroids, assignments, dists, n, d, k)
 
 
 def kmeans_inertia(X, centroids, assignments, n, d, k) -> float:
     """Sum of squared distances to the assigned centroids (GPU); -1.0 on failure, as the reference."""
+    _f32c(X, "X"), _f32c(centroids, "centroids"), _i32c(assignments, "assignments")
+    _check_sizes(n, d, k, X, centroids, assignments)
     ensure_warmed_up()
     return float(_lib.skmetal_kmeans_inertia(X.ctypes.data, centroids.ctypes.data, assignments.ctypes.data,
                                              n, d, k))

@@ -1,16 +1,28 @@
-"""Configuration API (mirrors skmetal/_config.py of the reference).
+"""Dispatch configuration: the API of skmetal/_config.py.
 
-Thread-safe global configuration with a per-thread device override used by
-``accelerate_context``.  Only the KMeans entry of the per-estimator
-threshold table is consulted by this package; the other names are kept so
-that code written against skmetal's configuration functions keeps working.
+Functions kept by name, signature and meaning (skmetal/_config.py:119-199):
+``get_config``, ``set_device``, ``set_threshold``, ``set_dtype``,
+``set_verbose``, ``set_thresholds``, ``update_threshold``,
+``reset_thresholds``, and the ``PER_ESTIMATOR_THRESHOLDS`` table
+(skmetal/_config.py:6-32).
+
+State is one process-wide ``Config`` plus, per thread, an optional device
+override.  ``accelerate_context`` keeps a stack of those overrides per
+thread; ``set_device`` sets the process-wide value and the calling thread's
+override together, so the caller reads back what it set even inside a
+context.  Writers hold one lock; readers do not need it (every field is a
+single reference replaced atomically).
 """
+
+from __future__ import annotations
 
 import threading
 
+# (min_rows, min_cols) below which an estimator stays on scikit-learn.  The
+# values are skmetal's (skmetal/_config.py:6-32); this package consults the
+# KMeans entry only and keeps the rest so that configuration code written for
+# skmetal runs unchanged.
 PER_ESTIMATOR_THRESHOLDS: dict[str, tuple[int, int]] = {
-    # (min_rows, min_cols) below which an estimator stays on the CPU
-    # (skmetal/_config.py:6-32; KMeans :20)
     "KMeans": (1_000, 10),
     "StandardScaler": (1_000, 10),
     "LinearRegression": (50_000, 50),
@@ -33,108 +45,131 @@ PER_ESTIMATOR_THRESHOLDS: dict[str, tuple[int, int]] = {
     "NearestNeighbors": (5_000, 10),
 }
 
+DEVICES = ("gpu", "cpu", "auto")
+DTYPES = ("float32",)
+
+
+class _ThreadState(threading.local):
+    """Per-thread routing state: the device override (None: the process-wide
+    value applies) and the stack accelerate_context saves overrides on."""
+
+    def __init__(self):
+        self.device: str | None = None
+        self.saved: list[str | None] = []
+
+
+_thread = _ThreadState()
+_write_lock = threading.Lock()
+
 
 class Config:
-    """Global configuration for GPU dispatch.
+    """Routing configuration.
 
-    Attributes
-    ----------
-    device : str
-        ``"gpu"``, ``"cpu"`` (scikit-learn) or ``"auto"``.
-    threshold : int
-        Minimum ``n_samples * n_features`` for GPU dispatch.
-    dtype : str
-        Compute dtype; only ``"float32"``.
-    verbose : bool
-        Print every routing decision.
-    thresholds : dict
-        Per-estimator ``(min_rows, min_cols)``.
+    device      "gpu" (default), "cpu" (always scikit-learn) or "auto"; reading
+                it gives the calling thread's value
+    threshold   smallest n_samples * n_features sent to the GPU
+    dtype       compute dtype; "float32" only
+    verbose     print every routing decision
+    thresholds  class name -> (min_rows, min_cols)
     """
 
-    def __init__(self, device="gpu", threshold=1, dtype="float32", verbose=False, thresholds=None):
-        self._device = device
+    def __init__(self, device: str = "gpu", threshold: int = 1, dtype: str = "float32", verbose: bool = False,
+                 thresholds: dict | None = None):
+        self.global_device = device
         self.threshold = threshold
         self.dtype = dtype
         self.verbose = verbose
-        self.thresholds = thresholds if thresholds is not None else dict(PER_ESTIMATOR_THRESHOLDS)
+        self.thresholds = dict(PER_ESTIMATOR_THRESHOLDS) if thresholds is None else thresholds
 
     @property
     def device(self) -> str:
-        val = getattr(_thread_local, "device", _UNSET)
-        return self._device if val is _UNSET else val
+        return self.global_device if _thread.device is None else _thread.device
 
     @device.setter
-    def device(self, val: str):
-        self._device = val
+    def device(self, value: str) -> None:
+        self.global_device = value
 
-    def __repr__(self):
-        n_gpu = sum(1 for v in self.thresholds.values() if v[0] < 1e8)
-        n_cpu = len(self.thresholds) - n_gpu
-        return (
-            f"device={self.device}, threshold={self.threshold}, verbose={self.verbose}\n"
-            f"  estimators routed to GPU: {n_gpu}  |  estimators routed to CPU: {n_cpu}"
-        )
+    def __repr__(self) -> str:
+        on_gpu = [name for name, (rows, _) in self.thresholds.items() if rows < 10**8]
+        return (f"Config(device={self.device!r}, threshold={self.threshold}, dtype={self.dtype!r}, "
+                f"verbose={self.verbose}, {len(on_gpu)} of {len(self.thresholds)} estimators GPU-eligible)")
 
 
 _config = Config()
-_lock = threading.Lock()
-_thread_local = threading.local()
-_UNSET = object()
 
 
 def get_config() -> Config:
+    """The configuration object (its ``device`` reads the calling thread's value)."""
     return _config
 
 
 def _get_device() -> str:
-    val = getattr(_thread_local, "device", _UNSET)
-    return _config._device if val is _UNSET else val
+    """The device routing uses on the calling thread."""
+    return _config.device
 
 
-def _set_thread_device(device) -> None:
-    if device is None:
-        if hasattr(_thread_local, "device"):
-            del _thread_local.device
-    else:
-        _thread_local.device = device
+def _set_thread_device(device: str | None) -> None:
+    """Set the calling thread's device override, or drop it (None)."""
+    _thread.device = device
+
+
+def _push_thread_device(device: str) -> None:
+    """accelerate_context's entry: save the thread's device, then override it."""
+    _thread.saved.append(_thread.device)
+    _thread.device = device
+
+
+def _pop_thread_device() -> None:
+    """accelerate_context's exit: restore the device saved by the matching push."""
+    if _thread.saved:
+        _thread.device = _thread.saved.pop()
 
 
 def set_device(device: str) -> None:
-    """``"gpu"`` (default), ``"cpu"`` (force scikit-learn) or ``"auto"``."""
-    with _lock:
-        if device not in ("gpu", "cpu", "auto"):
-            raise ValueError("device must be 'gpu', 'cpu', or 'auto'")
-        _config._device = device
-        _thread_local.device = device
+    """Route to "gpu", "cpu" (scikit-learn everywhere) or "auto".  Sets the
+    process-wide value and the calling thread's override."""
+    if device not in DEVICES:
+        raise ValueError(f"device must be one of {', '.join(repr(d) for d in DEVICES)}, not {device!r}")
+    with _write_lock:
+        _config.global_device = device
+        _thread.device = device
 
 
 def set_threshold(threshold: int) -> None:
-    with _lock:
+    """Inputs with fewer than ``threshold`` elements (n * d) stay on the CPU."""
+    with _write_lock:
         _config.threshold = int(threshold)
 
 
 def set_dtype(dtype: str) -> None:
-    with _lock:
-        if dtype != "float32":
-            raise ValueError("Only float32 is supported for GPU operations.")
+    """Compute dtype of the GPU path; only "float32" is accepted."""
+    if dtype not in DTYPES:
+        raise ValueError(f"dtype {dtype!r} is not supported on the GPU path (float32 only)")
+    with _write_lock:
         _config.dtype = dtype
 
 
 def set_verbose(verbose: bool) -> None:
-    with _lock:
+    """Print every routing decision (True) or none (False)."""
+    with _write_lock:
         _config.verbose = bool(verbose)
 
 
 def set_thresholds(thresholds: dict) -> None:
-    with _lock:
+    """Replace the whole per-estimator table (class name -> (min_rows, min_cols))."""
+    with _write_lock:
         _config.thresholds = dict(thresholds)
 
 
 def update_threshold(name: str, min_rows: int, min_cols: int) -> None:
-    with _lock:
-        _config.thresholds[name] = (min_rows, min_cols)
+    """Set one estimator's (min_rows, min_cols): smaller inputs stay on the CPU."""
+    with _write_lock:
+        table = dict(_config.thresholds)
+        table[name] = (min_rows, min_cols)
+        _config.thresholds = table
 
 
 def reset_thresholds() -> None:
-    with _lock:
+    """Restore PER_ESTIMATOR_THRESHOLDS."""
+    with _write_lock:
         _config.thresholds = dict(PER_ESTIMATOR_THRESHOLDS)

@@ -46,14 +46,23 @@ def _tolerance(X: np.ndarray, tol: float) -> float:
 
 
 def _same_clustering(a: np.ndarray, b: np.ndarray, k: int) -> bool:
-    """True when two labelings are equal up to a permutation of cluster ids."""
-    mapping = np.full(k, -1, dtype=np.int64)
-    for i in range(a.shape[0]):
-        if mapping[a[i]] == -1:
-            mapping[a[i]] = b[i]
-        elif mapping[a[i]] != b[i]:
-            return False
-    return True
+    """scikit-learn's _is_same_clustering (sklearn/cluster/_k_means_common.pyx:
+    _is_same_clustering): True when every label of `a` is paired with one label
+    of `b` only.  rep[j] takes the b of some row labelled j in a (whichever
+    write lands); the pairing is a function exactly when every row's b equals
+    its label's rep."""
+    a = np.asarray(a, dtype=np.intp)
+    rep = np.empty(k, dtype=np.asarray(b).dtype)
+    rep[a] = b
+    return bool(np.array_equal(rep[a], b))
+
+
+def _check_n_features(est, X) -> None:
+    """scikit-learn's feature-count check for a fitted estimator."""
+    expected = getattr(est, "n_features_in_", None)
+    if expected is not None and X.shape[1] != expected:
+        raise ValueError(f"X has {X.shape[1]} features, but {type(est).__name__} is expecting {expected} "
+                         "features as input.")
 
 
 class HipKMeans(BaseGPUEstimator):
@@ -173,6 +182,7 @@ class HipKMeans(BaseGPUEstimator):
         X, _ = self._validate_data(X)
         if not self._gpu_ready(X):
             return self._fallback_predict(X)
+        _check_n_features(self._estimator, X)
         n, d = X.shape
         C = np.ascontiguousarray(self._estimator.cluster_centers_, dtype=np.float32)
         out = np.empty(n, dtype=np.int32)
@@ -184,6 +194,7 @@ class HipKMeans(BaseGPUEstimator):
         X, _ = self._validate_data(X)
         if not self._gpu_ready(X):
             return self._fallback_transform(X)
+        _check_n_features(self._estimator, X)
         C = np.ascontiguousarray(self._estimator.cluster_centers_, dtype=np.float32)
         return _bridge.kmeans_transform(X, C)
 
@@ -197,6 +208,7 @@ class HipKMeans(BaseGPUEstimator):
         X, _ = self._validate_data(X)
         if sample_weight is not None or not self._gpu_ready(X):
             return self._estimator.score(X, y, sample_weight=sample_weight)
+        _check_n_features(self._estimator, X)
         n, d = X.shape
         C = np.ascontiguousarray(self._estimator.cluster_centers_, dtype=np.float32)
         lab = np.empty(n, dtype=np.int32)
@@ -314,6 +326,7 @@ class MetalKMeans(BaseGPUEstimator):
         X, _ = self._validate_data(X)
         if not self._fitted or not self._should_use_gpu(X):
             return self._fallback_predict(X)
+        _check_n_features(self._estimator, X)
         C = np.ascontiguousarray(self._estimator.cluster_centers_, dtype=np.float32)
         out = np.empty(X.shape[0], dtype=np.int32)
         _bridge.kmeans_assign(X, C, out, X.shape[0], X.shape[1], C.shape[0])
@@ -323,5 +336,6 @@ class MetalKMeans(BaseGPUEstimator):
         X, _ = self._validate_data(X)
         if not self._fitted or not self._should_use_gpu(X):
             return self._fallback_transform(X)
+        _check_n_features(self._estimator, X)
         C = np.ascontiguousarray(self._estimator.cluster_centers_, dtype=np.float32)
         return _bridge.kmeans_transform(X, C)
