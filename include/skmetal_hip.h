@@ -62,18 +62,20 @@ SKMETAL_API int skmetal_device_info(char* name, int name_capacity, size_t* max_t
 SKMETAL_API int skmetal_kmeans_assign(const void* X, const void* centroids, void* assignments,
                           size_t n, size_t d, size_t k);
 
-/* Whole Lloyd fit, sklearn KMeans(init=centroids, n_init=1, algorithm="lloyd")
- * semantics: X is centred on its column mean for the distance evaluations;
- * the loop stops on strict label convergence, or when
- * sum_j ||c_j_new - c_j_old||^2 <= tol (tol is sklearn's absolute `_tol`,
- * i.e. mean feature variance x estimator tol; 0 disables the test), or after
- * max_iter steps; empty clusters are relocated as sklearn does; a final E-step
- * makes the labels match the returned centres.  centroids is in/out (initial
- * centres in, final centres out, caller coordinates); assignments is out;
- * *n_iter_out receives sklearn's n_iter_.  num_groups is accepted for ABI
- * compatibility and ignored (the reference used it to size Metal threadgroup
- * partials).  Replaces skmetal_kmeans_batch_fused (bridge.h:39;
- * KMeansBridge.swift:187-320; _bridge.py:120-132, 591-617). */
+/* Lloyd loop with the reference's contract (KMeansBridge.swift:187-320): up
+ * to max_iter steps; after each, the loop stops when the fp32 root of the
+ * largest squared centre shift, max_j ||c_j_new - c_j_old||^2, is below tol
+ * (:306-310; tol as the caller's estimator passes it, tol <= 0 never stops
+ * early).  There is no label-based stop and no final E-step: assignments
+ * (out, 32-bit) are the labels of the last step's E-step and centroids (in:
+ * initial centres, out: the last step's centres, caller coordinates) those it
+ * produced; *n_iter_out = steps run.  With max_iter = 0 nothing is written
+ * but *n_iter_out = 0.  Each step is this library's: distances on X centred
+ * on its column mean, empty clusters relocated as sklearn does (the reference
+ * set them to 0).  num_groups is accepted for ABI compatibility and ignored
+ * (the reference sized Metal threadgroup partials with it).  Replaces
+ * skmetal_kmeans_batch_fused (bridge.h:39; _bridge.py:120-132, 591-617).
+ * scikit-learn's stopping rules are those of skmetal_hip_kmeans_fit below. */
 SKMETAL_API int skmetal_kmeans_batch_fused(const void* X, void* centroids, void* assignments,
                                size_t n, size_t d, size_t k, size_t num_groups,
                                size_t max_iter, float tol, int32_t* n_iter_out);
@@ -97,9 +99,15 @@ SKMETAL_API const char* skmetal_hip_last_error(void);
 /* Release the device buffers the library keeps cached between calls. */
 SKMETAL_API int skmetal_hip_release_cache(void);
 
-/* skmetal_kmeans_batch_fused plus the final inertia (fp64), so a fit needs a
- * single upload of X.  flags: SKMETAL_FIT_STRICT (stop on strict label
- * convergence, as sklearn) -- pass it for sklearn semantics. */
+/* Whole Lloyd fit with sklearn KMeans(init=centroids, n_init=1,
+ * algorithm="lloyd") semantics, plus the final inertia (fp64), with a single
+ * upload of X: X centred on its column mean for the distance evaluations; the
+ * loop stops when sum_j ||c_j_new - c_j_old||^2 <= tol (sklearn's absolute
+ * `_tol`: mean feature variance x estimator tol), with SKMETAL_FIT_STRICT also
+ * on strict label convergence (pass it for sklearn semantics), or after
+ * max_iter steps; empty clusters are relocated as sklearn does; a final E-step
+ * makes the labels those of the returned centres; *n_iter_out = sklearn's
+ * n_iter_. */
 #define SKMETAL_FIT_STRICT 1
 SKMETAL_API int skmetal_hip_kmeans_fit(const float* X, float* centroids, int32_t* labels,
                            size_t n, size_t d, size_t k, size_t max_iter, double tol,

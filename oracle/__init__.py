@@ -25,6 +25,10 @@ Parity status per function (what pins it, see tests/test_oracle.py):
 * ``lloyd``       -- sklearn golden trajectories (tests/golden/*.npz written by
                      tests/golden/make_fixtures.py), the unit-weight toy case,
                      strict-convergence n_iter, monotone inertia.
+* ``reference_loop`` -- skmetal's batch_fused stopping contract over ``assign`` /
+                     ``mstep``: the unit toy case's closed-form shift sequence
+                     (0.25, then 0) at tol just above, at and below 0.25, tol 0,
+                     max_iter 0 (tests/test_oracle.py).
 * ``inertia``     -- closed form (sum of squares about the mean for k=1),
                      sklearn golden inertia.
 * ``mean_f32``    -- bit-exact against numpy's float32 X.mean(axis=0).
@@ -202,6 +206,38 @@ def lloyd(X, C_init, max_iter: int, tol_abs: float = 0.0, trace: bool = False):
     if trace:
         out["trace"] = tr[:n_iter]
     return out
+
+
+def reference_loop(X, C_init, max_iter: int, tol: float):
+    """skmetal's loop contract for skmetal_kmeans_batch_fused
+    (skmetal_bridge/Sources/SkMetalBridge/KMeansBridge.swift:187-320) over this
+    oracle's Lloyd step: up to max_iter steps of ``assign`` + ``mstep`` on X
+    centred on its fp32 column mean (empty clusters relocated as scikit-learn
+    does); after each step the loop stops when the fp32 root of the largest
+    squared centre shift is below tol, strictly (:306-310); no label-based
+    stop and no final E-step.  The squared shifts are fp64 sums of the fp32
+    coordinates' differences, rounded to fp32, as the library computes them.
+    Returns dict(centers (caller coordinates), labels (the last step's E-step;
+    None when max_iter = 0), estep_centers (the centres that E-step used),
+    n_iter)."""
+    X = _f32(X)
+    mean = X.mean(axis=0)
+    Xc = X - mean
+    C = _f32(C_init) - mean
+    labels = None
+    C_prev = C
+    n_iter = 0
+    for it in range(int(max_iter)):
+        labels = assign(Xc, C)
+        C_prev = C
+        C_new, _, _ = mstep(Xc, labels, C)
+        sq = ((C_new.astype(np.float64) - C.astype(np.float64)) ** 2).sum(axis=1).astype(np.float32)
+        C = C_new
+        n_iter = it + 1
+        if np.sqrt(np.float32(sq.max(initial=0.0))) < np.float32(tol):
+            break
+    return dict(centers=(C + mean).astype(np.float32), labels=labels,
+                estep_centers=(C_prev + mean).astype(np.float32), n_iter=n_iter)
 
 
 def sklearn_tolerance(X, tol: float) -> float:

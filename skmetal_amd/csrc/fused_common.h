@@ -76,13 +76,16 @@ __device__ __forceinline__ void step_norms(const FusedArgs& a, int lane, float* 
         }
         const int n_empty = wave_sum(j < k && count == 0 ? 1 : 0);
         const double tot = wave_sum(j < k ? (double)(float)tsq : 0.0);
+        float mx = j < k ? (float)tsq : 0.f;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
         const int chg = *a.prev_changed;
         int done = 0;
         if (n_empty > 0)
             done = 3;
         else if ((a.flags & kStopStrict) && chg == 0)
             done = 1;
-        else if (a.tol >= 0.0 && tot <= a.tol)  // tol < 0: no shift rule (fixed iterations)
+        else if (shift_rule_stops(a.flags, a.tol, tot, mx))
             done = 2;
         if (blockIdx.x == 0) {
             LoopState* st = a.state;

@@ -33,7 +33,20 @@ struct LoopState {
 
 enum StepFlags : int {
     kStopStrict = 1,   // stop when an E-step changes no label (sklearn rule)
+    // the shift rule is sqrtf(max_j ||c_j_new - c_j_old||^2) < tol (skmetal's
+    // KMeansBridge.swift:306-310) instead of sum_j ||..||^2 <= tol (sklearn's)
+    kStopMaxShift = 2,
 };
+
+// The loop's shift rule: sum of squared shifts <= tol (sklearn), or, with
+// kStopMaxShift, the largest shift's fp32 root < tol (skmetal's reference
+// loop).  tol < 0: no shift rule (fixed iterations).
+__host__ __device__ inline bool shift_rule_stops(int flags, double tol, double sum_sq, float max_sq)
+{
+    if (tol < 0.0) return false;
+    if (flags & kStopMaxShift) return sqrtf(max_sq) < (float)tol;
+    return sum_sq <= tol;
+}
 
 // ---- kernel launchers (kmeans_kernels.hip) -------------------------------
 // All return hipSuccess or the launch error; all enqueue on `s`.

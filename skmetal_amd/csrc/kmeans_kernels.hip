@@ -663,6 +663,18 @@ __device__ __forceinline__ T block_sum(T v, T* sh)
     return t;
 }
 
+// Largest value over a 256-thread block (every thread gets it), as block_sum.
+__device__ __forceinline__ float block_max(float v, float* sh)
+{
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float t = fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+    __syncthreads();
+    return t;
+}
+
 constexpr int kFinUnroll = 8;  // partials in flight per thread
 
 __global__ __launch_bounds__(256) void k_finalize_cols(FinalizeArgs a)
@@ -763,8 +775,10 @@ __global__ __launch_bounds__(256) void k_finalize_loop(FinalizeArgs a, int nch)
     const int tid = threadIdx.x;
     __shared__ double shd[4];
     __shared__ int shi[4];
+    __shared__ float shm[4];
     int n_empty = 0;
     double tot = 0.0;
+    float mx = 0.f;
     for (int j = tid; j < a.k; j += 256) {
         double tsq = 0.0, tnr = 0.0;
         for (int c = 0; c < nch; ++c) {
@@ -776,9 +790,11 @@ __global__ __launch_bounds__(256) void k_finalize_loop(FinalizeArgs a, int nch)
         if (count > 0 || a.after_reloc) a.cnorm[j] = (float)tnr;
         n_empty += count == 0;
         tot += (double)(float)tsq;
+        mx = fmaxf(mx, (float)tsq);
     }
     n_empty = block_sum(n_empty, shi);
     tot = block_sum(tot, shd);
+    mx = block_max(mx, shm);
     if (tid == 0) {
         const int changed = *a.chg_cur;
         st->n_empty = n_empty;
@@ -790,7 +806,7 @@ __global__ __launch_bounds__(256) void k_finalize_loop(FinalizeArgs a, int nch)
             done = 3;
         else if ((a.flags & kStopStrict) && changed == 0)
             done = 1;
-        else if (a.tol >= 0.0 && tot <= a.tol)  // tol < 0: no shift rule (fixed iterations)
+        else if (shift_rule_stops(a.flags, a.tol, tot, mx))
             done = 2;
         if (done != 0) st->halt_iter = a.iter;
         st->done = done;

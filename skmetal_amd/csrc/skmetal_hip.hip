@@ -676,6 +676,7 @@ struct Lloyd {
         }
         std::vector<float> Cn(kl, 0.f), cn(static_cast<size_t>(k));
         double shift_tot = 0.0;
+        float shift_max = 0.f;
         for (int j = 0; j < k; ++j) {
             double sq = 0.0, nr = 0.0;
             for (int c = 0; c < d; ++c) {
@@ -686,6 +687,7 @@ struct Lloyd {
                 nr += (double)v * (double)v;
             }
             shift_tot += (double)(float)sq;
+            shift_max = std::max(shift_max, (float)sq);
             cn[size_t(j)] = (float)nr;
         }
         TRY(upload_bytes(*C, Cn.data(), kl * sizeof(float), cen[old ^ 1], s));
@@ -693,7 +695,7 @@ struct Lloyd {
         int done = 0;
         if ((flags & kStopStrict) && hs.last_changed == 0)
             done = 1;
-        else if (tol >= 0.0 && shift_tot <= tol)
+        else if (shift_rule_stops(flags, tol, shift_tot, shift_max))
             done = 2;
         hs.done = done;
         hs.n_iter = t + 1;
@@ -1021,16 +1023,38 @@ int skmetal_hip_kmeans_fit(const float* X, float* centroids, int32_t* labels, si
     return 0;
 }
 
+// skmetal's own loop contract (KMeansBridge.swift:187-320): up to max_iter
+// Lloyd steps; after each, stop when the largest centre shift's fp32 root is
+// below tol (:306-310); no label-based stop and no final E-step, so the
+// assignments are those of the last step's E-step (against the centres it
+// started from) and the centroids those it produced; n_iter = steps run.
+// The steps themselves are this library's (X centred on its column mean,
+// empty clusters relocated as scikit-learn does, where the reference set
+// them to 0).  num_groups sized the reference's partial buffers; unused here.
 int skmetal_kmeans_batch_fused(const void* X, void* centroids, void* assignments, size_t n, size_t d, size_t k,
                                size_t num_groups, size_t max_iter, float tol, int32_t* n_iter_out)
 {
     (void)num_groups;
-    int32_t it = 0;
-    const int rc = skmetal_hip_kmeans_fit(static_cast<const float*>(X), static_cast<float*>(centroids),
-                                          static_cast<int32_t*>(assignments), n, d, k, max_iter, (double)tol,
-                                          SKMETAL_FIT_STRICT, &it, nullptr);
-    if (rc == 0 && n_iter_out) *n_iter_out = it;
-    return rc;
+    Context& c = ctx();
+    Guard g(c);
+    if (!X || !centroids || !assignments) return fail(SKMETAL_EINVAL, "null pointer argument");
+    TRY(check_sizes(n, d, k));
+    if (k > n) return fail(SKMETAL_EINVAL, "n_samples=%zu should be >= n_clusters=%zu", n, k);
+    if (max_iter > (size_t(1) << 30)) return fail(SKMETAL_ERANGE, "max_iter too large");
+    TRY(c.init());
+    Scoped sc;
+    Lloyd& L = sc.L;
+    TRY(L.create(&c, (long)n, (int)d, (int)k));
+    TRY(L.load_X(static_cast<const float*>(X), true));
+    TRY(L.set_centers(static_cast<const float*>(centroids)));
+    int it = 0, done = 0;
+    TRY(L.run_loop((long)max_iter, (double)tol, kStopMaxShift, false, &it, &done));
+    if (max_iter > 0) {
+        TRY(L.get_labels(static_cast<int32_t*>(assignments)));
+        TRY(L.get_centers(static_cast<float*>(centroids)));
+    }
+    if (n_iter_out) *n_iter_out = it;
+    return 0;
 }
 
 static int rowdist_call(const void* X, const void* centroids, const void* assignments, void* dists, size_t n,

@@ -535,6 +535,35 @@ def _separated_blobs(n, d, k, seed):
     return X, C0
 
 
+@pytest.mark.parametrize("tol,max_iter", [(0.0, 6), (1e-4, 50), (1e3, 50), (0.5, 50)])
+@pytest.mark.parametrize("n,d,k", [(20000, 100, 50), (5000, 130, 150), (3000, 12, 7)])
+def test_batch_fused_reference_contract(bridge, n, d, k, tol, max_iter):
+    """skmetal_kmeans_batch_fused through the C ABI against the oracle running
+    skmetal's loop contract (KMeansBridge.swift:187-320): the stop on the root
+    of the largest centre shift (strict '<' tol), no label stop, the labels of
+    the last step's E-step, n_iter = steps run.  Separated blobs with one
+    initial centre per blob: step 1 moves every centre by ~sqrt(d), step 2 by
+    exactly 0."""
+    _say(f"batch_fused n={n} d={d} k={k} tol={tol} max_iter={max_iter}")
+    X, C0 = _separated_blobs(n, d, k, seed=n + k)
+    C = C0.copy()
+    lab = np.full(n, -7, np.int32)
+    n_iter = bridge.kmeans_batch_fused(X, C, lab, n, d, k, (n + 255) // 256, max_iter, tol)
+    ref = oracle.reference_loop(X, C0, max_iter, tol)
+    assert n_iter == ref["n_iter"]
+    np.testing.assert_array_equal(lab, ref["labels"])
+    parity.check_centers(C, ref["centers"], what="batch_fused centres")
+
+
+def test_batch_fused_zero_iterations_writes_nothing(bridge):
+    X, C0 = _separated_blobs(2000, 20, 5, seed=3)
+    C = C0.copy()
+    lab = np.full(2000, -7, np.int32)
+    assert bridge.kmeans_batch_fused(X, C, lab, 2000, 20, 5, 8, 0, 1e-4) == 0
+    np.testing.assert_array_equal(C, C0)
+    assert (lab == -7).all()
+
+
 def test_accelerate_kmeans_matches_sklearn(bridge):
     """skmetal's user-facing path: accelerate(KMeans(...)).fit/predict/score on the
     GPU against scikit-learn's own KMeans from the same initial centres."""

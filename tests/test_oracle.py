@@ -224,3 +224,30 @@ def test_planted_mistakes_are_caught():
     Cdup = np.concatenate([Cr, Cr])
     assert _assign_last_tie(Xr, Cdup).min() >= 6  # would fail the duplicate-centre check
     assert oracle.assign(Xr, Cdup).max() < 6
+
+
+@pytest.mark.parametrize("tol,n_iter", [(0.3, 1), (0.25001, 1), (0.25, 2), (0.1, 2), (0.0, 5), (-1.0, 5)])
+def test_reference_loop_stopping_rule(tol, n_iter):
+    """skmetal's batch_fused stop (KMeansBridge.swift:306-310) on the unit toy:
+    step 1 moves both centres by exactly 0.25, step 2 by 0, so the loop stops
+    after step 1 when 0.25 < tol, after step 2 when 0 < tol <= 0.25, and never
+    early for tol <= 0."""
+    X = np.array([[0, 0], [0.5, 0], [0.5, 1], [1, 1]], np.float32)
+    C0 = np.array([[0, 0], [1, 1]], np.float32)
+    out = oracle.reference_loop(X, C0, 5, tol)
+    assert out["n_iter"] == n_iter
+    np.testing.assert_array_equal(out["labels"], [0, 0, 1, 1])
+    np.testing.assert_allclose(out["centers"], [[0.25, 0], [0.75, 1]], atol=1e-7)
+
+
+def test_reference_loop_zero_iterations_and_last_estep_labels():
+    X = np.array([[0, 0], [0.5, 0], [0.5, 1], [1, 1]], np.float32)
+    out = oracle.reference_loop(X, np.array([[0, 0], [1, 1]], np.float32), 0, 1.0)
+    assert out["n_iter"] == 0 and out["labels"] is None
+    # labels are the last step's E-step, against the centres that step started from:
+    # one step from centres where row 1 sits on centre 0's side, which the update then moves
+    X2 = np.array([[0.0], [1.0], [2.0], [10.0]], np.float32)
+    C2 = np.array([[1.4], [10.0]], np.float32)
+    one = oracle.reference_loop(X2, C2, 1, 0.0)
+    np.testing.assert_array_equal(one["labels"], [0, 0, 0, 1])
+    np.testing.assert_allclose(one["centers"], [[1.0], [10.0]], atol=1e-6)
