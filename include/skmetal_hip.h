@@ -93,6 +93,24 @@ SKMETAL_API int skmetal_compute_mindists(const void* X, const void* centroids, c
 
 /* ---- additions without a counterpart in the reference ---- */
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture around it, tight serving loops,
+ * harnesses that forbid hipMalloc): skmetal_kmeans_batch_fused's loop
+ * contract on caller-owned DEVICE memory, allocating nothing.  X is [n x d]
+ * fp32 in device memory, used as given (not centred); centroids is [k x d] in
+ * device memory, in/out; assignments is [n] int32 in device memory, out;
+ * *n_iter_out (host) = steps run.  Every other buffer comes from a static
+ * 32 MiB device array per GPU, whose address skmetal_init takes: skmetal_init
+ * must have succeeded first.  Limits: k <= 64, d one of 4, 8, 16, 32, 48, 64,
+ * 80, 100 (the fused kernels' row lengths), n <= 4,194,304; beyond them the
+ * call returns SKMETAL_ERANGE.  Calls are serialised by the library's lock;
+ * calls that overlap on one GPU from different processes each have their own
+ * array.  The call is synchronous (it waits for the device before it
+ * returns). */
+SKMETAL_API int skmetal_hip_kmeans_batch_fused_noalloc(const float* X, float* centroids, int32_t* assignments,
+                                                      size_t n, size_t d, size_t k, size_t max_iter, float tol,
+                                                      int32_t* n_iter_out);
+
 /* Message of the last failure on the calling thread ("" if none). */
 SKMETAL_API const char* skmetal_hip_last_error(void);
 

@@ -67,6 +67,8 @@ _REGISTRY = [
     ("skmetal_hip_column_variance", ctypes.c_int, _vp, _c_size, _c_size, _vp),
     ("skmetal_hip_lloyd_max_abs", ctypes.c_int, _vp, ctypes.POINTER(ctypes.c_float)),
     ("skmetal_hip_lloyd_mindists", ctypes.c_int, _vp, _vp, _c_size, ctypes.c_int, _vp),
+    ("skmetal_hip_kmeans_batch_fused_noalloc", ctypes.c_int, _vp, _vp, _vp, _c_size, _c_size, _c_size, _c_size,
+     ctypes.c_float, ctypes.POINTER(ctypes.c_int32)),
 ]
 
 SKMETAL_FIT_STRICT = 1

@@ -29,7 +29,20 @@
 
 using namespace skm;
 
+// Device memory of skmetal_hip_kmeans_batch_fused_noalloc: every buffer that
+// entry point needs besides its inputs and outputs is carved from this array,
+// one copy per GPU, held until the process ends.  Host code never passes the
+// array's name to a kernel: it uses the device address taken once per device
+// with hipGetSymbolAddress at initialisation (scratch_address below).
+constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
 namespace {
+
+constexpr int kMaxDevices = 64;
+void* g_scratch_addr[kMaxDevices] = {};  // device address of `scratch`, per device id (guarded by the context lock)
+constexpr long kNoAllocMaxRows = long(1) << 22;  // rows the scratch holds relocation distances for
+
 
 thread_local std::string g_err;
 
@@ -65,6 +78,20 @@ int hip_fail(hipError_t e, const char* what)
         if (rc_ != 0) return rc_; \
     } while (0)
 
+// The device address of `scratch` on device `dev` (current), taken once.
+int scratch_address(int dev, void** out)
+{
+    if (dev < 0 || dev >= kMaxDevices) return fail(SKMETAL_ERANGE, "device id %d out of range", dev);
+    if (g_scratch_addr[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return fail(SKMETAL_EHIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_scratch_addr[dev] = p;
+    }
+    *out = g_scratch_addr[dev];
+    return 0;
+}
+
 constexpr size_t kPinBytes = size_t(32) << 20;  // per staging buffer
 // finalize in record mode (sorted update): sized as for 128 partials, i.e.
 // 16 columns x 16 lanes per block; a cluster's records are read in batches
@@ -85,6 +112,7 @@ struct Context {
     size_t total_mem = 0;
     std::string name;
     hipStream_t stream = nullptr;
+    void* scratch = nullptr;  // device address of this device's `scratch` array
     void* pin[2] = {nullptr, nullptr};
     hipEvent_t pin_ev[2] = {nullptr, nullptr};
     std::multimap<size_t, void*> free_blocks;
@@ -108,6 +136,7 @@ struct Context {
         total_mem = p.totalGlobalMem;
         name = p.name;
         HIP_TRY(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
+        TRY(scratch_address(dev, &scratch));
         for (int i = 0; i < 2; ++i) {
             HIP_TRY(hipHostMalloc(&pin[i], kPinBytes, hipHostMallocDefault), "hipHostMalloc(staging)");
             HIP_TRY(hipEventCreateWithFlags(&pin_ev[i], hipEventDisableTiming), "hipEventCreate");
@@ -360,10 +389,73 @@ struct Lloyd {
     std::vector<float> h_mean;
     std::vector<void*> owned;
 
+    // no-allocation mode: buffers are carved from [arena, arena + arena_cap)
+    // instead of the context's cache
+    char* arena = nullptr;
+    size_t arena_cap = 0, arena_used = 0;
+
     int grab(void** p, size_t bytes)
     {
+        if (arena != nullptr) {
+            const size_t b = (std::max<size_t>(bytes, 1) + 255) & ~size_t(255);
+            if (arena_used + b > arena_cap)
+                return fail(SKMETAL_ERANGE, "the problem needs more than the %zu bytes of scratch", arena_cap);
+            *p = arena + arena_used;
+            arena_used += b;
+            return 0;
+        }
         TRY(C->alloc(p, bytes));
         owned.push_back(*p);
+        return 0;
+    }
+
+    // A problem on caller-owned device memory (X [n x d], rows of exactly the
+    // fused kernels' stride, used as given; the centres are read from Cdev;
+    // labels written to labdev) with every other buffer in the arena.  Only the
+    // fused step applies (fused_ld(d, k) == d); set-up and the Lloyd loop
+    // allocate nothing.
+    int create_noalloc(Context* c, long n_, int d_, int k_, const float* Xdev, float* Cdev, int* labdev)
+    {
+        C = c;
+        n = n_;
+        d = d_;
+        k = k_;
+        ld = d;
+        s = C->stream;
+        ug = update_geometry(n, d, k, C->num_cu);
+        fblocks = fused_blocks(n, ld, k, C->num_cu);
+        f3cap = fused3_ready(k, ld);
+        a3cap = assign3_ready(d, k);
+        const int chunks = std::max(finalize_col_chunks(d, fblocks), (d + kRelocCW - 1) / kRelocCW);
+        const size_t kl = size_t(k) * ld;
+        X = const_cast<float*>(Xdev);
+        labels = labdev;
+        cen[0] = Cdev;
+        cur = 0;
+        centred = false;
+        TRY(grab((void**)&cen[1], kl * sizeof(float)));
+        TRY(grab((void**)&cnorm, size_t(k) * sizeof(float)));
+        TRY(grab((void**)&psum, size_t(fblocks) * kl * sizeof(float)));
+        TRY(grab((void**)&pcnt, size_t(fblocks) * k * sizeof(int)));
+        TRY(grab((void**)&sums, kl * sizeof(double)));
+        TRY(grab((void**)&counts, size_t(k) * sizeof(int)));
+        TRY(grab((void**)&part, size_t(k) * chunks * 2 * sizeof(double)));
+        TRY(grab((void**)&shift_sq, size_t(k) * sizeof(float)));
+        TRY(grab((void**)&rowpart, size_t(rowdist_grid(n)) * sizeof(double)));
+        TRY(grab((void**)&st, sizeof(LoopState)));
+        TRY(grab((void**)&absmax, sizeof(unsigned)));
+        // relocation of empty clusters (k <= 64: always on the device)
+        TRY(grab((void**)&rowout, size_t(n) * sizeof(float)));
+        TRY(grab((void**)&r_cand_d, size_t(kRelocBlocks) * kMaxReloc * sizeof(float)));
+        TRY(grab((void**)&r_cand_i, size_t(kRelocBlocks) * kMaxReloc * sizeof(long)));
+        TRY(grab((void**)&r_amax, sizeof(int)));
+        HIP_TRY(hipMemsetAsync(cen[1], 0, kl * sizeof(float), s), "hipMemsetAsync");
+        HIP_TRY(hipMemsetAsync(st, 0, sizeof(LoopState), s), "hipMemsetAsync");
+        if (f3cap || a3cap) {
+            TRY(measure_xmax());
+            split_on = split_range_ok(xmax);
+        }
+        HIP_TRY(launch_cnorm(cen[0], k, ld, cnorm, s), "cnorm launch");
         return 0;
     }
 
@@ -734,7 +826,8 @@ struct Lloyd {
                 const int old = (c0 + (t - (int)it)) & 1;
                 // SKMETAL_HIP_HOST_RELOCATE=1 keeps the host path (A/B checks)
                 const char* env = getenv("SKMETAL_HIP_HOST_RELOCATE");
-                const bool on_host = (env != nullptr && env[0] == '1') || hs.n_empty < 1 || hs.n_empty > kMaxReloc;
+                const bool on_host =
+                    arena == nullptr && ((env != nullptr && env[0] == '1') || hs.n_empty < 1 || hs.n_empty > kMaxReloc);
                 if (on_host)
                     TRY(host_relocate(t, old, tol, flags, hs));
                 else
@@ -1052,6 +1145,43 @@ int skmetal_kmeans_batch_fused(const void* X, void* centroids, void* assignments
     if (max_iter > 0) {
         TRY(L.get_labels(static_cast<int32_t*>(assignments)));
         TRY(L.get_centers(static_cast<float*>(centroids)));
+    }
+    if (n_iter_out) *n_iter_out = it;
+    return 0;
+}
+
+int skmetal_hip_kmeans_batch_fused_noalloc(const float* X, float* centroids, int32_t* assignments, size_t n,
+                                           size_t d, size_t k, size_t max_iter, float tol, int32_t* n_iter_out)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!X || !centroids || !assignments) return fail(SKMETAL_EINVAL, "null pointer argument");
+    TRY(check_sizes(n, d, k));
+    if (k > n) return fail(SKMETAL_EINVAL, "n_samples=%zu should be >= n_clusters=%zu", n, k);
+    if (max_iter > (size_t(1) << 30)) return fail(SKMETAL_ERANGE, "max_iter too large");
+    if (!c.ready || c.scratch == nullptr)
+        return fail(SKMETAL_EINVAL, "skmetal_init must run first: this entry point does not set the library up");
+    if (k > 64) return fail(SKMETAL_ERANGE, "k=%zu: this entry point takes at most 64 clusters", k);
+    if (fused_ld((int)d, (int)k) != (int)d)
+        return fail(SKMETAL_ERANGE, "d=%zu: this entry point takes rows of 4, 8, 16, 32, 48, 64, 80 or 100 floats", d);
+    if (n > size_t(kNoAllocMaxRows))
+        return fail(SKMETAL_ERANGE, "n=%zu: this entry point takes at most %ld rows", n, kNoAllocMaxRows);
+    int it = 0;
+    if (max_iter > 0) {
+        Lloyd L;
+        L.arena = static_cast<char*>(c.scratch);
+        L.arena_cap = kScratchBytes;
+        int rc = L.create_noalloc(&c, (long)n, (int)d, (int)k, X, centroids, assignments);
+        int done = 0;
+        if (rc == 0) rc = L.run_loop((long)max_iter, (double)tol, kStopMaxShift, false, &it, &done);
+        if (rc == 0 && L.cur != 0) {
+            const hipError_t e = hipMemcpyAsync(centroids, L.cen[L.cur], k * d * sizeof(float),
+                                                hipMemcpyDeviceToDevice, L.s);
+            if (e != hipSuccess) rc = hip_fail(e, "hipMemcpyAsync(centres)");
+        }
+        const hipError_t e = hipStreamSynchronize(L.s);
+        if (rc == 0 && e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
+        if (rc != 0) return rc;
     }
     if (n_iter_out) *n_iter_out = it;
     return 0;
