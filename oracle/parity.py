@@ -74,6 +74,8 @@ def center_col_err(C, C_ref):
 def center_member_err(C, C_ref, X, labels):
     """max over (j, c) of |C_jc - R_jc| / mean_{i in cluster j} |x_ic|, over the
     clusters that have rows in `labels`."""
+    from scipy import sparse
+
     C = np.asarray(C, dtype=np.float64)
     R = np.asarray(C_ref, dtype=np.float64)
     X = np.asarray(X)
@@ -81,16 +83,14 @@ def center_member_err(C, C_ref, X, labels):
     k = R.shape[0]
     cnt = np.bincount(lab, minlength=k).astype(np.float64)
     absum = np.zeros_like(R)
-    order = np.argsort(lab, kind="stable")
     xmax = 0.0
-    step = 1 << 17
-    for s0 in range(0, len(order), step):
-        idx = order[s0:s0 + step]
-        lb = lab[idx]
-        blk = np.abs(X[idx].astype(np.float64))
+    step = 1 << 18
+    for s0 in range(0, len(lab), step):
+        lb = lab[s0:s0 + step]
+        blk = np.abs(X[s0:s0 + step])
         xmax = max(xmax, float(blk.max(initial=0.0)))
-        starts = np.flatnonzero(np.r_[True, lb[1:] != lb[:-1]])
-        absum[lb[starts]] += np.add.reduceat(blk, starts, axis=0)
+        onehot = sparse.csr_matrix((np.ones(len(lb), np.float64), (lb, np.arange(len(lb)))), shape=(k, len(lb)))
+        absum += onehot @ blk.astype(np.float64)
     has = cnt > 0
     if not has.any():
         return 0.0

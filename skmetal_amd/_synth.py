@@ -85,6 +85,37 @@ def _fill_blobs(rng, centres: np.ndarray, sizes: np.ndarray, sigma: float) -> np
     return X
 
 
+def _fill_directions_parallel(rng, u: np.ndarray, sizes: np.ndarray, sigma: float) -> np.ndarray:
+    """c5's rows, normalise(u_label + sigma z), filled in blocks of 65,536 rows
+    on host threads.  Each block draws from its own generator spawned from
+    `rng` (after the label permutation), so the result does not depend on the
+    thread count."""
+    import os
+    from concurrent.futures import ThreadPoolExecutor
+
+    n = int(sizes.sum())
+    d = u.shape[1]
+    lab = np.repeat(np.arange(len(sizes)), sizes)[rng.permutation(n)]
+    block = 1 << 16
+    nblk = (n + block - 1) // block
+    gens = rng.spawn(nblk)
+    u32 = u.astype(np.float32)
+    X = np.empty((n, d), dtype=np.float32)
+
+    def fill(b):
+        r0, r1 = b * block, min(n, (b + 1) * block)
+        blk = X[r0:r1]
+        gens[b].standard_normal(out=blk, dtype=np.float32)
+        blk *= np.float32(sigma)
+        blk += u32[lab[r0:r1]]
+        blk /= np.linalg.norm(blk, axis=1, keepdims=True).astype(np.float32)
+
+    workers = max(1, min(16, len(os.sched_getaffinity(0))))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        list(pool.map(fill, range(nblk)))
+    return X
+
+
 def generate(name: str, seed: int = 0, scale: float = 1.0):
     """Return (X, C0) for workload ``name`` (fp32 C-order)."""
     w = WORKLOADS[name]
@@ -102,11 +133,7 @@ def generate(name: str, seed: int = 0, scale: float = 1.0):
     elif name == "c5":
         u = rng.standard_normal((w.k, w.d))
         u /= np.linalg.norm(u, axis=1, keepdims=True)
-        X = _fill_blobs(rng, u, _blob_sizes_equal(n, w.k), 0.2)
-        step = 1 << 18
-        for s in range(0, n, step):
-            blk = X[s : s + step]
-            blk /= np.linalg.norm(blk, axis=1, keepdims=True).astype(np.float32)
+        X = _fill_directions_parallel(rng, u, _blob_sizes_equal(n, w.k), 0.2)
     else:
         raise KeyError(name)
     X = np.ascontiguousarray(X, dtype=np.float32)
