@@ -12,6 +12,8 @@
 // MFMA accumulators).
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "fused_common.h"
 
 namespace skm {
@@ -109,140 +111,93 @@ __device__ __forceinline__ v4f dot6(const P& a, const P& b, v4f acc)
 
 // ---------------------------------------------------------------------------
 // k_fused3: the fused step with the E-step and the per-cluster sums on bf16
-// MFMAs over the three-part split (v_mfma_f32_16x16x32_bf16, and
-// v_mfma_f32_16x16x16_bf16 for a last 4-, 8- or 16-feature slice).
+// MFMAs over the three-part split (v_mfma_f32_16x16x32_bf16).
 //
 // MFMA operand layout (16x16x32, checked on the device): lane l holds A[m =
 // l%16][kk = 8(l/16) + j] and B[kk = 8(l/16) + j][n = l%16], j < 8, and
-// receives D[m = 4(l/16) + i][n = l%16], i < 4; 16x16x16 the same with 4
-// values per lane.  In the E-step A = 16 centres (block cb, parts from LDS)
-// and B = 16 rows of the tile (group g, from registers), so lane l ends with
-// the x.c of row 16g + l%16 and centres 16cb + 4(l/16) + i: the first minimum
-// over the lane's 4 CB centres, then over the four lanes l%16 + 16h (lower
-// index wins ties: the first minimum over all centres), and lane 16g + r
-// keeps row 16g + r's label -- lane = row for the labels and counts.
+// receives D[m = 4(l/16) + i][n = l%16], i < 4.
 //
-// A block is 12 waves, three per SIMD.  E-step waves e = 0..7 (two per SIMD)
-// each work on their own 32-row tiles t = 8b + e + r P, with their own LDS
-// tile; sums wave 8 + m serves the two E-step waves m and m + 4 of its SIMD,
-// taking their tiles in turn.  Each lane loads its 8 (K32 step) or 4 (tail)
-// features of its rows straight from HBM into registers, writes them to the
-// wave's LDS tile for the sums wave and reloads them with tile t + P once the
-// sums wave has read those columns of the previous tile.  The waves hand over
-// work through LDS flags; there is no block barrier until the end.
-
-// The sums wave of SIMD m serves E-step waves m and m + 4 (the same SIMD),
-// taking their 32-row tiles in turn: round r of wave m, then round r of wave
-// m + 4.  The per-cluster sums of a tile are onehot^T x on
-// v_mfma_f32_16x16x32_bf16, once for each part of x.  A = one-hot (16
-// clusters x the tile's 32 rows: lane l holds rows 8(l/16) + j for cluster
-// 16cb + l%16), B = a part of x (the 32 rows x 16 features of block fb, read
-// transposed from the LDS tile); D lane l: clusters 16cb + 4(l/16) + i,
-// feature 16fb + l%16.  Progress is published per 16-feature block (all rows
-// read).  Columns at and past ld hold whatever the LDS has there (the next
-// row's values, never-written padding): their sums are never published.
-template <int CB, int NQ, int XS, int NFB>
-__device__ __forceinline__ void msum_tiles3(v4f (&S)[CB][NFB], int rounds0, int rounds1, int* ready0, int* ready1,
-                                            int* prog0, int* prog1, unsigned* mask0, unsigned* mask1,
-                                            const v8bf* onehot, const float* tile0, const float* tile1, int lane)
-{
-    const int h = lane >> 4, r16 = lane & 15;
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-#pragma unroll
-        for (int fb = 0; fb < NFB; ++fb) S[cb][fb] = v4f{0.f, 0.f, 0.f, 0.f};
-    }
-    const int rmax = rounds0 > rounds1 ? rounds0 : rounds1;
-    for (int r = 0; r < rmax; ++r) {
-        for (int u = 0; u < 2; ++u) {
-            // (selects, not an indexed array: the pointers stay in registers)
-            if (r >= (u == 0 ? rounds0 : rounds1)) continue;
-            int* const ready = u == 0 ? ready0 : ready1;
-            int* const prog = u == 0 ? prog0 : prog1;
-            unsigned* const mask = u == 0 ? mask0 : mask1;
-            const float* const tile = u == 0 ? tile0 : tile1;
-            wait_flag(ready, r + 1);
-            // A[cb][j] = 1 when row 8h + j has label 16 cb + r16: byte h of that
-            // cluster's row mask, through the one-hot table; then the masks
-            // are cleared for the next round (the E-step wave sets the next
-            // bits only after this tile's progress flags, which follow)
-            v8bf A[CB];
-            {
-                unsigned mw[CB];
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb) mw[cb] = mask[16 * cb + r16];
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb) A[cb] = onehot[(mw[cb] >> (8 * h)) & 0xffu];
-                if (h == 0) {
-#pragma unroll
-                    for (int cb = 0; cb < CB; ++cb) mask[16 * cb + r16] = 0u;
-                }
-            }
-            const float* col = tile + 8 * h * XS + 16 * h + r16;  // rows 8h .. 8h + 7 sit 16 h floats further
-#pragma unroll
-            for (int fb = 0; fb < NFB; ++fb) {
-                float cur[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) cur[j] = col[j * XS + 16 * fb];
-                // columns of feature block fb have been read for every row
-                set_flag(prog, r * NQ + (4 * fb + 4 < NQ ? 4 * fb + 4 : NQ));
-                const Parts8 b = split8(make_float4(cur[0], cur[1], cur[2], cur[3]),
-                                        make_float4(cur[4], cur[5], cur[6], cur[7]));
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb) {
-                    S[cb][fb] = mfma_bf16(A[cb], b.l, S[cb][fb]);
-                    S[cb][fb] = mfma_bf16(A[cb], b.m, S[cb][fb]);
-                    S[cb][fb] = mfma_bf16(A[cb], b.h, S[cb][fb]);
-                }
-            }
-        }
-    }
-}
-
-// M-step sums into red = [4][CPC][ld], once every pair is done.
-template <int CB, int NFB>
-__device__ __forceinline__ void publish_msums(const v4f (&S)[CB][NFB], float* red, int ld, int pair, int lane)
-{
-    const int h = lane >> 4, r16 = lane & 15;
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-#pragma unroll
-        for (int fb = 0; fb < NFB; ++fb) {
-            const int f = 16 * fb + r16;
-            if (f < ld) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) red[(pair * 16 * CB + 16 * cb + 4 * h + i) * ld + f] = S[cb][fb][i];
-            }
-        }
-    }
-}
+// A block is 16 waves, four per SIMD: E-step waves m and m + 4 and sums waves
+// 8 + m and 12 + m on SIMD m share the 32-row tiles t = 4b + m + r P (P = 4 x
+// blocks), E-step wave m taking rows 0..15 of each and wave m + 4 rows
+// 16..31.  An E-step wave loads its 16 rows straight from HBM into registers
+// (one tile ahead), splits each value once, takes the E-step's MFMAs with the
+// parts as B (its 16 rows as the columns n) against 16-centre blocks of the
+// centre parts as A, and writes the parts to the SIMD's LDS tile, row-major.
+// Lane l then holds x.c of row l%16 and centres 16cb + 4(l/16) + i: the first
+// minimum over the lane's centres, then over the four lanes l%16 + 16h (lower
+// index wins ties: the first minimum over all centres); lane r < 16 keeps row
+// r's label.
+//
+// The centre operands sit in LDS in fragment order -- 1 KB per MFMA operand,
+// lane l's 16 bytes at 16 l -- so every A read is one contiguous block.
+//
+// The sums waves read the 32-row tile back transposed (ds_read_b64_tr_b16
+// returns the B operand with K = the tile's rows) and add onehot^T x once per
+// part, wave 8 + m over the first half of the 16-feature blocks and 12 + m
+// over the rest.  The waves hand over through LDS flags: ready (half tiles
+// labelled, their row masks set) and progress (blocks of a tile read, per
+// sums wave); there is no block barrier until the end.
+//
+// Features past the last 32-feature K step (a tail of TAIL = 4 or 16): the
+// six products of the E-step are laid side by side along K, block b (TAIL
+// values) pairing centre part PC[b] with x part PX[b] for (PC, PX) = (h, h),
+// (m, h), (l, h), (h, m), (m, m), (h, l).  One MFMA (TAIL = 4) or three (TAIL
+// = 16) take the six products in place of six each.
+//
+// When the last 16-centre block holds at most 4 real centres (STK), its A
+// rows m = 4 slot + p carry part p of centre 16(CB-1) + slot (p = 3: zero)
+// and the B operands are the three x parts in turn: three MFMAs per K step
+// give all nine part products, and lane l's D[0..2] are the parts of the dot
+// product with centre 16(CB-1) + l/16.
 
 // Geometry of k_fused3 for a row of NQ float4s.
 template <int NQ>
 struct Fused3Geom {
-    static constexpr int LDX = 4 * NQ;                       // == ld
-    static constexpr int NK = LDX / 32;                      // 32-feature K steps
-    static constexpr int TAIL = LDX - 32 * NK;               // features of the last, 16-wide step (0: none)
-    static constexpr int NS = NK + (TAIL > 0 ? 1 : 0);       // K steps
-    static constexpr int QG = 2 * NK + (TAIL > 0 ? 1 : 0);   // float4s per lane per 16-row group
-    static constexpr int TQ = TAIL > 0 ? 2 * NK : 0;         // the tail's float4 (dead code without a tail)
-    static constexpr int KP = 32 * NK + (TAIL > 0 ? 16 : 0); // features the MFMAs cover
-    static constexpr int CSTR = KP + 8;                      // bf16 per centre row: an odd number of 16-byte units
-    static constexpr int XS = fused_stride(NQ);              // LDS row: >= ld floats
-    static constexpr int NFB = KP / 16;                      // 16-feature blocks of the sums
-    // a wave's tile: row rho at rho * XS + 16 (rho >> 3).  XS is 4 x odd, so
-    // 8 XS = 32 (mod 64): without the shift the sums wave's column reads of
-    // rows 8h + j (lanes h = 0..3) fall on the same banks in pairs; with it
-    // the four h start 48 h (mod 64) apart, distinct in every 32-lane pass.
-    // The sums wave reads KP columns of every row: rows past XS floats run
-    // into the next row (KP - XS floats of padding after the last one).
-    static constexpr int TS = 32 * XS + 48 + (KP > XS ? KP - XS : 0);
-    static_assert(TAIL == 0 || TAIL == 4 || TAIL == 8 || TAIL == 16, "one 16-wide step covers the tail");
-    static_assert(TS % 4 == 0, "16-byte aligned tiles");
+    static constexpr int LDX = 4 * NQ;                        // == ld
+    static constexpr int NK = LDX / 32;                       // 32-feature K steps
+    static constexpr int TAIL = LDX - 32 * NK;                // features after them: 0, 4 or 16
+    static constexpr int KP = 32 * NK + (TAIL > 0 ? 16 : 0);  // features per part in a tile row
+    static constexpr int NFB = KP / 16;                       // 16-feature blocks of the sums
+    static constexpr int QG = 2 * NK + TAIL / 8 + (TAIL == 4 ? 1 : 0);  // float4s per lane
+    static constexpr int NT = TAIL == 4 ? 1 : TAIL == 16 ? 3 : 0;      // tail MFMAs per block
+    static constexpr int NTS = TAIL == 4 ? 1 : TAIL == 16 ? 2 : 0;     // tail MFMAs of a stacked block
+    // a tile row is hi | mid | lo, KP bf16 each: 6 KP bytes, padded so that
+    // the row stride is 32 or 96 mod 128 bytes
+    static constexpr int RSB = (6 * KP) % 128 == 0 || (6 * KP) % 128 == 64 ? 6 * KP + 32 : 6 * KP;
+    static constexpr int TILEB = 32 * RSB;
+    // centre fragments (1 KB each): [cb][s][part], then [cb][tail MFMA], then
+    // the stacked block's [s] and [tail MFMA]
+    static constexpr int frags(int cb) { return cb * (3 * NK + NT) + NK + NTS; }
+    static constexpr size_t lds(int cb)
+    {
+        const size_t work = (size_t)4 * TILEB + (size_t)1024 * frags(cb);
+        const size_t red = (size_t)4 * 16 * cb * LDX * sizeof(float);  // the sums of the four sums waves
+        return work > red ? work : red;
+    }
+    static_assert(TAIL == 0 || TAIL == 4 || TAIL == 16, "tails of 4 or 16 features");
+    static_assert(RSB % 16 == 0 && (2 * KP) % 16 == 0, "16-byte aligned rows and parts");
 };
 
-template <int CB, int NQ>
-__global__ __launch_bounds__(768, 1) void k_fused3(FusedArgs a)
+__device__ __forceinline__ v4s lds_tr16(const char* p)
+{
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(p));
+}
+
+__device__ __forceinline__ v8bf cat8(v4s a, v4s b)
+{
+    return __builtin_bit_cast(v8bf, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// part p (0 hi, 1 mid, 2 lo) of a split
+__device__ __forceinline__ v8bf part_of(const Parts8& x, int p) { return p == 0 ? x.h : p == 1 ? x.m : x.l; }
+__device__ __forceinline__ v4s part_of(const Parts4& x, int p) { return p == 0 ? x.h : p == 1 ? x.m : x.l; }
+
+// centre part (0 hi, 1 mid, 2 lo) of tail block b: (h, m, l, h, m, h)
+__device__ __forceinline__ int tail_cpart(int b) { return b == 1 || b == 4 ? 1 : b == 2 ? 2 : 0; }
+
+template <int CB, int NQ, bool STK>
+__global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
 {
     using G = Fused3Geom<NQ>;
     const float* __restrict__ X = a.X;
@@ -253,250 +208,473 @@ __global__ __launch_bounds__(768, 1) void k_fused3(FusedArgs a)
     int* __restrict__ labels = a.labels;
     LoopState* st = a.state;
     constexpr int CPC = 16 * CB;  // clusters padded to 16-centre blocks
-    constexpr int LDX = G::LDX, NK = G::NK, TAIL = G::TAIL, NS = G::NS, QG = G::QG, TQ = G::TQ, KP = G::KP;
-    constexpr int CSTR = G::CSTR, XS = G::XS, NFB = G::NFB, TS = G::TS;
-    constexpr int CPART = CPC * CSTR;  // bf16 from one centre part to the next
-    // LDS: 8 wave tiles [TS floats] | centre parts hi, mid, lo [CPC x CSTR] bf16
+    constexpr int LDX = G::LDX, NK = G::NK, TAIL = G::TAIL, KP = G::KP, NFB = G::NFB, QG = G::QG, NT = G::NT;
+    constexpr int RSB = G::RSB, TILEB = G::TILEB;
+    constexpr int CBF = STK ? CB - 1 : CB;  // blocks taken as 16 centres
+    constexpr int NFA = (NFB + 1) / 2;      // feature blocks of the first sums wave of a SIMD
+    constexpr int NFZ = NFB - NFA;          // and of the second
+    // fragment indices (units of 64 v8bf)
+    constexpr int FT = CB * 3 * NK;         // tail fragments
+    constexpr int FS = CB * (3 * NK + NT);  // stacked block: K steps, then its tail
+    // LDS: 4 SIMD tiles [32 x RSB bytes] | centre fragments [frags x 1 KB]
     extern __shared__ __attribute__((aligned(16))) float lds[];
-    __shared__ unsigned sMask[8][64];                           // a tile's rows of each cluster (bit = row)
+    // rows of each cluster in E-step wave e's half of a tile (bit = row), by
+    // round parity
+    __shared__ unsigned sMask[2][8][64];
     __shared__ __attribute__((aligned(16))) v8bf sOneHot[256];  // byte b -> its 8 bits as bf16 0 / 1
     __shared__ int sCnt[4][64];                                 // rows per cluster, per SIMD
     __shared__ __attribute__((aligned(16))) float sN[CPC];
-    __shared__ int sReady[8];  // tiles E-step wave e has labelled
-    __shared__ int sProg[8];   // columns of e's tile the sums wave has read: tile * NQ + chunk
+    __shared__ int sReady[8];  // half tiles E-step wave e has labelled
+    __shared__ int sProg[8];   // feature blocks sums wave w has read: tile * (its blocks) + blocks
     __shared__ int sDone;      // nonzero: the loop has halted, nothing to do
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 4;    // this lane's K slice / centre quad in the MFMA layout
-    const int r16 = lane & 15;  // this lane's row of a 16-row group / centre of a block
+    const int r16 = lane & 15;  // this lane's row / centre of a block
 
-    float* tiles = lds;
-    __bf16* sCP = reinterpret_cast<__bf16*>(tiles + 8 * TS);
+    char* const tiles = reinterpret_cast<char*>(lds);
+    v8bf* const sFr = reinterpret_cast<v8bf*>(tiles + 4 * TILEB);
 
-    // 32-row tiles: E-step wave e of block b handles t = 8b + e + r*P
+    // 32-row tiles: SIMD m of block b handles t = 4b + m + r*P
     const long ntiles = (n + 31) >> 5;
-    const long P = (long)gridDim.x * 8;
-    auto rounds_of = [&](int e) {
-        const long t0 = (long)blockIdx.x * 8 + e;
+    const long P = (long)gridDim.x * 4;
+    auto rounds_of = [&](int m) {
+        const long t0 = (long)blockIdx.x * 4 + m;
         return t0 < ntiles ? (int)((ntiles - t0 + P - 1) / P) : 0;
     };
 
     if (wave < 8) {
-        // E-step wave e (SIMD e % 4).  xr[g] holds this lane's features of
-        // row 16g + l%16 of the tile: K32 step s in xr[g][2s], xr[g][2s + 1]
-        // (features 32s + 8h + 0..7), the tail in xr[g][2NK] (features 32NK +
-        // 4h + 0..3; lanes past the row's last feature load nothing: zeros)
-        const int e = wave;
-        const long t0 = (long)blockIdx.x * 8 + e;
-        const int rounds = rounds_of(e);
-        float4 xr[2][QG];
-        auto rsrc32 = [&](long t) {
-            const long r0 = t * 32;
-            const long rows = n - r0 < 32 ? (n - r0 > 0 ? n - r0 : 0) : 32;
+        // E-step wave e: SIMD m = e & 3, rows 16 hf .. 16 hf + 15 of the
+        // tiles.  xr holds this lane's features of row l%16: K32 step s in
+        // xr[2s], xr[2s + 1] (features 32s + 8h + 0..7); the tail in xr[2NK]
+        // (TAIL = 4: features 32NK + 0..3 in every h) or xr[2NK], xr[2NK + 1]
+        // (TAIL = 16: features 32NK + 8(h&1) + 0..7)
+        const int e = wave, m = wave & 3, hf = wave >> 2;
+        const long t0 = (long)blockIdx.x * 4 + m;
+        const int rounds = rounds_of(m);
+        float4 xr[QG];
+        auto rsrc16 = [&](long t) {
+            const long r0 = t * 32 + 16 * hf;
+            const long rows = n - r0 < 16 ? (n - r0 > 0 ? n - r0 : 0) : 16;
             return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(X + (rows > 0 ? r0 * ld : 0)), (short)0,
                                                      (int)(rows * ld * 4), 0x00020000);
         };
-        auto load_step = [&](__amdgpu_buffer_rsrc_t rs, int g, int s) {
+        auto load_step = [&](__amdgpu_buffer_rsrc_t rs, int s) {
+            const int row = r16 * LDX;
             if (s < NK) {
-                const int o = ((16 * g + r16) * LDX + 32 * s + 8 * h) * 4;
-                xr[g][2 * s] = load_quad(rs, o);
-                xr[g][2 * s + 1] = load_quad(rs, o + 16);
-            } else {
-                const int o = ((16 * g + r16) * LDX + 32 * NK + 4 * h) * 4;
-                xr[g][TQ] = load_quad(rs, 4 * h < TAIL ? o : 0x40000000);
+                const int o = (row + 32 * s + 8 * h) * 4;
+                xr[2 * s] = load_quad(rs, o);
+                xr[2 * s + 1] = load_quad(rs, o + 16);
+            } else if constexpr (TAIL == 4) {
+                xr[2 * NK] = load_quad(rs, (row + 32 * NK) * 4);
+            } else if constexpr (TAIL == 16) {
+                const int o = (row + 32 * NK + 8 * (h & 1)) * 4;
+                xr[2 * NK] = load_quad(rs, o);
+                xr[QG - 1] = load_quad(rs, o + 16);
             }
         };
+        constexpr int NS = NK + (TAIL > 0 ? 1 : 0);
         {
             // in the order of the reloads in the rounds below (the waits at
-            // the top of a round then count the same loads either way)
-            const __amdgpu_buffer_rsrc_t r0 = rsrc32(t0);
+            // the top of a step then count the same loads either way)
+            const __amdgpu_buffer_rsrc_t r0 = rsrc16(t0);
 #pragma unroll
             for (int s = 0; s < NS; ++s) {
-                load_step(r0, 0, s);
-                load_step(r0, 1, s);
+                load_step(r0, s);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
         __syncthreads();  // LDS set up by the sums waves
         if (sDone != 0) return;
-        float* const trow = tiles + e * TS + r16 * XS + 16 * (r16 >> 3);  // group 0's row; group g's: + g * GS
-        constexpr int GS = 16 * XS + 32;
-        // this lane's centre operands: one base address, the block, step and
-        // part as constant offsets (no per-block address registers)
-        const __bf16* const cbase = sCP + r16 * CSTR + 8 * h;
+        char* const trow = tiles + m * TILEB + (16 * hf + r16) * RSB;  // this lane's row of the tile
+        const v8bf* const fr = sFr + lane;                            // this lane's 16 bytes of fragment f: fr[64 f]
+        // before feature blocks f0 .. f1 of the tile are rewritten for round r,
+        // the sums waves have read them for round r - 1
+        auto wait_blocks = [&](int r, int f0, int f1) {
+            if (r == 0) return;
+            if (f0 < NFA) wait_flag(&sProg[m], (r - 1) * NFA + (f1 + 1 < NFA ? f1 + 1 : NFA));
+            if (f1 >= NFA) wait_flag(&sProg[4 + m], (r - 1) * NFZ + (f1 + 1 - NFA));
+        };
         int changed = 0;
         for (int r = 0; r < rounds; ++r) {
             const long t = t0 + (long)r * P;
-            const long nrow = n - t * 32 < 32 ? n - t * 32 : 32;
+            const long nrow = n - t * 32 - 16 * hf < 16 ? n - t * 32 - 16 * hf : 16;
             const bool valid = lane < nrow;
-            const __amdgpu_buffer_rsrc_t rl =
-                __builtin_amdgcn_make_buffer_rsrc(labels + t * 32, (short)0, (int)(nrow * 4), 0x00020000);
+            const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(
+                labels + t * 32 + 16 * hf, (short)0, (int)(nrow > 0 ? nrow * 4 : 0), 0x00020000);
             const int old = __builtin_amdgcn_raw_buffer_load_b32(rl, lane * 4, 0, 0);
-            const __amdgpu_buffer_rsrc_t rn = rsrc32(t + P);
-            int seen = 0;  // sums-wave progress last read
-            v4f acc[2][CB];
+            const __amdgpu_buffer_rsrc_t rn = rsrc16(t + P);
+            v4f acc[CB];
 #pragma unroll
-            for (int g = 0; g < 2; ++g) {
+            for (int cb = 0; cb < CB; ++cb) acc[cb] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int cb = 0; cb < CB; ++cb) acc[g][cb] = v4f{0.f, 0.f, 0.f, 0.f};
-            }
+            for (int s = 0; s < NK; ++s) {
+                // the step's centre fragments first: their LDS latency runs
+                // under the split
+                Parts8 cpt[CBF > 0 ? CBF : 1];
 #pragma unroll
-            for (int s = 0; s < NS; ++s) {
-                // the columns of step s are rewritten below once the sums
-                // wave has read them for tile t - P
-                if (r > 0) {
-                    const int need = (r - 1) * NQ + (s < NK ? min(NQ, 8 * s + 8) : NQ);
-                    if (seen < need) seen = wait_flag(&sProg[e], need);
+                for (int cb = 0; cb < CBF; ++cb) {
+                    const int f = (cb * NK + s) * 3;
+                    cpt[cb] = Parts8{fr[64 * f], fr[64 * (f + 1)], fr[64 * (f + 2)]};
                 }
-                if (s < NK) {
-                    Parts8 xp[2];
+                v8bf cs;
+                if constexpr (STK) cs = fr[64 * (FS + s)];
+                const Parts8 xp = split8(xr[2 * s], xr[2 * s + 1]);
+                wait_blocks(r, 2 * s, 2 * s + 1);
+                {
+                    char* dst = trow + (32 * s + 8 * h) * 2;
+                    *reinterpret_cast<v8bf*>(dst) = xp.h;
+                    *reinterpret_cast<v8bf*>(dst + 2 * KP) = xp.m;
+                    *reinterpret_cast<v8bf*>(dst + 4 * KP) = xp.l;
+                }
+                load_step(rn, s);
+                // product-major: consecutive MFMAs write different accumulators
 #pragma unroll
-                    for (int g = 0; g < 2; ++g) {
-                        float* dst = trow + g * GS + 32 * s + 8 * h;
-                        *reinterpret_cast<float4*>(dst) = xr[g][2 * s];
-                        *reinterpret_cast<float4*>(dst + 4) = xr[g][2 * s + 1];
-                        xp[g] = split8(xr[g][2 * s], xr[g][2 * s + 1]);
-                        load_step(rn, g, s);
+                for (int pr = 0; pr < 6; ++pr) {
+#pragma unroll
+                    for (int cb = 0; cb < CBF; ++cb) {
+                        const Parts8& c = cpt[cb];
+                        const v8bf ca = pr == 0 ? c.m : pr == 1 ? c.l : pr == 2 ? c.h : pr == 3 ? c.m : c.h;
+                        const v8bf xb = pr == 0 ? xp.m : pr == 1 ? xp.h : pr == 2 ? xp.l : pr == 3 ? xp.h
+                                                                                                 : pr == 4 ? xp.m : xp.h;
+                        acc[cb] = mfma_bf16(ca, xb, acc[cb]);
                     }
+                    if constexpr (STK) {
+                        if (pr < 3) acc[CB - 1] = mfma_bf16(cs, pr == 0 ? xp.l : pr == 1 ? xp.m : xp.h, acc[CB - 1]);
+                    }
+                }
+            }
+            if constexpr (TAIL > 0) {
+                const v4s z4 = v4s{0, 0, 0, 0};
+                if constexpr (TAIL == 4) {
+                    const Parts4 xt = split4(xr[2 * NK]);
+                    wait_blocks(r, NFB - 1, NFB - 1);
+                    if (h == 0) {
+                        char* dst = trow + 32 * NK * 2;
+                        *reinterpret_cast<v4s*>(dst) = xt.h;
+                        *reinterpret_cast<v4s*>(dst + 2 * KP) = xt.m;
+                        *reinterpret_cast<v4s*>(dst + 4 * KP) = xt.l;
+                    }
+                    load_step(rn, NK);
+                    // blocks 2h, 2h + 1 of (x_h, x_h, x_h, x_m, x_m, x_l, 0, 0)
+                    const v8bf bt = cat8(h < 2 ? xt.h : h == 2 ? xt.m : z4,
+                                         h == 0 ? xt.h : h == 1 ? xt.m : h == 2 ? xt.l : z4);
 #pragma unroll
-                    for (int cb = 0; cb < CB; ++cb) {
-                        const __bf16* cp = cbase + 16 * cb * CSTR + 32 * s;
-                        const Parts8 cpt{*reinterpret_cast<const v8bf*>(cp),
-                                         *reinterpret_cast<const v8bf*>(cp + CPART),
-                                         *reinterpret_cast<const v8bf*>(cp + 2 * CPART)};
-#pragma unroll
-                        for (int g = 0; g < 2; ++g) acc[g][cb] = dot6(cpt, xp[g], acc[g][cb]);
+                    for (int cb = 0; cb < CBF; ++cb) acc[cb] = mfma_bf16(fr[64 * (FT + cb)], bt, acc[cb]);
+                    if constexpr (STK) {
+                        // blocks 2h, 2h + 1 of (x_h, x_m, x_l, 0, ...)
+                        const v8bf bs = cat8(h == 0 ? xt.h : h == 1 ? xt.l : z4, h == 0 ? xt.m : z4);
+                        acc[CB - 1] = mfma_bf16(fr[64 * (FS + NK)], bs, acc[CB - 1]);
                     }
                 } else {
-                    Parts4 xp[2];
-#pragma unroll
-                    for (int g = 0; g < 2; ++g) {
-                        // lanes past the row's last feature hold zeros and
-                        // store nothing: the LDS row may be shorter than KP
-                        if (4 * h < TAIL)
-                            *reinterpret_cast<float4*>(trow + g * GS + 32 * NK + 4 * h) = xr[g][TQ];
-                        xp[g] = split4(xr[g][TQ]);
-                        load_step(rn, g, s);
+                    const Parts8 xt = split8(xr[2 * NK], xr[QG - 1]);
+                    wait_blocks(r, NFB - 1, NFB - 1);
+                    if (h < 2) {
+                        char* dst = trow + (32 * NK + 8 * h) * 2;
+                        *reinterpret_cast<v8bf*>(dst) = xt.h;
+                        *reinterpret_cast<v8bf*>(dst + 2 * KP) = xt.m;
+                        *reinterpret_cast<v8bf*>(dst + 4 * KP) = xt.l;
                     }
+                    load_step(rn, NK);
+                    // MFMA q, lane h: block 2q + h/2 of (x_h, x_h, x_h, x_m, x_m, x_l)
+                    const v8bf b1 = h < 2 ? xt.h : xt.m, b2 = h < 2 ? xt.m : xt.l;
 #pragma unroll
-                    for (int cb = 0; cb < CB; ++cb) {
-                        const __bf16* cp = cbase - 4 * h + 16 * cb * CSTR + 32 * NK;  // features 32 NK + 4h ..
-                        const Parts4 cpt{*reinterpret_cast<const v4s*>(cp),
-                                         *reinterpret_cast<const v4s*>(cp + CPART),
-                                         *reinterpret_cast<const v4s*>(cp + 2 * CPART)};
+                    for (int q = 0; q < 3; ++q) {
 #pragma unroll
-                        for (int g = 0; g < 2; ++g) acc[g][cb] = dot6(cpt, xp[g], acc[g][cb]);
+                        for (int cb = 0; cb < CBF; ++cb)
+                            acc[cb] = mfma_bf16(fr[64 * (FT + cb * NT + q)], q == 0 ? xt.h : q == 1 ? b1 : b2, acc[cb]);
+                    }
+                    if constexpr (STK) {
+                        // blocks of (x_h, x_m, x_l, 0): lanes h < 2 take the
+                        // first of each MFMA's two, h >= 2 the second
+                        acc[CB - 1] = mfma_bf16(fr[64 * (FS + NK)], b1, acc[CB - 1]);
+                        acc[CB - 1] = mfma_bf16(fr[64 * (FS + NK + 1)], h < 2 ? xt.l : cat8(z4, z4), acc[CB - 1]);
                     }
                 }
-                __builtin_amdgcn_sched_barrier(0);
             }
             // ||c||^2 - 2 x.c, first minimum wins (_k_means_lloyd.pyx:196-212)
-            int mylab = 0;
+            float bd = INFINITY;
+            int bi = 4 * h;
 #pragma unroll
-            for (int g = 0; g < 2; ++g) {
-                float bd = INFINITY;
-                int bi = 4 * h;
+            for (int cb = 0; cb < CBF; ++cb) {
+                const float4 c4 = *reinterpret_cast<const float4*>(&sN[16 * cb + 4 * h]);
+                const float cn[4] = {c4.x, c4.y, c4.z, c4.w};
 #pragma unroll
-                for (int cb = 0; cb < CB; ++cb) {
-                    const float4 c4 = *reinterpret_cast<const float4*>(&sN[16 * cb + 4 * h]);
-                    const float cn[4] = {c4.x, c4.y, c4.z, c4.w};
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        // a NaN distance compares false: it never wins
-                        const float dd = fmaf(-2.0f, acc[g][cb][i], cn[i]);
-                        const bool take = dd < bd;
-                        bd = take ? dd : bd;
-                        bi = take ? 16 * cb + 4 * h + i : bi;
-                    }
+                for (int i = 0; i < 4; ++i) {
+                    // a NaN distance compares false: it never wins
+                    const float dd = fmaf(-2.0f, acc[cb][i], cn[i]);
+                    const bool take = dd < bd;
+                    bd = take ? dd : bd;
+                    bi = take ? 16 * cb + 4 * h + i : bi;
                 }
-#pragma unroll
-                for (int m = 16; m <= 32; m *= 2) {
-                    const float od = __shfl_xor(bd, m);
-                    const int oi = __shfl_xor(bi, m);
-                    const bool take = (od < bd) | ((od == bd) & (oi < bi));  // no branch
-                    bd = take ? od : bd;
-                    bi = take ? oi : bi;
-                }
-                if (h == g) mylab = bi;  // lanes 0..31: row = lane
             }
-            __builtin_amdgcn_raw_buffer_store_b32(mylab, rl, lane * 4, 0, 0);
-            changed += (int)__popcll(__ballot(valid && old != mylab));
-            // the tile's rows per cluster for the sums wave (an OR of bits:
-            // any order gives the same mask); the counts (integer adds)
-            if (valid) atomicOr(&sMask[e][mylab], 1u << lane);
-            if (valid) atomicAdd(&sCnt[e & 3][mylab], 1);
+            if constexpr (STK) {
+                // centre 16(CB-1) + h: the sum of its three parts' products
+                const float dot = (acc[CB - 1][2] + acc[CB - 1][1]) + acc[CB - 1][0];
+                const float dd = fmaf(-2.0f, dot, sN[16 * (CB - 1) + h]);
+                const bool take = dd < bd;
+                bd = take ? dd : bd;
+                bi = take ? 16 * (CB - 1) + h : bi;
+            }
+#pragma unroll
+            for (int sh = 16; sh <= 32; sh *= 2) {
+                const float od = __shfl_xor(bd, sh);
+                const int oi = __shfl_xor(bi, sh);
+                const bool take = (od < bd) | ((od == bd) & (oi < bi));  // no branch
+                bd = take ? od : bd;
+                bi = take ? oi : bi;
+            }
+            // lanes 0..15: row = lane
+            __builtin_amdgcn_raw_buffer_store_b32(bi, rl, lane * 4, 0, 0);
+            changed += (int)__popcll(__ballot(valid && old != bi));
+            if (valid) atomicAdd(&sCnt[m][bi], 1);  // the counts (integer adds)
+            // this half tile's rows per cluster: the words of round r - 2, read
+            // by both sums waves before they read any block of round r - 1
+            // (waited on above), are cleared, then the bits set (an OR: any
+            // order gives the same mask)
+            unsigned* const mw = sMask[r & 1][e];
+            mw[lane] = 0u;
+            if (valid) atomicOr(&mw[bi], 1u << lane);
             set_flag(&sReady[e], r + 1);
         }
         if (lane == 0 && changed != 0) atomicAdd(a.changed, changed);
         __syncthreads();  // every sums wave is done: the tile area is free
         __syncthreads();  // the sums are in LDS
     } else {
-        // the E-step waves wait on the sums wave's progress before rewriting
-        // their tile: issue priority for the sums wave
+        // the E-step waves wait on the sums waves' progress before rewriting
+        // their tile: issue priority for the sums waves
         __builtin_amdgcn_s_setprio(2);
-        // sums waves 8..11: the halt test, then the centres' three parts
-        // (rows >= k and columns >= ld zero) and ||c||^2
+        // sums waves 8..15: the halt test, then the centre fragments (centres
+        // >= k and features >= ld zero) and ||c||^2
         const int prev = st->done;
         if (prev != 0) {
             if (tid == 512) sDone = prev;
             __syncthreads();
             return;
         }
-        const int wt = tid - 512;
-        constexpr int CQ = KP / 4;
-        constexpr int NF = (CPC * CQ + 255) / 256;
-        float4 cf[NF];
+        const int wt = tid - 512;  // 0 .. 511
+        {
+            // fragments (cb, s, 0..2): lane l = 16h + r of each holds the parts
+            // of centre 16cb + r, features 32s + 8h .. 32s + 8h + 7
+            constexpr int NE = CB * NK * 64;
+            constexpr int NU = (NE + 511) / 512;
+            float4 cf[NU][2];
 #pragma unroll
-        for (int u = 0; u < NF; ++u) {
-            const int idx = wt + 256 * u;
-            const int cl = idx / CQ;
-            const int q = idx - cl * CQ;
-            cf[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (idx < CPC * CQ && cl < k && 4 * q < LDX)
-                cf[u] = *reinterpret_cast<const float4*>(C + (long)cl * ld + 4 * q);
+            for (int u = 0; u < NU; ++u) {
+                const int idx = wt + 512 * u;
+                const int l = idx & 63, cs = idx >> 6;  // cs = cb * NK + s
+                const int cb = cs / NK, s = cs - cb * NK;
+                const int cl = 16 * cb + (l & 15);
+                cf[u][0] = cf[u][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (idx < NE && cl < k) {
+                    const float* p = C + (long)cl * ld + 32 * s + 8 * (l >> 4);
+                    cf[u][0] = *reinterpret_cast<const float4*>(p);
+                    cf[u][1] = *reinterpret_cast<const float4*>(p + 4);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < NU; ++u) {
+                const int idx = wt + 512 * u;
+                if (idx < NE) {
+                    const int l = idx & 63, cs = idx >> 6;
+                    const Parts8 p = split8(cf[u][0], cf[u][1]);
+                    sFr[64 * (3 * cs) + l] = p.h;
+                    sFr[64 * (3 * cs + 1) + l] = p.m;
+                    sFr[64 * (3 * cs + 2) + l] = p.l;
+                }
+            }
         }
+        if constexpr (TAIL > 0) {
+            // tail fragments (cb, q): lane l = 16h + r holds values 32q + 8h ..
+            // of centre 16cb + r's tail row (blocks of TAIL values: parts (h, m,
+            // l, h, m, h) of its features 32NK .., zeros after them)
+            if (wt < CB * 64) {
+                const int l = wt & 63, cb = wt >> 6, hh = l >> 4;
+                const int cl = 16 * cb + (l & 15);
+                if constexpr (TAIL == 4) {
+                    float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (cl < k) c = *reinterpret_cast<const float4*>(C + (long)cl * ld + 32 * NK);
+                    const Parts4 p = split4(c);
+                    const v4s z4 = v4s{0, 0, 0, 0};
+                    // blocks 2hh, 2hh + 1
+                    const v4s q0 = hh < 3 ? part_of(p, tail_cpart(2 * hh)) : z4;
+                    const v4s q1 = hh < 3 ? part_of(p, tail_cpart(2 * hh + 1)) : z4;
+                    sFr[64 * (FT + cb) + l] = cat8(q0, q1);
+                } else {
+                    float4 c0 = make_float4(0.f, 0.f, 0.f, 0.f), c1 = c0;
+                    if (cl < k) {
+                        const float* p = C + (long)cl * ld + 32 * NK + 8 * (hh & 1);
+                        c0 = *reinterpret_cast<const float4*>(p);
+                        c1 = *reinterpret_cast<const float4*>(p + 4);
+                    }
+                    const Parts8 p = split8(c0, c1);
 #pragma unroll
-        for (int u = 0; u < NF; ++u) {
-            const int idx = wt + 256 * u;
-            const int cl = idx / CQ;
-            const int q = idx - cl * CQ;
-            if (idx < CPC * CQ) {
-                const Parts4 p = split4(cf[u]);
-                __bf16* dst = sCP + cl * CSTR + 4 * q;
-                *reinterpret_cast<v4s*>(dst) = p.h;
-                *reinterpret_cast<v4s*>(dst + CPART) = p.m;
-                *reinterpret_cast<v4s*>(dst + 2 * CPART) = p.l;
+                    for (int q = 0; q < 3; ++q) sFr[64 * (FT + cb * NT + q) + l] = part_of(p, tail_cpart(2 * q + (hh >> 1)));
+                }
+            }
+        }
+        if constexpr (STK) {
+            // stacked fragments: lane l = 16h + 4 slot + p holds part p of centre
+            // 16(CB-1) + slot (p = 3: zero): K steps s, then the tail
+            if (wt < 64 * NK) {
+                const int l = wt & 63, s = wt >> 6;
+                const int p = l & 3, cl = 16 * (CB - 1) + ((l & 15) >> 2);
+                float4 c0 = make_float4(0.f, 0.f, 0.f, 0.f), c1 = c0;
+                if (p < 3 && cl < k) {
+                    const float* q = C + (long)cl * ld + 32 * s + 8 * (l >> 4);
+                    c0 = *reinterpret_cast<const float4*>(q);
+                    c1 = *reinterpret_cast<const float4*>(q + 4);
+                }
+                sFr[64 * (FS + s) + l] = part_of(split8(c0, c1), p < 3 ? p : 0);
+            }
+            if constexpr (TAIL > 0) {
+                if (wt >= 64 * NK && wt < 64 * NK + 64) {
+                    const int l = wt - 64 * NK, hh = l >> 4;
+                    const int p = l & 3, cl = 16 * (CB - 1) + ((l & 15) >> 2);
+                    const v4s z4 = v4s{0, 0, 0, 0};
+                    if constexpr (TAIL == 4) {
+                        float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
+                        if (p < 3 && cl < k) c = *reinterpret_cast<const float4*>(C + (long)cl * ld + 32 * NK);
+                        const v4s cp = part_of(split4(c), p < 3 ? p : 0);
+                        // blocks 2hh, 2hh + 1 of (c_p, c_p, c_p, 0, ...)
+                        sFr[64 * (FS + NK) + l] = cat8(hh < 2 ? cp : z4, hh == 0 ? cp : z4);
+                    } else {
+                        float4 c0 = make_float4(0.f, 0.f, 0.f, 0.f), c1 = c0;
+                        if (p < 3 && cl < k) {
+                            const float* q = C + (long)cl * ld + 32 * NK + 8 * (hh & 1);
+                            c0 = *reinterpret_cast<const float4*>(q);
+                            c1 = *reinterpret_cast<const float4*>(q + 4);
+                        }
+                        const v8bf cp = part_of(split8(c0, c1), p < 3 ? p : 0);
+                        sFr[64 * (FS + NK) + l] = cp;
+                        sFr[64 * (FS + NK + 1) + l] = hh < 2 ? cp : cat8(z4, z4);
+                    }
+                }
             }
         }
         if (wt < 8) {
             sReady[wt] = 0;
             sProg[wt] = 0;
         }
-        sCnt[wt >> 6][wt & 63] = 0;
-        sMask[wt >> 6][wt & 63] = 0u;
-        sMask[4 + (wt >> 6)][wt & 63] = 0u;
-        {
+        if (wt < 256) {
+            sCnt[wt >> 6][wt & 63] = 0;
             unsigned w[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 w[j] = ((wt >> (2 * j)) & 1 ? 0x3f80u : 0u) | ((wt >> (2 * j + 1)) & 1 ? 0x3f800000u : 0u);
             sOneHot[wt] = __builtin_bit_cast(v8bf, v4u{w[0], w[1], w[2], w[3]});
         }
+        (&sMask[0][0][0])[wt] = 0u;
+        (&sMask[0][0][0])[512 + wt] = 0u;
         if (wave == 8) step_norms<CPC>(a, lane, sN, &sDone);
         __syncthreads();
         if (sDone != 0) return;
-        // the sums wave of SIMD m serves E-step waves m and m + 4
-        const int m = wave - 8;
-        v4f S[CB][NFB];
-        msum_tiles3<CB, NQ, XS, NFB>(S, rounds_of(m), rounds_of(m + 4), &sReady[m], &sReady[m + 4], &sProg[m],
-                                     &sProg[m + 4], sMask[m], sMask[m + 4], sOneHot, tiles + m * TS,
-                                     tiles + (m + 4) * TS, lane);
-        __syncthreads();  // every wave is done with its tile
-        publish_msums<CB, NFB>(S, tiles, ld, m, lane);
+        // sums wave 8 + w: SIMD m = w & 3, feature blocks [0, NFA) (w < 4) or
+        // [NFA, NFB) of its tiles
+        const int w = wave - 8, m = w & 3;
+        const int rounds = rounds_of(m);
+        const char* const tile = tiles + m * TILEB;
+        // transposed reads: lane 16h + 4q + jr supplies the address of row 8h
+        // + jr (+ 4 for the second read), features 4q .. 4q + 3 of a block, and
+        // receives rows 8h .. 8h + 3 (+ 4) of feature 4(l%16/4) + l%4 = l%16
+        const int q4 = r16 & 3, jr = r16 >> 2;
+        const char* const src = tile + (8 * h + jr) * RSB + 8 * q4;
+        // TAIL = 4, the last block: column n = 4p + f is part p of feature
+        // 32NK + f (p = 3: part 0 again, never published)
+        const char* const srct = tile + (8 * h + jr) * RSB + (q4 < 3 ? q4 : 0) * 2 * KP + 64 * NK;
+        auto sums = [&](auto fb0c, auto nfc) {
+            constexpr int FB0 = decltype(fb0c)::value, NF = decltype(nfc)::value;
+            v4f S[CB][NF];
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+                for (int j = 0; j < NF; ++j) S[cb][j] = v4f{0.f, 0.f, 0.f, 0.f};
+            }
+            for (int r = 0; r < rounds; ++r) {
+                wait_flag(&sReady[m], r + 1);
+                wait_flag(&sReady[m + 4], r + 1);
+                // A[cb][j] = 1 when row 8h + j has label 16 cb + r16: byte h of
+                // that cluster's row mask (rows 0..15 from E-step wave m, 16..31
+                // from wave m + 4), through the one-hot table
+                v8bf A[CB];
+                {
+                    const unsigned* mw = sMask[r & 1][h < 2 ? m : m + 4];
+                    const int sft = 8 * (h & 1);
+                    unsigned mv[CB];
+#pragma unroll
+                    for (int cb = 0; cb < CB; ++cb) mv[cb] = mw[16 * cb + r16];
+#pragma unroll
+                    for (int cb = 0; cb < CB; ++cb) A[cb] = sOneHot[(mv[cb] >> sft) & 0xffu];
+                }
+                // the B operands of block j + 1 are read before block j's MFMAs
+                auto read_block = [&](int j, v8bf (&b)[3]) {
+                    const int fb = FB0 + j;
+                    if (TAIL == 4 && fb == NFB - 1) {
+                        b[0] = cat8(lds_tr16(srct), lds_tr16(srct + 4 * RSB));
+                    } else {
+#pragma unroll
+                        for (int p = 0; p < 3; ++p) {
+                            const char* s0 = src + p * 2 * KP + 32 * fb;
+                            b[p] = cat8(lds_tr16(s0), lds_tr16(s0 + 4 * RSB));
+                        }
+                    }
+                    // feature block fb of the tile has been read
+                    set_flag(&sProg[w], r * NF + j + 1);
+                };
+                v8bf bc[3], bn[3];
+                read_block(0, bc);
+#pragma unroll
+                for (int j = 0; j < NF; ++j) {
+                    if (j + 1 < NF) read_block(j + 1, bn);
+                    if (TAIL == 4 && FB0 + j == NFB - 1) {
+#pragma unroll
+                        for (int cb = 0; cb < CB; ++cb) S[cb][j] = mfma_bf16(A[cb], bc[0], S[cb][j]);
+                    } else {
+                        // lo, mid, hi; consecutive MFMAs write different accumulators
+#pragma unroll
+                        for (int p = 2; p >= 0; --p) {
+#pragma unroll
+                            for (int cb = 0; cb < CB; ++cb) S[cb][j] = mfma_bf16(A[cb], bc[p], S[cb][j]);
+                        }
+                    }
+#pragma unroll
+                    for (int p = 0; p < 3; ++p) bc[p] = bn[p];
+                }
+            }
+            __syncthreads();  // every wave is done with its tile
+            // the sums into red = [4][CPC][ld] (D lane l: clusters 16cb +
+            // 4(l/16) + i, column l%16 of block fb)
+            float* const red = lds;
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+                for (int j = 0; j < NF; ++j) {
+                    const int fb = FB0 + j;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int row = (m * CPC + 16 * cb + 4 * h + i) * ld;
+                        const float v = S[cb][j][i];
+                        if (TAIL == 4 && fb == NFB - 1) {
+                            // columns f, 4 + f, 8 + f: parts h, m, l of feature 32NK + f
+                            const float vm = __shfl_down(v, 4, 16);
+                            const float vl = __shfl_down(v, 8, 16);
+                            if (r16 < 4) red[row + 32 * NK + r16] = (vl + vm) + v;
+                        } else {
+                            const int f = 16 * fb + r16;
+                            if (f < ld) red[row + f] = v;
+                        }
+                    }
+                }
+            }
+        };
+        if (w < 4)
+            sums(std::integral_constant<int, 0>{}, std::integral_constant<int, NFA>{});
+        else
+            sums(std::integral_constant<int, NFA>{}, std::integral_constant<int, NFZ>{});
         __syncthreads();
     }
-    combine_sums<CPC, 768>(tiles, ld, k, a.psum, a.pcnt, sCnt, tid);
+    combine_sums<CPC, 1024>(lds, ld, k, a.psum, a.pcnt, sCnt, tid);
 }
 
 // ---------------------------------------------------------------------------
@@ -720,31 +898,29 @@ typedef void (*fused_fn)(FusedArgs);
 
 template <int NQ, int... CBs>
 struct Fused3Table {
-    static fused_fn get(int cb)
+    static fused_fn get(int cb, bool stk)
     {
         fused_fn f = nullptr;
-        ((cb == CBs ? (f = &k_fused3<CBs, NQ>, 0) : 0), ...);
+        ((cb == CBs ? (f = stk ? &k_fused3<CBs, NQ, true> : &k_fused3<CBs, NQ, false>, 0) : 0), ...);
         return f;
     }
-    static size_t dyn_lds(int cb)
-    {
-        using G = Fused3Geom<NQ>;
-        return (size_t)8 * G::TS * sizeof(float) + (size_t)3 * 16 * cb * G::CSTR * sizeof(__bf16);
-    }
+    static size_t dyn_lds(int cb) { return Fused3Geom<NQ>::lds(cb); }
 };
 
 // The split kernel for row strides of 32 floats and more (below that the K
-// steps would be mostly padding).
+// steps would be mostly padding).  The last 16-centre block is stacked when
+// it holds at most 4 centres.
 static fused_fn fused3_kernel(int k, int ld, size_t* dyn)
 {
     if (k < 1 || k > 64) return nullptr;
     const int cb = (k + 15) / 16;
+    const bool stk = k - 16 * (cb - 1) <= 4;
     switch (ld) {
-    case 32: *dyn = Fused3Table<8, 1, 2, 3, 4>::dyn_lds(cb); return Fused3Table<8, 1, 2, 3, 4>::get(cb);
-    case 48: *dyn = Fused3Table<12, 1, 2, 3, 4>::dyn_lds(cb); return Fused3Table<12, 1, 2, 3, 4>::get(cb);
-    case 64: *dyn = Fused3Table<16, 1, 2, 3, 4>::dyn_lds(cb); return Fused3Table<16, 1, 2, 3, 4>::get(cb);
-    case 80: *dyn = Fused3Table<20, 1, 2, 3, 4>::dyn_lds(cb); return Fused3Table<20, 1, 2, 3, 4>::get(cb);
-    case 100: *dyn = Fused3Table<25, 1, 2, 3, 4>::dyn_lds(cb); return Fused3Table<25, 1, 2, 3, 4>::get(cb);
+    case 32: *dyn = Fused3Table<8, 1, 2, 3, 4>::dyn_lds(cb); return Fused3Table<8, 1, 2, 3, 4>::get(cb, stk);
+    case 48: *dyn = Fused3Table<12, 1, 2, 3, 4>::dyn_lds(cb); return Fused3Table<12, 1, 2, 3, 4>::get(cb, stk);
+    case 64: *dyn = Fused3Table<16, 1, 2, 3, 4>::dyn_lds(cb); return Fused3Table<16, 1, 2, 3, 4>::get(cb, stk);
+    case 80: *dyn = Fused3Table<20, 1, 2, 3, 4>::dyn_lds(cb); return Fused3Table<20, 1, 2, 3, 4>::get(cb, stk);
+    case 100: *dyn = Fused3Table<25, 1, 2, 3, 4>::dyn_lds(cb); return Fused3Table<25, 1, 2, 3, 4>::get(cb, stk);
     default: return nullptr;
     }
 }
@@ -755,7 +931,7 @@ int fused3_ready(int k, int ld)
     size_t dyn = 0;
     fused_fn f = fused3_kernel(k, ld, &dyn);
     // sMask, sOneHot, sCnt, sN, flags
-    const size_t stat = 8 * 64 * sizeof(unsigned) + 256 * 16 + 4 * 64 * sizeof(int) + 64 * sizeof(float) + 128;
+    const size_t stat = 2 * 8 * 64 * sizeof(unsigned) + 256 * 16 + 4 * 64 * sizeof(int) + 64 * sizeof(float) + 80;
     if (f == nullptr || dyn + stat > 160 * 1024) return 0;
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(f), hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) !=
         hipSuccess) {
@@ -770,7 +946,7 @@ hipError_t launch_fused3(const FusedArgs& a, hipStream_t s)
     size_t dyn = 0;
     fused_fn f = fused3_kernel(a.k, a.ld, &dyn);
     if (f == nullptr || a.blocks < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(f, dim3(a.blocks), dim3(768), dyn, s, a);
+    hipLaunchKernelGGL(f, dim3(a.blocks), dim3(1024), dyn, s, a);
     return hipGetLastError();
 }
 
