@@ -81,7 +81,8 @@ __device__ __forceinline__ void step_norms(const FusedArgs& a, int lane, float* 
         for (int off = 1; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
         const int chg = *a.prev_changed;
         int done = 0;
-        if (n_empty > 0)
+        // (empty clusters k_reloc has already relocated do not stop the loop)
+        if (n_empty > 0 && a.state->reloc_iter != a.iter - 1)
             done = 3;
         else if ((a.flags & kStopStrict) && chg == 0)
             done = 1;

@@ -25,8 +25,10 @@ struct LoopState {
     int last_changed;  // changes of the last decided iteration
     int halt_iter;     // iteration index at which `done` was set
     int n_empty;       // empty clusters found by the last finalise
-    unsigned rowdist_ctr; // row-distance reduction: blocks completed
-    unsigned pad_;
+    unsigned reloc_ctr;  // k_reloc: blocks done with their rows (the last resets it)
+    int empty_iter;      // last iteration whose k_finalize_cols met an empty cluster (-1: none)
+    int reloc_iter;      // iteration whose empty clusters k_reloc relocated (-1: none)
+    int pad_;
     double shift_tot;  // sum_j ||c_j_new - c_j_old||^2 of the last step
     double inertia;    // result of the last row-distance reduction
 };
@@ -183,7 +185,7 @@ struct RowDistArgs {
     const float* C; int k; const int* labels;  // rows with a label outside [0, k) count 0
     float* out_rows;       // nullable: per-row squared distance
     double* block_part;    // [grid]
-    LoopState* state;      // holds rowdist_ctr and receives `inertia`
+    LoopState* state;      // receives `inertia`
 };
 int rowdist_grid(long n);
 // Row distances and their fixed-order total (two launches).
@@ -208,6 +210,29 @@ struct RelocArgs {
 };
 // E = number of empty clusters (1 <= E <= kMaxReloc).
 hipError_t launch_relocate(const RelocArgs& a, int E, hipStream_t s);
+
+// In-stream relocation (k_reloc, launched after every step's
+// k_finalize_cols): when step `iter` left 1..kMaxReloc clusters empty, the
+// rows farthest from their centres move to them and the centres and chunk
+// partials of the clusters involved are redone, before the step's loop
+// decision; with no empty cluster the kernel returns at once.
+struct InRelocArgs {
+    const float* X; long n; int ld; int d; int k;
+    const int* labels;     // step iter's labels
+    const float* C_old;    // the centres those labels were taken against
+    float* C_new;          // the step's new centres (k_finalize_cols's, rewritten)
+    double* sums;          // [k x ld] the step's fp64 sums (updated in place)
+    int* counts;           // [k] (updated in place)
+    double* part;          // [k x nch x 2] the finalize's chunk partials (rewritten)
+    int nch;               // chunks of finalize_cols(.) columns
+    float* dist;           // [n] scratch: row distances
+    float* cand_d;         // [kRelocInlineBlocks x kMaxReloc]
+    long* cand_i;          // [kRelocInlineBlocks x kMaxReloc]
+    int* amax;             // [1]
+    LoopState* state; int iter;
+};
+constexpr int kRelocInlineBlocks = 256;  // grid of k_reloc
+hipError_t launch_reloc_inline(const InRelocArgs& a, hipStream_t s);
 
 // Greedy k-means++ seeding (plusplus_kernels.hip): sklearn's _kmeans_plusplus
 // with unit weights and the random draws made by the caller.

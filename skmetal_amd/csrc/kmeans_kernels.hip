@@ -764,6 +764,7 @@ __global__ __launch_bounds__(256) void k_finalize_cols(FinalizeArgs a)
         a.part[((long)j * nch + cc) * 2 + 0] = sq;
         a.part[((long)j * nch + cc) * 2 + 1] = nrm;
         if (cc == 0) a.counts[j] = count;
+        if (cc == 0 && count == 0) a.state->empty_iter = a.iter;  // for k_reloc
         if (j == 0 && cc == 0 && a.chg_next != nullptr) *a.chg_next = 0;
     }
 }
@@ -802,7 +803,7 @@ __global__ __launch_bounds__(256) void k_finalize_loop(FinalizeArgs a, int nch)
         st->last_changed = changed;
         st->n_iter = a.iter + 1;
         int done = 0;
-        if (n_empty > 0 && !a.after_reloc)
+        if (n_empty > 0 && !a.after_reloc && st->reloc_iter != a.iter)
             done = 3;
         else if ((a.flags & kStopStrict) && changed == 0)
             done = 1;
@@ -834,37 +835,82 @@ hipError_t launch_finalize_loop(const FinalizeArgs& a, hipStream_t s, int nch)
 //
 // Per row in fp32, in the association order of sklearn's
 // _euclidean_dense_dense (_k_means_common.pyx:16-43): groups of four squared
-// differences summed left to right, each group added to the running sum.
+// differences summed left to right, each group added to the running sum, the
+// remainder one by one.  A wave takes 64 consecutive rows at a time; their
+// features come in slabs of 64 columns, loaded coalesced (16 lanes per
+// 256-byte piece of a row) into the wave's LDS tile, and lane l carries row
+// l's running sum from slab to slab.
 
-__global__ __launch_bounds__(256) void k_rowdist(RowDistArgs a)
+constexpr int kRowSlab = 64;                  // columns per slab
+constexpr int kRowTileStride = kRowSlab + 1;  // floats per tile row: lane l's column reads fall on distinct banks
+constexpr int kRowTileFloats = 64 * kRowTileStride;
+
+// Squared distance of row row0 + lane (ok: the row exists and has label lab
+// in [0, k)); rows row0 .. row0 + nrows - 1 exist.  tile: this wave's LDS tile.
+__device__ float wave_row_dist(const float* __restrict__ X, int ld, int d, const float* __restrict__ C, long row0,
+                               int nrows, int lab, bool ok, float* tile)
 {
 #pragma clang fp contract(off)
-    const long row = (long)blockIdx.x * 256 + threadIdx.x;
-    double v = 0.0;
+    const int lane = threadIdx.x & 63;
+    const float* c = C + (long)(ok ? lab : 0) * ld;
+    float res = 0.f;
+    for (int f0 = 0; f0 < d; f0 += kRowSlab) {
+        const int w = min(kRowSlab, d - f0);
+        // float4 q = 64 i + lane: row q / 16, columns f0 + 4 (q % 16) ..
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int q = 64 * i + lane;
+            const int r = q >> 4, c4 = 4 * (q & 15);
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (r < nrows && c4 < w) v = *reinterpret_cast<const float4*>(X + (row0 + r) * ld + f0 + c4);
+            float* t = tile + r * kRowTileStride + c4;
+            t[0] = v.x;
+            t[1] = v.y;
+            t[2] = v.z;
+            t[3] = v.w;
+        }
+        // (a wave's LDS accesses complete in order: the tile is written
+        // before any lane reads it)
+        __builtin_amdgcn_wave_barrier();
+        if (ok) {
+            const float* t = tile + lane * kRowTileStride;
+            int f = 0;
+            for (; f + 4 <= w; f += 4) {
+                const float4 cv = *reinterpret_cast<const float4*>(c + f0 + f);
+                const float t0 = t[f] - cv.x, t1 = t[f + 1] - cv.y, t2 = t[f + 2] - cv.z, t3 = t[f + 3] - cv.w;
+                res += ((t0 * t0 + t1 * t1) + t2 * t2) + t3 * t3;
+            }
+            for (; f < w; ++f) {
+                const float tt = t[f] - c[f0 + f];
+                res += tt * tt;
+            }
+        }
+        __builtin_amdgcn_wave_barrier();  // every lane is done with the tile
+    }
+    return res;
+}
+
+// Block b: rows 256 b .. 256 b + 255, wave w the 64 from 256 b + 64 w.
+__global__ __launch_bounds__(256) void k_rowdist(RowDistArgs a)
+{
+    __shared__ float tiles[4 * kRowTileFloats];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const long row0 = (long)blockIdx.x * 256 + 64 * w;
+    const long row = row0 + lane;
+    const int nrows = (int)max(0L, min(64L, a.n - row0));
     const int lab = row < a.n ? a.labels[row] : -1;
-    if (lab >= 0 && lab < a.k) {
-        const float* x = a.X + row * a.ld;
-        const float* c = a.C + (long)lab * a.ld;
-        float res = 0.f;
-        int f = 0;
-        for (; f + 4 <= a.d; f += 4) {
-            const float4 xv = *reinterpret_cast<const float4*>(x + f);
-            const float4 cv = *reinterpret_cast<const float4*>(c + f);
-            const float t0 = xv.x - cv.x, t1 = xv.y - cv.y, t2 = xv.z - cv.z, t3 = xv.w - cv.w;
-            res += ((t0 * t0 + t1 * t1) + t2 * t2) + t3 * t3;
-        }
-        for (; f < a.d; ++f) {
-            const float t = x[f] - c[f];
-            res += t * t;
-        }
+    const bool ok = lab >= 0 && lab < a.k;
+    const float res = wave_row_dist(a.X, a.ld, a.d, a.C, row0, nrows, lab, ok, tiles + w * kRowTileFloats);
+    double v = 0.0;
+    if (ok) {
         if (a.out_rows != nullptr) a.out_rows[row] = res;
         v = (double)res;
     }
     __shared__ double red[256];
     red[threadIdx.x] = v;
     __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    for (int s2 = 128; s2 > 0; s2 >>= 1) {
+        if (threadIdx.x < s2) red[threadIdx.x] += red[threadIdx.x + s2];
         __syncthreads();
     }
     if (threadIdx.x == 0) a.block_part[blockIdx.x] = red[0];
@@ -1077,6 +1123,192 @@ hipError_t launch_relocate(const RelocArgs& a, int E, hipStream_t s)
     hipLaunchKernelGGL(k_far_select, dim3(nb), dim3(256), 0, s, a, E, rpb);
     hipLaunchKernelGGL(k_far_apply, dim3(1), dim3(256), 0, s, a, E, nb);
     hipLaunchKernelGGL(k_finalize_sums, dim3(a.k, (a.d + kRelocCW - 1) / kRelocCW), dim3(256), 0, s, a, kRelocCW);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// in-stream relocation: k_reloc
+// ---------------------------------------------------------------------------
+//
+// Launched after every step's k_finalize_cols, which records in
+// state->empty_iter the step of any cluster it found empty; for any other
+// step the kernel returns at its first load.  Otherwise, as the device path
+// above but in one kernel: (A) each block takes the distances of its
+// contiguous share of the rows and its E farthest, in order, and counts
+// itself done; (B) the last block to finish merges the candidates, moves the
+// rows in the fp64 sums and counts, and (C) redoes the centres and chunk
+// partials (the finalize's 32-column chunks) of the clusters involved -- the
+// empty ones, those that gave a row, and any still empty -- as
+// k_finalize_sums does; every other cluster keeps what k_finalize_cols
+// wrote.  state->reloc_iter = iter then tells the loop decision that this
+// step's empty clusters were handled.  No block waits for another.
+
+__global__ __launch_bounds__(256) void k_reloc(InRelocArgs a)
+{
+    __shared__ float tiles[4 * kRowTileFloats];
+    __shared__ float sd[256];
+    __shared__ long si[256];
+    __shared__ int shi[4];
+    __shared__ double shd[2][4];
+    __shared__ int last_s;
+    LoopState* st = a.state;
+    const int tid = threadIdx.x;
+    if (st->empty_iter != a.iter || st->done != 0) return;
+    int ne = 0;
+    for (int j = tid; j < a.k; j += 256) ne += a.counts[j] == 0;
+    const int E = block_sum(ne, shi);
+    if (E == 0 || E > kMaxReloc) return;
+
+    // (A) distances of rows [r0, r1), then this block's E farthest, in order
+    const long rpb = (a.n + gridDim.x - 1) / gridDim.x;
+    const long r0 = min(a.n, (long)blockIdx.x * rpb), r1 = min(a.n, r0 + rpb);
+    {
+        const int lane = tid & 63, w = tid >> 6;
+        for (long c0 = r0 + 64L * w; c0 < r1; c0 += 256) {
+            const long row = c0 + lane;
+            const int nrows = (int)min(64L, r1 - c0);
+            const int lab = row < r1 ? a.labels[row] : -1;
+            const bool ok = lab >= 0 && lab < a.k;
+            const float res = wave_row_dist(a.X, a.ld, a.d, a.C_old, c0, nrows, lab, ok, tiles + w * kRowTileFloats);
+            if (row < r1) a.dist[row] = ok ? res : 0.f;
+        }
+    }
+    __threadfence_block();
+    __syncthreads();
+    {
+        float dl = INFINITY;
+        long il = -1;
+        for (int e = 0; e < E; ++e) {
+            float bd = 0.f;
+            long bi = -1;
+            for (long r = r0 + tid; r < r1; r += 256) far_pick(bd, bi, a.dist[r], r, dl, il);
+            far_block_reduce(bd, bi, sd, si);
+            if (tid == 0) {
+                a.cand_d[(long)blockIdx.x * kMaxReloc + e] = bd;
+                a.cand_i[(long)blockIdx.x * kMaxReloc + e] = bi;
+            }
+            dl = bd;
+            il = bi;
+        }
+    }
+    // the last block to get here takes (B) and (C)
+    __syncthreads();
+    if (tid == 0) {
+        __threadfence();  // the candidates, to the device
+        last_s = atomicAdd(&st->reloc_ctr, 1u) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last_s) return;
+    if (tid == 0) st->reloc_ctr = 0u;
+    __threadfence();  // every block's candidates
+
+    // (B) the E farthest overall, moved to the empty clusters in ascending order
+    __shared__ long far[kMaxReloc];
+    __shared__ int empt[kMaxReloc];
+    __shared__ int donor[kMaxReloc];
+    __shared__ int ne_s;
+    if (tid == 0) {
+        int q = 0;
+        for (int j = 0; j < a.k && q < E; ++j)
+            if (a.counts[j] == 0) empt[q++] = j;
+        ne_s = q;
+    }
+    {
+        float dl = INFINITY;
+        long il = -1;
+        for (int e = 0; e < E; ++e) {
+            float bd = 0.f;
+            long bi = -1;
+            for (int c = tid; c < (int)gridDim.x * E; c += 256) {
+                const int b = c / E, ee = c - b * E;
+                const long i = a.cand_i[(long)b * kMaxReloc + ee];
+                if (i >= 0) far_pick(bd, bi, a.cand_d[(long)b * kMaxReloc + ee], i, dl, il);
+            }
+            far_block_reduce(bd, bi, sd, si);
+            if (tid == 0) far[e] = bi;
+            dl = bd;
+            il = bi;
+            // the farthest distance decides whether anything moves (all zero: no)
+            if (e == 0 && tid == 0 && (bi < 0 || bd <= 0.f)) ne_s = 0;
+        }
+    }
+    __syncthreads();
+    const int nm = ne_s;
+    for (int e = 0; e < nm; ++e) {
+        const long fr = far[e];
+        const int j = empt[e];
+        const int o = a.labels[fr];
+        const float* x = a.X + fr * a.ld;
+        for (int c = tid; c < a.d; c += 256) {
+            a.sums[(long)o * a.ld + c] -= (double)x[c];
+            a.sums[(long)j * a.ld + c] = (double)x[c];
+        }
+        __threadfence_block();
+        __syncthreads();
+        if (tid == 0) {
+            a.counts[j] = 1;
+            a.counts[o] -= 1;
+            donor[e] = o;
+        }
+        __threadfence_block();
+        __syncthreads();
+    }
+    __shared__ int amax_s;
+    if (tid == 0) {
+        int am = 0;
+        for (int j = 1; j < a.k; ++j)
+            if (a.counts[j] > a.counts[am]) am = j;
+        amax_s = am;
+    }
+    __syncthreads();
+    const int amax = amax_s;
+
+    // (C) centres and chunk partials of the clusters involved: list entry q
+    // < nm the filled cluster, nm <= q < 2 nm the donor, then every cluster
+    // still empty (repeats are harmless: the same values are written)
+    constexpr int CW = 32;
+    for (int j0 = 0; j0 < 2 * nm + a.k; ++j0) {
+        int j;
+        if (j0 < nm) {
+            j = empt[j0];
+        } else if (j0 < 2 * nm) {
+            j = donor[j0 - nm];
+        } else {
+            j = j0 - 2 * nm;
+            if (a.counts[j] != 0) continue;  // (uniform across the block)
+        }
+        const int cnt = a.counts[j];
+        for (int cc = 0; cc < a.nch; ++cc) {
+            const int col = cc * CW + tid;
+            double sq = 0.0, nrm = 0.0;
+            if (tid < CW && col < a.d) {
+                double v;
+                if (cnt > 0) {
+                    v = a.sums[(long)j * a.ld + col] / (double)cnt;
+                } else {
+                    const double sa = a.sums[(long)amax * a.ld + col];
+                    v = amax < j ? sa / (double)a.counts[amax] : sa;
+                }
+                const float cn = (float)v;
+                a.C_new[(long)j * a.ld + col] = cn;
+                const double df = (double)cn - (double)a.C_old[(long)j * a.ld + col];
+                sq = df * df;
+                nrm = (double)cn * (double)cn;
+            }
+            sq = block_sum(sq, shd[0]);
+            nrm = block_sum(nrm, shd[1]);
+            if (tid == 0) {
+                a.part[((long)j * a.nch + cc) * 2 + 0] = sq;
+                a.part[((long)j * a.nch + cc) * 2 + 1] = nrm;
+            }
+        }
+    }
+    if (tid == 0) st->reloc_iter = a.iter;
+}
+
+hipError_t launch_reloc_inline(const InRelocArgs& a, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_reloc, dim3(kRelocInlineBlocks), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -449,6 +449,7 @@ struct Lloyd {
         TRY(grab((void**)&r_cand_d, size_t(kRelocBlocks) * kMaxReloc * sizeof(float)));
         TRY(grab((void**)&r_cand_i, size_t(kRelocBlocks) * kMaxReloc * sizeof(long)));
         TRY(grab((void**)&r_amax, sizeof(int)));
+        reloc_inline = inline_relocation_on();
         HIP_TRY(hipMemsetAsync(cen[1], 0, kl * sizeof(float), s), "hipMemsetAsync");
         HIP_TRY(hipMemsetAsync(st, 0, sizeof(LoopState), s), "hipMemsetAsync");
         if (f3cap || a3cap) {
@@ -493,6 +494,13 @@ struct Lloyd {
         TRY(grab((void**)&colpart, size_t(colsum_grid(n)) * d * sizeof(double)));
         TRY(grab((void**)&st, sizeof(LoopState)));
         TRY(grab((void**)&absmax, sizeof(unsigned)));
+        reloc_inline = inline_relocation_on();
+        if (reloc_inline) {
+            TRY(grab((void**)&rowout, size_t(n) * sizeof(float)));
+            TRY(grab((void**)&r_cand_d, size_t(kRelocBlocks) * kMaxReloc * sizeof(float)));
+            TRY(grab((void**)&r_cand_i, size_t(kRelocBlocks) * kMaxReloc * sizeof(long)));
+            TRY(grab((void**)&r_amax, sizeof(int)));
+        }
         if (sg.on) {
             TRY(grab((void**)&s_hist, size_t(sg.nw) * k * sizeof(int)));
             TRY(grab((void**)&s_seg, size_t(sg.nseg) * k * sizeof(int)));
@@ -664,7 +672,13 @@ struct Lloyd {
         }
         if (ev) HIP_TRY(hipEventRecord(ev[2], s), "hipEventRecord");
         const FinalizeArgs f = finalize_args(iter, tol, flags);
-        HIP_TRY(launch_finalize(f, s, fblocks == 0 || last), "finalize launch");
+        HIP_TRY(launch_finalize(f, s, false), "finalize launch");
+        if (reloc_inline) {
+            InRelocArgs r{X, n, ld, d, k, labels, cen[cur], cen[cur ^ 1], sums, counts, part,
+                          finalize_col_chunks(d, f.R), rowout, r_cand_d, r_cand_i, r_amax, st, iter};
+            HIP_TRY(launch_reloc_inline(r, s), "relocation launch");
+        }
+        if (fblocks == 0 || last) HIP_TRY(launch_finalize_loop(f, s), "finalize launch");
         if (ev) HIP_TRY(hipEventRecord(ev[3], s), "hipEventRecord");
         cur ^= 1;
         return 0;
@@ -678,6 +692,16 @@ struct Lloyd {
     float* r_cand_d = nullptr;
     long* r_cand_i = nullptr;
     int* r_amax = nullptr;
+    // k_reloc after every step (empty clusters relocated in-stream); off:
+    // the loop halts on an empty cluster and the host starts the relocation
+    // (SKMETAL_HIP_HOST_RELOCATE=1 or SKMETAL_HIP_INLINE_RELOCATE=0)
+    bool reloc_inline = false;
+    bool inline_relocation_on() const
+    {
+        const char* h = getenv("SKMETAL_HIP_HOST_RELOCATE");
+        const char* i = getenv("SKMETAL_HIP_INLINE_RELOCATE");
+        return !((h != nullptr && h[0] == '1') || (i != nullptr && i[0] == '0'));
+    }
     int device_relocate(int t, int old, double tol, int flags, LoopState& hs)
     {
         if (rowout == nullptr) TRY(grab((void**)&rowout, size_t(n) * sizeof(float)));
@@ -808,13 +832,17 @@ struct Lloyd {
             tol = -1.0;  // no shift rule: sklearn's `shift <= tol` stops at tol = 0 on a zero shift
         }
         LoopState hs{};
+        hs.reloc_iter = -1;
+        hs.empty_iter = -1;
         TRY(write_state(hs));
         HIP_TRY(hipMemsetAsync(labels, 0xff, size_t(n) * sizeof(int), s), "hipMemsetAsync(labels)");
         long it = 0;
         // Steps are enqueued in growing batches and the loop state is read
-        // back after each: a halt (convergence, or an empty cluster that the
-        // host relocates) then skips at most one batch of launches.
-        long batch = fixed ? 8 : 4;
+        // back after each: a halt (convergence, or more empty clusters than
+        // k_reloc takes, which the host relocates) then skips at most one
+        // batch of launches.  A fixed-iteration run has no convergence stop:
+        // with the relocation in-stream it is one batch.
+        long batch = fixed ? (reloc_inline ? max_iter : 8) : 4;
         int final_done = 0;
         while (it < max_iter) {
             const long nb = std::min(batch, max_iter - it);

@@ -403,29 +403,54 @@ def test_empty_cluster_relocation_matches_oracle(bridge):
     parity.check_centers(C, out["centers"], what="relocation fit")
 
 
-@pytest.mark.parametrize("n_dup", [1, 4, 9])
-def test_relocation_of_several_empty_clusters(bridge, n_dup, monkeypatch):
-    """Duplicated initial centres leave n_dup clusters empty after the first
-    E-step (lowest index wins ties); the device relocation must follow the
-    oracle's (sklearn's) rule, and agree with the host relocation path."""
-    rng = np.random.default_rng(40 + n_dup)
-    cen = rng.uniform(-8, 8, (6, 8))
-    X = (cen[rng.integers(0, 6, 6000)] + rng.standard_normal((6000, 8))).astype(np.float32)
-    base = X[np.sort(rng.choice(6000, 12, replace=False))]
-    C0 = np.concatenate([base, base[:n_dup]])  # the copies come later: they get no rows
-    out = oracle.lloyd(X, C0, 60)
+# the relocation paths: k_reloc after every step (default), the loop's halt
+# with the device kernels started by the host, and the host relocation
+_RELOC_PATHS = {
+    "in-stream": {},
+    "halt+device": {"SKMETAL_HIP_INLINE_RELOCATE": "0"},
+    "host": {"SKMETAL_HIP_HOST_RELOCATE": "1"},
+}
+
+
+def _fit_each_relocation_path(bridge, monkeypatch, X, C0, max_iter):
     res = {}
-    for where in ("device", "host"):
-        if where == "host":
-            monkeypatch.setenv("SKMETAL_HIP_HOST_RELOCATE", "1")
+    for where, env in _RELOC_PATHS.items():
+        for var in ("SKMETAL_HIP_INLINE_RELOCATE", "SKMETAL_HIP_HOST_RELOCATE"):
+            monkeypatch.delenv(var, raising=False)
+        for var, val in env.items():
+            monkeypatch.setenv(var, val)
         C = C0.copy()
         lab = np.empty(X.shape[0], np.int32)
-        res[where] = bridge.kmeans_fit(X, C, lab, 60, 0.0, strict=True) + (C,)
-    monkeypatch.delenv("SKMETAL_HIP_HOST_RELOCATE", raising=False)
+        res[where] = bridge.kmeans_fit(X, C, lab, max_iter, 0.0, strict=True) + (C,)
+    for var in ("SKMETAL_HIP_INLINE_RELOCATE", "SKMETAL_HIP_HOST_RELOCATE"):
+        monkeypatch.delenv(var, raising=False)
+    return res
+
+
+@pytest.mark.parametrize("n_dup", [1, 4, 9])
+@pytest.mark.parametrize("k_base", [12, 72])
+def test_relocation_of_several_empty_clusters(bridge, n_dup, k_base, monkeypatch):
+    """Duplicated initial centres leave n_dup clusters empty after the first
+    E-step (lowest index wins ties); every relocation path must follow the
+    oracle's (sklearn's) rule and agree with the others.  k_base = 12 runs
+    the fused step to convergence; 72 runs the assign + update step for the
+    first 3 steps (the relocation is in the first; with up to 81 centres on 6
+    blobs later steps meet near ties that fp32 rounding may settle either
+    way)."""
+    rng = np.random.default_rng(40 + n_dup + k_base)
+    cen = rng.uniform(-8, 8, (6, 8))
+    X = (cen[rng.integers(0, 6, 6000)] + rng.standard_normal((6000, 8))).astype(np.float32)
+    base = X[np.sort(rng.choice(6000, k_base, replace=False))]
+    C0 = np.concatenate([base, base[:n_dup]])  # the copies come later: they get no rows
+    max_iter = 60 if k_base == 12 else 3
+    out = oracle.lloyd(X, C0, max_iter)
+    res = _fit_each_relocation_path(bridge, monkeypatch, X, C0, max_iter)
     for where, (n_iter, inertia, C) in res.items():
         assert n_iter == out["n_iter"], f"{where}: n_iter {n_iter} vs oracle {out['n_iter']}"
-        parity.check_centers(C, out["centers"], what=f"{where} relocation n_dup={n_dup}")
-    parity.check_centers(res["device"][2], res["host"][2], rtol=1e-5, what="device vs host relocation")
+        parity.check_centers(C, out["centers"], what=f"{where} relocation n_dup={n_dup} k={len(C0)}")
+    for where in ("halt+device", "host"):
+        parity.check_centers(res["in-stream"][2], res[where][2], rtol=1e-5,
+                             what=f"in-stream vs {where} relocation")
 
 
 @pytest.mark.parametrize("wl,steps", [("c1", 4), ("c2", 3)])
