@@ -51,6 +51,31 @@ def _traffic_from_profile(name: str):
     return float(m.group(1)) if m else None
 
 
+MFMA_16x16x32_FLOP = 2 * 16 * 16 * 32
+
+
+def fused3_mfma_per_tile(k: int, d: int):
+    """v_mfma_f32_16x16x32_bf16 instructions of k_fused3 (split_kernels.hip,
+    Fused3Geom and the E-step / sums waves): (per 16-row half tile in the
+    E-step, per 32-row tile in the sums).  ld = d rounded up to 4; NK 32-feature
+    K steps and a tail of 4 or 16 features.  E-step: per 16-centre block six
+    part products per K step (hh, mh, lh, hm, mm, hl) and 1 (tail 4) or 3
+    (tail 16) tail MFMAs; a last block of at most 4 centres is stacked (three
+    MFMAs per K step for all nine products, 1 or 2 tail MFMAs).  Sums: per
+    centre block and 16-feature block, one MFMA per part (the tail-4 block
+    packs its three parts into one)."""
+    ld = -(-d // 4) * 4
+    nk, tail = ld // 32, ld % 32
+    cb = -(-k // 16)
+    nt = {0: 0, 4: 1, 16: 3}[tail]
+    nts = {0: 0, 4: 1, 16: 2}[tail]
+    stacked = k - 16 * (cb - 1) <= 4
+    e16 = (cb - 1) * (6 * nk + nt) + ((3 * nk + nts) if stacked else (6 * nk + nt))
+    nfb = (32 * nk + (16 if tail else 0)) // 16
+    s32 = cb * (3 * (nfb - 1) + 1) if tail == 4 else cb * 3 * nfb
+    return e16, s32
+
+
 def copy_probe(mib: int) -> None:
     """One device-to-device copy of `mib` MiB (hipMemcpy), a known-size kernel the
     rocprofv3 FETCH_SIZE / WRITE_SIZE counters are calibrated against."""
@@ -191,13 +216,11 @@ def main():
     traffic = _traffic_from_profile(f"{kname}_{args.workload}_pmc.txt")
     if split:
         # HBM roofline with the assign bytes per step: X once, the labels
-        # written, the centres read (4nd + 4n + 4kd).  The kernel's MFMA work
-        # over the padded shapes (64 centres, 112 features) is reported beside
-        # it: 6 part products in the E-step, 3 in the sums.
+        # written, the centres read (4nd + 4n + 4kd).  The kernel's MFMA
+        # instructions are reported beside it (fused3_mfma_per_tile).
         nbytes = 4.0 * n * d + 4.0 * n + 4.0 * k * d
-        kp = -(-k // 16) * 16
-        dp = -(-d // 32) * 32 if d % 32 == 0 or d % 32 > 16 else (d // 32) * 32 + 16
-        bf16_flops = (6.0 + 3.0) * 2.0 * n * kp * dp
+        e16, s32 = fused3_mfma_per_tile(k, d)
+        bf16_flops = -(-n // 32) * (2 * e16 + s32) * MFMA_16x16x32_FLOP
         roofline = {
             "kernel": ("k_fused3: E-step (||c||^2 - 2 x.c) + argmin + per-cluster sums, bf16 MFMAs over the exact "
                        "three-part split, fp32 accumulation"),
@@ -212,6 +235,7 @@ def main():
             "fp32_mfma_frac": round(flops / assign_s / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
             "bf16_mfma_tflops": round(bf16_flops / assign_s / 1e12, 1),
             "bf16_mfma_frac": round(bf16_flops / assign_s / 1e12 / PEAK_BF16_MFMA_TFLOPS, 4),
+            "mfma_per_32_rows": {"e_step": 2 * e16, "sums": s32},
         }
     elif asplit:
         # MFMA roofline of the split E-step: six bf16 products per x.c term,
@@ -263,8 +287,9 @@ def main():
         "dist_evals_per_s": round(n * k * it_s, 1),
         "wall_s_timed": round(wall, 4),
         "h2d_s": round(h2d_s, 4),
-        "step_mode": (f"fused: {kname} (E-step + per-cluster sums) + k_finalize" if fused
-                      else f"{kname} + sorted update + k_finalize"),
+        "step_mode": (f"fused: {kname} (E-step + per-cluster sums) + k_finalize_cols + k_reloc (in-stream "
+                      "empty-cluster relocation; returns at once when no cluster is empty)" if fused
+                      else f"{kname} + sorted update + k_finalize_cols + k_reloc"),
         "e_step": ("fp32-equivalent: exact three-part bf16 split of x and c (x = hi + mid + lo), 6 of 9 part "
                    "products on v_mfma_f32_16x16x32_bf16, fp32 accumulation; the 3 left out total <= 2^-23 |x_i c_i|"
                    if (split or (asplit and not fused)) else "fp32 MFMA (v_mfma_f32_4x4x1_16b_f32)"),
@@ -275,9 +300,9 @@ def main():
                            "ms_per_step": round(ms32 / args.steps, 5),
                            "kernel": "k_fused" if fp32_mode["fused"] else "k_assign"},
         "partials": mode["partials"],
-        "kernels_ms": ({kname: round(ms_assign, 5), "k_finalize": round(ms_final, 5)} if fused
+        "kernels_ms": ({kname: round(ms_assign, 5), "k_finalize_cols+k_reloc": round(ms_final, 5)} if fused
                        else {kname: round(ms_assign, 5), "update": round(ms_update, 5),
-                             "k_finalize": round(ms_final, 5)}),
+                             "k_finalize_cols+k_reloc": round(ms_final, 5)}),
         "roofline": roofline,
         "kmeans_plusplus_ms": round(pp_ms, 3),
         "fit_kmeanspp_ms": round(fit_ms, 2),

@@ -111,9 +111,11 @@ __device__ __forceinline__ void step_norms(const FusedArgs& a, int lane, float* 
     }
 }
 
+// The block's partial sums and counts; its clusters with a row go into the
+// presence bits (*present, k <= 64).
 template <int CPC, int NT = 512>
 __device__ __forceinline__ void combine_sums(const float* red, int ld, int k, float* psum, int* pcnt, int (*sCnt)[64],
-                                             int tid)
+                                             int tid, unsigned long long* present)
 {
     const int kl = k * ld;
     float* out = psum + (long)blockIdx.x * kl;
@@ -123,7 +125,12 @@ __device__ __forceinline__ void combine_sums(const float* red, int ld, int k, fl
         const float* p = red + j * ld + col;
         out[i] = ((p[0] + p[CPC * ld]) + p[2 * CPC * ld]) + p[3 * CPC * ld];
     }
-    if (tid < k) pcnt[(long)blockIdx.x * k + tid] = ((sCnt[0][tid] + sCnt[1][tid]) + sCnt[2][tid]) + sCnt[3][tid];
+    if (tid < 64) {
+        const int c = tid < k ? ((sCnt[0][tid] + sCnt[1][tid]) + sCnt[2][tid]) + sCnt[3][tid] : 0;
+        if (tid < k) pcnt[(long)blockIdx.x * k + tid] = c;
+        const unsigned long long m = __ballot(c > 0);
+        if (tid == 0 && m != 0ull) atomicOr(present, m);
+    }
 }
 
 }  // namespace skm

@@ -355,7 +355,7 @@ __global__ __launch_bounds__(512, 1) void k_fused(FusedArgs a)
         publish_sums<CPC, NQ>(S, cnt, zrow + XS, ld, pair, lane, sCnt);
         __syncthreads();
     }
-    combine_sums<CPC>(zrow + XS, ld, k, psum, pcnt, sCnt, tid);
+    combine_sums<CPC>(zrow + XS, ld, k, psum, pcnt, sCnt, tid, &st->present[a.iter & 1]);
 }
 
 typedef void (*fused_fn)(FusedArgs);

@@ -26,11 +26,14 @@ struct LoopState {
     int halt_iter;     // iteration index at which `done` was set
     int n_empty;       // empty clusters found by the last finalise
     unsigned reloc_ctr;  // k_reloc: blocks done with their rows (the last resets it)
-    int empty_iter;      // last iteration whose k_finalize_cols met an empty cluster (-1: none)
     int reloc_iter;      // iteration whose empty clusters k_reloc relocated (-1: none)
-    int pad_;
+    int empty_cnt[2];    // clusters k_finalize_cols of iteration i found empty: empty_cnt[i & 1]
+    unsigned rowdist_ctr;  // k_rowdist: blocks done with their rows (the last resets it)
     double shift_tot;  // sum_j ||c_j_new - c_j_old||^2 of the last step
     double inertia;    // result of the last row-distance reduction
+    // fused steps (k <= 64): bit j set when a block of iteration i's fused
+    // kernel labelled a row j: present[i & 1]
+    unsigned long long present[2];
 };
 
 enum StepFlags : int {
@@ -187,8 +190,10 @@ struct RowDistArgs {
     double* block_part;    // [grid]
     LoopState* state;      // receives `inertia`
 };
+constexpr int kRowDistBlocks = 512;  // k_rowdist grid (two 256-thread blocks per CU)
 int rowdist_grid(long n);
-// Row distances and their fixed-order total (two launches).
+// Row distances and their fixed-order total (one launch: the last block to
+// finish adds the block totals in block order).
 hipError_t launch_rowdist(const RowDistArgs& a, hipStream_t s);
 
 // Device relocation of up to kMaxReloc empty clusters at once (see
@@ -231,8 +236,15 @@ struct InRelocArgs {
     int* amax;             // [1]
     LoopState* state; int iter;
 };
-constexpr int kRelocInlineBlocks = 256;  // grid of k_reloc
+constexpr int kRelocInlineBlocks = 512;  // grid of k_reloc (two blocks per CU)
+constexpr int kRelocCandBlocks = kRelocInlineBlocks > kRelocBlocks ? kRelocInlineBlocks : kRelocBlocks;  // candidate list rows
 hipError_t launch_reloc_inline(const InRelocArgs& a, hipStream_t s);
+// The fused step's k_finalize_cols and k_reloc in one launch (k <= 64, at
+// most kRelocInlineBlocks finalize chunks, no update records): the empty
+// clusters come from the fused kernel's presence bits.
+hipError_t launch_finalize_reloc(const FinalizeArgs& f, const InRelocArgs& a, hipStream_t s);
+// Writes v to *st (a one-thread kernel: no host synchronisation).
+hipError_t launch_state_reset(LoopState* st, const LoopState& v, hipStream_t s);
 
 // Greedy k-means++ seeding (plusplus_kernels.hip): sklearn's _kmeans_plusplus
 // with unit weights and the random draws made by the caller.

@@ -677,11 +677,9 @@ __device__ __forceinline__ float block_max(float v, float* sh)
 
 constexpr int kFinUnroll = 8;  // partials in flight per thread
 
-__global__ __launch_bounds__(256) void k_finalize_cols(FinalizeArgs a)
+// One (cluster j, column chunk cc of nch) of the finalize; a whole block.
+__device__ __forceinline__ void finalize_cols_block(const FinalizeArgs& a, int j, int cc, int nch)
 {
-    const int j = blockIdx.x;
-    const int cc = blockIdx.y;
-    const int nch = gridDim.y;
     const int tid = threadIdx.x;
     const int q = tid & 7;          // float4 column of the block
     const int rs = tid >> 3;        // partial lane, 0..31
@@ -764,9 +762,17 @@ __global__ __launch_bounds__(256) void k_finalize_cols(FinalizeArgs a)
         a.part[((long)j * nch + cc) * 2 + 0] = sq;
         a.part[((long)j * nch + cc) * 2 + 1] = nrm;
         if (cc == 0) a.counts[j] = count;
-        if (cc == 0 && count == 0) a.state->empty_iter = a.iter;  // for k_reloc
-        if (j == 0 && cc == 0 && a.chg_next != nullptr) *a.chg_next = 0;
+        if (cc == 0 && count == 0) atomicAdd(&a.state->empty_cnt[a.iter & 1], 1);  // for k_reloc
+        if (j == 0 && cc == 0) {
+            if (a.chg_next != nullptr) *a.chg_next = 0;
+            a.state->empty_cnt[(a.iter + 1) & 1] = 0;  // read by k_reloc of iteration iter - 1, which has run
+        }
     }
+}
+
+__global__ __launch_bounds__(256) void k_finalize_cols(FinalizeArgs a)
+{
+    finalize_cols_block(a, blockIdx.x, blockIdx.y, gridDim.y);
 }
 
 __global__ __launch_bounds__(256) void k_finalize_loop(FinalizeArgs a, int nch)
@@ -836,109 +842,302 @@ hipError_t launch_finalize_loop(const FinalizeArgs& a, hipStream_t s, int nch)
 // Per row in fp32, in the association order of sklearn's
 // _euclidean_dense_dense (_k_means_common.pyx:16-43): groups of four squared
 // differences summed left to right, each group added to the running sum, the
-// remainder one by one.  A wave takes 64 consecutive rows at a time; their
-// features come in slabs of 64 columns, loaded coalesced (16 lanes per
-// 256-byte piece of a row) into the wave's LDS tile, and lane l carries row
-// l's running sum from slab to slab.
+// remainder one by one.  A block takes a contiguous share of the rows (1024
+// blocks: four per CU), a wave 64 consecutive rows at a time; their features
+// come in slabs of 32 columns, loaded coalesced (8 lanes per 128-byte piece
+// of a row) into the wave's LDS tile, and lane l carries row l's running sum
+// from slab to slab.  The total is summed in fp64: each lane over its rows,
+// then the lanes and waves of a block, then the blocks in order.
 
-constexpr int kRowSlab = 64;                  // columns per slab
-constexpr int kRowTileStride = kRowSlab + 1;  // floats per tile row: lane l's column reads fall on distinct banks
+constexpr int kRowSlab = 32;                  // columns per slab
+constexpr int kRowPiece = kRowSlab / 4;       // float4s per row of a slab = lanes per row in a load
+constexpr int kRowVec = kRowSlab / 4;         // float4s per lane per slab (64 rows x kRowSlab / 64 lanes / 4)
+constexpr int kRowTileStride = kRowSlab + 1;  // floats per tile row: lane l's column reads spread over the banks
 constexpr int kRowTileFloats = 64 * kRowTileStride;
 
-// Squared distance of row row0 + lane (ok: the row exists and has label lab
-// in [0, k)); rows row0 .. row0 + nrows - 1 exist.  tile: this wave's LDS tile.
-__device__ float wave_row_dist(const float* __restrict__ X, int ld, int d, const float* __restrict__ C, long row0,
-                               int nrows, int lab, bool ok, float* tile)
+// Squared distances of rows [r0, r1) to their centres into dist (nullable);
+// returns the lane's fp64 total over its rows.  Wave w takes the 64-row
+// chunks r0 + 64 w + 256 t, lane l row l of a chunk, a 32-column slab at a
+// time; the slab's float4 q = 64 i + lane (row q / 8, columns 4 (q % 8)..)
+// is loaded coalesced into the wave's LDS tile, and each slab's loads are
+// issued before the previous slab is summed.  Out-of-range parts of a slab
+// load clamped addresses and are never summed.  A row whose label is
+// outside [0, k) counts 0.
+__device__ __forceinline__ double rows_dist(const float* __restrict__ X, int ld, int d, const float* __restrict__ C,
+                            const int* __restrict__ labels, int k, long r0, long r1, float* __restrict__ dist,
+                            float* tile)
 {
 #pragma clang fp contract(off)
-    const int lane = threadIdx.x & 63;
-    const float* c = C + (long)(ok ? lab : 0) * ld;
-    float res = 0.f;
-    for (int f0 = 0; f0 < d; f0 += kRowSlab) {
-        const int w = min(kRowSlab, d - f0);
-        // float4 q = 64 i + lane: row q / 16, columns f0 + 4 (q % 16) ..
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int ns = (d + kRowSlab - 1) / kRowSlab;
+    long c0 = r0 + 64L * w;
+    double total = 0.0;
+    if (c0 >= r1) return total;
+    float4 v[kRowVec];
+    auto load = [&](long cc, int sl) {
+        const int f0 = sl * kRowSlab;
+        const int wd4 = ((min(kRowSlab, d - f0) + 3) & ~3) - 4;  // last float4 of the slab in the row
+        const int last = (int)min(64L, r1 - cc) - 1;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+        for (int i = 0; i < kRowVec; ++i) {
             const int q = 64 * i + lane;
-            const int r = q >> 4, c4 = 4 * (q & 15);
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (r < nrows && c4 < w) v = *reinterpret_cast<const float4*>(X + (row0 + r) * ld + f0 + c4);
-            float* t = tile + r * kRowTileStride + c4;
-            t[0] = v.x;
-            t[1] = v.y;
-            t[2] = v.z;
-            t[3] = v.w;
+            const int r = min(q / kRowPiece, last), c4 = min(4 * (q % kRowPiece), wd4);
+            v[i] = *reinterpret_cast<const float4*>(X + (cc + r) * ld + f0 + c4);
+        }
+    };
+    load(c0, 0);
+    int sl = 0;
+    float res = 0.f;
+    bool ok = false;
+    const float* crow = C;
+    while (c0 < r1) {
+        const long row = c0 + lane;
+        if (sl == 0) {
+            const int lab = row < r1 ? labels[row] : -1;
+            ok = lab >= 0 && lab < k;
+            crow = C + (long)(ok ? lab : 0) * ld;
+            res = 0.f;
+        }
+        const int f0 = sl * kRowSlab, wd = min(kRowSlab, d - f0);
+        const int wd4 = ((wd + 3) & ~3) - 4;
+        float4 cv[kRowVec];
+#pragma unroll
+        for (int i = 0; i < kRowVec; ++i) cv[i] = *reinterpret_cast<const float4*>(crow + f0 + min(4 * i, wd4));
+        // the centre loads go out before the next slab's (the sums then wait
+        // for them alone)
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < kRowVec; ++i) {
+            const int q = 64 * i + lane;
+            float* t = tile + (q / kRowPiece) * kRowTileStride + 4 * (q % kRowPiece);
+            t[0] = v[i].x;
+            t[1] = v[i].y;
+            t[2] = v[i].z;
+            t[3] = v[i].w;
         }
         // (a wave's LDS accesses complete in order: the tile is written
         // before any lane reads it)
         __builtin_amdgcn_wave_barrier();
-        if (ok) {
+        long nc0 = c0;
+        int nsl = sl + 1;
+        if (nsl == ns) {
+            nsl = 0;
+            nc0 += 256;
+        }
+        // in flight while this slab is summed; past the last job the current
+        // slab loads again, so every pass issues the same loads (the wait
+        // counts before the sums then cover only the centre loads)
+        load(nc0 < r1 ? nc0 : c0, nc0 < r1 ? nsl : sl);
+        {  // every lane sums (a row without a valid label uses centre 0 and is dropped below)
             const float* t = tile + lane * kRowTileStride;
-            int f = 0;
-            for (; f + 4 <= w; f += 4) {
-                const float4 cv = *reinterpret_cast<const float4*>(c + f0 + f);
-                const float t0 = t[f] - cv.x, t1 = t[f + 1] - cv.y, t2 = t[f + 2] - cv.z, t3 = t[f + 3] - cv.w;
-                res += ((t0 * t0 + t1 * t1) + t2 * t2) + t3 * t3;
-            }
-            for (; f < w; ++f) {
-                const float tt = t[f] - c[f0 + f];
-                res += tt * tt;
+#pragma unroll
+            for (int i = 0; i < kRowVec; ++i) {
+                if (4 * i + 4 <= wd) {
+                    const float t0 = t[4 * i] - cv[i].x, t1 = t[4 * i + 1] - cv[i].y;
+                    const float t2 = t[4 * i + 2] - cv[i].z, t3 = t[4 * i + 3] - cv[i].w;
+                    res += ((t0 * t0 + t1 * t1) + t2 * t2) + t3 * t3;
+                } else if (4 * i < wd) {  // the row's last features, one by one
+                    float tt = t[4 * i] - cv[i].x;
+                    res += tt * tt;
+                    if (4 * i + 1 < wd) {
+                        tt = t[4 * i + 1] - cv[i].y;
+                        res += tt * tt;
+                    }
+                    if (4 * i + 2 < wd) {
+                        tt = t[4 * i + 2] - cv[i].z;
+                        res += tt * tt;
+                    }
+                }
             }
         }
         __builtin_amdgcn_wave_barrier();  // every lane is done with the tile
+        if (sl == ns - 1 && row < r1) {
+            if (dist != nullptr) dist[row] = ok ? res : 0.f;
+            total += ok ? (double)res : 0.0;
+        }
+        c0 = nc0;
+        sl = nsl;
     }
-    return res;
+    return total;
 }
 
-// Block b: rows 256 b .. 256 b + 255, wave w the 64 from 256 b + 64 w.
+// Rows of at most LDM floats (ld <= LDM) take a contiguous path: a wave
+// takes the 32-row chunks r0 + 32 w + 128 t; a chunk's rows are one span of
+// 32 ld floats, loaded as lane-linear float4s (whole cache lines, NV per
+// lane) and scattered into the wave's LDS tile with row stride ld + 1, and
+// lanes 0..31 sum rows 0..31 of the chunk in the association order above.
+// The column slabs of rows_dist read 128-byte pieces of rows that need not
+// start on a cache line, and fetch such lines twice when their neighbours
+// have left the L2 in between.  Each chunk's centre loads are issued before
+// the next chunk's loads, and the sums wait for the centres alone.
+template <int LDM>
+struct CtgGeom {
+    static constexpr int NV = (8 * LDM + 63) / 64;  // float4s per lane per chunk (32 LDM / 4 / 64)
+    static constexpr int NG = LDM / 4;              // float4 groups per row
+    static constexpr int TILE = 32 * (LDM + 1);     // floats per wave tile
+};
+
+// ld: the row stride, a multiple of 4 (<= LDM); tile: the wave's
+// CtgGeom<LDM>::TILE floats.  As rows_dist otherwise.
+template <int LDM>
+__device__ __forceinline__ double rows_dist_ctg(const float* __restrict__ X, int ld, int d,
+                                                const float* __restrict__ C, const int* __restrict__ labels, int k,
+                                                long r0, long r1, float* __restrict__ dist, float* tile)
+{
+#pragma clang fp contract(off)
+    using G = CtgGeom<LDM>;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int S = ld + 1;
+    const float inv_ld = 1.0f / (float)ld;
+    long c0 = r0 + 32L * w;
+    double total = 0.0;
+    if (c0 >= r1) return total;
+    float4 P[G::NV];
+    int plab = -1;
+    auto load = [&](long cc) {
+        const int nrows = (int)min(32L, r1 - cc);
+        const int e4 = nrows * ld / 4;  // float4s of the chunk's rows
+        const float4* base = reinterpret_cast<const float4*>(X + cc * ld);
+#pragma unroll
+        for (int i = 0; i < G::NV; ++i) P[i] = base[min(64 * i + lane, e4 - 1)];
+        plab = labels[cc + min(lane, nrows - 1)];
+    };
+    load(c0);
+    while (c0 < r1) {
+        const int nrows = (int)min(32L, r1 - c0);
+        const int e4 = nrows * ld / 4;
+        // float p = 4 q of the span: row p / ld (p + 1/2 keeps the float
+        // quotient clear of integers), column p % ld
+#pragma unroll
+        for (int i = 0; i < G::NV; ++i) {
+            const int q = 64 * i + lane;
+            if (q < e4) {
+                const int p = 4 * q;
+                const int r = (int)(((float)p + 0.5f) * inv_ld);
+                float* t = tile + r * S + (p - r * ld);
+                t[0] = P[i].x;
+                t[1] = P[i].y;
+                t[2] = P[i].z;
+                t[3] = P[i].w;
+            }
+        }
+        const int lab = plab;
+        const bool ok = lane < nrows && lab >= 0 && lab < k;
+        const float* crow = C + (long)(ok ? lab : 0) * ld;
+        float4 cv[G::NG];
+#pragma unroll
+        for (int g = 0; g < G::NG; ++g) cv[g] = *reinterpret_cast<const float4*>(crow + min(4 * g, ld - 4));
+        // the centre loads go out before the next chunk's (the sums then
+        // wait for them alone); past the last chunk the current one loads
+        // again, so every pass issues the same loads
+        __builtin_amdgcn_sched_barrier(0);
+        const long nc0 = c0 + 128;
+        load(nc0 < r1 ? nc0 : c0);
+        // (a wave's LDS accesses complete in order: the tile is written
+        // before any lane reads it)
+        __builtin_amdgcn_wave_barrier();
+        float res = 0.f;
+        {
+            const float* t = tile + min(lane, 31) * S;
+#pragma unroll
+            for (int g = 0; g < G::NG; ++g) {
+                if (4 * g + 4 <= d) {
+                    const float t0 = t[4 * g] - cv[g].x, t1 = t[4 * g + 1] - cv[g].y;
+                    const float t2 = t[4 * g + 2] - cv[g].z, t3 = t[4 * g + 3] - cv[g].w;
+                    res += ((t0 * t0 + t1 * t1) + t2 * t2) + t3 * t3;
+                } else if (4 * g < d) {  // the row's last features, one by one
+                    float tt = t[4 * g] - cv[g].x;
+                    res += tt * tt;
+                    if (4 * g + 1 < d) {
+                        tt = t[4 * g + 1] - cv[g].y;
+                        res += tt * tt;
+                    }
+                    if (4 * g + 2 < d) {
+                        tt = t[4 * g + 2] - cv[g].z;
+                        res += tt * tt;
+                    }
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();  // every lane is done with the tile
+        if (lane < nrows) {
+            if (dist != nullptr) dist[c0 + lane] = ok ? res : 0.f;
+            total += ok ? (double)res : 0.0;
+        }
+        c0 = nc0;
+    }
+    return total;
+}
+
+// Floats of one wave's tile for the path LDM (0: the column slabs).
+template <int LDM>
+constexpr int row_tile_floats()
+{
+    if constexpr (LDM == 0)
+        return kRowTileFloats;
+    else
+        return CtgGeom<LDM>::TILE;
+}
+
+template <int LDM>
+__device__ __forceinline__ double rows_dist_any(const float* __restrict__ X, int ld, int d,
+                                                const float* __restrict__ C, const int* __restrict__ labels, int k,
+                                                long r0, long r1, float* __restrict__ dist, float* tile)
+{
+    if constexpr (LDM == 0)
+        return rows_dist(X, ld, d, C, labels, k, r0, r1, dist, tile);
+    else
+        return rows_dist_ctg<LDM>(X, ld, d, C, labels, k, r0, r1, dist, tile);
+}
+
+// The path for rows of stride ld: the narrowest contiguous one that holds
+// them, else the column slabs.
+int row_path(int ld) { return ld <= 32 ? 32 : ld <= 64 ? 64 : ld <= 104 ? 104 : ld <= 128 ? 128 : 0; }
+
+// Block b: rows [b rpb, (b + 1) rpb); its fp64 total (lanes, then waves in
+// order) goes to block_part[b].
+template <int LDM>
 __global__ __launch_bounds__(256) void k_rowdist(RowDistArgs a)
 {
-    __shared__ float tiles[4 * kRowTileFloats];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const long row0 = (long)blockIdx.x * 256 + 64 * w;
-    const long row = row0 + lane;
-    const int nrows = (int)max(0L, min(64L, a.n - row0));
-    const int lab = row < a.n ? a.labels[row] : -1;
-    const bool ok = lab >= 0 && lab < a.k;
-    const float res = wave_row_dist(a.X, a.ld, a.d, a.C, row0, nrows, lab, ok, tiles + w * kRowTileFloats);
-    double v = 0.0;
-    if (ok) {
-        if (a.out_rows != nullptr) a.out_rows[row] = res;
-        v = (double)res;
+    constexpr int TF = row_tile_floats<LDM>();
+    __shared__ float tiles[4 * TF];
+    __shared__ double sh[4];
+    const long rpb = (a.n + gridDim.x - 1) / gridDim.x;
+    const long r0 = min(a.n, (long)blockIdx.x * rpb), r1 = min(a.n, r0 + rpb);
+    const double v = rows_dist_any<LDM>(a.X, a.ld, a.d, a.C, a.labels, a.k, r0, r1, a.out_rows,
+                                        tiles + (threadIdx.x >> 6) * TF);
+    const double t = block_sum(v, sh);
+    // the last block to finish adds the block totals, in block order
+    __shared__ int last_s;
+    if (threadIdx.x == 0) {
+        a.block_part[blockIdx.x] = t;
+        __threadfence();  // the block total, to the device
+        last_s = atomicAdd(&a.state->rowdist_ctr, 1u) == gridDim.x - 1;
     }
-    __shared__ double red[256];
-    red[threadIdx.x] = v;
     __syncthreads();
-    for (int s2 = 128; s2 > 0; s2 >>= 1) {
-        if (threadIdx.x < s2) red[threadIdx.x] += red[threadIdx.x + s2];
-        __syncthreads();
+    if (!last_s) return;
+    __threadfence();  // every block's total
+    double s = 0.0;
+    for (int b = threadIdx.x; b < (int)gridDim.x; b += 256) s += a.block_part[b];
+    s = block_sum(s, sh);
+    if (threadIdx.x == 0) {
+        a.state->inertia = s;
+        a.state->rowdist_ctr = 0u;
     }
-    if (threadIdx.x == 0) a.block_part[blockIdx.x] = red[0];
 }
 
-// Fixed-order total of the block partials (a second launch: the kernel
-// boundary replaces a cross-block fence).
-__global__ __launch_bounds__(256) void k_rowdist_total(RowDistArgs a, int nblk)
-{
-    __shared__ double red[256];
-    double t = 0.0;
-    for (int b = threadIdx.x; b < nblk; b += 256) t += a.block_part[b];
-    red[threadIdx.x] = t;
-    __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) a.state->inertia = red[0];
-}
-
-int rowdist_grid(long n) { return (int)max(1L, (n + 255) / 256); }
+int rowdist_grid(long n) { return (int)max(1L, min((long)kRowDistBlocks, (n + 255) / 256)); }
 
 hipError_t launch_rowdist(const RowDistArgs& a, hipStream_t s)
 {
     const int nblk = rowdist_grid(a.n);
-    hipLaunchKernelGGL(k_rowdist, dim3(nblk), dim3(256), 0, s, a);
-    hipLaunchKernelGGL(k_rowdist_total, dim3(1), dim3(256), 0, s, a, nblk);
+    switch (row_path(a.ld)) {
+    case 32: hipLaunchKernelGGL(k_rowdist<32>, dim3(nblk), dim3(256), 0, s, a); break;
+    case 64: hipLaunchKernelGGL(k_rowdist<64>, dim3(nblk), dim3(256), 0, s, a); break;
+    case 104: hipLaunchKernelGGL(k_rowdist<104>, dim3(nblk), dim3(256), 0, s, a); break;
+    case 128: hipLaunchKernelGGL(k_rowdist<128>, dim3(nblk), dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL(k_rowdist<0>, dim3(nblk), dim3(256), 0, s, a); break;
+    }
     return hipGetLastError();
 }
 
@@ -969,24 +1168,33 @@ __device__ __forceinline__ void far_pick(float& bd, long& bi, float d, long i, f
     }
 }
 
+// The first of the block's candidates in far_before order (bi < 0: none);
+// every thread gets it.  The order is total on rows, so the xor butterflies
+// leave the same candidate in every lane.  sd / si: 4 entries each.
 __device__ void far_block_reduce(float& bd, long& bi, float* sd, long* si)
 {
-    sd[threadIdx.x] = bd;
-    si[threadIdx.x] = bi;
-    __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if (threadIdx.x < w) {
-            const float d2 = sd[threadIdx.x + w];
-            const long i2 = si[threadIdx.x + w];
-            if (i2 >= 0 && (si[threadIdx.x] < 0 || far_before(d2, i2, sd[threadIdx.x], si[threadIdx.x]))) {
-                sd[threadIdx.x] = d2;
-                si[threadIdx.x] = i2;
-            }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const float d2 = __shfl_xor(bd, off, 64);
+        const long i2 = __shfl_xor(bi, off, 64);
+        if (i2 >= 0 && (bi < 0 || far_before(d2, i2, bd, bi))) {
+            bd = d2;
+            bi = i2;
         }
-        __syncthreads();
     }
+    if ((threadIdx.x & 63) == 0) {
+        sd[threadIdx.x >> 6] = bd;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
     bd = sd[0];
     bi = si[0];
+    for (int w = 1; w < 4; ++w) {
+        if (si[w] >= 0 && (bi < 0 || far_before(sd[w], si[w], bd, bi))) {
+            bd = sd[w];
+            bi = si[w];
+        }
+    }
     __syncthreads();
 }
 
@@ -1130,49 +1338,60 @@ hipError_t launch_relocate(const RelocArgs& a, int E, hipStream_t s)
 // in-stream relocation: k_reloc
 // ---------------------------------------------------------------------------
 //
-// Launched after every step's k_finalize_cols, which records in
-// state->empty_iter the step of any cluster it found empty; for any other
-// step the kernel returns at its first load.  Otherwise, as the device path
-// above but in one kernel: (A) each block takes the distances of its
-// contiguous share of the rows and its E farthest, in order, and counts
-// itself done; (B) the last block to finish merges the candidates, moves the
-// rows in the fp64 sums and counts, and (C) redoes the centres and chunk
-// partials (the finalize's 32-column chunks) of the clusters involved -- the
-// empty ones, those that gave a row, and any still empty -- as
-// k_finalize_sums does; every other cluster keeps what k_finalize_cols
-// wrote.  state->reloc_iter = iter then tells the loop decision that this
-// step's empty clusters were handled.  No block waits for another.
+// Launched after every step's k_finalize_cols, which counts the clusters it
+// finds empty in state->empty_cnt[iter & 1]; with none the kernel returns at
+// its first load.  Otherwise, as the device path above but in one kernel:
+// (A) each block takes the distances of its contiguous share of the rows and
+// its E farthest, in order, and counts itself done; (B) the last block to
+// finish merges the blocks' lists, moves the rows in the fp64 sums and
+// counts, and (C) redoes the centres and chunk partials (the finalize's
+// 32-column chunks) of the clusters involved -- the filled ones, those that
+// gave a row, and any still empty -- as k_finalize_sums does; every other
+// cluster keeps what k_finalize_cols wrote.  state->reloc_iter = iter then
+// tells the loop decision that this step's empty clusters were handled.  No
+// block waits for another.
 
-__global__ __launch_bounds__(256) void k_reloc(InRelocArgs a)
+// Exclusive prefix sum over a 256-thread block; *total gets the block's sum.
+// sh: 4 ints.  Ends with a barrier.
+__device__ int block_excl_scan(int v, int* sh, int* total)
 {
-    __shared__ float tiles[4 * kRowTileFloats];
-    __shared__ float sd[256];
-    __shared__ long si[256];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    if (lane == 63) sh[w] = x;
+    __syncthreads();
+    int base = 0, tot = 0;
+    for (int i = 0; i < 4; ++i) {
+        base += i < w ? sh[i] : 0;
+        tot += sh[i];
+    }
+    __syncthreads();
+    *total = tot;
+    return base + x - v;
+}
+
+// The relocation of E (1..kMaxReloc) empty clusters by every block of the
+// grid (gridDim.x <= kRelocCandBlocks): phases A, B and C above.
+template <int LDM>
+__device__ __forceinline__ void reloc_body(const InRelocArgs& a, int E)
+{
+    constexpr int TF = row_tile_floats<LDM>();
+    __shared__ float tiles[4 * TF];
+    __shared__ float sd[4];
+    __shared__ long si[4];
     __shared__ int shi[4];
-    __shared__ double shd[2][4];
     __shared__ int last_s;
     LoopState* st = a.state;
-    const int tid = threadIdx.x;
-    if (st->empty_iter != a.iter || st->done != 0) return;
-    int ne = 0;
-    for (int j = tid; j < a.k; j += 256) ne += a.counts[j] == 0;
-    const int E = block_sum(ne, shi);
-    if (E == 0 || E > kMaxReloc) return;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
 
     // (A) distances of rows [r0, r1), then this block's E farthest, in order
     const long rpb = (a.n + gridDim.x - 1) / gridDim.x;
     const long r0 = min(a.n, (long)blockIdx.x * rpb), r1 = min(a.n, r0 + rpb);
-    {
-        const int lane = tid & 63, w = tid >> 6;
-        for (long c0 = r0 + 64L * w; c0 < r1; c0 += 256) {
-            const long row = c0 + lane;
-            const int nrows = (int)min(64L, r1 - c0);
-            const int lab = row < r1 ? a.labels[row] : -1;
-            const bool ok = lab >= 0 && lab < a.k;
-            const float res = wave_row_dist(a.X, a.ld, a.d, a.C_old, c0, nrows, lab, ok, tiles + w * kRowTileFloats);
-            if (row < r1) a.dist[row] = ok ? res : 0.f;
-        }
-    }
+    (void)rows_dist_any<LDM>(a.X, a.ld, a.d, a.C_old, a.labels, a.k, r0, r1, a.dist, tiles + w * TF);
     __threadfence_block();
     __syncthreads();
     {
@@ -1202,113 +1421,249 @@ __global__ __launch_bounds__(256) void k_reloc(InRelocArgs a)
     if (tid == 0) st->reloc_ctr = 0u;
     __threadfence();  // every block's candidates
 
-    // (B) the E farthest overall, moved to the empty clusters in ascending order
+    // each thread's contiguous share of the clusters
+    const int per = (a.k + 255) / 256;
+    const int j0 = min(a.k, tid * per), j1 = min(a.k, j0 + per);
+
+    // (B) the first E empty clusters in ascending order
     __shared__ long far[kMaxReloc];
     __shared__ int empt[kMaxReloc];
     __shared__ int donor[kMaxReloc];
+    __shared__ int still[kMaxReloc];
     __shared__ int ne_s;
-    if (tid == 0) {
-        int q = 0;
-        for (int j = 0; j < a.k && q < E; ++j)
-            if (a.counts[j] == 0) empt[q++] = j;
-        ne_s = q;
-    }
     {
-        float dl = INFINITY;
-        long il = -1;
+        int mine = 0;
+        for (int j = j0; j < j1; ++j) mine += a.counts[j] == 0;
+        int tot;
+        int pos = block_excl_scan(mine, shi, &tot);
+        for (int j = j0; j < j1 && pos < E; ++j)
+            if (a.counts[j] == 0) empt[pos++] = j;
+        if (tid == 0) ne_s = min(tot, E);
+    }
+    // the E farthest rows overall: a merge of the blocks' ordered lists,
+    // thread t holding the heads of blocks t + 256 j
+    {
+        constexpr int HPT = (kRelocInlineBlocks + 255) / 256;
+        const int nb = (int)gridDim.x;  // <= 256 HPT
+        int h[HPT];
+        float hd[HPT];
+        long hi[HPT];
+#pragma unroll
+        for (int j = 0; j < HPT; ++j) {
+            const int b = tid + 256 * j;
+            h[j] = 0;
+            hd[j] = 0.f;
+            hi[j] = -1;
+            if (b < nb) {
+                hd[j] = a.cand_d[(long)b * kMaxReloc];
+                hi[j] = a.cand_i[(long)b * kMaxReloc];
+            }
+        }
         for (int e = 0; e < E; ++e) {
-            float bd = 0.f;
-            long bi = -1;
-            for (int c = tid; c < (int)gridDim.x * E; c += 256) {
-                const int b = c / E, ee = c - b * E;
-                const long i = a.cand_i[(long)b * kMaxReloc + ee];
-                if (i >= 0) far_pick(bd, bi, a.cand_d[(long)b * kMaxReloc + ee], i, dl, il);
+            float bd = hd[0];
+            long bi = hi[0];
+#pragma unroll
+            for (int j = 1; j < HPT; ++j) {
+                if (hi[j] >= 0 && (bi < 0 || far_before(hd[j], hi[j], bd, bi))) {
+                    bd = hd[j];
+                    bi = hi[j];
+                }
             }
             far_block_reduce(bd, bi, sd, si);
-            if (tid == 0) far[e] = bi;
-            dl = bd;
-            il = bi;
-            // the farthest distance decides whether anything moves (all zero: no)
-            if (e == 0 && tid == 0 && (bi < 0 || bd <= 0.f)) ne_s = 0;
+            if (tid == 0) {
+                far[e] = bi;
+                // the farthest distance decides whether anything moves (all zero: no)
+                if (e == 0 && (bi < 0 || bd <= 0.f)) ne_s = 0;
+            }
+#pragma unroll
+            for (int j = 0; j < HPT; ++j) {
+                if (bi >= 0 && hi[j] == bi) {
+                    const long b = tid + 256 * j;
+                    ++h[j];
+                    hd[j] = 0.f;
+                    hi[j] = -1;
+                    if (h[j] < E) {
+                        hd[j] = a.cand_d[b * kMaxReloc + h[j]];
+                        hi[j] = a.cand_i[b * kMaxReloc + h[j]];
+                    }
+                }
+            }
         }
     }
     __syncthreads();
     const int nm = ne_s;
-    for (int e = 0; e < nm; ++e) {
-        const long fr = far[e];
-        const int j = empt[e];
-        const int o = a.labels[fr];
-        const float* x = a.X + fr * a.ld;
-        for (int c = tid; c < a.d; c += 256) {
-            a.sums[(long)o * a.ld + c] -= (double)x[c];
-            a.sums[(long)j * a.ld + c] = (double)x[c];
+    // move far[e] to empt[e], in order: each thread owns columns of the sums
+    if (tid < nm) donor[tid] = a.labels[far[tid]];
+    __syncthreads();
+    for (int c = tid; c < a.d; c += 256) {
+        for (int e = 0; e < nm; ++e) {
+            const double xv = (double)a.X[far[e] * a.ld + c];
+            a.sums[(long)donor[e] * a.ld + c] -= xv;
+            a.sums[(long)empt[e] * a.ld + c] = xv;
         }
-        __threadfence_block();
-        __syncthreads();
-        if (tid == 0) {
-            a.counts[j] = 1;
-            a.counts[o] -= 1;
-            donor[e] = o;
-        }
-        __threadfence_block();
-        __syncthreads();
     }
-    __shared__ int amax_s;
-    if (tid == 0) {
-        int am = 0;
-        for (int j = 1; j < a.k; ++j)
-            if (a.counts[j] > a.counts[am]) am = j;
-        amax_s = am;
+    if (tid < nm) {
+        a.counts[empt[tid]] = 1;
+        // a donor's first move takes all of its moves off its count
+        int m = 0;
+        bool first = true;
+        for (int e = 0; e < nm; ++e) {
+            if (donor[e] == donor[tid]) {
+                ++m;
+                first = first && e >= tid;
+            }
+        }
+        if (first) a.counts[donor[tid]] -= m;
+    }
+    __threadfence_block();
+    __syncthreads();
+
+    // the largest cluster (lowest index on ties) and the clusters still empty
+    __shared__ int amax_s, nstill_s;
+    {
+        int bc = -1, bj = a.k, mine = 0;
+        for (int j = j0; j < j1; ++j) {
+            const int c = a.counts[j];
+            if (c > bc) {
+                bc = c;
+                bj = j;
+            }
+            mine += c == 0;
+        }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int oc = __shfl_xor(bc, off, 64), oj = __shfl_xor(bj, off, 64);
+            if (oc > bc || (oc == bc && oj < bj)) {
+                bc = oc;
+                bj = oj;
+            }
+        }
+        __shared__ int mc[4], mj[4];
+        if (lane == 0) {
+            mc[w] = bc;
+            mj[w] = bj;
+        }
+        int tot;
+        int pos = block_excl_scan(mine, shi, &tot);  // (its first barrier publishes mc, mj)
+        for (int j = j0; j < j1 && pos < kMaxReloc; ++j)
+            if (a.counts[j] == 0) still[pos++] = j;
+        if (tid == 0) {
+            int c = mc[0], jj = mj[0];
+            for (int q = 1; q < 4; ++q) {
+                if (mc[q] > c || (mc[q] == c && mj[q] < jj)) {
+                    c = mc[q];
+                    jj = mj[q];
+                }
+            }
+            amax_s = jj;
+            nstill_s = min(tot, kMaxReloc);
+        }
     }
     __syncthreads();
     const int amax = amax_s;
 
-    // (C) centres and chunk partials of the clusters involved: list entry q
-    // < nm the filled cluster, nm <= q < 2 nm the donor, then every cluster
-    // still empty (repeats are harmless: the same values are written)
+    // (C) centres and chunk partials of the clusters involved, one (cluster,
+    // chunk) per wave at a time: entries q < nm the filled clusters, nm <= q
+    // < 2 nm the donors, then the clusters still empty (repeats write the
+    // same values).  The chunk sums are the wave sums k_finalize_cols forms.
     constexpr int CW = 32;
-    for (int j0 = 0; j0 < 2 * nm + a.k; ++j0) {
-        int j;
-        if (j0 < nm) {
-            j = empt[j0];
-        } else if (j0 < 2 * nm) {
-            j = donor[j0 - nm];
-        } else {
-            j = j0 - 2 * nm;
-            if (a.counts[j] != 0) continue;  // (uniform across the block)
-        }
+    const int nitems = 2 * nm + nstill_s;
+    for (int p = w; p < nitems * a.nch; p += 4) {
+        const int q = p / a.nch, cc = p - q * a.nch;
+        const int j = q < nm ? empt[q] : q < 2 * nm ? donor[q - nm] : still[q - 2 * nm];
         const int cnt = a.counts[j];
-        for (int cc = 0; cc < a.nch; ++cc) {
-            const int col = cc * CW + tid;
-            double sq = 0.0, nrm = 0.0;
-            if (tid < CW && col < a.d) {
-                double v;
-                if (cnt > 0) {
-                    v = a.sums[(long)j * a.ld + col] / (double)cnt;
-                } else {
-                    const double sa = a.sums[(long)amax * a.ld + col];
-                    v = amax < j ? sa / (double)a.counts[amax] : sa;
-                }
-                const float cn = (float)v;
-                a.C_new[(long)j * a.ld + col] = cn;
-                const double df = (double)cn - (double)a.C_old[(long)j * a.ld + col];
-                sq = df * df;
-                nrm = (double)cn * (double)cn;
+        const int col = cc * CW + lane;
+        double sq = 0.0, nrm = 0.0;
+        if (lane < CW && col < a.d) {
+            double v;
+            if (cnt > 0) {
+                v = a.sums[(long)j * a.ld + col] / (double)cnt;
+            } else {
+                const double sa = a.sums[(long)amax * a.ld + col];
+                v = amax < j ? sa / (double)a.counts[amax] : sa;
             }
-            sq = block_sum(sq, shd[0]);
-            nrm = block_sum(nrm, shd[1]);
-            if (tid == 0) {
-                a.part[((long)j * a.nch + cc) * 2 + 0] = sq;
-                a.part[((long)j * a.nch + cc) * 2 + 1] = nrm;
-            }
+            const float cn = (float)v;
+            a.C_new[(long)j * a.ld + col] = cn;
+            const double df = (double)cn - (double)a.C_old[(long)j * a.ld + col];
+            sq = df * df;
+            nrm = (double)cn * (double)cn;
+        }
+        sq = wave_sum(sq);
+        nrm = wave_sum(nrm);
+        if (lane == 0) {
+            a.part[((long)j * a.nch + cc) * 2 + 0] = sq;
+            a.part[((long)j * a.nch + cc) * 2 + 1] = nrm;
         }
     }
     if (tid == 0) st->reloc_iter = a.iter;
 }
 
+// After k_finalize_cols: the clusters it counted empty.
+template <int LDM>
+__global__ __launch_bounds__(256) void k_reloc(InRelocArgs a)
+{
+    if (a.state->done != 0) return;
+    const int E = a.state->empty_cnt[a.iter & 1];
+    if (E == 0 || E > kMaxReloc) return;
+    reloc_body<LDM>(a, E);
+}
+
+// The fused step's finalize and relocation in one launch: blocks b < k nch
+// take finalize chunk (b % k, b / k); then, when some cluster received no
+// row (the fused kernel's presence bits, so every block knows at once),
+// every block joins the relocation.  The last block to finish its rows
+// finds every finalize chunk written.
+template <int LDM>
+__global__ __launch_bounds__(256) void k_finalize_reloc(FinalizeArgs f, InRelocArgs a, int nch)
+{
+    const int b = blockIdx.x;
+    if (b < f.k * nch) finalize_cols_block(f, b % f.k, b / f.k, nch);
+    LoopState* st = f.state;
+    const unsigned long long pres = st->present[f.iter & 1];
+    if (b == 0 && threadIdx.x == 0) st->present[(f.iter + 1) & 1] = 0ull;  // for the next fused kernel
+    if (st->done != 0) return;
+    const unsigned long long all = f.k >= 64 ? ~0ull : (1ull << f.k) - 1ull;
+    const int E = __popcll(all & ~pres);
+    if (E == 0 || E > kMaxReloc) return;
+    reloc_body<LDM>(a, E);
+}
+
+hipError_t launch_finalize_reloc(const FinalizeArgs& f, const InRelocArgs& a, hipStream_t s)
+{
+    const int nch = finalize_col_chunks(f.d, f.R);
+    if (f.k > 64 || f.k * nch > kRelocInlineBlocks || f.rec_off != nullptr) return hipErrorInvalidValue;
+    const dim3 g(kRelocInlineBlocks);
+    switch (row_path(a.ld)) {
+    case 32: hipLaunchKernelGGL(k_finalize_reloc<32>, g, dim3(256), 0, s, f, a, nch); break;
+    case 64: hipLaunchKernelGGL(k_finalize_reloc<64>, g, dim3(256), 0, s, f, a, nch); break;
+    case 104: hipLaunchKernelGGL(k_finalize_reloc<104>, g, dim3(256), 0, s, f, a, nch); break;
+    case 128: hipLaunchKernelGGL(k_finalize_reloc<128>, g, dim3(256), 0, s, f, a, nch); break;
+    default: hipLaunchKernelGGL(k_finalize_reloc<0>, g, dim3(256), 0, s, f, a, nch); break;
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_reloc_inline(const InRelocArgs& a, hipStream_t s)
 {
-    hipLaunchKernelGGL(k_reloc, dim3(kRelocInlineBlocks), dim3(256), 0, s, a);
+    const dim3 g(kRelocInlineBlocks);
+    switch (row_path(a.ld)) {
+    case 32: hipLaunchKernelGGL(k_reloc<32>, g, dim3(256), 0, s, a); break;
+    case 64: hipLaunchKernelGGL(k_reloc<64>, g, dim3(256), 0, s, a); break;
+    case 104: hipLaunchKernelGGL(k_reloc<104>, g, dim3(256), 0, s, a); break;
+    case 128: hipLaunchKernelGGL(k_reloc<128>, g, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL(k_reloc<0>, g, dim3(256), 0, s, a); break;
+    }
+    return hipGetLastError();
+}
+
+__global__ void k_state_reset(LoopState* st, LoopState v)
+{
+    if (threadIdx.x == 0) *st = v;
+}
+
+hipError_t launch_state_reset(LoopState* st, const LoopState& v, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_state_reset, dim3(1), dim3(64), 0, s, st, v);
     return hipGetLastError();
 }
 

@@ -446,8 +446,8 @@ struct Lloyd {
         TRY(grab((void**)&absmax, sizeof(unsigned)));
         // relocation of empty clusters (k <= 64: always on the device)
         TRY(grab((void**)&rowout, size_t(n) * sizeof(float)));
-        TRY(grab((void**)&r_cand_d, size_t(kRelocBlocks) * kMaxReloc * sizeof(float)));
-        TRY(grab((void**)&r_cand_i, size_t(kRelocBlocks) * kMaxReloc * sizeof(long)));
+        TRY(grab((void**)&r_cand_d, size_t(kRelocCandBlocks) * kMaxReloc * sizeof(float)));
+        TRY(grab((void**)&r_cand_i, size_t(kRelocCandBlocks) * kMaxReloc * sizeof(long)));
         TRY(grab((void**)&r_amax, sizeof(int)));
         reloc_inline = inline_relocation_on();
         HIP_TRY(hipMemsetAsync(cen[1], 0, kl * sizeof(float), s), "hipMemsetAsync");
@@ -497,8 +497,8 @@ struct Lloyd {
         reloc_inline = inline_relocation_on();
         if (reloc_inline) {
             TRY(grab((void**)&rowout, size_t(n) * sizeof(float)));
-            TRY(grab((void**)&r_cand_d, size_t(kRelocBlocks) * kMaxReloc * sizeof(float)));
-            TRY(grab((void**)&r_cand_i, size_t(kRelocBlocks) * kMaxReloc * sizeof(long)));
+            TRY(grab((void**)&r_cand_d, size_t(kRelocCandBlocks) * kMaxReloc * sizeof(float)));
+            TRY(grab((void**)&r_cand_i, size_t(kRelocCandBlocks) * kMaxReloc * sizeof(long)));
             TRY(grab((void**)&r_amax, sizeof(int)));
         }
         if (sg.on) {
@@ -527,6 +527,9 @@ struct Lloyd {
     // (after a halt) records again.
     std::vector<hipEvent_t> kev;
     long kev_base = -1;
+    // When set, run_loop records it right after each batch of steps is
+    // enqueued (before the state read-back): the end of a timed run.
+    hipEvent_t batch_end = nullptr;
 
     void destroy()
     {
@@ -672,11 +675,14 @@ struct Lloyd {
         }
         if (ev) HIP_TRY(hipEventRecord(ev[2], s), "hipEventRecord");
         const FinalizeArgs f = finalize_args(iter, tol, flags);
-        HIP_TRY(launch_finalize(f, s, false), "finalize launch");
-        if (reloc_inline) {
-            InRelocArgs r{X, n, ld, d, k, labels, cen[cur], cen[cur ^ 1], sums, counts, part,
-                          finalize_col_chunks(d, f.R), rowout, r_cand_d, r_cand_i, r_amax, st, iter};
-            HIP_TRY(launch_reloc_inline(r, s), "relocation launch");
+        const InRelocArgs r{X, n, ld, d, k, labels, cen[cur], cen[cur ^ 1], sums, counts, part,
+                            finalize_col_chunks(d, f.R), rowout, r_cand_d, r_cand_i, r_amax, st, iter};
+        if (reloc_inline && fblocks > 0 && k <= 64 && k * r.nch <= kRelocInlineBlocks) {
+            // the fused kernel's presence bits name the empty clusters: one launch
+            HIP_TRY(launch_finalize_reloc(f, r, s), "finalize launch");
+        } else {
+            HIP_TRY(launch_finalize(f, s, false), "finalize launch");
+            if (reloc_inline) HIP_TRY(launch_reloc_inline(r, s), "relocation launch");
         }
         if (fblocks == 0 || last) HIP_TRY(launch_finalize_loop(f, s), "finalize launch");
         if (ev) HIP_TRY(hipEventRecord(ev[3], s), "hipEventRecord");
@@ -706,8 +712,8 @@ struct Lloyd {
     {
         if (rowout == nullptr) TRY(grab((void**)&rowout, size_t(n) * sizeof(float)));
         if (r_cand_d == nullptr) {
-            TRY(grab((void**)&r_cand_d, size_t(kRelocBlocks) * kMaxReloc * sizeof(float)));
-            TRY(grab((void**)&r_cand_i, size_t(kRelocBlocks) * kMaxReloc * sizeof(long)));
+            TRY(grab((void**)&r_cand_d, size_t(kRelocCandBlocks) * kMaxReloc * sizeof(float)));
+            TRY(grab((void**)&r_cand_i, size_t(kRelocCandBlocks) * kMaxReloc * sizeof(long)));
             TRY(grab((void**)&r_amax, sizeof(int)));
         }
         LoopState w = hs;
@@ -833,8 +839,8 @@ struct Lloyd {
         }
         LoopState hs{};
         hs.reloc_iter = -1;
-        hs.empty_iter = -1;
-        TRY(write_state(hs));
+        // the reset is a kernel on the stream: nothing waits for the host
+        HIP_TRY(launch_state_reset(st, hs, s), "state reset launch");
         HIP_TRY(hipMemsetAsync(labels, 0xff, size_t(n) * sizeof(int), s), "hipMemsetAsync(labels)");
         long it = 0;
         // Steps are enqueued in growing batches and the loop state is read
@@ -848,6 +854,7 @@ struct Lloyd {
             const long nb = std::min(batch, max_iter - it);
             const int c0 = cur;
             for (long t = it; t < it + nb; ++t) TRY(enqueue_step((int)t, tol, flags, t > it, t + 1 == it + nb));
+            if (batch_end) HIP_TRY(hipEventRecord(batch_end, s), "hipEventRecord");
             TRY(read_state(&hs));
             if (hs.done == 3) {
                 const int t = hs.halt_iter;
@@ -860,6 +867,7 @@ struct Lloyd {
                     TRY(host_relocate(t, old, tol, flags, hs));
                 else
                     TRY(device_relocate(t, old, tol, flags, hs));
+                if (batch_end) HIP_TRY(hipEventRecord(batch_end, s), "hipEventRecord");
                 it = t + 1;
                 if (hs.done != 0) {
                     final_done = hs.done;
@@ -1339,9 +1347,14 @@ int skmetal_hip_lloyd_iterate(skmetal_hip_lloyd* h, size_t iters, float* ms_out,
         hipError_t er = hipEventRecord(e0, L.s);
         if (er != hipSuccess) rc = hip_fail(er, "hipEventRecord");
         int n_iter = 0, done = 0;
+        // e1 is recorded by the loop right after the last step's kernels
+        L.batch_end = e1;
         if (rc == 0) rc = L.run_loop((long)iters, 0.0, 0, true, &n_iter, &done);
-        er = hipEventRecord(e1, L.s);
-        if (rc == 0 && er != hipSuccess) rc = hip_fail(er, "hipEventRecord");
+        L.batch_end = nullptr;
+        if (rc == 0 && iters == 0) {
+            er = hipEventRecord(e1, L.s);
+            if (er != hipSuccess) rc = hip_fail(er, "hipEventRecord");
+        }
         L.kev_base = -1;
         hipError_t e = hipEventSynchronize(e1);
         if (rc == 0 && e != hipSuccess) rc = hip_fail(e, "hipEventSynchronize");

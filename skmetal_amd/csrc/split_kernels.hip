@@ -674,7 +674,7 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
             sums(std::integral_constant<int, NFA>{}, std::integral_constant<int, NFZ>{});
         __syncthreads();
     }
-    combine_sums<CPC, 1024>(lds, ld, k, a.psum, a.pcnt, sCnt, tid);
+    combine_sums<CPC, 1024>(lds, ld, k, a.psum, a.pcnt, sCnt, tid, &a.state->present[a.iter & 1]);
 }
 
 // ---------------------------------------------------------------------------

@@ -101,9 +101,13 @@ def test_assign_duplicate_centres_lowest_index(bridge):
     assert out.max() < 7
 
 
-def test_mindists_and_inertia_vs_oracle(bridge):
-    rng = np.random.default_rng(2)
-    n, d, k = 5000, 37, 13
+@pytest.mark.parametrize("d", [3, 37, 100, 128, 161])
+def test_mindists_and_inertia_vs_oracle(bridge, d):
+    """Per-row distances and their total; d covers each row-distance path
+    (contiguous chunks for row strides of at most 32, 64, 104 and 128 floats,
+    column slabs above)."""
+    rng = np.random.default_rng(2 + d)
+    n, k = 5000, 13
     X = (rng.standard_normal((n, d)) * 2).astype(np.float32)
     C = rng.standard_normal((k, d)).astype(np.float32)
     lab = rng.integers(0, k, n).astype(np.int32)
@@ -451,6 +455,30 @@ def test_relocation_of_several_empty_clusters(bridge, n_dup, k_base, monkeypatch
     for where in ("halt+device", "host"):
         parity.check_centers(res["in-stream"][2], res[where][2], rtol=1e-5,
                              what=f"in-stream vs {where} relocation")
+
+
+@pytest.mark.parametrize("d", [100, 200])
+def test_relocation_wide_rows(bridge, d, monkeypatch):
+    """Four empty clusters relocated on rows of 100 and 200 features (the
+    contiguous and the column-slab row-distance paths of the relocation):
+    the step that relocates against the oracle, then three steps across the
+    relocation paths (16 centres on 6 blobs meet near ties in later steps
+    that the oracle's fp64 distances may settle otherwise)."""
+    rng = np.random.default_rng(70 + d)
+    cen = rng.uniform(-8, 8, (6, d))
+    X = (cen[rng.integers(0, 6, 6000)] + rng.standard_normal((6000, d))).astype(np.float32)
+    base = X[np.sort(rng.choice(6000, 12, replace=False))]
+    C0 = np.concatenate([base, base[:4]])
+    out = oracle.lloyd(X, C0, 1)
+    res = _fit_each_relocation_path(bridge, monkeypatch, X, C0, 1)
+    for where, (n_iter, inertia, C) in res.items():
+        assert n_iter == out["n_iter"], f"{where}: n_iter {n_iter} vs oracle {out['n_iter']}"
+        parity.check_centers(C, out["centers"], what=f"{where} relocation d={d}")
+    res = _fit_each_relocation_path(bridge, monkeypatch, X, C0, 3)
+    for where in ("halt+device", "host"):
+        assert res["in-stream"][0] == res[where][0]
+        parity.check_centers(res["in-stream"][2], res[where][2], rtol=1e-5,
+                             what=f"in-stream vs {where} relocation d={d}, 3 steps")
 
 
 @pytest.mark.parametrize("wl,steps", [("c1", 4), ("c2", 3)])
