@@ -41,11 +41,13 @@ Parity status per function (what pins it, see tests/test_oracle.py):
 * ``kmeans_parallel_init`` (skmetal's k-means||) -- its distances against
                      scikit-learn's euclidean_distances(squared=True) and brute
                      force; the first draw, the round count, the {0} taken-set
-                     rule and the cyclic fill by properties
-                     (tests/test_kpar_oracle.py).  The sampling loop itself is
-                     parity unpinned: the reference runs it over its Metal
-                     kernels, which cannot run here, and its tests hold no
-                     vectors for it.
+                     rule and the cyclic fill by properties; the whole
+                     seeding (every round's candidate rows, the final list,
+                     the centroids) bit for bit against golden vectors of the
+                     reference's own MetalKMeans._kmeans_parallel_init, run in
+                     the build container with numpy distances in place of its
+                     two Metal calls (tests/golden/kpar.npz, 6 cases;
+                     tests/test_kpar_oracle.py).
 """
 
 from __future__ import annotations

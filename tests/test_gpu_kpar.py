@@ -99,6 +99,22 @@ def test_parallel_init_matches_oracle(bridge, n, d, k, seed):
     np.testing.assert_array_equal(got, ref)
 
 
+def test_parallel_init_matches_reference_method(bridge):
+    """The device path against the reference method's own draws and prune
+    (tests/golden/kpar.npz, written by make_kpar_fixtures.py)."""
+    from skmetal_amd.estimators.cluster import kmeans_parallel_init
+    from test_kpar_oracle import KPAR
+
+    for c, a in KPAR:
+        X = a["X"]
+        n, d = X.shape
+        _say(f"k-means|| vs reference vectors {c['name']}")
+        with bridge.LloydHandle(n, d, c["k"]) as h:
+            h.load(X, center=False)
+            got = kmeans_parallel_init(X, c["k"], np.random.RandomState(c["seed"]), h)
+        np.testing.assert_array_equal(got, a["centroids"], err_msg=c["name"])
+
+
 def test_metal_kmeans_fit(bridge):
     from sklearn.cluster import KMeans
 

@@ -1,17 +1,59 @@
 """The oracle's restatement of skmetal's k-means|| seeding
 (MetalKMeans._kmeans_parallel_init, skmetal/estimators/cluster.py:70-116),
-checked on the CPU: its distances against scikit-learn and brute force, and
-the loop's rules (first draw, round count, the {0} taken set, the cyclic fill)
-by properties.  The sampling loop has no reference vectors (the reference runs
-it over its Metal kernels): parity unpinned there."""
+checked on the CPU: its distances against scikit-learn and brute force, the
+loop's rules (first draw, round count, the {0} taken set, the cyclic fill) by
+properties, and the whole seeding against golden vectors of the reference's
+own method (tests/golden/kpar.npz, written by make_kpar_fixtures.py, which runs
+MetalKMeans._kmeans_parallel_init with numpy distances in place of its two
+bridge calls): the candidate rows of every round, the final candidate list and
+the k centroids, bit for bit."""
 
 from __future__ import annotations
+
+import json
+from pathlib import Path
 
 import numpy as np
 import pytest
 from sklearn.metrics.pairwise import euclidean_distances
 
 import oracle
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def kpar_cases():
+    """(case metadata, arrays) of the reference's k-means|| fixtures."""
+    meta = json.loads((GOLDEN / "kpar.json").read_text())
+    with np.load(GOLDEN / "kpar.npz") as z:
+        arrays = {key: z[key] for key in z.files}
+    return [(c, {key[len(c["name"]) + 2:]: v for key, v in arrays.items() if key.startswith(c["name"] + "__")})
+            for c in meta["cases"]]
+
+
+KPAR = kpar_cases()
+
+
+@pytest.mark.parametrize("case", KPAR, ids=[c[0]["name"] for c in KPAR])
+def test_oracle_matches_reference_method(case):
+    c, a = case
+    X = a["X"]
+    C, rows = oracle.kmeans_parallel_init(X, c["k"], np.random.RandomState(c["seed"]), trace=True)
+    rows = np.asarray(rows, dtype=np.int64)
+    for r in range(c["rounds"]):
+        ref = a[f"round{r}_rows"]
+        np.testing.assert_array_equal(rows[: len(ref)], ref, err_msg=f"candidates at round {r}")
+    np.testing.assert_array_equal(rows, a["final_rows"])
+    np.testing.assert_array_equal(C, a["centroids"])
+
+
+def test_reference_vectors_show_the_taken_set_quirk():
+    # the reference's taken set starts as {0} (cluster.py:86): in the case that
+    # draws every row, row 0 never joins and the first row joins twice
+    c, a = next(x for x in KPAR if x[0]["name"] == "all_rows_10x3_k10")
+    rows = list(a["final_rows"])
+    first = np.random.RandomState(c["seed"]).randint(c["n"])
+    assert first != 0 and 0 not in rows and rows.count(first) == 2
 
 
 def _blobs(n, d, k, seed):
