@@ -520,10 +520,11 @@ template <int CPT>
 __global__ __launch_bounds__(256) void k_segsum(SortArgs a, int B, int G)
 {
     if (a.state->done != 0) return;
-    constexpr int U = 16;  // sorted rows in flight
-    const int groups = 256 / G;
+    constexpr int U = 64 / CPT;  // sorted rows per batch: 64 loads in flight per thread
+    const int groups = 256 / G;  // G >= 64: a wave lies in one group
     const int grp = threadIdx.x / G;
     const int t = threadIdx.x - grp * G;
+    const int lane = threadIdx.x & 63;
     const long c = (long)blockIdx.x * groups + grp;
     const long p0 = c * B;
     if (p0 >= a.n) return;
@@ -549,38 +550,38 @@ __global__ __launch_bounds__(256) void k_segsum(SortArgs a, int B, int G)
             acc[i] = 0.f;
         }
     };
-    // the labels and row ids of a batch are loaded one batch ahead, so a
-    // batch's X rows and the next batch's ids are in flight together
-    int lab[U], rid[U];
+    // lane u holds the label and row id of sorted row p + u (clamped to the
+    // chunk); a batch's ids are loaded one batch ahead, and each row's id is
+    // read out of its lane, so the row loads have a scalar base
+    int labv, ridv;
     auto load_ids = [&](long p) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const long q = p + u < p1 ? p + u : p1 - 1;
-            lab[u] = a.slab[q];
-            rid[u] = a.perm[q];
-        }
+        const long q = min(p + lane, p1 - 1);
+        labv = a.slab[q];
+        ridv = a.perm[q];
     };
     load_ids(p0);
     for (long p = p0; p < p1; p += U) {
         float v[U][CPT];
-        int lb[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            lb[u] = lab[u];
-            const float* row = a.X + (long)rid[u] * a.ld;
+            const float* row = a.X + (long)__builtin_amdgcn_readlane(ridv, u) * a.ld;
 #pragma unroll
             for (int i = 0; i < CPT; ++i) v[u][i] = on[i] ? row[cols[i]] : 0.f;
         }
+        const int labb = labv;
         if (p + U < p1) load_ids(p + U);
+        const int nb = (int)min((long)U, p1 - p);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            if (p + u >= p1) break;
-            if (lb[u] != cur) {
-                flush(cur);
-                cur = lb[u];
-            }
+            if (u < nb) {
+                const int lb = __builtin_amdgcn_readlane(labb, u);
+                if (lb != cur) {
+                    flush(cur);
+                    cur = lb;
+                }
 #pragma unroll
-            for (int i = 0; i < CPT; ++i) acc[i] += v[u][i];
+                for (int i = 0; i < CPT; ++i) acc[i] += v[u][i];
+            }
         }
     }
     flush(cur);
