@@ -197,6 +197,7 @@ __global__ __launch_bounds__(512, 1) void k_fused(FusedArgs a)
     __shared__ int sReady[4];  // tiles the MFMA wave has put in LDS
     __shared__ int sProg[4];   // chunks the walker has read: tile * NQ + chunk
     __shared__ int sDone;      // nonzero: the loop has halted, nothing to do
+    __shared__ int sChg;       // labels the block's MFMA waves changed
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps descriptors scalar
@@ -308,7 +309,8 @@ __global__ __launch_bounds__(512, 1) void k_fused(FusedArgs a)
             round(r + 1, preB);
         }
         if (r < rounds) round(r, preA);
-        if (lane == 0 && changed != 0) atomicAdd(a.changed, changed);
+        // one global atomic per block (below), not one per wave
+        if (lane == 0 && changed != 0) atomicAdd(&sChg, changed);
         __syncthreads();  // every pair's walker is done: the tile area is free
         __syncthreads();  // the walkers' sums are in LDS
     } else {
@@ -343,6 +345,7 @@ __global__ __launch_bounds__(512, 1) void k_fused(FusedArgs a)
             sReady[wt] = 0;
             sProg[wt] = 0;
         }
+        if (wt == 0) sChg = 0;
         if (wave == 4) step_norms<CPC>(a, lane, sN, &sDone);
         __syncthreads();
         if (sDone != 0) return;
@@ -355,6 +358,7 @@ __global__ __launch_bounds__(512, 1) void k_fused(FusedArgs a)
         publish_sums<CPC, NQ>(S, cnt, zrow + XS, ld, pair, lane, sCnt);
         __syncthreads();
     }
+    if (tid == 0 && sChg != 0) atomicAdd(a.changed, sChg);
     combine_sums<CPC>(zrow + XS, ld, k, psum, pcnt, sCnt, tid, &st->present[a.iter & 1]);
 }
 

@@ -51,10 +51,13 @@ __global__ __launch_bounds__(256, 1) void k_assign(const float* __restrict__ X, 
     constexpr int LS = SEG + 4;   // LDS row stride (floats): conflict-free b128 reads
     __shared__ __attribute__((aligned(16))) float sC[CPC * LS];
     __shared__ float sN[CPC];
+    __shared__ int sChg;  // labels the block changed
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps descriptors scalar
+    if (tid == 0) sChg = 0;  // (published by the first staging barrier, or read back by this thread)
+    int nchg = 0;            // lane 0: labels this wave changed
     const int nchunk = (k + CPC - 1) / CPC;
     const int nseg = (ld + SEG - 1) / SEG;
     const bool single = (nchunk == 1) && (nseg == 1);
@@ -129,15 +132,19 @@ __global__ __launch_bounds__(256, 1) void k_assign(const float* __restrict__ X, 
                 }
             }
         }
+        int moved = 0;
         if (row < n) {
-            int moved = 0;
             if (changed != nullptr) moved = labels[row] != bidx;
             labels[row] = bidx;
-            if (changed != nullptr) {
-                const unsigned long long m = __ballot(moved);
-                if (lane == 0 && m != 0ull) atomicAdd(changed, (int)__popcll(m));
-            }
         }
+        if (changed != nullptr) nchg += (int)__popcll(__ballot(moved));
+    }
+    // one global atomic per block: a wave-level atomic per 64 rows on one
+    // address serialises thousands of them while labels move
+    if (changed != nullptr) {
+        if (lane == 0 && nchg != 0) atomicAdd(&sChg, nchg);
+        __syncthreads();
+        if (tid == 0 && sChg != 0) atomicAdd(changed, sChg);
     }
 }
 

@@ -227,6 +227,7 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
     __shared__ int sReady[8];  // half tiles E-step wave e has labelled
     __shared__ int sProg[8];   // feature blocks sums wave w has read: tile * (its blocks) + blocks
     __shared__ int sDone;      // nonzero: the loop has halted, nothing to do
+    __shared__ int sChg;       // labels the block's E-step waves changed
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -438,7 +439,9 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
             if (valid) atomicOr(&mw[bi], 1u << lane);
             set_flag(&sReady[e], r + 1);
         }
-        if (lane == 0 && changed != 0) atomicAdd(a.changed, changed);
+        // one global atomic per block (below): 2,048 waves adding to one
+        // address at the end of a step cost up to 16 us while labels move
+        if (lane == 0 && changed != 0) atomicAdd(&sChg, changed);
         __syncthreads();  // every sums wave is done: the tile area is free
         __syncthreads();  // the sums are in LDS
     } else {
@@ -557,6 +560,7 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
             sReady[wt] = 0;
             sProg[wt] = 0;
         }
+        if (wt == 0) sChg = 0;
         if (wt < 256) {
             sCnt[wt >> 6][wt & 63] = 0;
             unsigned w[4];
@@ -674,6 +678,7 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
             sums(std::integral_constant<int, NFA>{}, std::integral_constant<int, NFZ>{});
         __syncthreads();
     }
+    if (tid == 0 && sChg != 0) atomicAdd(a.changed, sChg);
     combine_sums<CPC, 1024>(lds, ld, k, a.psum, a.pcnt, sCnt, tid, &a.state->present[a.iter & 1]);
 }
 
@@ -706,10 +711,13 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
     constexpr int CPC = G::CPC, SEG = G::SEG, NKS = G::NKS, CSTR = G::CSTR, CPART = G::CPART;
     extern __shared__ __attribute__((aligned(16))) __bf16 cs[];  // [3][CPC][CSTR]
     __shared__ __attribute__((aligned(16))) float sN[CPC];
+    __shared__ int sChg;  // labels the block changed
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 4, r16 = lane & 15;
+    if (tid == 0) sChg = 0;  // (published by the first staging barrier, or read back by this thread)
+    int nchg = 0;            // lane 0: labels this wave changed
     const int npass = (k + CPC - 1) / CPC;
     const int nseg = (ld + SEG - 1) / SEG;
     const __bf16* const cbase = cs + r16 * CSTR + 8 * h;
@@ -841,10 +849,14 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
             if (changed != nullptr) moved = labels[row] != mylab;
             labels[row] = mylab;
         }
-        if (changed != nullptr) {
-            const unsigned long long mm = __ballot(moved);
-            if (lane == 0 && mm != 0ull) atomicAdd(changed, (int)__popcll(mm));
-        }
+        if (changed != nullptr) nchg += (int)__popcll(__ballot(moved));
+    }
+    // one global atomic per block: a wave-level atomic per 32 rows on one
+    // address serialises thousands of them while labels move
+    if (changed != nullptr) {
+        if (lane == 0 && nchg != 0) atomicAdd(&sChg, nchg);
+        __syncthreads();
+        if (tid == 0 && sChg != 0) atomicAdd(changed, sChg);
     }
 }
 
