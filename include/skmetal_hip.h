@@ -39,6 +39,7 @@ extern "C" {
 #define SKMETAL_ELAUNCH 4  /* kernel launch failed */
 #define SKMETAL_EHIP 5     /* any other HIP runtime error */
 #define SKMETAL_ERANGE 6   /* a size exceeds what the library supports */
+#define SKMETAL_ENOSYS 7   /* a registry name outside the KMeans path (not provided) */
 
 /* ---- set-up: skmetal_bridge/Sources/SkMetalBridgeC/include/bridge.h:11-12,60;
  *      Bridge.swift:19-48,52-144; bound at skmetal/_bridge.py:352-363 ---- */
@@ -90,6 +91,67 @@ SKMETAL_API float skmetal_kmeans_inertia(const void* X, const void* centroids, c
  * (bridge.h:45; KMeansBridge.swift:89-134; _bridge.py:133-142, 620-624). */
 SKMETAL_API int skmetal_compute_mindists(const void* X, const void* centroids, const void* assignments,
                              void* dists, size_t n, size_t d, size_t k);
+
+/* C = alpha op(A) op(B) + beta C in fp32, row-major A [M x K] (or [K x M] when
+ * transpose_A), B [K x N] (or [N x K]), C [M x N]; with beta == 0 C is
+ * write-only.  rocBLAS sgemm on the library's stream (librocblas is opened on
+ * the first call).  Replaces skmetal_gemm (bridge.h:14-19; the MPS matrix
+ * multiply bound at skmetal/_bridge.py:143-155 and called by
+ * skmetal/_bridge.py:499-560), which skmetal's MetalKMeans.transform uses for
+ * x.c^T (skmetal/estimators/cluster.py:135-146). */
+SKMETAL_API int skmetal_gemm(const void* A, const void* B, void* C, size_t M, size_t N, size_t K, float alpha,
+                             float beta, int transpose_A, int transpose_B);
+
+/* ---- the rest of skmetal's ctypes registry (skmetal/_bridge.py:107-345) ----
+ * skmetal's loader binds every registry name when the library loads
+ * (skmetal/_bridge.py:345-349), so the names outside the KMeans path are
+ * exported; each returns SKMETAL_ENOSYS with a message naming it, and
+ * skmetal's wrappers raise RuntimeError("<name> failed with code 7").  The
+ * argument lists follow the registry's argtypes. */
+SKMETAL_API int skmetal_pairwise_distance(const void* X, void* D, size_t n, size_t d);
+SKMETAL_API int skmetal_scaler_fit(const void* X, void* mean_out, void* var_out, size_t n, size_t d);
+SKMETAL_API int skmetal_column_minmax(const void* X, void* min_out, void* max_out, size_t n, size_t d);
+SKMETAL_API int skmetal_fista_fit(const void* X, const void* y, void* w, size_t n, size_t d, float alpha,
+                                  float l1_ratio, float tol, int32_t max_iter, int32_t* n_iter_out);
+SKMETAL_API int skmetal_column_transform(const void* input, void* output, const void* center, const void* scale,
+                                         size_t n, size_t d);
+SKMETAL_API int skmetal_sv_init(void* parent, size_t n);
+SKMETAL_API int skmetal_sv_hook(void* parent, const void* edges, size_t n, size_t m);
+SKMETAL_API int skmetal_sv_shortcut(void* parent, size_t n);
+SKMETAL_API int skmetal_knn_vote_classify(const void* indices, const void* train_labels, void* predictions,
+                                          size_t n, size_t k, size_t n_classes);
+SKMETAL_API int skmetal_knn_vote_regress(const void* indices, const void* train_targets, void* predictions,
+                                         size_t n, size_t k, size_t n_outputs);
+SKMETAL_API int skmetal_knn_vote_classify_weighted(const void* indices, const void* weights, const void* train_labels,
+                                                   void* predictions, size_t n, size_t k, size_t n_classes);
+SKMETAL_API int skmetal_knn_vote_regress_weighted(const void* indices, const void* weights, const void* train_targets,
+                                                  void* predictions, size_t n, size_t k, size_t n_outputs);
+SKMETAL_API int skmetal_knn_tiled_kneighbors(const void* Q, const void* X, void* out_indices, void* out_dists,
+                                             size_t nq, size_t nx, size_t d, size_t k, size_t tile, int32_t metric);
+SKMETAL_API int skmetal_rbf_kernel_square(const void* X, void* K, float gamma, size_t n, size_t d);
+SKMETAL_API int skmetal_rbf_kernel_cross(const void* X, const void* Y, void* K, float gamma, size_t n, size_t m,
+                                         size_t d);
+SKMETAL_API int skmetal_tree_predict_all(const void* X, const void* feature, const void* threshold,
+                                         const void* left, const void* right, const void* value,
+                                         const void* tree_offsets, const void* value_offsets, const void* n_nodes,
+                                         const void* weights, void* out, size_t n, size_t d, size_t n_trees);
+SKMETAL_API int skmetal_svc_predict_binary(const void* X, const void* sv, const void* dual_coef,
+                                           const void* intercept, void* out, size_t n, size_t n_sv, size_t d,
+                                           float gamma);
+SKMETAL_API int skmetal_logreg_irls_fit(const void* X, const void* y, void* w, float C, float tol, int32_t max_iter,
+                                        int32_t fit_intercept, size_t n, size_t d, int32_t* n_iter_out);
+SKMETAL_API int skmetal_logreg_lbfgs_fit(const void* X, const void* y, void* w, float C, float tol, int32_t max_iter,
+                                         int32_t fit_intercept, size_t n, size_t d, int32_t* n_iter_out);
+SKMETAL_API int skmetal_ridge_fit_solve(const void* X, const void* y, void* coef, void* intercept, float alpha,
+                                        size_t n, size_t d);
+SKMETAL_API int skmetal_multinomial_lbfgs_fit(const void* X, const void* y, void* W, float C, float tol,
+                                              int32_t max_iter, size_t n, size_t d, size_t n_classes,
+                                              int32_t* n_iter_out);
+SKMETAL_API int skmetal_minmax_transform(const void* X, void* X_out, const void* min_vals, const void* max_vals,
+                                         size_t n, size_t d, float feature_min, float feature_max);
+SKMETAL_API int skmetal_convert_f32_to_f16(const void* input, void* output, size_t n);
+SKMETAL_API int skmetal_convert_f16_to_f32(const void* input, void* output, size_t n);
+SKMETAL_API int skmetal_gemm_f16(const void* A, const void* B, void* C, size_t M, size_t N, size_t K);
 
 /* ---- additions without a counterpart in the reference ---- */
 

@@ -44,6 +44,8 @@ _REGISTRY = [
     ("skmetal_kmeans_batch_fused", ctypes.c_int, _vp, _vp, _vp, _c_size, _c_size, _c_size, _c_size, _c_size,
      ctypes.c_float, ctypes.POINTER(ctypes.c_int32)),
     ("skmetal_compute_mindists", ctypes.c_int, _vp, _vp, _vp, _vp, _c_size, _c_size, _c_size),
+    ("skmetal_gemm", ctypes.c_int, _vp, _vp, _vp, _c_size, _c_size, _c_size, ctypes.c_float, ctypes.c_float,
+     ctypes.c_int, ctypes.c_int),
     ("skmetal_kmeans_inertia", ctypes.c_float, _vp, _vp, _vp, _c_size, _c_size, _c_size),
     ("skmetal_hip_last_error", ctypes.c_char_p),
     ("skmetal_hip_release_cache", ctypes.c_int),
@@ -208,6 +210,35 @@ def kmeans_inertia(X, centroids, assignments, n, d, k) -> float:
     ensure_warmed_up()
     return float(_lib.skmetal_kmeans_inertia(X.ctypes.data, centroids.ctypes.data, assignments.ctypes.data,
                                              n, d, k))
+
+
+def gemm(A, B, alpha: float = 1.0, beta: float = 0.0, trans_A: bool = False, trans_B: bool = False, C=None):
+    """C = alpha * op(A) @ op(B) + beta * C in fp32 on the device (skmetal_gemm).
+
+    The reference's gemm (skmetal/_bridge.py:499-560) with its argument checks;
+    its last route, the bridge's fp32 GEMM, is the only one here.  C is read
+    only when beta != 0 (then it must be given, [M x N] float32)."""
+    _require()
+    if A.dtype != np.float32 or B.dtype != np.float32:
+        raise TypeError("A and B must be float32")
+    if not (A.flags["C_CONTIGUOUS"] and B.flags["C_CONTIGUOUS"]):
+        raise ValueError("A and B must be C-contiguous")
+    M, K = (A.shape[1], A.shape[0]) if trans_A else (A.shape[0], A.shape[1])
+    K2, N = (B.shape[1], B.shape[0]) if trans_B else (B.shape[0], B.shape[1])
+    if K != K2:
+        raise ValueError(f"Incompatible dimensions: A {A.shape}, B {B.shape}")
+    if beta != 0.0:
+        if C is None:
+            raise ValueError("beta != 0 needs C")
+        _f32c(C, "C")
+        if C.shape != (M, N):
+            raise ValueError(f"C has shape {C.shape}, expected {(M, N)}")
+        out = C
+    else:
+        out = np.empty((M, N), dtype=np.float32)
+    _bridge_call(_lib.skmetal_gemm, A, B, out, M, N, K, ctypes.c_float(alpha), ctypes.c_float(beta),
+                 ctypes.c_int(int(trans_A)), ctypes.c_int(int(trans_B)), context=f"M={M} N={N} K={K}")
+    return out
 
 
 def device_info() -> dict:

@@ -24,6 +24,9 @@
 #include <thread>
 #include <vector>
 
+#include <dlfcn.h>
+#include <rocblas/rocblas.h>  // types only: librocblas is opened on the first skmetal_gemm
+
 #include "skmetal_hip.h"
 #include "internal.h"
 
@@ -1047,6 +1050,41 @@ struct skmetal_hip_lloyd {
     Lloyd L;
 };
 
+// rocBLAS, opened on the first skmetal_gemm call
+namespace {
+struct Blas {
+    bool tried = false;
+    void* so = nullptr;
+    rocblas_handle handle = nullptr;
+    decltype(&rocblas_create_handle) create = nullptr;
+    decltype(&rocblas_set_stream) set_stream = nullptr;
+    decltype(&rocblas_sgemm) sgemm = nullptr;
+};
+Blas g_blas;
+
+int blas_ready(Context& c)
+{
+    Blas& b = g_blas;
+    if (b.handle) return 0;
+    if (b.tried) return fail(SKMETAL_ENODEV, "rocBLAS is not available (librocblas could not be opened earlier)");
+    b.tried = true;
+    for (const char* name : {"librocblas.so.5", "librocblas.so"}) {
+        b.so = dlopen(name, RTLD_NOW | RTLD_LOCAL);
+        if (b.so) break;
+    }
+    if (!b.so) return fail(SKMETAL_ENODEV, "skmetal_gemm needs rocBLAS: %s", dlerror());
+    b.create = reinterpret_cast<decltype(b.create)>(dlsym(b.so, "rocblas_create_handle"));
+    b.set_stream = reinterpret_cast<decltype(b.set_stream)>(dlsym(b.so, "rocblas_set_stream"));
+    b.sgemm = reinterpret_cast<decltype(b.sgemm)>(dlsym(b.so, "rocblas_sgemm"));
+    if (!b.create || !b.set_stream || !b.sgemm) return fail(SKMETAL_ENODEV, "librocblas lacks rocblas_sgemm");
+    rocblas_handle h = nullptr;
+    if (b.create(&h) != rocblas_status_success) return fail(SKMETAL_EHIP, "rocblas_create_handle failed");
+    if (b.set_stream(h, c.stream) != rocblas_status_success) return fail(SKMETAL_EHIP, "rocblas_set_stream failed");
+    b.handle = h;
+    return 0;
+}
+}  // namespace
+
 extern "C" {
 
 const char* skmetal_hip_last_error(void) { return g_err.c_str(); }
@@ -1476,6 +1514,139 @@ int skmetal_hip_kmeans_transform(const float* X, const float* centroids, float* 
     }
     return 0;
 }
+
+// ---------------------------------------------------------------------------
+// skmetal_gemm: the reference's fp32 GEMM entry point (its MPS matrix
+// multiply), which skmetal's MetalKMeans.transform calls for x.c^T.  A plain
+// library GEMM: rocBLAS sgemm on the library's stream, with librocblas opened
+// on the first call (the rest of the library does not depend on it).
+// ---------------------------------------------------------------------------
+
+int skmetal_gemm(const void* A, const void* B, void* C, size_t M, size_t N, size_t K, float alpha, float beta,
+                 int transpose_A, int transpose_B)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!A || !B || !C) return fail(SKMETAL_EINVAL, "null pointer argument");
+    if (M == 0 || N == 0 || K == 0) return fail(SKMETAL_EINVAL, "M, N and K must be positive (M=%zu N=%zu K=%zu)", M, N, K);
+    const size_t lim = size_t(INT32_MAX);
+    if (M > lim || N > lim || K > lim || M * K > (size_t(1) << 36) || K * N > (size_t(1) << 36) ||
+        M * N > (size_t(1) << 36))
+        return fail(SKMETAL_ERANGE, "gemm sizes too large (M=%zu N=%zu K=%zu)", M, N, K);
+    TRY(c.init());
+    TRY(blas_ready(c));
+    struct Bufs {
+        Context& c;
+        std::vector<void*> p;
+        ~Bufs() { for (void* q : p) c.release(q); }
+        int get(void** out, size_t bytes)
+        {
+            TRY(c.alloc(out, bytes));
+            p.push_back(*out);
+            return 0;
+        }
+    } b{c, {}};
+    float *dA = nullptr, *dB = nullptr, *dC = nullptr;
+    TRY(b.get((void**)&dA, M * K * sizeof(float)));
+    TRY(b.get((void**)&dB, K * N * sizeof(float)));
+    TRY(b.get((void**)&dC, M * N * sizeof(float)));
+    TRY(upload_bytes(c, A, M * K * sizeof(float), dA, c.stream));
+    TRY(upload_bytes(c, B, K * N * sizeof(float), dB, c.stream));
+    // beta == 0 ignores C's contents (the caller's C may be uninitialised)
+    if (beta != 0.f) TRY(upload_bytes(c, C, M * N * sizeof(float), dC, c.stream));
+    // row-major C = op(A) op(B) is column-major C^T = op(B)^T op(A)^T: the
+    // row-major buffers read as column-major are the transposes
+    const rocblas_operation ta = transpose_A ? rocblas_operation_transpose : rocblas_operation_none;
+    const rocblas_operation tb = transpose_B ? rocblas_operation_transpose : rocblas_operation_none;
+    const int lda = (int)(transpose_A ? M : K), ldb = (int)(transpose_B ? K : N);
+    if (g_blas.sgemm(g_blas.handle, tb, ta, (int)N, (int)M, (int)K, &alpha, dB, ldb, dA, lda, &beta, dC, (int)N) !=
+        rocblas_status_success)
+        return fail(SKMETAL_EHIP, "rocblas_sgemm failed");
+    return download_bytes(c, dC, M * N * sizeof(float), C, c.stream);
+}
+
+// ---------------------------------------------------------------------------
+// The other names of skmetal's ctypes registry (skmetal/_bridge.py:107-345):
+// its loader binds every one of them when the library loads, so they are
+// exported; each returns SKMETAL_ENOSYS (skmetal's wrappers then raise
+// RuntimeError("<name> failed with code 7"), as for any failed call).
+// ---------------------------------------------------------------------------
+#define SKM_NOT_PROVIDED(name) return fail(SKMETAL_ENOSYS, "%s is not provided: libskmetal_hip.so is skmetal's KMeans path", name)
+
+int skmetal_pairwise_distance(const void*, void*, size_t, size_t) { SKM_NOT_PROVIDED("skmetal_pairwise_distance"); }
+int skmetal_scaler_fit(const void*, void*, void*, size_t, size_t) { SKM_NOT_PROVIDED("skmetal_scaler_fit"); }
+int skmetal_column_minmax(const void*, void*, void*, size_t, size_t) { SKM_NOT_PROVIDED("skmetal_column_minmax"); }
+int skmetal_fista_fit(const void*, const void*, void*, size_t, size_t, float, float, float, int32_t, int32_t*)
+{
+    SKM_NOT_PROVIDED("skmetal_fista_fit");
+}
+int skmetal_column_transform(const void*, void*, const void*, const void*, size_t, size_t)
+{
+    SKM_NOT_PROVIDED("skmetal_column_transform");
+}
+int skmetal_sv_init(void*, size_t) { SKM_NOT_PROVIDED("skmetal_sv_init"); }
+int skmetal_sv_hook(void*, const void*, size_t, size_t) { SKM_NOT_PROVIDED("skmetal_sv_hook"); }
+int skmetal_sv_shortcut(void*, size_t) { SKM_NOT_PROVIDED("skmetal_sv_shortcut"); }
+int skmetal_knn_vote_classify(const void*, const void*, void*, size_t, size_t, size_t)
+{
+    SKM_NOT_PROVIDED("skmetal_knn_vote_classify");
+}
+int skmetal_knn_vote_regress(const void*, const void*, void*, size_t, size_t, size_t)
+{
+    SKM_NOT_PROVIDED("skmetal_knn_vote_regress");
+}
+int skmetal_knn_vote_classify_weighted(const void*, const void*, const void*, void*, size_t, size_t, size_t)
+{
+    SKM_NOT_PROVIDED("skmetal_knn_vote_classify_weighted");
+}
+int skmetal_knn_vote_regress_weighted(const void*, const void*, const void*, void*, size_t, size_t, size_t)
+{
+    SKM_NOT_PROVIDED("skmetal_knn_vote_regress_weighted");
+}
+int skmetal_knn_tiled_kneighbors(const void*, const void*, void*, void*, size_t, size_t, size_t, size_t, size_t,
+                                 int32_t)
+{
+    SKM_NOT_PROVIDED("skmetal_knn_tiled_kneighbors");
+}
+int skmetal_rbf_kernel_square(const void*, void*, float, size_t, size_t) { SKM_NOT_PROVIDED("skmetal_rbf_kernel_square"); }
+int skmetal_rbf_kernel_cross(const void*, const void*, void*, float, size_t, size_t, size_t)
+{
+    SKM_NOT_PROVIDED("skmetal_rbf_kernel_cross");
+}
+int skmetal_tree_predict_all(const void*, const void*, const void*, const void*, const void*, const void*, const void*,
+                             const void*, const void*, const void*, void*, size_t, size_t, size_t)
+{
+    SKM_NOT_PROVIDED("skmetal_tree_predict_all");
+}
+int skmetal_svc_predict_binary(const void*, const void*, const void*, const void*, void*, size_t, size_t, size_t, float)
+{
+    SKM_NOT_PROVIDED("skmetal_svc_predict_binary");
+}
+int skmetal_logreg_irls_fit(const void*, const void*, void*, float, float, int32_t, int32_t, size_t, size_t, int32_t*)
+{
+    SKM_NOT_PROVIDED("skmetal_logreg_irls_fit");
+}
+int skmetal_logreg_lbfgs_fit(const void*, const void*, void*, float, float, int32_t, int32_t, size_t, size_t, int32_t*)
+{
+    SKM_NOT_PROVIDED("skmetal_logreg_lbfgs_fit");
+}
+int skmetal_ridge_fit_solve(const void*, const void*, void*, void*, float, size_t, size_t)
+{
+    SKM_NOT_PROVIDED("skmetal_ridge_fit_solve");
+}
+int skmetal_multinomial_lbfgs_fit(const void*, const void*, void*, float, float, int32_t, size_t, size_t, size_t,
+                                  int32_t*)
+{
+    SKM_NOT_PROVIDED("skmetal_multinomial_lbfgs_fit");
+}
+int skmetal_minmax_transform(const void*, void*, const void*, const void*, size_t, size_t, float, float)
+{
+    SKM_NOT_PROVIDED("skmetal_minmax_transform");
+}
+int skmetal_convert_f32_to_f16(const void*, void*, size_t) { SKM_NOT_PROVIDED("skmetal_convert_f32_to_f16"); }
+int skmetal_convert_f16_to_f32(const void*, void*, size_t) { SKM_NOT_PROVIDED("skmetal_convert_f16_to_f32"); }
+int skmetal_gemm_f16(const void*, const void*, void*, size_t, size_t, size_t) { SKM_NOT_PROVIDED("skmetal_gemm_f16"); }
+#undef SKM_NOT_PROVIDED
 
 int skmetal_hip_column_variance(const float* X, size_t n, size_t d, float* out)
 {

@@ -42,6 +42,22 @@ REFERENCE_KMEANS_ABI = {
     "skmetal_compute_mindists",
 }
 
+# every name of skmetal's ctypes registry (skmetal/_bridge.py:107-345), which
+# its loader binds eagerly when the library loads (:345-349)
+REFERENCE_REGISTRY = [
+    "skmetal_pairwise_distance", "skmetal_scaler_fit", "skmetal_column_minmax", "skmetal_kmeans_assign",
+    "skmetal_kmeans_batch_fused", "skmetal_compute_mindists", "skmetal_gemm", "skmetal_fista_fit",
+    "skmetal_column_transform", "skmetal_sv_init", "skmetal_sv_hook", "skmetal_sv_shortcut",
+    "skmetal_knn_vote_classify", "skmetal_knn_vote_regress", "skmetal_knn_vote_classify_weighted",
+    "skmetal_knn_vote_regress_weighted", "skmetal_knn_tiled_kneighbors", "skmetal_rbf_kernel_square",
+    "skmetal_rbf_kernel_cross", "skmetal_tree_predict_all", "skmetal_svc_predict_binary", "skmetal_logreg_irls_fit",
+    "skmetal_logreg_lbfgs_fit", "skmetal_ridge_fit_solve", "skmetal_multinomial_lbfgs_fit",
+    "skmetal_minmax_transform", "skmetal_convert_f32_to_f16", "skmetal_convert_f16_to_f32", "skmetal_gemm_f16",
+]
+# the registry names this library implements; the others return SKMETAL_ENOSYS
+PROVIDED = REFERENCE_KMEANS_ABI | {"skmetal_gemm"}
+NOT_PROVIDED = set(REFERENCE_REGISTRY) - PROVIDED
+
 
 def _declared() -> set[str]:
     text = HEADER.read_text()
@@ -60,8 +76,31 @@ def lib_path() -> Path:
 def test_header_declares_reference_kmeans_abi():
     names = _declared()
     assert REFERENCE_KMEANS_ABI <= names
-    extra = names - REFERENCE_KMEANS_ABI
+    assert set(REFERENCE_REGISTRY) <= names
+    extra = names - REFERENCE_KMEANS_ABI - set(REFERENCE_REGISTRY)
     assert all(n.startswith("skmetal_hip_") for n in extra), extra
+
+
+def test_reference_loader_binds_every_registry_name(lib_path):
+    # what skmetal/_bridge.py:345-349 does when the library loads: getattr of
+    # every registry name (a missing one raises AttributeError at import)
+    lib = ctypes.CDLL(str(lib_path))
+    for name in REFERENCE_REGISTRY:
+        f = getattr(lib, name)
+        f.restype = ctypes.c_int
+    assert len(NOT_PROVIDED) == 25
+
+
+def test_registry_names_outside_kmeans_return_enosys(lib_path):
+    # the stubs touch no device: callable without a GPU
+    lib = ctypes.CDLL(str(lib_path))
+    lib.skmetal_hip_last_error.restype = ctypes.c_char_p
+    for name in sorted(NOT_PROVIDED):
+        f = getattr(lib, name)
+        f.restype = ctypes.c_int
+        assert f() == 7, name  # SKMETAL_ENOSYS
+        assert name in lib.skmetal_hip_last_error().decode()
+    lib.skmetal_init()  # the library's last error is shared: leave it at the init result
 
 
 def test_library_exports_every_declared_symbol(lib_path):
@@ -83,7 +122,7 @@ def test_ctypes_registry_binds_the_header():
     from skmetal_amd import _bridge
 
     bound = {entry[0] for entry in _bridge._REGISTRY}
-    assert bound == _declared()
+    assert bound == _declared() - NOT_PROVIDED
 
 
 def test_without_gpu_the_package_imports_and_refuses_to_compute():
