@@ -798,14 +798,37 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
                         const int o = ((16 * g + r16) * ld + f0 + 32 * ks + 8 * h) * 4;
                         xp[g] = split8(load_quad(rs, o), load_quad(rs, o + 16));
                     }
+                    // four centre blocks at a time, product-major over their
+                    // eight accumulators: consecutive MFMAs write different
+                    // accumulators (a block's six products back to back wait
+                    // on each other).  Each accumulator takes dot6's products
+                    // in dot6's order.
+                    constexpr int CG = 4;
 #pragma unroll
-                    for (int cb = 0; cb < CB; ++cb) {
-                        const __bf16* cp = cbase + 16 * cb * CSTR + 32 * ks;
-                        const Parts8 cpt{*reinterpret_cast<const v8bf*>(cp),
-                                         *reinterpret_cast<const v8bf*>(cp + CPART),
-                                         *reinterpret_cast<const v8bf*>(cp + 2 * CPART)};
+                    for (int cb0 = 0; cb0 < CB; cb0 += CG) {
+                        Parts8 cpt[CG];
 #pragma unroll
-                        for (int g = 0; g < 2; ++g) acc[g][cb] = dot6(cpt, xp[g], acc[g][cb]);
+                        for (int c = 0; c < CG; ++c) {
+                            const __bf16* cp = cbase + 16 * (cb0 + c) * CSTR + 32 * ks;
+                            cpt[c] = Parts8{*reinterpret_cast<const v8bf*>(cp),
+                                            *reinterpret_cast<const v8bf*>(cp + CPART),
+                                            *reinterpret_cast<const v8bf*>(cp + 2 * CPART)};
+                        }
+#pragma unroll
+                        for (int pr = 0; pr < 6; ++pr) {
+#pragma unroll
+                            for (int c = 0; c < CG; ++c) {
+                                const Parts8& cc = cpt[c];
+                                const v8bf ca = pr == 0 ? cc.m : pr == 1 ? cc.l : pr == 2 ? cc.h : pr == 3 ? cc.m : cc.h;
+#pragma unroll
+                                for (int g = 0; g < 2; ++g) {
+                                    const Parts8& x = xp[g];
+                                    const v8bf xb = pr == 0 ? x.m : pr == 1 ? x.h : pr == 2 ? x.l : pr == 3 ? x.h
+                                                                                               : pr == 4 ? x.m : x.h;
+                                    acc[g][cb0 + c] = mfma_bf16(ca, xb, acc[g][cb0 + c]);
+                                }
+                            }
+                        }
                     }
                 }
             }
