@@ -693,8 +693,6 @@ __device__ __forceinline__ void finalize_cols_block(const FinalizeArgs& a, int j
     const int rs = tid >> 3;        // partial lane, 0..31
     const int c4 = cc * 32 + 4 * q; // first column of this thread
     __shared__ double red[4][8][4];
-    __shared__ double shd[2][4];
-    __shared__ int shi[4];
 
     // block partials: the halt flag, the old centres, the counts and the
     // partials are all requested before any of them is used (one memory
@@ -709,11 +707,14 @@ __device__ __forceinline__ void finalize_cols_block(const FinalizeArgs& a, int j
     const int R = recs ? a.rec_cnt[j] : a.R;
     const float* src = a.psum + (recs ? (long)a.rec_off[j] * a.ld : (long)j * a.ld) + c4;
     const long step = recs ? (long)a.ld : (long)a.k * a.ld;
+    // the count is summed by wave 0 alone, which also forms the centres
     int cnt = 0;
-    if (recs) {
-        cnt = tid == 0 ? a.cnt_in[j] : 0;
-    } else {
-        for (int r = tid; r < a.R; r += 256) cnt += a.pcnt[(long)r * a.k + j];
+    if (tid < 64) {
+        if (recs) {
+            cnt = tid == 0 ? a.cnt_in[j] : 0;
+        } else {
+            for (int r = tid; r < a.R; r += 64) cnt += a.pcnt[(long)r * a.k + j];
+        }
     }
     double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
     if (c4 < a.ld && R > 0) {  // ld is a multiple of 4: the float4 is in or out
@@ -749,8 +750,12 @@ __device__ __forceinline__ void finalize_cols_block(const FinalizeArgs& a, int j
         red[tid >> 6][q][2] = s2;
         red[tid >> 6][q][3] = s3;
     }
-    const int count = block_sum(cnt, shi);  // its barrier also publishes red[]
-
+    __syncthreads();  // red[] from every wave
+    if (tid >= 64) return;
+    // wave 0: the count, then the new centres of the chunk's columns and
+    // their shift^2 and ||c||^2 partials (fp64 sums over lanes 0..31 in a
+    // fixed butterfly order; lanes 32..63 add zeros)
+    const int count = wave_sum(cnt);
     double sq = 0.0, nrm = 0.0;
     if (tid < 32 && ccol < a.d) {
         const int qq = tid >> 2, e = tid & 3;
@@ -764,8 +769,8 @@ __device__ __forceinline__ void finalize_cols_block(const FinalizeArgs& a, int j
             nrm = (double)cn * (double)cn;
         }
     }
-    sq = block_sum(sq, shd[0]);
-    nrm = block_sum(nrm, shd[1]);
+    sq = wave_sum(sq);
+    nrm = wave_sum(nrm);
     if (tid == 0) {
         a.part[((long)j * nch + cc) * 2 + 0] = sq;
         a.part[((long)j * nch + cc) * 2 + 1] = nrm;
