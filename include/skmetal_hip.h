@@ -270,6 +270,28 @@ SKMETAL_API int skmetal_hip_lloyd_max_abs(skmetal_hip_lloyd* h, float* out);
  * points. */
 SKMETAL_API int skmetal_hip_lloyd_mindists(skmetal_hip_lloyd* h, const int64_t* rows, size_t m, int reset,
                                            float* dists_out);
+/* numpy's legacy RandomState.choice(n, size, replace=False, p=w / w.sum())
+ * over the loaded rows, on the device, for fp32 weights w: weights = 0 takes
+ * the k-means|| distances of skmetal_hip_lloyd_mindists floored at 1e-30
+ * (numpy maximum), as MetalKMeans._kmeans_parallel_init draws its candidates
+ * (skmetal/estimators/cluster.py:94-98); weights = 1 takes unit weights, as
+ * scikit-learn's init="random" (sklearn/cluster/_kmeans.py:1010-1013).
+ * sample_prepare forms p in numpy's arithmetic (fp32 sum in numpy's pairwise
+ * order, fp32 quotient, fp64) and returns the fp64 sum of p and the count of
+ * p > 0, which choice checks before drawing.  Each sample_draw is one of
+ * choice's passes: p is zeroed at the n_zero rows found so far, then
+ * rows_out[t] = searchsorted(cumsum(p) / cumsum(p)[-1], uniforms[t],
+ * side="right") with numpy's sequential fp64 cumsum, for the m uniforms the
+ * caller drew with rand(size - found).  The row is found on a cumsum of
+ * another order and kept when it is provably the same; the rest (about
+ * 4 n 2^-53 of the draws) are searched on numpy's own cumsum, every draw with
+ * exact = 1.  *n_exact_out (nullable) = the draws searched that way.  The
+ * caller drops repeated rows and draws again, as choice does. */
+SKMETAL_API int skmetal_hip_lloyd_sample_prepare(skmetal_hip_lloyd* h, int weights, double* p_sum_out,
+                                                 int64_t* nonzero_out);
+SKMETAL_API int skmetal_hip_lloyd_sample_draw(skmetal_hip_lloyd* h, const int64_t* zero_rows, size_t n_zero,
+                                              const double* uniforms, size_t m, int64_t* rows_out, int exact,
+                                              int* n_exact_out);
 /* *fused & 3 = 0 when a step runs as separate E-step and update kernels, 1
  * when as one fused E-step + sums kernel with the E-step on fp32 MFMA
  * (k <= 64, d <= 100), 2 when that kernel's E-step and sums run on bf16 MFMAs

@@ -69,6 +69,10 @@ _REGISTRY = [
     ("skmetal_hip_column_variance", ctypes.c_int, _vp, _c_size, _c_size, _vp),
     ("skmetal_hip_lloyd_max_abs", ctypes.c_int, _vp, ctypes.POINTER(ctypes.c_float)),
     ("skmetal_hip_lloyd_mindists", ctypes.c_int, _vp, _vp, _c_size, ctypes.c_int, _vp),
+    ("skmetal_hip_lloyd_sample_prepare", ctypes.c_int, _vp, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+     ctypes.POINTER(ctypes.c_int64)),
+    ("skmetal_hip_lloyd_sample_draw", ctypes.c_int, _vp, _vp, _c_size, _vp, _c_size, _vp, ctypes.c_int,
+     ctypes.POINTER(ctypes.c_int)),
     ("skmetal_hip_kmeans_batch_fused_noalloc", ctypes.c_int, _vp, _vp, _vp, _c_size, _c_size, _c_size, _c_size,
      ctypes.c_float, ctypes.POINTER(ctypes.c_int32)),
 ]
@@ -408,15 +412,65 @@ class LloydHandle:
         _check(_lib.skmetal_hip_lloyd_max_abs(self._h, ctypes.byref(v)), "skmetal_hip_lloyd_max_abs")
         return float(v.value)
 
-    def mindists(self, rows, reset: bool = False):
+    def mindists(self, rows, reset: bool = False, download: bool = True):
         """k-means|| round: squared distance of every loaded row to its nearest
         candidate so far, lowered with the candidate rows `rows` (indices into X);
-        reset starts from +inf.  Returns float32 [n]."""
+        reset starts from +inf.  Returns float32 [n] (None with download=False:
+        the distances stay on the device for choice(weights="mindists"))."""
         r = np.ascontiguousarray(rows, dtype=np.int64).reshape(-1)
-        out = np.empty(self.n, np.float32)
+        out = np.empty(self.n, np.float32) if download else None
         _check(_lib.skmetal_hip_lloyd_mindists(self._h, r.ctypes.data if r.size else None, r.size, int(bool(reset)),
-                                               out.ctypes.data), "skmetal_hip_lloyd_mindists")
+                                               out.ctypes.data if download else None), "skmetal_hip_lloyd_mindists")
         return out
+
+    def choice(self, random_state, size: int, weights: str = "mindists", exact: bool = False):
+        """numpy's legacy ``random_state.choice(n, size, replace=False, p=w / w.sum())``
+        on the device, for fp32 weights w: "mindists" = the k-means|| distances
+        floored at 1e-30 (``np.maximum(dists, 1e-30)``), "unit" = ones.  Same
+        rows, same draws taken from random_state, same errors.  The pass loop is
+        numpy's: rand(size - found) uniforms, their rows, repeats dropped (first
+        occurrence kept, in draw order), found rows zeroed, again until size rows.
+        exact=True searches numpy's own cumsum for every draw; the default keeps
+        the rows of a cumsum of another order where they provably agree.  The
+        count of draws searched exactly is kept in ``self.sample_exact``."""
+        if weights not in ("mindists", "unit"):
+            raise ValueError(f"weights={weights!r} is not 'mindists' or 'unit'")
+        n = self.n
+        size = int(size)
+        psum = ctypes.c_double(0.0)
+        nnz = ctypes.c_int64(0)
+        _check(_lib.skmetal_hip_lloyd_sample_prepare(self._h, 0 if weights == "mindists" else 1, ctypes.byref(psum),
+                                                     ctypes.byref(nnz)), "skmetal_hip_lloyd_sample_prepare")
+        # numpy's checks, in numpy's order (fp32 p: atol = sqrt of fp32 epsilon)
+        atol = max(np.sqrt(np.finfo(np.float64).eps), np.sqrt(np.finfo(np.float32).eps))
+        if np.isnan(psum.value):
+            raise ValueError("probabilities contain NaN")
+        if abs(psum.value - 1.0) > atol:
+            raise ValueError("probabilities do not sum to 1")
+        if size > n:
+            raise ValueError("Cannot take a larger sample than population when 'replace=False'")
+        if size < 0:
+            raise ValueError("negative dimensions are not allowed")
+        if nnz.value < size:
+            raise ValueError("Fewer non-zero entries in p than size")
+        found = np.zeros(size, dtype=np.int64)
+        n_uniq = 0
+        n_exact = ctypes.c_int(0)
+        self.sample_exact = 0
+        while n_uniq < size:
+            u = np.ascontiguousarray(random_state.rand(size - n_uniq), dtype=np.float64)
+            rows = np.empty(u.size, dtype=np.int64)
+            zero = found[:n_uniq]
+            _check(_lib.skmetal_hip_lloyd_sample_draw(self._h, zero.ctypes.data if n_uniq else None, n_uniq,
+                                                      u.ctypes.data, u.size, rows.ctypes.data, int(bool(exact)),
+                                                      ctypes.byref(n_exact)), "skmetal_hip_lloyd_sample_draw")
+            self.sample_exact += int(n_exact.value)
+            _, first = np.unique(rows, return_index=True)
+            first.sort()
+            new = rows.take(first)
+            found[n_uniq:n_uniq + new.size] = new
+            n_uniq += new.size
+        return found
 
     def info(self):
         fused = ctypes.c_int(0)

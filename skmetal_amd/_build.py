@@ -39,6 +39,7 @@ SOURCES = [
     ("split_kernels.hip", []),
     ("plusplus_kernels.hip", []),
     ("transform_kernels.hip", []),
+    ("sample_kernels.hip", []),
     ("skmetal_hip.hip", VGPR_FORM),
 ]
 

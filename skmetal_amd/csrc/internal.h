@@ -275,6 +275,39 @@ hipError_t launch_pp_mindist(const PPArgs& a, int m, hipStream_t s);
 // Pick centre c - 1 among its candidates; for c < k draw centre c's candidates.
 hipError_t launch_pp_select(const PPArgs& a, int c, hipStream_t s);
 
+// Weighted draws without replacement in numpy's RandomState.choice form
+// (sample_kernels.hip): probabilities p = fp32(w / sum(w)) as fp64, then per
+// pass of uniforms the rows searchsorted(cumsum(p) / cumsum(p)[-1], u, "right").
+constexpr int kWSBlock = 8192;  // numpy reduces a contiguous fp32 array one 8192-element buffer at a time
+constexpr int kWSChunk = 2048;  // rows per search chunk
+struct WSArgs {
+    const float* w; long n;     // weights (nullptr: unit weights)
+    float floor;                // numpy maximum(w, floor), NaN kept
+    float* bsum;                // [ws_blocks(n)] fp32 pairwise sum of each 8192-weight block
+    float* total;               // [1] fp32 sum of the weights, numpy's order
+    double* p;                  // [n] probabilities (fp64 of the fp32 quotient)
+    double* ctot;               // [ws_chunks(n)] fp64 sum of each chunk of p
+    int* cnz;                   // [ws_chunks(n)] rows with p > 0 per chunk
+    double* pfx;                // [ws_chunks(n) + 1] chunk sums' running total, pfx[0] = 0
+    long long* nnz;             // [1] rows with p > 0
+    double* ex;                 // [n] numpy's cumsum of p (exact search only)
+    const double* u; int m;     // this pass's uniforms
+    const long* zero; int nz;   // rows whose p is zeroed before the pass
+    long* out;                  // [m] picked rows
+    int* unsure;                // [m] 1: the certified search left the draw to the exact search
+};
+int ws_blocks(long n);
+int ws_chunks(long n);
+// p, chunk sums, prefix and the non-zero count from the weights.
+hipError_t launch_ws_prepare(const WSArgs& a, hipStream_t s);
+// p[zero[0 .. nz-1]] = 0, then chunk sums and prefix again.
+hipError_t launch_ws_zero(const WSArgs& a, hipStream_t s);
+// Certified search of the m uniforms: out, unsure.
+hipError_t launch_ws_search(const WSArgs& a, hipStream_t s);
+// numpy's sequential cumsum, then the search of the unsure draws (all != 0:
+// every draw).
+hipError_t launch_ws_exact(const WSArgs& a, int all, hipStream_t s);
+
 // KMeans.transform (transform_kernels.hip): out[i, j] = ||x_i - c_j|| in
 // scikit-learn's fp32 form (fp64 expanded distance, fp32 cast, clamp, sqrt).
 struct TransformArgs {

@@ -1011,6 +1011,98 @@ struct Lloyd {
         return 0;
     }
 
+    // numpy's RandomState.choice(n, size, replace=False, p=w / w.sum()) on
+    // the device: sample_prepare forms p from the weights (0: the k-means||
+    // distances floored at 1e-30, 1: unit weights), sample_draw runs one of
+    // choice's passes for the caller's uniforms.
+    WSArgs ws{};
+    bool ws_ready = false;
+    long ws_mcap = 0;
+
+    int sample_prepare(int weights, double* psum, long long* nnz)
+    {
+        if (weights != 0 && weights != 1) return fail(SKMETAL_EINVAL, "weights=%d is not 0 or 1", weights);
+        if (weights == 0 && !kp_valid) return fail(SKMETAL_EINVAL, "no k-means|| distances to sample from");
+        if (arena != nullptr) return fail(SKMETAL_EINVAL, "sampling needs the device buffer cache");
+        if (n >= (1L << 31)) return fail(SKMETAL_ERANGE, "sampling supports n < 2^31 rows (n=%ld)", n);
+        if (ws.p == nullptr) {
+            const int nb = ws_blocks(n), nc = ws_chunks(n);
+            TRY(grab((void**)&ws.p, size_t(n) * sizeof(double)));
+            TRY(grab((void**)&ws.bsum, size_t(nb) * sizeof(float)));
+            TRY(grab((void**)&ws.total, sizeof(float)));
+            TRY(grab((void**)&ws.ctot, size_t(nc) * sizeof(double)));
+            TRY(grab((void**)&ws.cnz, size_t(nc) * sizeof(int)));
+            TRY(grab((void**)&ws.pfx, size_t(nc + 1) * sizeof(double)));
+            TRY(grab((void**)&ws.nnz, sizeof(long long)));
+        }
+        ws.n = n;
+        ws.w = weights == 0 ? kp_mind : nullptr;
+        ws.floor = 1e-30f;
+        HIP_TRY(launch_ws_prepare(ws, s), "sampling prepare launch");
+        double st[1];
+        long long z = 0;
+        TRY(download_bytes(*C, ws.pfx + ws_chunks(n), sizeof(double), st, s));
+        TRY(download_bytes(*C, ws.nnz, sizeof(long long), &z, s));
+        *psum = st[0];
+        *nnz = z;
+        ws_ready = true;
+        return 0;
+    }
+
+    // Rows for the m uniforms u after zeroing p at the nz rows `zero`; exact
+    // = 1 searches numpy's own cumsum for every draw.  *n_exact = draws the
+    // certified search left to the exact one.
+    int sample_draw(const long* zero, long nz, const double* u, long m, long* out, int exact, int* n_exact)
+    {
+        if (!ws_ready) return fail(SKMETAL_EINVAL, "sample_draw before sample_prepare");
+        if (m < 0 || m > (1L << 24) || nz < 0 || nz > n)
+            return fail(SKMETAL_ERANGE, "m=%ld draws or %ld zeroed rows out of range", m, nz);
+        if ((m > 0 && (u == nullptr || out == nullptr)) || (nz > 0 && zero == nullptr))
+            return fail(SKMETAL_EINVAL, "null pointer argument");
+        for (long i = 0; i < m; ++i)
+            if (!(u[i] >= 0.0 && u[i] < 1.0)) return fail(SKMETAL_EINVAL, "uniform %ld not in [0, 1)", i);
+        for (long i = 0; i < nz; ++i)
+            if (zero[i] < 0 || zero[i] >= n) return fail(SKMETAL_EINVAL, "zeroed row %ld not in [0, %ld)", zero[i], n);
+        *n_exact = 0;
+        if (m == 0) return 0;
+        const long need = std::max(m, nz);
+        if (need > ws_mcap) {
+            const long cap = std::max<long>(need, 2 * ws_mcap);
+            for (void* q : {(void*)ws.u, (void*)ws.out, (void*)ws.unsure, (void*)ws.zero}) {
+                if (q == nullptr) continue;
+                const auto it = std::find(owned.begin(), owned.end(), q);
+                if (it != owned.end()) owned.erase(it);
+                C->release(q);
+            }
+            TRY(grab((void**)&ws.u, size_t(cap) * sizeof(double)));
+            TRY(grab((void**)&ws.out, size_t(cap) * sizeof(long)));
+            TRY(grab((void**)&ws.unsure, size_t(cap) * sizeof(int)));
+            TRY(grab((void**)&ws.zero, size_t(cap) * sizeof(long)));
+            ws_mcap = cap;
+        }
+        ws.m = (int)m;
+        ws.nz = (int)nz;
+        if (nz > 0) {
+            TRY(upload_bytes(*C, zero, size_t(nz) * sizeof(long), const_cast<long*>(ws.zero), s));
+            HIP_TRY(launch_ws_zero(ws, s), "sampling zero launch");
+        }
+        TRY(upload_bytes(*C, u, size_t(m) * sizeof(double), const_cast<double*>(ws.u), s));
+        std::vector<int> uns(size_t(m), 1);
+        if (!exact) {
+            HIP_TRY(launch_ws_search(ws, s), "sampling search launch");
+            TRY(download_bytes(*C, ws.unsure, size_t(m) * sizeof(int), uns.data(), s));
+        }
+        long left = 0;
+        for (long i = 0; i < m; ++i) left += uns[i] != 0;
+        if (left > 0) {
+            if (ws.ex == nullptr) TRY(grab((void**)&ws.ex, size_t(n) * sizeof(double)));
+            HIP_TRY(launch_ws_exact(ws, exact ? 1 : 0, s), "sampling exact launch");
+        }
+        TRY(download_bytes(*C, ws.out, size_t(m) * sizeof(long), out, s));
+        *n_exact = (int)left;
+        return 0;
+    }
+
     // Full sklearn fit from the current centres: loop, final E-step, inertia.
     int fit(long max_iter, double tol, int flags, int* n_iter_out, double* inertia_out)
     {
@@ -1454,6 +1546,33 @@ int skmetal_hip_lloyd_mindists(skmetal_hip_lloyd* h, const int64_t* rows, size_t
     if (m > (size_t(1) << 30)) return fail(SKMETAL_ERANGE, "m=%zu candidate rows out of range", m);
     TRY(h->L.mindists(reinterpret_cast<const long*>(rows), (long)m, reset, dists_out));
     HIP_TRY(hipStreamSynchronize(h->L.s), "hipStreamSynchronize");
+    return 0;
+}
+
+int skmetal_hip_lloyd_sample_prepare(skmetal_hip_lloyd* h, int weights, double* p_sum_out, int64_t* nonzero_out)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!h || !p_sum_out || !nonzero_out) return fail(SKMETAL_EINVAL, "null pointer argument");
+    long long z = 0;
+    TRY(h->L.sample_prepare(weights, p_sum_out, &z));
+    *nonzero_out = (int64_t)z;
+    return 0;
+}
+
+int skmetal_hip_lloyd_sample_draw(skmetal_hip_lloyd* h, const int64_t* zero_rows, size_t n_zero, const double* uniforms,
+                                  size_t m, int64_t* rows_out, int exact, int* n_exact_out)
+{
+    Context& c = ctx();
+    Guard g(c);
+    if (!h) return fail(SKMETAL_EINVAL, "null pointer argument");
+    if (m > (size_t(1) << 24) || n_zero > (size_t(1) << 40))
+        return fail(SKMETAL_ERANGE, "m=%zu draws or %zu zeroed rows out of range", m, n_zero);
+    int ne = 0;
+    TRY(h->L.sample_draw(reinterpret_cast<const long*>(zero_rows), (long)n_zero, uniforms, (long)m,
+                         reinterpret_cast<long*>(rows_out), exact, &ne));
+    HIP_TRY(hipStreamSynchronize(h->L.s), "hipStreamSynchronize");
+    if (n_exact_out) *n_exact_out = ne;
     return 0;
 }
 

@@ -90,13 +90,13 @@ class HipKMeans(BaseGPUEstimator):
             n_init = 1
         return int(n_init)
 
-    def _initial_centers(self, X, init, k, random_state):
+    def _initial_centers(self, X, init, k, random_state, h):
         """sklearn/cluster/_kmeans.py:958-1029 (_init_centroids), unit weights,
-        for the inits other than k-means++ (seeded on the device)."""
-        n = X.shape[0]
+        for the inits other than k-means++ (seeded on the device).  "random"
+        draws random_state.choice(n, k, replace=False, p=ones / n) on the device
+        (the same rows and draws as numpy's)."""
         if isinstance(init, str) and init == "random":
-            w = np.ones(n, dtype=X.dtype)  # _check_sample_weight(None, X, dtype=X.dtype)
-            seeds = random_state.choice(n, size=k, replace=False, p=w / w.sum())
+            seeds = h.choice(random_state, k, weights="unit")
             centers = X[seeds]
         elif callable(init):
             centers = init(X, k, random_state=random_state)
@@ -149,7 +149,7 @@ class HipKMeans(BaseGPUEstimator):
                     T, first, u = draws_f.result() if i == 0 else _bridge.plusplus_draws(random_state, n, k)
                     h.plusplus_with(T, first, u)
                 else:
-                    h.set_centers(self._initial_centers(X, init, k, random_state))
+                    h.set_centers(self._initial_centers(X, init, k, random_state, h))
                 if tol_abs is None:
                     tol_abs = tol_f.result()
                 n_iter, inertia = h.run(est.max_iter, tol_abs, strict=True)
@@ -219,18 +219,47 @@ class HipKMeans(BaseGPUEstimator):
         return -float(v)
 
 
-def kmeans_parallel_init(X: np.ndarray, k: int, rng, handle) -> np.ndarray:
+def _prune_candidates(cand: np.ndarray, k: int) -> np.ndarray:
+    """The reference's prune of more than k k-means|| candidates
+    (skmetal/estimators/cluster.py:112-116: scikit-learn
+    KMeans(n_clusters=k, init=cand[:k], n_init=1, max_iter=1).fit(cand)) on the
+    device: scikit-learn's fit rules for it (the candidates centred on their
+    mean, tol = 1e-4 times the mean column variance, one Lloyd iteration with
+    the strict-convergence rule, then the final E-step) on this library's Lloyd
+    loop, and scikit-learn's warning when fewer than k clusters stay
+    distinct.  scikit-learn's fit draws nothing from the random_state it is
+    given here, so neither does this."""
+    m, d = cand.shape
+    with _bridge.LloydHandle(m, d, k) as h:
+        h.load(cand, center=True)
+        h.set_centers(np.ascontiguousarray(cand[:k]))
+        h.run(1, _tolerance(cand, 1e-4), strict=True)
+        centers = h.centers()
+        distinct = len(np.unique(h.labels()))
+    if distinct < k:
+        warnings.warn(
+            f"Number of distinct clusters ({distinct}) found smaller than n_clusters ({k}). "
+            "Possibly due to duplicate points in X.",
+            ConvergenceWarning,
+            stacklevel=3,
+        )
+    return centers
+
+
+def kmeans_parallel_init(X: np.ndarray, k: int, rng, handle, trace: bool = False):
     """skmetal's k-means|| seeding, MetalKMeans._kmeans_parallel_init
-    (skmetal/estimators/cluster.py:70-116), with its distance rounds on the
-    device: `handle` holds X (uploaded once) and keeps every row's squared
-    distance to its nearest candidate, lowered with each round's new rows
-    (skmetal_hip_lloyd_mindists).  The distance to the assigned candidate that
-    the reference's kmeans_assign + compute_mindists pair gives is that
-    minimum.  Sampling and pruning are the reference's, on the host: rounds =
-    max(1, int(2 + ln k)); min(k, n) rows drawn without replacement with
-    probability proportional to max(dist, 1e-30); the set of taken indices
-    starts as {0}, as the reference's does; more than k candidates are pruned
-    by one scikit-learn KMeans iteration from the first k."""
+    (skmetal/estimators/cluster.py:70-116), on the device: `handle` holds X
+    (uploaded once) and keeps every row's squared distance to its nearest
+    candidate, lowered with each round's new rows (skmetal_hip_lloyd_mindists).
+    The distance to the assigned candidate that the reference's kmeans_assign +
+    compute_mindists pair gives is that minimum.  Each round's draw is numpy's
+    rng.choice(n, min(k, n), replace=False, p=maximum(dists, 1e-30) / sum) over
+    the resident distances (LloydHandle.choice: the same rows, the same
+    uniforms taken from rng); rounds = max(1, int(2 + ln k)); the set of taken
+    indices starts as {0}, as the reference's does; more than k candidates are
+    pruned by one Lloyd iteration from the first k in scikit-learn's rules
+    (_prune_candidates), fewer are repeated cyclically.  Returns the k
+    centroids (and, with trace, the candidate rows)."""
     n, d = X.shape
     first = int(rng.randint(n))
     n_rounds = max(1, int(2 + np.log(k)))
@@ -238,10 +267,8 @@ def kmeans_parallel_init(X: np.ndarray, k: int, rng, handle) -> np.ndarray:
     taken = {0}
     new = [first]
     for r in range(n_rounds):
-        dists = handle.mindists(new, reset=(r == 0))
-        dists = np.maximum(dists, 1e-30)
-        probs = dists / dists.sum()
-        idx = rng.choice(n, size=min(k, n), p=probs, replace=False)
+        handle.mindists(new, reset=(r == 0), download=False)
+        idx = handle.choice(rng, min(k, n), weights="mindists")
         new = []
         for i in idx:
             if i not in taken:
@@ -254,12 +281,9 @@ def kmeans_parallel_init(X: np.ndarray, k: int, rng, handle) -> np.ndarray:
         centroids[: cand.shape[0]] = cand
         for i in range(cand.shape[0], k):
             centroids[i] = cand[i % cand.shape[0]]
-        return centroids
-    from sklearn.cluster import KMeans as SklearnKMeans
-
-    km = SklearnKMeans(n_clusters=k, init=cand[:k], n_init=1, max_iter=1, random_state=rng)
-    km.fit(cand)
-    return km.cluster_centers_.astype(np.float32)
+    else:
+        centroids = _prune_candidates(np.ascontiguousarray(cand, dtype=np.float32), k)
+    return (centroids, rows) if trace else centroids
 
 
 class MetalKMeans(BaseGPUEstimator):

@@ -93,15 +93,29 @@ def test_parallel_init_matches_oracle(bridge, n, d, k, seed):
     X = _blobs(n, d, k, seed + 10)
     with bridge.LloydHandle(n, d, k) as h:
         h.load(X, center=False)
-        got = kmeans_parallel_init(X, k, np.random.RandomState(seed), h)
-    ref = oracle.kmeans_parallel_init(X, k, np.random.RandomState(seed))
+        got, got_rows = kmeans_parallel_init(X, k, np.random.RandomState(seed), h, trace=True)
+    ref, ref_rows = oracle.kmeans_parallel_init(X, k, np.random.RandomState(seed), trace=True)
     assert got.shape == (k, d) and got.dtype == np.float32
-    np.testing.assert_array_equal(got, ref)
+    _check_init(got, got_rows, ref, ref_rows, k, f"n={n} d={d} k={k}")
+
+
+def _check_init(got, got_rows, ref, ref_rows, k, what):
+    """Candidate rows are integer picks: identical, in order.  Up to k
+    candidates are the centroids themselves (bit for bit); more are pruned by
+    one Lloyd iteration, the device's against scikit-learn's (the reference's
+    prune): the same labels of the candidates give centres equal within the
+    fp32 parity tolerance."""
+    np.testing.assert_array_equal(np.asarray(got_rows), np.asarray(ref_rows), err_msg=f"{what}: candidate rows")
+    if len(ref_rows) <= k:
+        np.testing.assert_array_equal(got, ref, err_msg=what)
+    else:
+        parity.check_centers(got, ref, what=f"{what}: pruned centroids")
 
 
 def test_parallel_init_matches_reference_method(bridge):
     """The device path against the reference method's own draws and prune
-    (tests/golden/kpar.npz, written by make_kpar_fixtures.py)."""
+    (tests/golden/kpar.npz, written by make_kpar_fixtures.py): every
+    candidate row, then the centroids."""
     from skmetal_amd.estimators.cluster import kmeans_parallel_init
     from test_kpar_oracle import KPAR
 
@@ -111,8 +125,8 @@ def test_parallel_init_matches_reference_method(bridge):
         _say(f"k-means|| vs reference vectors {c['name']}")
         with bridge.LloydHandle(n, d, c["k"]) as h:
             h.load(X, center=False)
-            got = kmeans_parallel_init(X, c["k"], np.random.RandomState(c["seed"]), h)
-        np.testing.assert_array_equal(got, a["centroids"], err_msg=c["name"])
+            got, rows = kmeans_parallel_init(X, c["k"], np.random.RandomState(c["seed"]), h, trace=True)
+        _check_init(got, rows, a["centroids"], a["final_rows"], c["k"], c["name"])
 
 
 def test_metal_kmeans_fit(bridge):
