@@ -12,7 +12,9 @@
 //   k_ws_block    fp32 sum of each 8192-weight block in numpy's pairwise
 //                 order (leaves of <= 128 weights on eight accumulators,
 //                 halves split at a multiple of 8) -- numpy reduces a
-//                 contiguous fp32 array one 8192-element buffer at a time;
+//                 contiguous fp32 array one 8192-element buffer at a time; a
+//                 whole block is a perfect tree of 64 leaves (one lane each,
+//                 then a butterfly), the last one is walked by one thread;
 //   k_ws_total    the block sums added in order (numpy's running total);
 //   k_ws_prob     p_i = fp64(fp32(w_i / total)) (choice converts the fp32
 //                 probabilities to fp64), per-2048-row chunk fp64 sums and
@@ -72,6 +74,48 @@ __global__ __launch_bounds__(kWSThreads) void k_ws_block(WSArgs a)
     const int tid = threadIdx.x;
     const long b0 = (long)blockIdx.x * kWSBlock;
     const int L = (int)min((long)kWSBlock, a.n - b0);
+    if (L == kWSBlock) {
+        // a whole block is a perfect tree: 64 leaves of 128 (halves of 8192,
+        // 4096, .., 256), so lane t sums leaf t and a butterfly down the
+        // wave adds the subtrees in tree order
+        if (tid >= 64) return;
+        const float* src = a.w != nullptr ? a.w + b0 + kLeaf * tid : nullptr;
+        auto get8 = [&](int i, float* v) {
+            if (src == nullptr) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = 1.0f;
+                return;
+            }
+            const float4 p = *reinterpret_cast<const float4*>(src + i);
+            const float4 q = *reinterpret_cast<const float4*>(src + i + 4);
+            v[0] = floored(p.x, a.floor);
+            v[1] = floored(p.y, a.floor);
+            v[2] = floored(p.z, a.floor);
+            v[3] = floored(p.w, a.floor);
+            v[4] = floored(q.x, a.floor);
+            v[5] = floored(q.y, a.floor);
+            v[6] = floored(q.z, a.floor);
+            v[7] = floored(q.w, a.floor);
+        };
+        float r[8];
+        get8(0, r);
+#pragma unroll
+        for (int i = 8; i < kLeaf; i += 8) {
+            float v[8];
+            get8(i, v);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) r[j] += v[j];
+        }
+        float t = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float o = __shfl_down(t, off, 64);
+            t = t + o;
+        }
+        if (tid == 0) a.bsum[blockIdx.x] = t;
+        return;
+    }
+    // the last, partial block: the tree of its length, walked by one thread
     for (int i = tid; i < L; i += kWSThreads) wv[pad_idx(i)] = a.w != nullptr ? floored(a.w[b0 + i], a.floor) : 1.0f;
     if (tid == 0) {
         // leaves in order: depth-first, left half first
@@ -157,12 +201,50 @@ __global__ __launch_bounds__(kWSThreads) void k_ws_block(WSArgs a)
     }
 }
 
-// numpy's running total over the blocks, in block order.
-__global__ void k_ws_total(WSArgs a, int nb)
+constexpr int kSeqTile = 1024;  // values per LDS tile of a sequential running sum
+
+// Running sum of v[0 .. m) in order, by thread 0 over LDS tiles the block
+// fills: out[i] (nullable) = sum of v[0 .. i]; returns the total in thread 0.
+template <typename T>
+__device__ T seq_running_sum(const T* v, int m, T* out, T* tile)
 {
-    float r = 0.0f;
-    for (int b = 0; b < nb; ++b) r += a.bsum[b];
-    *a.total = r;
+    const int tid = threadIdx.x;
+    T s = T(0);
+    for (int c0 = 0; c0 < m; c0 += kSeqTile) {
+        const int len = min(kSeqTile, m - c0);
+        for (int i = tid; i < len; i += blockDim.x) tile[i] = v[c0 + i];
+        __syncthreads();
+        if (tid == 0) {
+            int i = 0;
+            for (; i + 8 <= len; i += 8) {
+                T u[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) u[j] = tile[i + j];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    s += u[j];
+                    tile[i + j] = s;
+                }
+            }
+            for (; i < len; ++i) {
+                s += tile[i];
+                tile[i] = s;
+            }
+        }
+        __syncthreads();
+        if (out != nullptr)
+            for (int i = tid; i < len; i += blockDim.x) out[c0 + i] = tile[i];
+        __syncthreads();
+    }
+    return s;
+}
+
+// numpy's running total over the blocks, in block order.
+__global__ __launch_bounds__(kWSThreads) void k_ws_total(WSArgs a, int nb)
+{
+    __shared__ float tile[kSeqTile];
+    const float r = seq_running_sum<float>(a.bsum, nb, nullptr, tile);
+    if (threadIdx.x == 0) *a.total = r;
 }
 
 // fp64 sum of this block's 8 values per thread, in a fixed order (thread,
@@ -234,17 +316,21 @@ __global__ __launch_bounds__(kWSThreads) void k_ws_ctot(WSArgs a)
 
 // pfx[c] = sum of chunks 0 .. c-1 in chunk order (non-decreasing), pfx[nc] =
 // the total; with counts: nnz = number of p > 0.
-__global__ void k_ws_prefix(WSArgs a, int nc, int counts)
+__global__ __launch_bounds__(kWSThreads) void k_ws_prefix(WSArgs a, int nc, int counts)
 {
-    double s = 0.0;
+    __shared__ double tile[kSeqTile];
+    __shared__ long long zs[kWSThreads / 64];
+    const int tid = threadIdx.x;
+    if (tid == 0) a.pfx[0] = 0.0;
+    (void)seq_running_sum<double>(a.ctot, nc, a.pfx + 1, tile);
+    if (!counts) return;
     long long z = 0;
-    a.pfx[0] = 0.0;
-    for (int c = 0; c < nc; ++c) {
-        s += a.ctot[c];
-        a.pfx[c + 1] = s;
-        if (counts) z += a.cnz[c];
-    }
-    if (counts) *a.nnz = z;
+    for (int c = tid; c < nc; c += kWSThreads) z += a.cnz[c];
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) z += __shfl_xor(z, off, 64);
+    if ((tid & 63) == 0) zs[tid >> 6] = z;
+    __syncthreads();
+    if (tid == 0) *a.nnz = zs[0] + zs[1] + zs[2] + zs[3];
 }
 
 // Certified searchsorted of u[t] (one block per draw).
@@ -406,9 +492,9 @@ hipError_t launch_ws_prepare(const WSArgs& a, hipStream_t s)
 {
     const int nb = ws_blocks(a.n), nc = ws_chunks(a.n);
     hipLaunchKernelGGL(k_ws_block, dim3(nb), dim3(kWSThreads), 0, s, a);
-    hipLaunchKernelGGL(k_ws_total, dim3(1), dim3(1), 0, s, a, nb);
+    hipLaunchKernelGGL(k_ws_total, dim3(1), dim3(kWSThreads), 0, s, a, nb);
     hipLaunchKernelGGL(k_ws_prob, dim3(nc), dim3(kWSThreads), 0, s, a);
-    hipLaunchKernelGGL(k_ws_prefix, dim3(1), dim3(1), 0, s, a, nc, 1);
+    hipLaunchKernelGGL(k_ws_prefix, dim3(1), dim3(kWSThreads), 0, s, a, nc, 1);
     return hipGetLastError();
 }
 
@@ -417,7 +503,7 @@ hipError_t launch_ws_zero(const WSArgs& a, hipStream_t s)
     const int nc = ws_chunks(a.n);
     hipLaunchKernelGGL(k_ws_zero, dim3((a.nz + 255) / 256), dim3(256), 0, s, a);
     hipLaunchKernelGGL(k_ws_ctot, dim3(nc), dim3(kWSThreads), 0, s, a);
-    hipLaunchKernelGGL(k_ws_prefix, dim3(1), dim3(1), 0, s, a, nc, 0);
+    hipLaunchKernelGGL(k_ws_prefix, dim3(1), dim3(kWSThreads), 0, s, a, nc, 0);
     return hipGetLastError();
 }
 
