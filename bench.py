@@ -10,8 +10,8 @@ products of the parts are exact in the fp32 accumulators of the bf16 MFMAs,
 the sums use all three parts and the E-step 6 of the 9 part products (the
 three left out total at most 2^-23 |x_i c_i| per feature).  The same steps on
 the fp32-MFMA kernel are timed beside it.  The measurements reported beside
-the metric (that fp32-MFMA run, the end-to-end estimator fit and the k-means++
-seeding) run first; then the headline handle runs the W warm-up steps and the
+the metric (that fp32-MFMA run, the end-to-end estimator fit, the k-means++
+seeding and skmetal's k-means|| seeding) run first; then the headline handle runs the W warm-up steps and the
 K timed steps from the seeded initial centres.  The steps are timed with HIP
 events on the library's stream (skmetal_hip_lloyd_iterate).  The same steps
 are then run again from the same initial centres with each step's kernels
@@ -174,7 +174,7 @@ def main():
                 fp32_mode = h32.info()
         finally:
             del os.environ["SKMETAL_HIP_SPLIT"]
-        fit_ms = pp_ms = None
+        fit_ms = pp_ms = kpar_ms = None
         if args.workload == "c2":
             # the whole estimator fit a user runs on this X (validation,
             # tolerance, upload, k-means++, Lloyd to convergence, final
@@ -198,6 +198,21 @@ def main():
             t = time.perf_counter()
             h.plusplus_with(T, first, u)
             pp_ms = round((time.perf_counter() - t) * 1e3, 3)
+            # skmetal's own MetalKMeans seeding (k-means||: max(1, int(2 + ln k))
+            # rounds of distances, numpy's weighted draws and the prune, all on
+            # the device) of the resident X for random_state=0
+            import warnings
+
+            from sklearn.exceptions import ConvergenceWarning
+
+            from skmetal_amd.estimators.cluster import kmeans_parallel_init
+
+            with warnings.catch_warnings():
+                warnings.simplefilter("ignore", ConvergenceWarning)
+                kmeans_parallel_init(X, k, np.random.RandomState(0), h)
+                t = time.perf_counter()
+                kmeans_parallel_init(X, k, np.random.RandomState(0), h)
+                kpar_ms = round((time.perf_counter() - t) * 1e3, 3)
         # the headline: W warm-up steps, then K timed steps from the same
         # initial centres
         h.set_centers(C0)
@@ -315,6 +330,7 @@ def main():
                              "k_finalize_cols+k_reloc": round(ms_final, 5)}),
         "roofline": roofline,
         "kmeans_plusplus_ms": pp_ms,
+        "kmeans_parallel_init_ms": kpar_ms,
         "fit_kmeanspp_ms": fit_ms,
         "cpu_baseline": cpu,
     }
