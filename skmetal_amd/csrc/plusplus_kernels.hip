@@ -365,8 +365,10 @@ hipError_t launch_pp_mindist(const PPArgs& a, int m, hipStream_t s)
     const dim3 grid((unsigned)a.nb), block(kPPRows);
     if (m <= 8)
         hipLaunchKernelGGL((k_pp_dist<8, true>), grid, block, 0, s, a, 0, m);
-    else
+    else if (m <= 16)
         hipLaunchKernelGGL((k_pp_dist<16, true>), grid, block, 0, s, a, 0, m);
+    else  // passes of 32 (64 at once holds one wave per SIMD: twice the time)
+        hipLaunchKernelGGL((k_pp_dist<32, true>), grid, block, 0, s, a, 0, m);
     return hipGetLastError();
 }
 
