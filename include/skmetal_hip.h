@@ -285,8 +285,10 @@ SKMETAL_API int skmetal_hip_lloyd_mindists(skmetal_hip_lloyd* h, const int64_t* 
  * caller drew with rand(size - found).  The row is found on a cumsum of
  * another order and kept when it is provably the same; the rest (about
  * 4 n 2^-53 of the draws) are searched on numpy's own cumsum, every draw with
- * exact = 1.  *n_exact_out (nullable) = the draws searched that way.  The
- * caller drops repeated rows and draws again, as choice does. */
+ * exact = 1; exact = 2 gives the proof a margin of at least 1/(4n), so that
+ * about half the draws take each search (for tests of both in one pass).
+ * *n_exact_out (nullable) = the draws searched that way.  The caller drops
+ * repeated rows and draws again, as choice does. */
 SKMETAL_API int skmetal_hip_lloyd_sample_prepare(skmetal_hip_lloyd* h, int weights, double* p_sum_out,
                                                  int64_t* nonzero_out);
 SKMETAL_API int skmetal_hip_lloyd_sample_draw(skmetal_hip_lloyd* h, const int64_t* zero_rows, size_t n_zero,

@@ -423,7 +423,7 @@ class LloydHandle:
                                                out.ctypes.data if download else None), "skmetal_hip_lloyd_mindists")
         return out
 
-    def choice(self, random_state, size: int, weights: str = "mindists", exact: bool = False):
+    def choice(self, random_state, size: int, weights: str = "mindists", exact=False):
         """numpy's legacy ``random_state.choice(n, size, replace=False, p=w / w.sum())``
         on the device, for fp32 weights w: "mindists" = the k-means|| distances
         floored at 1e-30 (``np.maximum(dists, 1e-30)``), "unit" = ones.  Same
@@ -431,8 +431,10 @@ class LloydHandle:
         numpy's: rand(size - found) uniforms, their rows, repeats dropped (first
         occurrence kept, in draw order), found rows zeroed, again until size rows.
         exact=True searches numpy's own cumsum for every draw; the default keeps
-        the rows of a cumsum of another order where they provably agree.  The
-        count of draws searched exactly is kept in ``self.sample_exact``."""
+        the rows of a cumsum of another order where they provably agree;
+        exact=2 gives that proof a margin of at least 1/(4n) (about half the
+        draws take each search).  The count of draws searched exactly is kept in
+        ``self.sample_exact``."""
         if weights not in ("mindists", "unit"):
             raise ValueError(f"weights={weights!r} is not 'mindists' or 'unit'")
         n = self.n
@@ -462,7 +464,7 @@ class LloydHandle:
             rows = np.empty(u.size, dtype=np.int64)
             zero = found[:n_uniq]
             _check(_lib.skmetal_hip_lloyd_sample_draw(self._h, zero.ctypes.data if n_uniq else None, n_uniq,
-                                                      u.ctypes.data, u.size, rows.ctypes.data, int(bool(exact)),
+                                                      u.ctypes.data, u.size, rows.ctypes.data, int(exact),
                                                       ctypes.byref(n_exact)), "skmetal_hip_lloyd_sample_draw")
             self.sample_exact += int(n_exact.value)
             _, first = np.unique(rows, return_index=True)

@@ -292,6 +292,7 @@ struct WSArgs {
     long long* nnz;             // [1] rows with p > 0
     double* ex;                 // [n] numpy's cumsum of p (exact search only)
     const double* u; int m;     // this pass's uniforms
+    double dmin;                // the certified search's least margin (0; larger sends more draws to the exact search)
     const long* zero; int nz;   // rows whose p is zeroed before the pass
     long* out;                  // [m] picked rows
     int* unsure;                // [m] 1: the certified search left the draw to the exact search

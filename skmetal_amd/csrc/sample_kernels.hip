@@ -351,7 +351,7 @@ __global__ __launch_bounds__(kWSThreads) void k_ws_search(WSArgs a, int nc)
     const double gam = ne / (1.0 - ne);
     const double B = 2.0 * gam * (T / (1.0 - gam));  // |cdf sums, either order - exact| summed
     const bool ok = T > 0.0 && B <= 0.01 * T;        // false for a NaN total
-    const double Dl = 2.1 * B / (T - B) + 8.0 * eps;
+    const double Dl = fmax(2.1 * B / (T - B) + 8.0 * eps, a.dmin);
     if (tid == 0) {
         // the last chunk whose prefix / T <= u (pfx[0] = 0)
         int lo = 1, hi = nc;

@@ -1050,8 +1050,10 @@ struct Lloyd {
     }
 
     // Rows for the m uniforms u after zeroing p at the nz rows `zero`; exact
-    // = 1 searches numpy's own cumsum for every draw.  *n_exact = draws the
-    // certified search left to the exact one.
+    // = 1 searches numpy's own cumsum for every draw, exact = 2 gives the
+    // certified search a margin of at least 1/(4n) (about half the draws then
+    // go to the exact search: both searches in one pass).  *n_exact = draws
+    // the certified search left to the exact one.
     int sample_draw(const long* zero, long nz, const double* u, long m, long* out, int exact, int* n_exact)
     {
         if (!ws_ready) return fail(SKMETAL_EINVAL, "sample_draw before sample_prepare");
@@ -1080,15 +1082,17 @@ struct Lloyd {
             TRY(grab((void**)&ws.zero, size_t(cap) * sizeof(long)));
             ws_mcap = cap;
         }
+        if (exact < 0 || exact > 2) return fail(SKMETAL_EINVAL, "exact=%d is not 0, 1 or 2", exact);
         ws.m = (int)m;
         ws.nz = (int)nz;
+        ws.dmin = exact == 2 ? 0.25 / (double)n : 0.0;
         if (nz > 0) {
             TRY(upload_bytes(*C, zero, size_t(nz) * sizeof(long), const_cast<long*>(ws.zero), s));
             HIP_TRY(launch_ws_zero(ws, s), "sampling zero launch");
         }
         TRY(upload_bytes(*C, u, size_t(m) * sizeof(double), const_cast<double*>(ws.u), s));
         std::vector<int> uns(size_t(m), 1);
-        if (!exact) {
+        if (exact != 1) {
             HIP_TRY(launch_ws_search(ws, s), "sampling search launch");
             TRY(download_bytes(*C, ws.unsure, size_t(m) * sizeof(int), uns.data(), s));
         }
@@ -1096,7 +1100,7 @@ struct Lloyd {
         for (long i = 0; i < m; ++i) left += uns[i] != 0;
         if (left > 0) {
             if (ws.ex == nullptr) TRY(grab((void**)&ws.ex, size_t(n) * sizeof(double)));
-            HIP_TRY(launch_ws_exact(ws, exact ? 1 : 0, s), "sampling exact launch");
+            HIP_TRY(launch_ws_exact(ws, exact == 1 ? 1 : 0, s), "sampling exact launch");
         }
         TRY(download_bytes(*C, ws.out, size_t(m) * sizeof(long), out, s));
         *n_exact = (int)left;

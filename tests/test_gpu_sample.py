@@ -62,6 +62,7 @@ def test_choice_matches_numpy(bridge, n, d, size, cand):
     with bridge.LloydHandle(n, d, 1) as h:
         h.load(X, center=False)
         dists = h.mindists(rows0, reset=True)
+        mixed = 0
         for seed in range(4):
             ref, ref_next = _numpy_choice(dists, size, seed)
             got, got_next, _ = _device_choice(h, size, seed)
@@ -70,6 +71,13 @@ def test_choice_matches_numpy(bridge, n, d, size, cand):
             got_x, _, n_exact = _device_choice(h, size, seed, exact=True)
             assert np.array_equal(got_x, ref)
             assert n_exact >= size
+            # a margin of 1/(4n): about half the draws take the exact search,
+            # the rest stay with the certified one, in the same pass
+            got_w, _, n_w = _device_choice(h, size, seed, exact=2)
+            assert np.array_equal(got_w, ref)
+            mixed += 0 < n_w < size
+        if size >= 8:
+            assert mixed > 0, "no pass split its draws between the two searches"
 
 
 def test_choice_repeats_take_more_passes(bridge):
