@@ -290,7 +290,8 @@ struct WSArgs {
     int* cnz;                   // [ws_chunks(n)] rows with p > 0 per chunk
     double* pfx;                // [ws_chunks(n) + 1] chunk sums' running total, pfx[0] = 0
     long long* nnz;             // [1] rows with p > 0
-    double* ex;                 // [n] numpy's cumsum of p (exact search only)
+    double* cst;                // [ws_chunks(n) + 1] numpy's cumsum before each chunk, then the total (exact search)
+    int* cseq;                  // [ws_chunks(n)] 1: the chunk's sums come from a walk in row order
     const double* u; int m;     // this pass's uniforms
     double dmin;                // the certified search's least margin (0; larger sends more draws to the exact search)
     const long* zero; int nz;   // rows whose p is zeroed before the pass
@@ -305,8 +306,8 @@ hipError_t launch_ws_prepare(const WSArgs& a, hipStream_t s);
 hipError_t launch_ws_zero(const WSArgs& a, hipStream_t s);
 // Certified search of the m uniforms: out, unsure.
 hipError_t launch_ws_search(const WSArgs& a, hipStream_t s);
-// numpy's sequential cumsum, then the search of the unsure draws (all != 0:
-// every draw).
+// numpy's sequential cumsum (exactly, per chunk), then the search of the
+// unsure draws (all != 0: every draw).
 hipError_t launch_ws_exact(const WSArgs& a, int all, hipStream_t s);
 
 // KMeans.transform (transform_kernels.hip): out[i, j] = ||x_i - c_j|| in

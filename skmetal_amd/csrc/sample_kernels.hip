@@ -31,10 +31,10 @@
 //                 Delta (below) at every row.  r is certified when
 //                 cdf~[r-1] < u - Delta and cdf~[r] > u + Delta; otherwise
 //                 the draw is marked unsure;
-//   k_ws_exact    (only for unsure draws) numpy's cumsum itself: one thread
-//                 adds p in row order while the block streams p in and the
-//                 sums out through LDS;
-//   k_ws_exact_search  binary search of u over cumsum / cumsum[n - 1].
+//   k_ws_chain    (only for unsure draws) numpy's cumsum itself, exactly,
+//                 chunk by chunk: inside one binade of the running sum the
+//                 additions are exact integer sums on that binade's grid;
+//   k_ws_exact_search  the draw's chunk, then its row, on those sums.
 //
 // An unsure draw needs u within Delta ~ 4 n 2^-53 of one of the n cdf values:
 // at n = 500,000 about 2e-4 of the draws.
@@ -49,7 +49,6 @@ namespace {
 constexpr int kWSThreads = 256;
 constexpr int kLeaf = 128;     // numpy's PW_BLOCKSIZE
 constexpr int kMaxLeaves = 72; // a block of <= 8192 has at most 65 leaves
-constexpr int kExTile = 2048;  // doubles per LDS tile of the exact cumsum
 
 __device__ __forceinline__ int pw_half(int l)
 {
@@ -422,65 +421,167 @@ __global__ __launch_bounds__(kWSThreads) void k_ws_search(WSArgs a, int nc)
     }
 }
 
-// numpy's cumsum of p: thread 0 adds in row order; the block streams p in and
-// the sums out through three LDS tiles (load t + 1, add t, store t - 1).
-__global__ __launch_bounds__(kWSThreads) void k_ws_exact(WSArgs a)
+// numpy's cumsum of p, exactly, chunk by chunk (one block): s = the sum before
+// chunk c.  While the running sum stays in one binade [2^e, 2^(e+1)), every
+// double there is a multiple of g = 2^(e-52), so fl(s + p) = s + g RN(p / g):
+// the chunk's sums are s + g Q_i with Q_i an exact int64 prefix of q_j =
+// RN(p_j / g).  A chunk is walked in row order by one thread instead when s is
+// 0, when its sum leaves the binade, or when some p_j / g ends in exactly .5
+// (a tie, whose rounding depends on the running sum's last bit).  cst[c] = s
+// before chunk c (cst[nc] = the total), cseq[c] = 1 for a walked chunk.
+__device__ __forceinline__ bool grid_q(double v, int e, long long& q)
 {
-    __shared__ double buf[3][kExTile];
-    const int tid = threadIdx.x;
-    const long nt = (a.n + kExTile - 1) / kExTile;
-    auto load = [&](long t) {
-        const long g0 = t * kExTile;
-        double* bp = buf[t % 3];
-        for (int i = tid; i < kExTile; i += kWSThreads) bp[i] = g0 + i < a.n ? a.p[g0 + i] : 0.0;
-    };
-    auto store = [&](long t) {
-        const long g0 = t * kExTile;
-        const double* bp = buf[t % 3];
-        for (int i = tid; i < kExTile; i += kWSThreads)
-            if (g0 + i < a.n) a.ex[g0 + i] = bp[i];
-    };
+    const double w = ldexp(v, 52 - e);  // exact
+    if (w >= 0x1p52) return false;
+    const double fl = floor(w), fr = w - fl;  // exact
+    if (fr == 0.5) return false;
+    q = (long long)fl + (fr > 0.5 ? 1 : 0);
+    return true;
+}
+
+__global__ __launch_bounds__(kWSThreads) void k_ws_chain(WSArgs a, int nc)
+{
+    constexpr int PT = kWSChunk / kWSThreads;
+    __shared__ double tile[kWSChunk];
+    __shared__ long long qred[kWSThreads / 64];
+    __shared__ int bred[kWSThreads / 64];
+    __shared__ double walked;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     double s = 0.0;
-    load(0);
-    __syncthreads();
-    for (long t = 0; t < nt; ++t) {
-        if (t + 1 < nt) load(t + 1);
-        if (t >= 1) store(t - 1);
-        if (tid == 0) {
-            double* bp = buf[t % 3];
-            for (int i = 0; i < kExTile; i += 16) {
-                double v[16];
+    for (int c = 0; c < nc; ++c) {
+        const long c0 = (long)c * kWSChunk;
+        const int len = (int)min((long)kWSChunk, a.n - c0);
+        double v[PT];
 #pragma unroll
-                for (int j = 0; j < 16; ++j) v[j] = bp[i + j];
+        for (int j = 0; j < PT; ++j) {
+            const int i = tid + kWSThreads * j;
+            v[j] = i < len ? a.p[c0 + i] : 0.0;
+            tile[i] = v[j];
+        }
+        long long q = 0;
+        int bad = s > 0.0 ? 0 : 1;
+        const int e = s > 0.0 ? ilogb(s) : 0;
+        if (!bad) {
 #pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    s += v[j];
-                    v[j] = s;
-                }
-#pragma unroll
-                for (int j = 0; j < 16; ++j) bp[i + j] = v[j];
+            for (int j = 0; j < PT; ++j) {
+                long long qj = 0;
+                if (!grid_q(v[j], e, qj)) bad = 1;
+                q += qj;
             }
         }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            q += __shfl_xor(q, off, 64);
+            bad |= __shfl_xor(bad, off, 64);
+        }
+        if (lane == 0) {
+            qred[wv] = q;
+            bred[wv] = bad;
+        }
         __syncthreads();
+        const long long Q = (qred[0] + qred[1]) + (qred[2] + qred[3]);
+        bool ok = (bred[0] | bred[1] | bred[2] | bred[3]) == 0 && Q < (1LL << 53);
+        double next = s;
+        if (ok) {
+            next = s + ldexp((double)Q, e - 52);  // a multiple of g: exact while below 2^(e+1)
+            ok = next < ldexp(1.0, e + 1);
+        }
+        if (tid == 0) {
+            a.cst[c] = s;
+            a.cseq[c] = ok ? 0 : 1;
+        }
+        if (!ok) {
+            if (tid == 0) {
+                double r = s;
+                for (int i = 0; i < len; ++i) r += tile[i];
+                walked = r;
+            }
+            __syncthreads();
+            next = walked;
+        }
+        s = next;
+        __syncthreads();  // the tile and the reductions are reused
     }
-    store(nt - 1);
+    if (tid == 0) a.cst[nc] = s;
 }
 
 // searchsorted(cumsum / cumsum[n - 1], u, side="right") for the unsure draws
-// (every draw with all != 0).
-__global__ void k_ws_exact_search(WSArgs a, int all)
+// (every draw with all != 0), one block per draw: the chunk whose end is the
+// first above u, then its sums rebuilt as k_ws_chain formed them.
+__global__ __launch_bounds__(kWSThreads) void k_ws_exact_search(WSArgs a, int nc, int all)
 {
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= a.m || !(all || a.unsure[t])) return;
+    constexpr int PT = kWSChunk / kWSThreads;
+    __shared__ int csh;
+    __shared__ long long qex[kWSThreads / 64];
+    __shared__ int cred[kWSThreads / 64];
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    if (!(all || a.unsure[t])) return;
     const double u = a.u[t];
-    const double last = a.ex[a.n - 1];
-    long lo = 0, hi = a.n;
-    while (lo < hi) {
-        const long mid = (lo + hi) >> 1;
-        if (a.ex[mid] / last <= u) lo = mid + 1;
-        else hi = mid;
+    const double T = a.cst[nc];
+    if (tid == 0) {
+        int lo = 0, hi = nc - 1;  // cst[nc] / T = 1 > u: the last chunk qualifies
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (a.cst[mid + 1] / T <= u) lo = mid + 1;
+            else hi = mid;
+        }
+        csh = lo;
     }
-    a.out[t] = lo;
+    __syncthreads();
+    const int c = csh;
+    const long c0 = (long)c * kWSChunk;
+    const int len = (int)min((long)kWSChunk, a.n - c0);
+    const double s0 = a.cst[c];
+    int count = 0;
+    if (a.cseq[c] != 0) {
+        if (tid == 0) {
+            double r = s0;
+            for (int i = 0; i < len; ++i) {
+                r += a.p[c0 + i];
+                if (r / T > u) break;
+                ++count;
+            }
+            cred[0] = count;
+        }
+        __syncthreads();
+        count = cred[0];
+    } else {
+        // thread tid holds rows PT tid .. PT tid + PT - 1: local prefixes, then
+        // an exclusive scan of the thread totals (int64, exact)
+        const int e = ilogb(s0);
+        long long loc[PT], run = 0;
+#pragma unroll
+        for (int j = 0; j < PT; ++j) {
+            const int i = PT * tid + j;
+            long long qj = 0;
+            if (i < len) (void)grid_q(a.p[c0 + i], e, qj);  // the chain checked every q_j
+            run += qj;
+            loc[j] = run;
+        }
+        long long inc = run;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const long long o = __shfl_up(inc, off, 64);
+            if (lane >= off) inc += o;
+        }
+        if (lane == 63) qex[wv] = inc;
+        __syncthreads();
+        long long base = inc - run;
+        for (int w = 0; w < wv; ++w) base += qex[w];
+        int cnt = 0;
+#pragma unroll
+        for (int j = 0; j < PT; ++j) {
+            const int i = PT * tid + j;
+            const double si = s0 + ldexp((double)(base + loc[j]), e - 52);
+            cnt += (i < len && si / T <= u) ? 1 : 0;
+        }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) cnt += __shfl_xor(cnt, off, 64);
+        if (lane == 0) cred[wv] = cnt;
+        __syncthreads();
+        count = cred[0] + cred[1] + cred[2] + cred[3];
+    }
+    if (tid == 0) a.out[t] = c0 + count;
 }
 
 }  // namespace
@@ -515,8 +616,9 @@ hipError_t launch_ws_search(const WSArgs& a, hipStream_t s)
 
 hipError_t launch_ws_exact(const WSArgs& a, int all, hipStream_t s)
 {
-    hipLaunchKernelGGL(k_ws_exact, dim3(1), dim3(kWSThreads), 0, s, a);
-    hipLaunchKernelGGL(k_ws_exact_search, dim3((a.m + 63) / 64), dim3(64), 0, s, a, all);
+    const int nc = ws_chunks(a.n);
+    hipLaunchKernelGGL(k_ws_chain, dim3(1), dim3(kWSThreads), 0, s, a, nc);
+    hipLaunchKernelGGL(k_ws_exact_search, dim3(a.m), dim3(kWSThreads), 0, s, a, nc, all);
     return hipGetLastError();
 }
 

@@ -1099,7 +1099,10 @@ struct Lloyd {
         long left = 0;
         for (long i = 0; i < m; ++i) left += uns[i] != 0;
         if (left > 0) {
-            if (ws.ex == nullptr) TRY(grab((void**)&ws.ex, size_t(n) * sizeof(double)));
+            if (ws.cst == nullptr) {
+                TRY(grab((void**)&ws.cst, size_t(ws_chunks(n) + 1) * sizeof(double)));
+                TRY(grab((void**)&ws.cseq, size_t(ws_chunks(n)) * sizeof(int)));
+            }
             HIP_TRY(launch_ws_exact(ws, exact == 1 ? 1 : 0, s), "sampling exact launch");
         }
         TRY(download_bytes(*C, ws.out, size_t(m) * sizeof(long), out, s));

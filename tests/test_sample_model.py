@@ -16,10 +16,14 @@ kernels restate three facts about it, each pinned here on numpy's own outputs:
 * the certified search's error bound: any order of adding non-negative terms
   whose every term passes through at most h roundings is within gamma_h of the
   exact sum relative to the total, so a tree-order prefix and numpy's
-  sequential cumsum differ by at most 2 gamma_n of the total.
+  sequential cumsum differ by at most 2 gamma_n of the total;
+* the exact search's cumsum: numpy's sequential fp64 cumsum rebuilt chunk by
+  chunk from exact integer sums on the running sum's binade grid.
 """
 
 from __future__ import annotations
+
+import math
 
 import numpy as np
 import pytest
@@ -145,3 +149,71 @@ def test_tree_prefix_within_bound_of_numpy_cumsum():
         # the bound is not vacuous: it is far below the smallest cdf step a
         # draw would have to fall between
         assert bound < 1e-9
+
+
+def _grid_q(v, e):
+    w = math.ldexp(v, 52 - e)
+    if w >= 2.0**52:
+        return None
+    fl = math.floor(w)
+    fr = w - fl
+    if fr == 0.5:
+        return None
+    return int(fl) + (1 if fr > 0.5 else 0)
+
+
+def _chunked_cumsum(p, ch=2048):
+    """The exact search's cumsum: per chunk, while the running sum s stays in
+    one binade [2^e, 2^(e+1)), fl(s + p) = s + 2^(e-52) RN(p / 2^(e-52)), so
+    the chunk's sums are s plus an exact integer prefix on that grid; a chunk
+    that starts at 0, leaves the binade or holds a tie (p / grid ending in
+    exactly .5) is added in row order instead."""
+    out = np.empty(len(p))
+    s, walked = 0.0, 0
+    for c0 in range(0, len(p), ch):
+        chunk = [float(v) for v in p[c0:c0 + ch]]
+        qs = None
+        if s > 0.0:
+            e = math.frexp(s)[1] - 1
+            qs = [_grid_q(v, e) for v in chunk]
+            if any(q is None for q in qs) or sum(qs) >= 2**53 or s + math.ldexp(float(sum(qs)), e - 52) >= 2.0**(e + 1):
+                qs = None
+        if qs is None:
+            walked += 1
+            r = s
+            for i, v in enumerate(chunk):
+                r = r + v
+                out[c0 + i] = r
+        else:
+            acc = 0
+            for i, q in enumerate(qs):
+                acc += q
+                out[c0 + i] = s + math.ldexp(float(acc), e - 52)
+        s = out[c0 + len(chunk) - 1]
+    return out, walked
+
+
+def test_chunked_cumsum_is_numpys():
+    # uniform, widely spread, a few dominant and many zero probabilities: the
+    # grid sums and the walked chunks both give numpy's cumsum bit for bit, and
+    # both kinds of chunk occur
+    rng = np.random.default_rng(3)
+    walked = chunks = 0
+    for kind in range(4):
+        n = 20_000 + 977 * kind
+        if kind == 0:
+            w = np.ones(n, np.float32)
+        elif kind == 1:
+            w = np.maximum((rng.random(n) ** 9).astype(np.float32), np.float32(1e-30))
+        elif kind == 2:
+            w = np.maximum((rng.random(n) * 1e-3).astype(np.float32), np.float32(1e-30))
+            w[rng.integers(0, n, 5)] = 1e3
+        else:
+            w = rng.exponential(1.0, n).astype(np.float32)
+            w[rng.choice(n, n // 3)] = 0.0
+        p = (w / w.sum()).astype(np.float64)
+        got, wk = _chunked_cumsum(p)
+        assert np.array_equal(got, np.cumsum(p))
+        walked += wk
+        chunks += -(-n // 2048)
+    assert 0 < walked < chunks
