@@ -184,3 +184,20 @@ def test_mindists_candidate_buffer_growth(bridge):
             rows = rng.choice(5000, m, replace=False)
             seen.extend(rows.tolist())
             _check(h.mindists(rows, reset=(i == 0)), f(rows, i == 0), X, seen, f"round {i} (m={m})")
+
+
+def test_parallel_init_large_k_matches_oracle(bridge):
+    """k = 512: int(2 + ln 512) = 8 rounds of 512 draws each (the draw blocks,
+    repeated passes, the candidate buffers growing), then ~4,000 candidates
+    pruned by one Lloyd iteration of k = 512 on the device's generic path."""
+    from skmetal_amd.estimators.cluster import kmeans_parallel_init
+
+    n, d, k = 60_000, 24, 512
+    X = _blobs(n, d, 40, 21)
+    _say(f"k-means|| init n={n} d={d} k={k}")
+    with bridge.LloydHandle(n, d, k) as h:
+        h.load(X, center=False)
+        got, got_rows = kmeans_parallel_init(X, k, np.random.RandomState(5), h, trace=True)
+    ref, ref_rows = oracle.kmeans_parallel_init(X, k, np.random.RandomState(5), trace=True)
+    assert len(ref_rows) > 8 * k // 2
+    _check_init(got, got_rows, ref, ref_rows, k, f"n={n} d={d} k={k}")
