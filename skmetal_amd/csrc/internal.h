@@ -62,6 +62,7 @@ struct AssignArgs {
     int* labels;
     LoopState* state;      // nullable: no early exit
     int* changed;          // nullable: compare with previous labels, add the changes here
+    char* img;             // k_assign3 only: [assign3_image_bytes(k, ld)] the centres' staged image
 };
 hipError_t launch_assign(const AssignArgs& a, int num_cu, hipStream_t s);
 // The same E-step on bf16 MFMAs over the exact three-part bf16 split of x
@@ -69,6 +70,8 @@ hipError_t launch_assign(const AssignArgs& a, int num_cu, hipStream_t s);
 // (sets its LDS attributes).  The data must be in the split's range
 // (split_range_ok).
 int assign3_ready(int d, int k);
+// Bytes of k_assign3's centre image (written by launch_assign3 before the E-step).
+size_t assign3_image_bytes(int k, int ld);
 hipError_t launch_assign3(const AssignArgs& a, int num_cu, hipStream_t s);
 // The three-part bf16 split is exact for finite values of magnitude >= 2^-103,
 // and the E-step's smallest kept part products stay normal fp32 numbers when

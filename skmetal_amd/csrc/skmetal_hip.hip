@@ -613,12 +613,17 @@ struct Lloyd {
         return 0;
     }
 
+    char* a3img = nullptr;  // k_assign3's centre image
+
     int assign(const float* cents, LoopState* state, int* changed)
     {
-        AssignArgs a{X, n, ld, cents, cnorm, k, labels, state, changed};
-        if (split_on && a3cap)
+        AssignArgs a{X, n, ld, cents, cnorm, k, labels, state, changed, nullptr};
+        // (the image is addressed with 32-bit buffer offsets)
+        if (split_on && a3cap && assign3_image_bytes(k, ld) < (size_t(1) << 31)) {
+            if (a3img == nullptr) TRY(grab((void**)&a3img, assign3_image_bytes(k, ld)));
+            a.img = a3img;
             HIP_TRY(launch_assign3(a, C->num_cu, s), "assign launch");
-        else
+        } else
             HIP_TRY(launch_assign(a, C->num_cu, s), "assign launch");
         return 0;
     }

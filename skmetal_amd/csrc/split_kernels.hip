@@ -686,44 +686,94 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
 // k_assign3: the E-step for any k (the generic path and the assign entry
 // point) on bf16 MFMA over the three-part split, with k_fused3's operand
 // layout.  A block of 8 waves owns 256 rows (32 per wave: two 16-row groups);
-// it takes the centres in passes of 16*CB (A operands from LDS, the three
-// parts staged per SEG-feature segment by the whole block) and keeps per lane
-// the first minimum over its centres 16cb + 4(l/16) + i, in ascending order
-// across passes; the four lanes of a row are combined after the last pass.
-// X is read once per pass (k/(16 CB) times), the centres once per 256 rows.
+// it takes the centres in passes of 16*CB (A operands from LDS) and keeps per
+// lane the first minimum over its centres 16cb + 4(l/16) + i, in ascending
+// order across passes; the four lanes of a row are combined after the last
+// pass.  X is read once per pass (k/(16 CB) times).
+//
+// The centres' parts come from an image that k_centre_image writes once per
+// step: per stage (pass p, SEG-feature segment sg) the three bf16 parts of
+// centres 16 CB p.. as rows of CSTR bf16 (zeros past k and ld), then the
+// pass's ||c||^2 (+inf past k), padded to whole KB -- the LDS layout itself.
+// Two LDS stages alternate: while the MFMAs of one run, the next stage's
+// image is copied in with direct-to-LDS loads (1 KB per wave instruction).
 template <int CB>
 struct Assign3Geom {
-    static constexpr int CPC = 16 * CB;               // centres per pass
-    static constexpr int SEG = CB >= 16 ? 64 : 128;   // features per staged segment
-    static constexpr int NKS = SEG / 32;              // K32 steps per segment
-    static constexpr int CSTR = SEG + 8;              // bf16 per centre row: an odd number of 16-byte units
-    static constexpr int CPART = CPC * CSTR;          // bf16 from one part to the next
-    static constexpr size_t LDS = size_t(3) * CPART * sizeof(__bf16);
+    static constexpr int CPC = 16 * CB;                             // centres per pass
+    static constexpr int SEG = CB >= 16 ? 32 : CB >= 8 ? 64 : 128;  // features per stage
+    static constexpr int NKS = SEG / 32;                            // K32 steps per stage
+    static constexpr int CSTR = SEG + 8;                            // bf16 per centre row: an odd number of 16-byte units
+    static constexpr int CPART = CPC * CSTR;                        // bf16 from one part to the next
+    static constexpr int PBYTES = 3 * CPART * 2;                    // the three parts
+    static constexpr int STAGE = (PBYTES + CPC * 4 + 1023) / 1024 * 1024;  // + ||c||^2, whole KB
+    static constexpr size_t LDS = size_t(2) * STAGE;
 };
 
 template <int CB>
+__global__ __launch_bounds__(256) void k_centre_image(const float* __restrict__ C, const float* __restrict__ cnorm,
+                                                      int k, int ld, int nseg, char* __restrict__ img)
+{
+    using G = Assign3Geom<CB>;
+    const int stg = blockIdx.x, p = stg / nseg, sg = stg - p * nseg;
+    char* const out = img + (size_t)stg * G::STAGE;
+    __bf16* const parts = reinterpret_cast<__bf16*>(out);
+    constexpr int Q = G::CSTR / 4;  // 4-feature groups per row, padding included
+    for (int e = threadIdx.x; e < G::CPC * Q; e += 256) {
+        const int c = e / Q, q = e - c * Q;
+        const int j = p * G::CPC + c, f = sg * G::SEG + 4 * q;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (4 * q < G::SEG && j < k && f < ld) v = *reinterpret_cast<const float4*>(C + (long)j * ld + f);
+        const Parts4 pt = split4(v);
+        __bf16* dst = parts + c * G::CSTR + 4 * q;
+        *reinterpret_cast<v4s*>(dst) = pt.h;
+        *reinterpret_cast<v4s*>(dst + G::CPART) = pt.m;
+        *reinterpret_cast<v4s*>(dst + 2 * G::CPART) = pt.l;
+    }
+    float* const sn = reinterpret_cast<float*>(out + G::PBYTES);
+    for (int c = threadIdx.x; c < G::STAGE / 4 - G::PBYTES / 4; c += 256) {
+        const int j = p * G::CPC + c;
+        sn[c] = c < G::CPC ? (j < k ? cnorm[j] : INFINITY) : 0.f;  // padding centres never win
+    }
+}
+
+template <int CB>
 __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X, long n, int ld,
-                                                   const float* __restrict__ C, const float* __restrict__ cnorm,
-                                                   int k, int* __restrict__ labels, LoopState* st, int* changed)
+                                                   const char* __restrict__ img, int k, int* __restrict__ labels,
+                                                   LoopState* st, int* changed)
 {
     if (st != nullptr && st->done != 0) return;
     using G = Assign3Geom<CB>;
     constexpr int CPC = G::CPC, SEG = G::SEG, NKS = G::NKS, CSTR = G::CSTR, CPART = G::CPART;
-    extern __shared__ __attribute__((aligned(16))) __bf16 cs[];  // [3][CPC][CSTR]
-    __shared__ __attribute__((aligned(16))) float sN[CPC];
+    extern __shared__ __attribute__((aligned(1024))) char smem[];  // two stages
     __shared__ int sChg;  // labels the block changed
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 4, r16 = lane & 15;
-    if (tid == 0) sChg = 0;  // (published by the first staging barrier, or read back by this thread)
+    if (tid == 0) sChg = 0;  // (published by the first barrier)
     int nchg = 0;            // lane 0: labels this wave changed
     const int npass = (k + CPC - 1) / CPC;
     const int nseg = (ld + SEG - 1) / SEG;
-    const __bf16* const cbase = cs + r16 * CSTR + 8 * h;
-    // one pass of one segment (k <= 16 CB, ld <= SEG): the staged operands
-    // are the same for every row block, so they are staged once
-    const bool once = npass == 1 && nseg == 1;
+    const int nst = npass * nseg;
+    // stage stg's image into LDS stage b: wave w copies KB w, w + 8, .. (the
+    // buffer descriptor spans the whole image)
+    const __amdgpu_buffer_rsrc_t irs = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(img), (short)0,
+                                                                         nst * G::STAGE, 0x00020000);
+    // (the offsets go through plain ints: a template-dependent argument of the
+    // builtin leaves the host side without the kernel's launch stub)
+    const int stage_bytes = G::STAGE;
+    auto copy_stage = [&](int stg, int b) {
+        char* dst = smem + b * stage_bytes;
+        for (int i = wave; i < stage_bytes / 1024; i += 8) {
+            const int soff = stg * stage_bytes + i * 1024;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(irs, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16,
+                                                     lane * 16, soff, 0, 0);
+        }
+    };
+    copy_stage(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    int cur = 0;  // the LDS stage holding the current stage
 
     for (long base = (long)blockIdx.x * 256; base < n; base += (long)gridDim.x * 256) {
         const long wrow = base + 32 * wave;  // this wave's first row
@@ -740,53 +790,9 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
                 for (int cb = 0; cb < CB; ++cb) acc[g][cb] = v4f{0.f, 0.f, 0.f, 0.f};
             }
             for (int sg = 0; sg < nseg; ++sg) {
+                const int stg = p * nseg + sg;
                 const int f0 = sg * SEG;
-                if (!once || base == (long)blockIdx.x * 256) {  // (uniform across the block)
-                __syncthreads();  // the previous segment's operands are consumed
-                // stage centres p*CPC.. x the features f0.. of the K steps this
-                // segment has (32 each; centres >= k and features >= ld zero),
-                // as the three bf16 parts: eight threads per (centre, K step),
-                // two K steps' loads in flight before the first split
-                constexpr int UPK = CPC * 8 / 512;  // float4s per thread per K step
-                const int nks_s = min(NKS, (ld - f0 + 31) / 32);
-                for (int ks0 = 0; ks0 < nks_s; ks0 += 2) {
-                    float4 v[2][UPK];
-#pragma unroll
-                    for (int kk = 0; kk < 2; ++kk) {
-#pragma unroll
-                        for (int u = 0; u < UPK; ++u) {
-                            const int idx = tid + 512 * u;
-                            const int j = p * CPC + (idx >> 3);
-                            const int f = f0 + 4 * (8 * (ks0 + kk) + (idx & 7));
-                            v[kk][u] = make_float4(0.f, 0.f, 0.f, 0.f);
-                            if (ks0 + kk < nks_s && j < k && f < ld)
-                                v[kk][u] = *reinterpret_cast<const float4*>(C + (long)j * ld + f);
-                        }
-                    }
-#pragma unroll
-                    for (int kk = 0; kk < 2; ++kk) {
-                        if (ks0 + kk >= nks_s) break;
-#pragma unroll
-                        for (int u = 0; u < UPK; ++u) {
-                            const int idx = tid + 512 * u;
-                            const int cl = idx >> 3;
-                            const int q = 8 * (ks0 + kk) + (idx & 7);
-                            const Parts4 pt = split4(v[kk][u]);
-                            __bf16* dst = cs + cl * CSTR + 4 * q;
-                            *reinterpret_cast<v4s*>(dst) = pt.h;
-                            *reinterpret_cast<v4s*>(dst + CPART) = pt.m;
-                            *reinterpret_cast<v4s*>(dst + 2 * CPART) = pt.l;
-                        }
-                    }
-                }
-                if (sg == 0) {
-                    for (int i = tid; i < CPC; i += 512) {
-                        const int j = p * CPC + i;
-                        sN[i] = j < k ? cnorm[j] : INFINITY;  // padding centres never win
-                    }
-                }
-                __syncthreads();
-                }
+                const __bf16* const cbase = reinterpret_cast<const __bf16*>(smem + cur * G::STAGE) + r16 * CSTR + 8 * h;
                 const int nks = min(NKS, (ld - f0 + 31) / 32);
                 for (int ks = 0; ks < nks; ++ks) {
                     // rows 16g + l%16, features f0 + 32ks + 8h..: past the
@@ -798,6 +804,9 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
                         const int o = ((16 * g + r16) * ld + f0 + 32 * ks + 8 * h) * 4;
                         xp[g] = split8(load_quad(rs, o), load_quad(rs, o + 16));
                     }
+                    // the next stage's copy goes out behind the stage's last
+                    // X loads (loads complete in order: X waits never wait on it)
+                    if (ks == nks - 1 && nst > 1) copy_stage(stg + 1 < nst ? stg + 1 : 0, cur ^ 1);
                     // four centre blocks at a time, product-major over their
                     // eight accumulators: consecutive MFMAs write different
                     // accumulators (a block's six products back to back wait
@@ -831,9 +840,20 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
                         }
                     }
                 }
+                if (nst > 1) {
+                    // the next stage is in (every wave's copies) and this one
+                    // is read: swap
+                    __builtin_amdgcn_s_waitcnt(0);
+                    __syncthreads();
+                    cur ^= 1;
+                }
             }
             // ||c||^2 - 2 x.c, first minimum wins (_k_means_lloyd.pyx:196-212);
-            // the lane's centres come in ascending order, passes too
+            // the lane's centres come in ascending order, passes too.
+            // ||c||^2 rides in every stage of the pass: the one just read
+            // (the other LDS stage after a swap) is rewritten only by the
+            // next stage's copy, issued after this.
+            const float* sN = reinterpret_cast<const float*>(smem + (nst > 1 ? cur ^ 1 : cur) * G::STAGE + G::PBYTES);
 #pragma unroll
             for (int g = 0; g < 2; ++g) {
 #pragma unroll
@@ -883,7 +903,8 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
     }
 }
 
-typedef void (*assign3_fn)(const float*, long, int, const float*, const float*, int, int*, LoopState*, int*);
+typedef void (*assign3_fn)(const float*, long, int, const char*, int, int*, LoopState*, int*);
+typedef void (*image_fn)(const float*, const float*, int, int, int, char*);
 
 static int assign3_cb(int k) { return k <= 64 ? 4 : k <= 128 ? 8 : 16; }
 
@@ -897,6 +918,25 @@ static size_t assign3_lds(int k)
 {
     const int cb = assign3_cb(k);
     return cb == 4 ? Assign3Geom<4>::LDS : cb == 8 ? Assign3Geom<8>::LDS : Assign3Geom<16>::LDS;
+}
+
+// (stages, bytes per stage) of k_assign3's centre image for (k, ld)
+static void assign3_stages(int k, int ld, int* nst, int* nseg, size_t* stage)
+{
+    const int cb = assign3_cb(k);
+    const int cpc = 16 * cb;
+    const int seg = cb == 4 ? Assign3Geom<4>::SEG : cb == 8 ? Assign3Geom<8>::SEG : Assign3Geom<16>::SEG;
+    *stage = cb == 4 ? Assign3Geom<4>::STAGE : cb == 8 ? Assign3Geom<8>::STAGE : Assign3Geom<16>::STAGE;
+    *nseg = (ld + seg - 1) / seg;
+    *nst = ((k + cpc - 1) / cpc) * *nseg;
+}
+
+size_t assign3_image_bytes(int k, int ld)
+{
+    int nst = 0, nseg = 0;
+    size_t stage = 0;
+    assign3_stages(k, ld, &nst, &nseg, &stage);
+    return size_t(nst) * stage;
 }
 
 // SKMETAL_HIP_SPLIT=0 keeps the fp32 MFMA E-step for every shape
@@ -923,10 +963,17 @@ int assign3_ready(int d, int k)
 hipError_t launch_assign3(const AssignArgs& a, int num_cu, hipStream_t s)
 {
     if (a.n <= 0) return hipSuccess;
+    if (a.img == nullptr) return hipErrorInvalidValue;
+    int nst = 0, nseg = 0;
+    size_t stage = 0;
+    assign3_stages(a.k, a.ld, &nst, &nseg, &stage);
+    const int cb = assign3_cb(a.k);
+    const image_fn img = cb == 4 ? &k_centre_image<4> : cb == 8 ? &k_centre_image<8> : &k_centre_image<16>;
+    hipLaunchKernelGGL(img, dim3((unsigned)nst), dim3(256), 0, s, a.C, a.cnorm, a.k, a.ld, nseg, a.img);
     long blocks = (a.n + 255) / 256;
     if (blocks > num_cu) blocks = num_cu;
     hipLaunchKernelGGL(assign3_kernel(a.k), dim3((unsigned)blocks), dim3(512), assign3_lds(a.k), s, a.X, a.n, a.ld,
-                       a.C, a.cnorm, a.k, a.labels, a.state, a.changed);
+                       a.img, a.k, a.labels, a.state, a.changed);
     return hipGetLastError();
 }
 typedef void (*fused_fn)(FusedArgs);
