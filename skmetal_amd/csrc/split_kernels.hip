@@ -770,6 +770,27 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
                                                      lane * 16, soff, 0, 0);
         }
     };
+    // this wave's 32 rows of the row block at base (past the last row the
+    // descriptor is empty: loads return 0)
+    auto rows_rsrc = [&](long base) {
+        const long wrow = base + 32 * wave;
+        const long nrow = n - wrow < 32 ? (n - wrow > 0 ? n - wrow : 0) : 32;
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(X + (nrow > 0 ? wrow * ld : 0)), (short)0,
+                                                 (int)(nrow * ld * 4), 0x00020000);
+    };
+    // rows 16g + l%16, features f + 8h..: past the row's end the next row's
+    // (finite) values meet zero centre parts.  The K step after the current
+    // one is loaded while the current one's MFMAs run.
+    float4 xr[2][2];
+    auto xload = [&](__amdgpu_buffer_rsrc_t r, int f) {
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const int o = ((16 * g + r16) * ld + f + 8 * h) * 4;
+            xr[g][0] = load_quad(r, o);
+            xr[g][1] = load_quad(r, o + 16);
+        }
+    };
+    xload(rows_rsrc((long)blockIdx.x * 256), 0);
     copy_stage(0, 0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -778,8 +799,7 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
     for (long base = (long)blockIdx.x * 256; base < n; base += (long)gridDim.x * 256) {
         const long wrow = base + 32 * wave;  // this wave's first row
         const long nrow = n - wrow < 32 ? (n - wrow > 0 ? n - wrow : 0) : 32;
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float*>(X + (nrow > 0 ? wrow * ld : 0)), (short)0, (int)(nrow * ld * 4), 0x00020000);
+        const __amdgpu_buffer_rsrc_t rs = rows_rsrc(base);
         float bd[2] = {INFINITY, INFINITY};
         int bi[2] = {0, 0};
         for (int p = 0; p < npass; ++p) {
@@ -795,17 +815,23 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
                 const __bf16* const cbase = reinterpret_cast<const __bf16*>(smem + cur * G::STAGE) + r16 * CSTR + 8 * h;
                 const int nks = min(NKS, (ld - f0 + 31) / 32);
                 for (int ks = 0; ks < nks; ++ks) {
-                    // rows 16g + l%16, features f0 + 32ks + 8h..: past the
-                    // row's end the next row's (finite) values meet zero
-                    // centre parts; past the last row the loads return 0
                     Parts8 xp[2];
 #pragma unroll
-                    for (int g = 0; g < 2; ++g) {
-                        const int o = ((16 * g + r16) * ld + f0 + 32 * ks + 8 * h) * 4;
-                        xp[g] = split8(load_quad(rs, o), load_quad(rs, o + 16));
+                    for (int g = 0; g < 2; ++g) xp[g] = split8(xr[g][0], xr[g][1]);
+                    // the next K step's rows: this stage's next, the next
+                    // segment's or pass's first (same rows), or the next row
+                    // block's first
+                    if (ks + 1 < nks) {
+                        xload(rs, f0 + 32 * (ks + 1));
+                    } else if (sg + 1 < nseg) {
+                        xload(rs, f0 + SEG);
+                    } else if (p + 1 < npass) {
+                        xload(rs, 0);
+                    } else if (base + (long)gridDim.x * 256 < n) {
+                        xload(rows_rsrc(base + (long)gridDim.x * 256), 0);
                     }
-                    // the next stage's copy goes out behind the stage's last
-                    // X loads (loads complete in order: X waits never wait on it)
+                    // the next stage's copy goes out behind the X loads that
+                    // this stage still waits on (loads complete in order)
                     if (ks == nks - 1 && nst > 1) copy_stage(stg + 1 < nst ? stg + 1 : 0, cur ^ 1);
                     // four centre blocks at a time, product-major over their
                     // eight accumulators: consecutive MFMAs write different
