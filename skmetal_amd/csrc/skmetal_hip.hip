@@ -428,7 +428,7 @@ struct Lloyd {
         ug = update_geometry(n, d, k, C->num_cu);
         fblocks = fused_blocks(n, ld, k, C->num_cu);
         f3cap = fused3_ready(k, ld);
-        a3cap = assign3_ready(d, k);
+        a3cap = assign3_ready(d, k) && assign3_image_bytes(k, ld) < (size_t(1) << 31);
         const int chunks = std::max(finalize_col_chunks(d, fblocks), (d + kRelocCW - 1) / kRelocCW);
         const size_t kl = size_t(k) * ld;
         X = const_cast<float*>(Xdev);
@@ -475,7 +475,8 @@ struct Lloyd {
         ug = update_geometry(n, d, k, C->num_cu);
         fblocks = lf > 0 ? fused_blocks(n, ld, k, C->num_cu) : 0;
         f3cap = fblocks > 0 ? fused3_ready(k, ld) : 0;
-        a3cap = assign3_ready(d, k);
+        // (k_assign3's centre image is addressed with 32-bit buffer offsets)
+        a3cap = assign3_ready(d, k) && assign3_image_bytes(k, ld) < (size_t(1) << 31);
         if (fblocks == 0) sg = sort_geometry(n, d, ld, k);
         const int Rmax = sg.on ? 1 : std::max(ug.R, fblocks);
         const int chunks = std::max({finalize_col_chunks(d, ug.R), fblocks > 0 ? finalize_col_chunks(d, fblocks) : 0,
@@ -618,8 +619,7 @@ struct Lloyd {
     int assign(const float* cents, LoopState* state, int* changed)
     {
         AssignArgs a{X, n, ld, cents, cnorm, k, labels, state, changed, nullptr};
-        // (the image is addressed with 32-bit buffer offsets)
-        if (split_on && a3cap && assign3_image_bytes(k, ld) < (size_t(1) << 31)) {
+        if (split_on && a3cap) {
             if (a3img == nullptr) TRY(grab((void**)&a3img, assign3_image_bytes(k, ld)));
             a.img = a3img;
             HIP_TRY(launch_assign3(a, C->num_cu, s), "assign launch");
