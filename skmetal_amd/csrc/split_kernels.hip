@@ -4,9 +4,10 @@
 // the sums and counts of :214-218.
 //
 //   k_fused3    E-step + per-cluster sums in one pass over X (k <= 64,
-//               17 <= d <= 100); 12 waves per block.
+//               17 <= d <= 100); 16 waves per block.
 //   k_assign3   E-step alone for any k (the generic path, the final E-step
-//               and the assign entry point).
+//               and the assign entry point), its centres staged from the
+//               per-step image that k_centre_image writes.
 //
 // Built without -amdgpu-mfma-vgpr-form (the register allocator places the
 // MFMA accumulators).
