@@ -240,24 +240,40 @@ def main():
     kname = "k_fused3" if split else "k_fused" if fused else "k_assign3" if asplit else "k_assign"
     traffic = _traffic_from_profile(f"{kname}_{args.workload}_pmc.txt")
     if split:
-        # HBM roofline with the assign bytes per step: X once, the labels
-        # written, the centres read (4nd + 4n + 4kd).  The kernel's MFMA
-        # instructions are reported beside it (fused3_mfma_per_tile).
+        # The binding roof of the assign work: its arithmetic intensity
+        # 2nkd / (4nd + 4n + 4kd) -- X read once, the labels written, the
+        # centres read -- against the fp32 ridge 157.3 TFLOP/s / 8 TB/s
+        # = 19.7 flop/B.  At or above the ridge the fp32 MFMA roof binds
+        # (2nkd / 157.3 TFLOP/s), below it HBM.  The other roof and the
+        # kernel's bf16 MFMA instructions (fused3_mfma_per_tile) against the
+        # bf16 peak are reported beside it.
         nbytes = 4.0 * n * d + 4.0 * n + 4.0 * k * d
+        ai = flops / nbytes
+        ridge = PEAK_FP32_MFMA_TFLOPS * 1e12 / (PEAK_HBM_GBPS * 1e9)
         e16, s32 = fused3_mfma_per_tile(k, d)
         bf16_flops = -(-n // 32) * (2 * e16 + s32) * MFMA_16x16x32_FLOP
+        hbm_gbps = nbytes / assign_s / 1e9
+        fp32_tflops = flops / assign_s / 1e12
+        on_mfma = ai >= ridge
         roofline = {
             "kernel": ("k_fused3: E-step (||c||^2 - 2 x.c) + argmin + per-cluster sums, bf16 MFMAs over the exact "
                        "three-part split, fp32 accumulation"),
-            "bound": "hbm",
-            "achieved": round(nbytes / assign_s / 1e9, 1),
-            "peak": PEAK_HBM_GBPS,
-            "unit": "GB/s",
-            "frac": round(nbytes / assign_s / 1e9 / PEAK_HBM_GBPS, 4),
+            "bound": "mfma" if on_mfma else "hbm",
+            "achieved": round(fp32_tflops, 2) if on_mfma else round(hbm_gbps, 1),
+            "peak": PEAK_FP32_MFMA_TFLOPS if on_mfma else PEAK_HBM_GBPS,
+            "unit": "TFLOP/s" if on_mfma else "GB/s",
+            "frac": round(fp32_tflops / PEAK_FP32_MFMA_TFLOPS if on_mfma else hbm_gbps / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
+            "roof": ("fp32 MFMA: 2nkd fp32-equivalent distance flops per launch" if on_mfma
+                     else "HBM: 4nd + 4n + 4kd bytes per launch"),
+            "arithmetic_intensity": round(ai, 2),
+            "ridge": round(ridge, 2),
+            "kernel_us": round(assign_s * 1e6, 2),
             "algorithmic_bytes": nbytes,
-            "fp32_equiv_tflops": round(flops / assign_s / 1e12, 2),
-            "fp32_mfma_frac": round(flops / assign_s / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
+            "hbm_gbps": round(hbm_gbps, 1),
+            "hbm_frac": round(hbm_gbps / PEAK_HBM_GBPS, 4),
+            "fp32_equiv_tflops": round(fp32_tflops, 2),
+            "fp32_mfma_frac": round(fp32_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
             "bf16_mfma_tflops": round(bf16_flops / assign_s / 1e12, 1),
             "bf16_mfma_frac": round(bf16_flops / assign_s / 1e12 / PEAK_BF16_MFMA_TFLOPS, 4),
             "mfma_per_32_rows": {"e_step": 2 * e16, "sums": s32},

@@ -156,9 +156,13 @@ SKMETAL_API int skmetal_gemm_f16(const void* A, const void* B, void* C, size_t M
 /* ---- additions without a counterpart in the reference ---- */
 
 /* No counterpart in the reference.  For callers that cannot allocate device
- * memory (code under HIP graph capture around it, tight serving loops,
- * harnesses that forbid hipMalloc): skmetal_kmeans_batch_fused's loop
- * contract on caller-owned DEVICE memory, allocating nothing.  X is [n x d]
+ * memory (tight serving loops, harnesses that forbid hipMalloc) and already
+ * hold X, the centres and the labels in device memory:
+ * skmetal_kmeans_batch_fused's loop contract on those caller-owned DEVICE
+ * buffers, with no hipMalloc, hipFree or allocating library call.  It is not
+ * for use under HIP graph capture: it runs on the library's own stream,
+ * clears its loop state and labels with hipMemsetAsync and waits for the
+ * device before it returns.  X is [n x d]
  * fp32 in device memory, used as given (not centred); centroids is [k x d] in
  * device memory, in/out; assignments is [n] int32 in device memory, out;
  * *n_iter_out (host) = steps run.  Every other buffer comes from a static

@@ -7,10 +7,11 @@ Functions kept by name, signature and meaning (skmetal/_config.py:119-199):
 (skmetal/_config.py:6-32).
 
 State is one process-wide ``Config`` plus, per thread, an optional device
-override.  ``accelerate_context`` keeps a stack of those overrides per
-thread; ``set_device`` sets the process-wide value and the calling thread's
-override together, so the caller reads back what it set even inside a
-context.  Writers hold one lock; readers do not need it (every field is a
+override.  ``accelerate_context`` keeps a stack per thread of the devices
+the thread routed to when each block began, and re-pins the thread to that
+device when the block ends (skmetal's semantics); ``set_device`` sets the
+process-wide value and the calling thread's override together, so the
+caller reads back what it set even inside a context.  Writers hold one lock; readers do not need it (every field is a
 single reference replaced atomically).
 """
 
@@ -114,13 +115,17 @@ def _set_thread_device(device: str | None) -> None:
 
 
 def _push_thread_device(device: str) -> None:
-    """accelerate_context's entry: save the thread's device, then override it."""
-    _thread.saved.append(_thread.device)
+    """accelerate_context's entry: save the device the thread routes to now
+    (its override, or the process-wide value), then override it."""
+    _thread.saved.append(_get_device())
     _thread.device = device
 
 
 def _pop_thread_device() -> None:
-    """accelerate_context's exit: restore the device saved by the matching push."""
+    """accelerate_context's exit: pin the thread to the device saved by the
+    matching push, as skmetal does (skmetal/accelerate.py:104-113): after
+    the block the thread keeps that device even if ``set_device`` later
+    changes the process-wide value from another thread."""
     if _thread.saved:
         _thread.device = _thread.saved.pop()
 

@@ -1423,12 +1423,13 @@ __device__ __forceinline__ void reloc_body(const InRelocArgs& a, int E)
             il = bi;
         }
     }
-    // the last block to get here takes (B) and (C)
+    // the last block to get here takes (B) and (C).  Every thread's stores
+    // (the candidates, and in k_finalize_reloc the finalize chunk's sums,
+    // counts, centres and partials, written by several waves) are made
+    // visible to the device before the block takes its ticket.
+    __threadfence();
     __syncthreads();
-    if (tid == 0) {
-        __threadfence();  // the candidates, to the device
-        last_s = atomicAdd(&st->reloc_ctr, 1u) == gridDim.x - 1;
-    }
+    if (tid == 0) last_s = atomicAdd(&st->reloc_ctr, 1u) == gridDim.x - 1;
     __syncthreads();
     if (!last_s) return;
     if (tid == 0) st->reloc_ctr = 0u;

@@ -1340,8 +1340,15 @@ int skmetal_hip_kmeans_batch_fused_noalloc(const float* X, float* centroids, int
     if (!c.ready || c.scratch == nullptr)
         return fail(SKMETAL_EINVAL, "skmetal_init must run first: this entry point does not set the library up");
     if (k > 64) return fail(SKMETAL_ERANGE, "k=%zu: this entry point takes at most 64 clusters", k);
-    if (fused_ld((int)d, (int)k) != (int)d)
+    bool row_ok = false;
+    for (const size_t ld : {4, 8, 16, 32, 48, 64, 80, 100}) row_ok = row_ok || d == ld;
+    if (!row_ok)
         return fail(SKMETAL_ERANGE, "d=%zu: this entry point takes rows of 4, 8, 16, 32, 48, 64, 80 or 100 floats", d);
+    if (fused_ld((int)d, (int)k) != (int)d)
+        return fail(SKMETAL_EINVAL,
+                    "d=%zu, k=%zu: the fused step kernels are switched off (SKMETAL_HIP_FUSED=0) or could not be "
+                    "configured, and this entry point runs only them",
+                    d, k);
     if (n > size_t(kNoAllocMaxRows))
         return fail(SKMETAL_ERANGE, "n=%zu: this entry point takes at most %ld rows", n, kNoAllocMaxRows);
     int it = 0;

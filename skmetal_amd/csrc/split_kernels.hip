@@ -867,33 +867,36 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
                         }
                     }
                 }
+                if (sg == nseg - 1) {
+                    // ||c||^2 - 2 x.c, first minimum wins
+                    // (_k_means_lloyd.pyx:196-212); the lane's centres come in
+                    // ascending order, passes too.  ||c||^2 rides in every
+                    // stage of the pass and is read here, from the stage in
+                    // use, before the barrier below: after it another wave may
+                    // already be copying the stage after next into this one.
+                    const float* sN = reinterpret_cast<const float*>(smem + cur * G::STAGE + G::PBYTES);
+#pragma unroll
+                    for (int g = 0; g < 2; ++g) {
+#pragma unroll
+                        for (int cb = 0; cb < CB; ++cb) {
+                            const float4 c4 = *reinterpret_cast<const float4*>(&sN[16 * cb + 4 * h]);
+                            const float cn[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const float dd = fmaf(-2.0f, acc[g][cb][i], cn[i]);  // NaN compares false
+                                const bool take = dd < bd[g];
+                                bd[g] = take ? dd : bd[g];
+                                bi[g] = take ? p * CPC + 16 * cb + 4 * h + i : bi[g];
+                            }
+                        }
+                    }
+                }
                 if (nst > 1) {
                     // the next stage is in (every wave's copies) and this one
                     // is read: swap
                     __builtin_amdgcn_s_waitcnt(0);
                     __syncthreads();
                     cur ^= 1;
-                }
-            }
-            // ||c||^2 - 2 x.c, first minimum wins (_k_means_lloyd.pyx:196-212);
-            // the lane's centres come in ascending order, passes too.
-            // ||c||^2 rides in every stage of the pass: the one just read
-            // (the other LDS stage after a swap) is rewritten only by the
-            // next stage's copy, issued after this.
-            const float* sN = reinterpret_cast<const float*>(smem + (nst > 1 ? cur ^ 1 : cur) * G::STAGE + G::PBYTES);
-#pragma unroll
-            for (int g = 0; g < 2; ++g) {
-#pragma unroll
-                for (int cb = 0; cb < CB; ++cb) {
-                    const float4 c4 = *reinterpret_cast<const float4*>(&sN[16 * cb + 4 * h]);
-                    const float cn[4] = {c4.x, c4.y, c4.z, c4.w};
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float dd = fmaf(-2.0f, acc[g][cb][i], cn[i]);  // NaN compares false
-                        const bool take = dd < bd[g];
-                        bd[g] = take ? dd : bd[g];
-                        bi[g] = take ? p * CPC + 16 * cb + 4 * h + i : bi[g];
-                    }
                 }
             }
         }

@@ -147,6 +147,42 @@ def test_context_nests_and_stays_on_its_thread():
     assert cfg.device == "gpu"
 
 
+def test_context_exit_pins_the_thread_to_its_entry_device():
+    """skmetal/accelerate.py:95-113: the block saves the device the thread
+    routed to at entry and sets it as the thread's own on exit, so a later
+    set_device from another thread no longer reaches that thread."""
+    cfg = skmetal_amd.get_config()
+    skmetal_amd.set_device("gpu")
+    seen = {}
+    exited = threading.Event()
+    changed = threading.Event()
+
+    def worker():
+        with skmetal_amd.accelerate_context(enabled=False):
+            seen["inside"] = cfg.device
+        seen["after_exit"] = cfg.device
+        exited.set()
+        changed.wait(5)
+        seen["after_set_device"] = cfg.device
+
+    th = threading.Thread(target=worker)
+    th.start()
+    exited.wait(5)
+    skmetal_amd.set_device("cpu")  # process-wide value and this thread's own
+    changed.set()
+    th.join()
+    try:
+        assert seen == {"inside": "cpu", "after_exit": "gpu", "after_set_device": "gpu"}
+        # a thread that never entered a block follows the process-wide value
+        fresh = {}
+        t2 = threading.Thread(target=lambda: fresh.setdefault("d", cfg.device))
+        t2.start()
+        t2.join()
+        assert fresh["d"] == "cpu"
+    finally:
+        skmetal_amd.set_device("gpu")
+
+
 def test_set_device_is_seen_by_its_caller_inside_a_context():
     with skmetal_amd.accelerate_context(enabled=True):
         skmetal_amd.set_device("cpu")
