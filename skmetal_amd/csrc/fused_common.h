@@ -38,51 +38,82 @@ __device__ __forceinline__ void set_flag(int* flag, int v)
     __hip_atomic_store(flag, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+// The loads of step_norms, issued together (one memory round trip) so that a
+// kernel can put them in flight beside its other set-up loads: the first
+// kNormChunks chunk partials of the lane's cluster (further chunks, if any,
+// are read by step_norms_apply).
+constexpr int kNormChunks = 4;
+struct StepNormsIn {
+    double v[2 * kNormChunks];  // lane j < k: chunk c's shift^2 and ||c||^2 in v[2c], v[2c + 1]
+    int count;                  // lane j < k: cluster j's count
+    int chg;                    // rows the previous step's E-step relabelled
+    int reloc_iter;             // the last step k_reloc relocated in
+    float cnorm;                // lane j < k: ||c||^2 from a.cnorm (no decision to take)
+};
+
+__device__ __forceinline__ StepNormsIn step_norms_load(const FusedArgs& a, int lane)
+{
+    StepNormsIn in;
+    in.count = 1;
+    in.chg = 0;
+    in.reloc_iter = 0;
+    in.cnorm = INFINITY;
+    const int j = lane;
+    if (a.decide) {
+        in.chg = *a.prev_changed;
+        in.reloc_iter = a.state->reloc_iter;
+        const double* pj = a.part + (long)(j < a.k ? j : 0) * a.nch * 2;
+#pragma unroll
+        for (int u = 0; u < kNormChunks; ++u) {
+            const int c = min(u, a.nch - 1);
+            in.v[2 * u] = pj[2 * c];
+            in.v[2 * u + 1] = pj[2 * c + 1];
+        }
+        if (j < a.k) in.count = a.counts[j];
+    } else if (j < a.k) {
+        in.cnorm = a.cnorm[j];
+    }
+    return in;
+}
+
 // Wave 4 of every block: the previous step's stopping rules when a.decide
 // (evaluated identically by every block: same loads, same order as
 // k_finalize_loop for k <= 64; block 0 records the decision), else nothing
 // to decide.  Writes ||c||^2 of this step's centres to sN (padding clusters
 // j >= k get +inf: their distance never wins) and the decision to *sDone.
 template <int CPC>
-__device__ __forceinline__ void step_norms(const FusedArgs& a, int lane, float* sN, int* sDone)
+__device__ __forceinline__ void step_norms_apply(const FusedArgs& a, int lane, const StepNormsIn& in, float* sN,
+                                                 int* sDone)
 {
     const int k = a.k;
     const int j = lane;
     if (a.decide) {
+        // the chunk partials in chunk order (the finalize's order)
         double tsq = 0.0, tnr = 0.0;
-        int count = 1;
         if (j < k) {
-            // all chunk partials in flight at once (the sum order is the
-            // finalize's: chunk 0, 1, ...)
-            const double* pj = a.part + (long)j * a.nch * 2;
-            constexpr int NB = 16;
-            for (int c0 = 0; c0 < a.nch; c0 += NB) {
-                double v[2 * NB];
 #pragma unroll
-                for (int u = 0; u < NB; ++u) {
-                    const int c = min(c0 + u, a.nch - 1);
-                    v[2 * u] = pj[2 * c];
-                    v[2 * u + 1] = pj[2 * c + 1];
-                }
-#pragma unroll
-                for (int u = 0; u < NB; ++u) {
-                    if (c0 + u < a.nch) {
-                        tsq += v[2 * u];
-                        tnr += v[2 * u + 1];
-                    }
+            for (int u = 0; u < kNormChunks; ++u) {
+                if (u < a.nch) {
+                    tsq += in.v[2 * u];
+                    tnr += in.v[2 * u + 1];
                 }
             }
-            count = a.counts[j];
+            const double* pj = a.part + (long)j * a.nch * 2;
+            for (int c = kNormChunks; c < a.nch; ++c) {
+                tsq += pj[2 * c];
+                tnr += pj[2 * c + 1];
+            }
         }
+        const int count = in.count;
         const int n_empty = wave_sum(j < k && count == 0 ? 1 : 0);
         const double tot = wave_sum(j < k ? (double)(float)tsq : 0.0);
         float mx = j < k ? (float)tsq : 0.f;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-        const int chg = *a.prev_changed;
+        const int chg = in.chg;
         int done = 0;
         // (empty clusters k_reloc has already relocated do not stop the loop)
-        if (n_empty > 0 && a.state->reloc_iter != a.iter - 1)
+        if (n_empty > 0 && in.reloc_iter != a.iter - 1)
             done = 3;
         else if ((a.flags & kStopStrict) && chg == 0)
             done = 1;
@@ -106,9 +137,15 @@ __device__ __forceinline__ void step_norms(const FusedArgs& a, int lane, float* 
         if (j < CPC) sN[j] = j < k ? (float)tnr : INFINITY;
         if (lane == 0) *sDone = done;
     } else {
-        if (j < CPC) sN[j] = j < k ? a.cnorm[j] : INFINITY;
+        if (j < CPC) sN[j] = j < k ? in.cnorm : INFINITY;
         if (lane == 0) *sDone = 0;
     }
+}
+
+template <int CPC>
+__device__ __forceinline__ void step_norms(const FusedArgs& a, int lane, float* sN, int* sDone)
+{
+    step_norms_apply<CPC>(a, lane, step_norms_load(a, lane), sN, sDone);
 }
 
 // The block's partial sums and counts; its clusters with a row go into the

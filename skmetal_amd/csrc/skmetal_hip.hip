@@ -1478,14 +1478,17 @@ int skmetal_hip_lloyd_iterate(skmetal_hip_lloyd* h, size_t iters, float* ms_out,
     Lloyd& L = h->L;
     if (kernel_ms) {
         if (iters > kMaxTimedSteps) return fail(SKMETAL_ERANGE, "iterate: kernel timing covers at most 4096 steps");
+        // timing-only markers: no system-scope fence (its L2 writeback and
+        // invalidation would sit inside the brackets and slow the next kernel);
+        // e1, recorded after them and synchronised on, orders them for the host
         while (L.kev.size() < 4 * iters) {
             hipEvent_t e;
-            HIP_TRY(hipEventCreate(&e), "hipEventCreate");
+            HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableSystemFence), "hipEventCreate");
             L.kev.push_back(e);
         }
     }
     hipEvent_t e0, e1;
-    HIP_TRY(hipEventCreate(&e0), "hipEventCreate");
+    HIP_TRY(hipEventCreateWithFlags(&e0, hipEventDisableSystemFence), "hipEventCreate");
     HIP_TRY(hipEventCreate(&e1), "hipEventCreate");
     int rc = 0;
     // the loop resets the device state and labels before the timed region

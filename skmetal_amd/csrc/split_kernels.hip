@@ -163,9 +163,12 @@ struct Fused3Geom {
     static constexpr int QG = 2 * NK + TAIL / 8 + (TAIL == 4 ? 1 : 0);  // float4s per lane
     static constexpr int NT = TAIL == 4 ? 1 : TAIL == 16 ? 3 : 0;      // tail MFMAs per block
     static constexpr int NTS = TAIL == 4 ? 1 : TAIL == 16 ? 2 : 0;     // tail MFMAs of a stacked block
-    // a tile row is hi | mid | lo, KP bf16 each: 6 KP bytes, padded so that
-    // the row stride is 32 or 96 mod 128 bytes
-    static constexpr int RSB = (6 * KP) % 128 == 0 || (6 * KP) % 128 == 64 ? 6 * KP + 32 : 6 * KP;
+    // a tile row is hi | mid | lo, KP bf16 each: 6 KP bytes (a multiple of 32),
+    // padded to an odd number of 16-byte units: the E-step waves' 16-byte
+    // stores of 16 rows at one column then fall in distinct banks (a stride of
+    // 32 mod 128 bytes costs 8 conflict cycles per store), and the transposed
+    // reads cost the same as at any other stride
+    static constexpr int RSB = 6 * KP + 16;
     static constexpr int TILEB = 32 * RSB;
     // centre fragments (1 KB each): [cb][s][part], then [cb][tail MFMA], then
     // the stacked block's [s] and [tail MFMA]
@@ -177,7 +180,7 @@ struct Fused3Geom {
         return work > red ? work : red;
     }
     static_assert(TAIL == 0 || TAIL == 4 || TAIL == 16, "tails of 4 or 16 features");
-    static_assert(RSB % 16 == 0 && (2 * KP) % 16 == 0, "16-byte aligned rows and parts");
+    static_assert(RSB % 32 == 16 && (2 * KP) % 16 == 0, "rows of an odd number of 16-byte units, aligned parts");
 };
 
 __device__ __forceinline__ v4s lds_tr16(const char* p)
@@ -196,6 +199,44 @@ __device__ __forceinline__ v4s part_of(const Parts4& x, int p) { return p == 0 ?
 
 // centre part (0 hi, 1 mid, 2 lo) of tail block b: (h, m, l, h, m, h)
 __device__ __forceinline__ int tail_cpart(int b) { return b == 1 || b == 4 ? 1 : b == 2 ? 2 : 0; }
+
+// (a & ma) | (b & mb) per 32-bit word: a lane-dependent choice between
+// operands, or zero, without a branch (ma, mb are all-ones or zero).
+__device__ __forceinline__ v4s pick2(v4s a, unsigned ma, v4s b, unsigned mb)
+{
+    const v2u ua = __builtin_bit_cast(v2u, a), ub = __builtin_bit_cast(v2u, b);
+    return __builtin_bit_cast(v4s, (ua & ma) | (ub & mb));
+}
+__device__ __forceinline__ v8bf pick2(v8bf a, unsigned ma, v8bf b, unsigned mb)
+{
+    const v4u ua = __builtin_bit_cast(v4u, a), ub = __builtin_bit_cast(v4u, b);
+    return __builtin_bit_cast(v8bf, (ua & ma) | (ub & mb));
+}
+
+// The first minimum of (d, i) over lanes l and l ^ 16 (X = 16) or l ^ 32 (X =
+// 32), lower index first on ties, in both lanes.  v_permlane16_swap_b32 /
+// v_permlane32_swap_b32 of a register with itself leave lane l's value in one
+// result and lane l ^ X's in the other (which is which depends on the lane);
+// the lexicographic minimum of the two pairs is the same either way.  Plain
+// VALU: no LDS round trip.
+template <int X>
+__device__ __forceinline__ void argmin_swap(float& d, int& i)
+{
+    const unsigned du = __float_as_uint(d), iu = (unsigned)i;
+    v2u pd, pi;
+    if constexpr (X == 16) {
+        pd = __builtin_amdgcn_permlane16_swap(du, du, false, false);
+        pi = __builtin_amdgcn_permlane16_swap(iu, iu, false, false);
+    } else {
+        pd = __builtin_amdgcn_permlane32_swap(du, du, false, false);
+        pi = __builtin_amdgcn_permlane32_swap(iu, iu, false, false);
+    }
+    const float d0 = __uint_as_float(pd[0]), d1 = __uint_as_float(pd[1]);
+    const int i0 = (int)pi[0], i1 = (int)pi[1];
+    const bool take1 = (d1 < d0) | ((d1 == d0) & (i1 < i0));  // no branch
+    d = take1 ? d1 : d0;
+    i = take1 ? i1 : i0;
+}
 
 template <int CB, int NQ, bool STK>
 __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
@@ -298,6 +339,9 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
             if (f0 < NFA) wait_flag(&sProg[m], (r - 1) * NFA + (f1 + 1 < NFA ? f1 + 1 : NFA));
             if (f1 >= NFA) wait_flag(&sProg[4 + m], (r - 1) * NFZ + (f1 + 1 - NFA));
         };
+        // lane masks of the tail's operands (all ones when the lane's h matches)
+        const unsigned mh0 = h == 0 ? ~0u : 0u, mh1 = h == 1 ? ~0u : 0u, mh2 = h == 2 ? ~0u : 0u;
+        const unsigned mlt2 = h < 2 ? ~0u : 0u, mge2 = ~mlt2;
         int changed = 0;
         for (int r = 0; r < rounds; ++r) {
             const long t = t0 + (long)r * P;
@@ -352,35 +396,41 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
                 if constexpr (TAIL == 4) {
                     const Parts4 xt = split4(xr[2 * NK]);
                     wait_blocks(r, NFB - 1, NFB - 1);
-                    if (h == 0) {
-                        char* dst = trow + 32 * NK * 2;
+                    {
+                        // every lane holds the same four features: lane h
+                        // writes them at features 32NK + 4h of the tail block,
+                        // whose features past 32NK + 3 are padding the sums
+                        // never read (no branch)
+                        char* dst = trow + (32 * NK + 4 * h) * 2;
                         *reinterpret_cast<v4s*>(dst) = xt.h;
                         *reinterpret_cast<v4s*>(dst + 2 * KP) = xt.m;
                         *reinterpret_cast<v4s*>(dst + 4 * KP) = xt.l;
                     }
                     load_step(rn, NK);
                     // blocks 2h, 2h + 1 of (x_h, x_h, x_h, x_m, x_m, x_l, 0, 0)
-                    const v8bf bt = cat8(h < 2 ? xt.h : h == 2 ? xt.m : z4,
-                                         h == 0 ? xt.h : h == 1 ? xt.m : h == 2 ? xt.l : z4);
+                    const v8bf bt = cat8(pick2(xt.h, mlt2, xt.m, mh2),
+                                         pick2(pick2(xt.h, mh0, xt.m, mh1), ~0u, xt.l, mh2));
 #pragma unroll
                     for (int cb = 0; cb < CBF; ++cb) acc[cb] = mfma_bf16(fr[64 * (FT + cb)], bt, acc[cb]);
                     if constexpr (STK) {
                         // blocks 2h, 2h + 1 of (x_h, x_m, x_l, 0, ...)
-                        const v8bf bs = cat8(h == 0 ? xt.h : h == 1 ? xt.l : z4, h == 0 ? xt.m : z4);
+                        const v8bf bs = cat8(pick2(xt.h, mh0, xt.l, mh1), pick2(xt.m, mh0, z4, 0u));
                         acc[CB - 1] = mfma_bf16(fr[64 * (FS + NK)], bs, acc[CB - 1]);
                     }
                 } else {
                     const Parts8 xt = split8(xr[2 * NK], xr[QG - 1]);
                     wait_blocks(r, NFB - 1, NFB - 1);
-                    if (h < 2) {
-                        char* dst = trow + (32 * NK + 8 * h) * 2;
+                    {
+                        // lanes h and h + 2 hold the same eight features
+                        // 32NK + 8(h&1): both write them (the same values)
+                        char* dst = trow + (32 * NK + 8 * (h & 1)) * 2;
                         *reinterpret_cast<v8bf*>(dst) = xt.h;
                         *reinterpret_cast<v8bf*>(dst + 2 * KP) = xt.m;
                         *reinterpret_cast<v8bf*>(dst + 4 * KP) = xt.l;
                     }
                     load_step(rn, NK);
                     // MFMA q, lane h: block 2q + h/2 of (x_h, x_h, x_h, x_m, x_m, x_l)
-                    const v8bf b1 = h < 2 ? xt.h : xt.m, b2 = h < 2 ? xt.m : xt.l;
+                    const v8bf b1 = pick2(xt.h, mlt2, xt.m, mge2), b2 = pick2(xt.m, mlt2, xt.l, mge2);
 #pragma unroll
                     for (int q = 0; q < 3; ++q) {
 #pragma unroll
@@ -391,7 +441,7 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
                         // blocks of (x_h, x_m, x_l, 0): lanes h < 2 take the
                         // first of each MFMA's two, h >= 2 the second
                         acc[CB - 1] = mfma_bf16(fr[64 * (FS + NK)], b1, acc[CB - 1]);
-                        acc[CB - 1] = mfma_bf16(fr[64 * (FS + NK + 1)], h < 2 ? xt.l : cat8(z4, z4), acc[CB - 1]);
+                        acc[CB - 1] = mfma_bf16(fr[64 * (FS + NK + 1)], pick2(xt.l, mlt2, xt.l, 0u), acc[CB - 1]);
                     }
                 }
             }
@@ -419,14 +469,8 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
                 bd = take ? dd : bd;
                 bi = take ? 16 * (CB - 1) + h : bi;
             }
-#pragma unroll
-            for (int sh = 16; sh <= 32; sh *= 2) {
-                const float od = __shfl_xor(bd, sh);
-                const int oi = __shfl_xor(bi, sh);
-                const bool take = (od < bd) | ((od == bd) & (oi < bi));  // no branch
-                bd = take ? od : bd;
-                bi = take ? oi : bi;
-            }
+            argmin_swap<16>(bd, bi);
+            argmin_swap<32>(bd, bi);
             // lanes 0..15: row = lane
             __builtin_amdgcn_raw_buffer_store_b32(bi, rl, lane * 4, 0, 0);
             changed += (int)__popcll(__ballot(valid && old != bi));
@@ -449,108 +493,121 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
         // the E-step waves wait on the sums waves' progress before rewriting
         // their tile: issue priority for the sums waves
         __builtin_amdgcn_s_setprio(2);
-        // sums waves 8..15: the halt test, then the centre fragments (centres
-        // >= k and features >= ld zero) and ||c||^2
+        // sums waves 8..15: the centre fragments (centres >= k and features
+        // >= ld zero), ||c||^2 and the halt test.  Every set-up load goes out
+        // at once, before any is used (one memory round trip): the halt flag,
+        // the centre values of every fragment (out-of-range items read centre
+        // 0 and are zeroed), and wave 8's loop state.
+        const int wt = tid - 512;  // 0 .. 511
         const int prev = st->done;
+        // full blocks: fragment (cb, s, part), item idx = 64 (cb NK + s) + lane
+        constexpr int NE = CB * NK * 64;
+        constexpr int NU = (NE + 511) / 512;
+        float4 cf[NU][2];
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+            const int idx = wt + 512 * u;
+            const int l = idx & 63, cs = idx >> 6;  // cs = cb * NK + s
+            const int cb = cs / NK, sk = cs - cb * NK;
+            const int cl = 16 * cb + (l & 15);
+            const bool ok = idx < NE && cl < k;
+            const float* p = C + (ok ? (long)cl * ld + 32 * sk + 8 * (l >> 4) : 0L);
+            cf[u][0] = *reinterpret_cast<const float4*>(p);
+            cf[u][1] = *reinterpret_cast<const float4*>(p + 4);
+        }
+        // full blocks' tail: fragment (cb, q), item wt = 64 cb + lane
+        float4 ct[2];
+        if constexpr (TAIL > 0) {
+            const int l = wt & 63, cb = wt >> 6, hh = l >> 4;
+            const int cl = 16 * cb + (l & 15);
+            const bool ok = wt < CB * 64 && cl < k;
+            const float* p = C + (ok ? (long)cl * ld + 32 * NK + (TAIL == 16 ? 8 * (hh & 1) : 0) : 0L);
+            ct[0] = *reinterpret_cast<const float4*>(p);
+            ct[1] = TAIL == 16 ? *reinterpret_cast<const float4*>(p + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        // stacked block: K-step fragment s, item wt = 64 s + lane (lane = 16h
+        // + 4 slot + p: part p of centre 16(CB-1) + slot, p = 3 zero); its
+        // tail fragments, item wt = 64 NK + lane
+        float4 cs4[2], cst[2];
+        if constexpr (STK) {
+            {
+                const int l = wt & 63, sk = wt >> 6;
+                const int pp = l & 3, cl = 16 * (CB - 1) + ((l & 15) >> 2);
+                const bool ok = wt < 64 * NK && pp < 3 && cl < k;
+                const float* q = C + (ok ? (long)cl * ld + 32 * sk + 8 * (l >> 4) : 0L);
+                cs4[0] = *reinterpret_cast<const float4*>(q);
+                cs4[1] = *reinterpret_cast<const float4*>(q + 4);
+            }
+            if constexpr (TAIL > 0) {
+                const int l = (wt - 64 * NK) & 63, hh = l >> 4;
+                const int pp = l & 3, cl = 16 * (CB - 1) + ((l & 15) >> 2);
+                const bool ok = wt >= 64 * NK && wt < 64 * NK + 64 && pp < 3 && cl < k;
+                const float* q = C + (ok ? (long)cl * ld + 32 * NK + (TAIL == 16 ? 8 * (hh & 1) : 0) : 0L);
+                cst[0] = *reinterpret_cast<const float4*>(q);
+                cst[1] = TAIL == 16 ? *reinterpret_cast<const float4*>(q + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+        StepNormsIn sni;
+        if (wave == 8) sni = step_norms_load(a, lane);
         if (prev != 0) {
             if (tid == 512) sDone = prev;
             __syncthreads();
             return;
         }
-        const int wt = tid - 512;  // 0 .. 511
-        {
-            // fragments (cb, s, 0..2): lane l = 16h + r of each holds the parts
-            // of centre 16cb + r, features 32s + 8h .. 32s + 8h + 7
-            constexpr int NE = CB * NK * 64;
-            constexpr int NU = (NE + 511) / 512;
-            float4 cf[NU][2];
+        const float4 z4f = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-            for (int u = 0; u < NU; ++u) {
-                const int idx = wt + 512 * u;
-                const int l = idx & 63, cs = idx >> 6;  // cs = cb * NK + s
-                const int cb = cs / NK, s = cs - cb * NK;
-                const int cl = 16 * cb + (l & 15);
-                cf[u][0] = cf[u][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (idx < NE && cl < k) {
-                    const float* p = C + (long)cl * ld + 32 * s + 8 * (l >> 4);
-                    cf[u][0] = *reinterpret_cast<const float4*>(p);
-                    cf[u][1] = *reinterpret_cast<const float4*>(p + 4);
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < NU; ++u) {
-                const int idx = wt + 512 * u;
-                if (idx < NE) {
-                    const int l = idx & 63, cs = idx >> 6;
-                    const Parts8 p = split8(cf[u][0], cf[u][1]);
-                    sFr[64 * (3 * cs) + l] = p.h;
-                    sFr[64 * (3 * cs + 1) + l] = p.m;
-                    sFr[64 * (3 * cs + 2) + l] = p.l;
-                }
+        for (int u = 0; u < NU; ++u) {
+            const int idx = wt + 512 * u;
+            const int l = idx & 63, cs = idx >> 6;
+            const int cl = 16 * (cs / NK) + (l & 15);
+            if (idx < NE) {
+                const bool ok = cl < k;
+                const Parts8 p = split8(ok ? cf[u][0] : z4f, ok ? cf[u][1] : z4f);
+                sFr[64 * (3 * cs) + l] = p.h;
+                sFr[64 * (3 * cs + 1) + l] = p.m;
+                sFr[64 * (3 * cs + 2) + l] = p.l;
             }
         }
         if constexpr (TAIL > 0) {
             // tail fragments (cb, q): lane l = 16h + r holds values 32q + 8h ..
-            // of centre 16cb + r's tail row (blocks of TAIL values: parts (h, m,
-            // l, h, m, h) of its features 32NK .., zeros after them)
+            // of centre 16cb + r's tail row (blocks of TAIL values: parts (h,
+            // m, l, h, m, h) of its features 32NK .., zeros after them)
             if (wt < CB * 64) {
                 const int l = wt & 63, cb = wt >> 6, hh = l >> 4;
-                const int cl = 16 * cb + (l & 15);
+                const bool ok = 16 * cb + (l & 15) < k;
                 if constexpr (TAIL == 4) {
-                    float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (cl < k) c = *reinterpret_cast<const float4*>(C + (long)cl * ld + 32 * NK);
-                    const Parts4 p = split4(c);
+                    const Parts4 p = split4(ok ? ct[0] : z4f);
                     const v4s z4 = v4s{0, 0, 0, 0};
                     // blocks 2hh, 2hh + 1
                     const v4s q0 = hh < 3 ? part_of(p, tail_cpart(2 * hh)) : z4;
                     const v4s q1 = hh < 3 ? part_of(p, tail_cpart(2 * hh + 1)) : z4;
                     sFr[64 * (FT + cb) + l] = cat8(q0, q1);
                 } else {
-                    float4 c0 = make_float4(0.f, 0.f, 0.f, 0.f), c1 = c0;
-                    if (cl < k) {
-                        const float* p = C + (long)cl * ld + 32 * NK + 8 * (hh & 1);
-                        c0 = *reinterpret_cast<const float4*>(p);
-                        c1 = *reinterpret_cast<const float4*>(p + 4);
-                    }
-                    const Parts8 p = split8(c0, c1);
+                    const Parts8 p = split8(ok ? ct[0] : z4f, ok ? ct[1] : z4f);
 #pragma unroll
                     for (int q = 0; q < 3; ++q) sFr[64 * (FT + cb * NT + q) + l] = part_of(p, tail_cpart(2 * q + (hh >> 1)));
                 }
             }
         }
         if constexpr (STK) {
-            // stacked fragments: lane l = 16h + 4 slot + p holds part p of centre
-            // 16(CB-1) + slot (p = 3: zero): K steps s, then the tail
             if (wt < 64 * NK) {
-                const int l = wt & 63, s = wt >> 6;
-                const int p = l & 3, cl = 16 * (CB - 1) + ((l & 15) >> 2);
-                float4 c0 = make_float4(0.f, 0.f, 0.f, 0.f), c1 = c0;
-                if (p < 3 && cl < k) {
-                    const float* q = C + (long)cl * ld + 32 * s + 8 * (l >> 4);
-                    c0 = *reinterpret_cast<const float4*>(q);
-                    c1 = *reinterpret_cast<const float4*>(q + 4);
-                }
-                sFr[64 * (FS + s) + l] = part_of(split8(c0, c1), p < 3 ? p : 0);
+                const int l = wt & 63, sk = wt >> 6;
+                const int pp = l & 3, cl = 16 * (CB - 1) + ((l & 15) >> 2);
+                const bool ok = pp < 3 && cl < k;
+                sFr[64 * (FS + sk) + l] = part_of(split8(ok ? cs4[0] : z4f, ok ? cs4[1] : z4f), pp < 3 ? pp : 0);
             }
             if constexpr (TAIL > 0) {
                 if (wt >= 64 * NK && wt < 64 * NK + 64) {
                     const int l = wt - 64 * NK, hh = l >> 4;
-                    const int p = l & 3, cl = 16 * (CB - 1) + ((l & 15) >> 2);
+                    const int pp = l & 3, cl = 16 * (CB - 1) + ((l & 15) >> 2);
+                    const bool ok = pp < 3 && cl < k;
                     const v4s z4 = v4s{0, 0, 0, 0};
                     if constexpr (TAIL == 4) {
-                        float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
-                        if (p < 3 && cl < k) c = *reinterpret_cast<const float4*>(C + (long)cl * ld + 32 * NK);
-                        const v4s cp = part_of(split4(c), p < 3 ? p : 0);
+                        const v4s cp = part_of(split4(ok ? cst[0] : z4f), pp < 3 ? pp : 0);
                         // blocks 2hh, 2hh + 1 of (c_p, c_p, c_p, 0, ...)
                         sFr[64 * (FS + NK) + l] = cat8(hh < 2 ? cp : z4, hh == 0 ? cp : z4);
                     } else {
-                        float4 c0 = make_float4(0.f, 0.f, 0.f, 0.f), c1 = c0;
-                        if (p < 3 && cl < k) {
-                            const float* q = C + (long)cl * ld + 32 * NK + 8 * (hh & 1);
-                            c0 = *reinterpret_cast<const float4*>(q);
-                            c1 = *reinterpret_cast<const float4*>(q + 4);
-                        }
-                        const v8bf cp = part_of(split8(c0, c1), p < 3 ? p : 0);
+                        const v8bf cp = part_of(split8(ok ? cst[0] : z4f, ok ? cst[1] : z4f), pp < 3 ? pp : 0);
                         sFr[64 * (FS + NK) + l] = cp;
                         sFr[64 * (FS + NK + 1) + l] = hh < 2 ? cp : cat8(z4, z4);
                     }
@@ -572,7 +629,7 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
         }
         (&sMask[0][0][0])[wt] = 0u;
         (&sMask[0][0][0])[512 + wt] = 0u;
-        if (wave == 8) step_norms<CPC>(a, lane, sN, &sDone);
+        if (wave == 8) step_norms_apply<CPC>(a, lane, sni, sN, &sDone);
         __syncthreads();
         if (sDone != 0) return;
         // sums wave 8 + w: SIMD m = w & 3, feature blocks [0, NFA) (w < 4) or
