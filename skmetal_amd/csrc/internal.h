@@ -28,7 +28,6 @@ struct LoopState {
     unsigned reloc_ctr;  // k_reloc: blocks done with their rows (the last resets it)
     int reloc_iter;      // iteration whose empty clusters k_reloc relocated (-1: none)
     int empty_cnt[2];    // clusters k_finalize_cols of iteration i found empty: empty_cnt[i & 1]
-    unsigned rowdist_ctr;  // k_rowdist: blocks done with their rows (the last resets it)
     double shift_tot;  // sum_j ||c_j_new - c_j_old||^2 of the last step
     double inertia;    // result of the last row-distance reduction
     // fused steps (k <= 64): bit j set when a block of iteration i's fused
@@ -190,13 +189,13 @@ struct RowDistArgs {
     const float* X; long n; int ld; int d;
     const float* C; int k; const int* labels;  // rows with a label outside [0, k) count 0
     float* out_rows;       // nullable: per-row squared distance
-    double* block_part;    // [grid]
+    double* block_part;    // [rowdist_grid(n)]: the blocks' totals
     LoopState* state;      // receives `inertia`
 };
-constexpr int kRowDistBlocks = 512;  // k_rowdist grid (two 256-thread blocks per CU)
-int rowdist_grid(long n);
-// Row distances and their fixed-order total (one launch: the last block to
-// finish adds the block totals in block order).
+constexpr int kRowDistBlocks = 512;  // largest row-distance grid
+int rowdist_grid(long n);            // block totals to allocate for n rows
+// Row distances and their fixed-order total (k_rowdist or k_rowdist_slab,
+// then k_rowdist_total adds the block totals in block order).
 hipError_t launch_rowdist(const RowDistArgs& a, hipStream_t s);
 
 // Device relocation of up to kMaxReloc empty clusters at once (see

@@ -855,12 +855,13 @@ hipError_t launch_finalize_loop(const FinalizeArgs& a, hipStream_t s, int nch)
 // Per row in fp32, in the association order of sklearn's
 // _euclidean_dense_dense (_k_means_common.pyx:16-43): groups of four squared
 // differences summed left to right, each group added to the running sum, the
-// remainder one by one.  A block takes a contiguous share of the rows (1024
-// blocks: four per CU), a wave 64 consecutive rows at a time; their features
-// come in slabs of 32 columns, loaded coalesced (8 lanes per 128-byte piece
-// of a row) into the wave's LDS tile, and lane l carries row l's running sum
-// from slab to slab.  The total is summed in fp64: each lane over its rows,
-// then the lanes and waves of a block, then the blocks in order.
+// remainder one by one.  Rows longer than 128 floats (rows_dist): a block
+// takes a contiguous share of the rows, a wave 64 consecutive rows at a time;
+// their features come in slabs of 32 columns, loaded coalesced (8 lanes per
+// 128-byte piece of a row) into the wave's LDS tile, and lane l carries row
+// l's running sum from slab to slab.  Shorter rows take the contiguous path
+// (rows_dist_ctg) below.  The total is summed in fp64: each lane over its
+// rows, then the lanes and waves of a block, then the blocks in order.
 
 constexpr int kRowSlab = 32;                  // columns per slab
 constexpr int kRowPiece = kRowSlab / 4;       // float4s per row of a slab = lanes per row in a load
@@ -974,102 +975,139 @@ __device__ __forceinline__ double rows_dist(const float* __restrict__ X, int ld,
     return total;
 }
 
-// Rows of at most LDM floats (ld <= LDM) take a contiguous path: a wave
-// takes the 32-row chunks r0 + 32 w + 128 t; a chunk's rows are one span of
-// 32 ld floats, loaded as lane-linear float4s (whole cache lines, NV per
-// lane) and scattered into the wave's LDS tile with row stride ld + 1, and
-// lanes 0..31 sum rows 0..31 of the chunk in the association order above.
-// The column slabs of rows_dist read 128-byte pieces of rows that need not
-// start on a cache line, and fetch such lines twice when their neighbours
-// have left the L2 in between.  Each chunk's centre loads are issued before
-// the next chunk's loads, and the sums wait for the centres alone.
-template <int LDM>
+// Rows of at most LDM floats (ld <= LDM, a multiple of 4) take a contiguous
+// path: a wave takes the ROWS-row chunks (ROWS = 32 or 64) r0 + ROWS w +
+// wstep t; a chunk's rows are one span of ROWS ld floats, loaded as
+// lane-linear float4s (whole cache lines) and stored as float4s into the
+// wave's LDS tile with row stride S = ctg_stride(ld), an odd number of
+// 16-byte units, so that the row-per-lane float4 reads of the sums fall in
+// distinct bank groups; lane l < ROWS sums row l of the chunk in the
+// association order above.  The column slabs of rows_dist read 128-byte
+// pieces of rows that need not start on a cache line, and fetch such lines
+// twice when their neighbours have left the L2 in between.
+// The centre rows come from Cs, row stride cs: with CL the block's LDS copy
+// of C, read group by group in a loop over the row's whole float4s; else C
+// itself, each chunk's centre float4s loaded into registers before the next
+// chunk's loads are issued, so the sums wait for the centres alone.
+template <int LDM, int ROWS>
 struct CtgGeom {
-    static constexpr int NV = (8 * LDM + 63) / 64;  // float4s per lane per chunk (32 LDM / 4 / 64)
-    static constexpr int NG = LDM / 4;              // float4 groups per row
-    static constexpr int TILE = 32 * (LDM + 1);     // floats per wave tile
+    static constexpr int NV = ROWS * LDM / 256;       // float4 loads per lane per chunk, at most
+    static constexpr int NG = LDM / 4;                // float4 groups per row, at most
+    static constexpr int SMAX = 4 * ((LDM / 4) | 1);  // largest tile row stride
+    static constexpr int TILE = ROWS * SMAX;          // floats per wave tile
+};
+
+// Tile row stride for rows of ld floats: an odd number of float4s.
+__host__ __device__ constexpr int ctg_stride(int ld) { return 4 * ((ld / 4) | 1); }
+
+// Native 4-float vector: arrays of it stay in registers (an array of the
+// float4 struct copied whole went to scratch memory).
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+struct NoPrologue {
+    __device__ void operator()() const {}
 };
 
 // ld: the row stride, a multiple of 4 (<= LDM); tile: the wave's
-// CtgGeom<LDM>::TILE floats.  As rows_dist otherwise.
-template <int LDM>
+// ROWS ctg_stride(ld) floats; pro: block-wide set-up run by every wave
+// once its first chunk's loads are in flight.  As rows_dist otherwise.
+template <int LDM, int ROWS, bool CL, typename Pro = NoPrologue>
 __device__ __forceinline__ double rows_dist_ctg(const float* __restrict__ X, int ld, int d,
-                                                const float* __restrict__ C, const int* __restrict__ labels, int k,
-                                                long r0, long r1, float* __restrict__ dist, float* tile)
+                                                const float* __restrict__ Cs, int cs,
+                                                const int* __restrict__ labels, int k, long r0, long r1,
+                                                long wstep, float* __restrict__ dist, float* tile, Pro pro = Pro())
 {
 #pragma clang fp contract(off)
-    using G = CtgGeom<LDM>;
+    using G = CtgGeom<LDM, ROWS>;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int S = ld + 1;
+    const int S = ctg_stride(ld);
     const float inv_ld = 1.0f / (float)ld;
-    long c0 = r0 + 32L * w;
+    long c0 = r0 + (long)ROWS * w;
     double total = 0.0;
-    if (c0 >= r1) return total;
-    float4 P[G::NV];
+    f4v P[G::NV];
     int plab = -1;
+    // loads past a chunk's span repeat its last float4 (NV covers LDM)
     auto load = [&](long cc) {
-        const int nrows = (int)min(32L, r1 - cc);
+        const int nrows = (int)min((long)ROWS, r1 - cc);
         const int e4 = nrows * ld / 4;  // float4s of the chunk's rows
-        const float4* base = reinterpret_cast<const float4*>(X + cc * ld);
+        const f4v* base = reinterpret_cast<const f4v*>(X + cc * ld);
 #pragma unroll
         for (int i = 0; i < G::NV; ++i) P[i] = base[min(64 * i + lane, e4 - 1)];
         plab = labels[cc + min(lane, nrows - 1)];
     };
-    load(c0);
-    while (c0 < r1) {
-        const int nrows = (int)min(32L, r1 - c0);
-        const int e4 = nrows * ld / 4;
-        // float p = 4 q of the span: row p / ld (p + 1/2 keeps the float
-        // quotient clear of integers), column p % ld
+    // float p = 4 q of a span: row p / ld (p + 1/2 keeps the float quotient
+    // clear of integers), column p % ld; a repeated float4 goes where the
+    // span's last one goes (same value)
+    auto tile_off = [&](int i, int e4) {
+        const int p = 4 * min(64 * i + lane, e4 - 1);
+        const int r = (int)(((float)p + 0.5f) * inv_ld);
+        return r * S + (p - r * ld);
+    };
+    int off[G::NV];  // a whole chunk's tile offsets
 #pragma unroll
-        for (int i = 0; i < G::NV; ++i) {
-            const int q = 64 * i + lane;
-            if (q < e4) {
-                const int p = 4 * q;
-                const int r = (int)(((float)p + 0.5f) * inv_ld);
-                float* t = tile + r * S + (p - r * ld);
-                t[0] = P[i].x;
-                t[1] = P[i].y;
-                t[2] = P[i].z;
-                t[3] = P[i].w;
-            }
+    for (int i = 0; i < G::NV; ++i) off[i] = tile_off(i, ROWS * ld / 4);
+    if (c0 < r1) load(c0);
+    pro();
+    while (c0 < r1) {
+        const int nrows = (int)min((long)ROWS, r1 - c0);
+        if (nrows == ROWS) {
+#pragma unroll
+            for (int i = 0; i < G::NV; ++i) *reinterpret_cast<f4v*>(tile + off[i]) = P[i];
+        } else {
+            const int e4 = nrows * ld / 4;
+#pragma unroll
+            for (int i = 0; i < G::NV; ++i) *reinterpret_cast<f4v*>(tile + tile_off(i, e4)) = P[i];
         }
         const int lab = plab;
         const bool ok = lane < nrows && lab >= 0 && lab < k;
-        const float* crow = C + (long)(ok ? lab : 0) * ld;
-        float4 cv[G::NG];
+        const float* crow = Cs + (long)(ok ? lab : 0) * cs;
+        f4v cv[CL ? 1 : G::NG];
+        if constexpr (!CL) {
 #pragma unroll
-        for (int g = 0; g < G::NG; ++g) cv[g] = *reinterpret_cast<const float4*>(crow + min(4 * g, ld - 4));
-        // the centre loads go out before the next chunk's (the sums then
-        // wait for them alone); past the last chunk the current one loads
-        // again, so every pass issues the same loads
+            for (int g = 0; g < G::NG; ++g)
+                if (4 * g < d) cv[g] = *reinterpret_cast<const f4v*>(crow + 4 * g);
+        }
         __builtin_amdgcn_sched_barrier(0);
-        const long nc0 = c0 + 128;
+        const long nc0 = c0 + wstep;
+        // in flight while this chunk is summed; past the last chunk the
+        // current one loads again, so every pass issues the same loads
         load(nc0 < r1 ? nc0 : c0);
         // (a wave's LDS accesses complete in order: the tile is written
         // before any lane reads it)
         __builtin_amdgcn_wave_barrier();
         float res = 0.f;
-        {
-            const float* t = tile + min(lane, 31) * S;
+        const float* t = tile + min(lane, ROWS - 1) * S;
+        auto group = [&](const f4v& x4, const f4v& c4) {
+            const float t0 = x4.x - c4.x, t1 = x4.y - c4.y;
+            const float t2 = x4.z - c4.z, t3 = x4.w - c4.w;
+            res += ((t0 * t0 + t1 * t1) + t2 * t2) + t3 * t3;
+        };
+        auto last = [&](const f4v& x4, const f4v& c4, int m) {  // the row's last m < 4 features, one by one
+            float tt = x4.x - c4.x;
+            res += tt * tt;
+            if (m > 1) {
+                tt = x4.y - c4.y;
+                res += tt * tt;
+            }
+            if (m > 2) {
+                tt = x4.z - c4.z;
+                res += tt * tt;
+            }
+        };
+        if constexpr (CL) {
+            const f4v* t4 = reinterpret_cast<const f4v*>(t);
+            const f4v* c4 = reinterpret_cast<const f4v*>(crow);
+            const int nfull = d >> 2;
+#pragma unroll 5
+            for (int g = 0; g < nfull; ++g) group(t4[g], c4[g]);
+            if (d & 3) last(t4[nfull], c4[nfull], d & 3);
+        } else {
 #pragma unroll
             for (int g = 0; g < G::NG; ++g) {
-                if (4 * g + 4 <= d) {
-                    const float t0 = t[4 * g] - cv[g].x, t1 = t[4 * g + 1] - cv[g].y;
-                    const float t2 = t[4 * g + 2] - cv[g].z, t3 = t[4 * g + 3] - cv[g].w;
-                    res += ((t0 * t0 + t1 * t1) + t2 * t2) + t3 * t3;
-                } else if (4 * g < d) {  // the row's last features, one by one
-                    float tt = t[4 * g] - cv[g].x;
-                    res += tt * tt;
-                    if (4 * g + 1 < d) {
-                        tt = t[4 * g + 1] - cv[g].y;
-                        res += tt * tt;
-                    }
-                    if (4 * g + 2 < d) {
-                        tt = t[4 * g + 2] - cv[g].z;
-                        res += tt * tt;
-                    }
-                }
+                if (4 * g + 4 <= d)
+                    group(*reinterpret_cast<const f4v*>(t + 4 * g), cv[g]);
+                else if (4 * g < d)
+                    last(*reinterpret_cast<const f4v*>(t + 4 * g), cv[g], d - 4 * g);
             }
         }
         __builtin_amdgcn_wave_barrier();  // every lane is done with the tile
@@ -1082,75 +1120,134 @@ __device__ __forceinline__ double rows_dist_ctg(const float* __restrict__ X, int
     return total;
 }
 
-// Floats of one wave's tile for the path LDM (0: the column slabs).
-template <int LDM>
-constexpr int row_tile_floats()
-{
-    if constexpr (LDM == 0)
-        return kRowTileFloats;
-    else
-        return CtgGeom<LDM>::TILE;
-}
-
-template <int LDM>
-__device__ __forceinline__ double rows_dist_any(const float* __restrict__ X, int ld, int d,
-                                                const float* __restrict__ C, const int* __restrict__ labels, int k,
-                                                long r0, long r1, float* __restrict__ dist, float* tile)
-{
-    if constexpr (LDM == 0)
-        return rows_dist(X, ld, d, C, labels, k, r0, r1, dist, tile);
-    else
-        return rows_dist_ctg<LDM>(X, ld, d, C, labels, k, r0, r1, dist, tile);
-}
-
 // The path for rows of stride ld: the narrowest contiguous one that holds
 // them, else the column slabs.
 int row_path(int ld) { return ld <= 32 ? 32 : ld <= 64 ? 64 : ld <= 104 ? 104 : ld <= 128 ? 128 : 0; }
 
-// Block b: rows [b rpb, (b + 1) rpb); its fp64 total (lanes, then waves in
-// order) goes to block_part[b].
+// The relocation's row distances (32-row chunks, centres from C): the
+// wave's tile, and the distances of rows [r0, r1) for the waves of a
+// 256-thread block.
 template <int LDM>
+constexpr int reloc_tile_floats()
+{
+    if constexpr (LDM == 0)
+        return kRowTileFloats;
+    else
+        return CtgGeom<LDM, 32>::TILE;
+}
+
+template <int LDM>
+__device__ __forceinline__ double reloc_rows_dist(const float* __restrict__ X, int ld, int d,
+                                                  const float* __restrict__ C, const int* __restrict__ labels, int k,
+                                                  long r0, long r1, float* __restrict__ dist, float* tile)
+{
+    if constexpr (LDM == 0)
+        return rows_dist(X, ld, d, C, labels, k, r0, r1, dist, tile);
+    else
+        return rows_dist_ctg<LDM, 32, false>(X, ld, d, C, ld, labels, k, r0, r1, 128, dist, tile);
+}
+
+// k_rowdist, 64-row chunks dealt round-robin to the grid's waves (wave w of
+// block b takes chunks b 4 + w + 4 gridDim t); dynamic LDS holds the four
+// wave tiles (64 ctg_stride(ld) floats each) and, with CL, the centres (k
+// rows of stride ctg_stride(ld)), copied in while the first chunks load.
+// Each block's fp64 total (lanes, then waves in order) goes to
+// block_part[b]; k_rowdist_total adds them.
+template <int LDM, bool CL>
 __global__ __launch_bounds__(256) void k_rowdist(RowDistArgs a)
 {
-    constexpr int TF = row_tile_floats<LDM>();
-    __shared__ float tiles[4 * TF];
+    extern __shared__ __attribute__((aligned(16))) float rd_lds[];
+    __shared__ double sh[4];
+    const int S = ctg_stride(a.ld);
+    float* sC = rd_lds + 4 * 64 * S;
+    auto copy_centres = [&]() {
+        if constexpr (CL) {
+            const int e4 = a.k * a.ld / 4;
+            const f4v* c4 = reinterpret_cast<const f4v*>(a.C);
+            for (int q = threadIdx.x; q < e4; q += 256) {
+                const int p = 4 * q, r = p / a.ld;
+                *reinterpret_cast<f4v*>(sC + r * S + (p - r * a.ld)) = c4[q];
+            }
+            __syncthreads();
+        }
+    };
+    const double v = rows_dist_ctg<LDM, 64, CL>(a.X, a.ld, a.d, CL ? sC : a.C, CL ? S : a.ld, a.labels, a.k,
+                                                (long)blockIdx.x * 256, a.n, (long)gridDim.x * 256, a.out_rows,
+                                                rd_lds + (threadIdx.x >> 6) * 64 * S, copy_centres);
+    const double t = block_sum(v, sh);
+    if (threadIdx.x == 0) a.block_part[blockIdx.x] = t;
+}
+
+// Rows longer than 128 floats: the column slabs, block b taking rows
+// [b rpb, (b + 1) rpb).
+__global__ __launch_bounds__(256) void k_rowdist_slab(RowDistArgs a)
+{
+    __shared__ float tiles[4 * kRowTileFloats];
     __shared__ double sh[4];
     const long rpb = (a.n + gridDim.x - 1) / gridDim.x;
     const long r0 = min(a.n, (long)blockIdx.x * rpb), r1 = min(a.n, r0 + rpb);
-    const double v = rows_dist_any<LDM>(a.X, a.ld, a.d, a.C, a.labels, a.k, r0, r1, a.out_rows,
-                                        tiles + (threadIdx.x >> 6) * TF);
+    const double v = rows_dist(a.X, a.ld, a.d, a.C, a.labels, a.k, r0, r1, a.out_rows,
+                               tiles + (threadIdx.x >> 6) * kRowTileFloats);
     const double t = block_sum(v, sh);
-    // the last block to finish adds the block totals, in block order
-    __shared__ int last_s;
-    if (threadIdx.x == 0) {
-        a.block_part[blockIdx.x] = t;
-        __threadfence();  // the block total, to the device
-        last_s = atomicAdd(&a.state->rowdist_ctr, 1u) == gridDim.x - 1;
-    }
-    __syncthreads();
-    if (!last_s) return;
-    __threadfence();  // every block's total
+    if (threadIdx.x == 0) a.block_part[blockIdx.x] = t;
+}
+
+// The inertia: the nb block totals added in block order (each thread its
+// strided share, then the block's fixed-order sum).  The kernel boundary
+// makes k_rowdist's totals visible without a device-scope fence in every
+// block, which cost 5 us of k_rowdist's 42 at 500000 x 100.
+__global__ __launch_bounds__(256) void k_rowdist_total(RowDistArgs a, int nb)
+{
+    __shared__ double sh[4];
     double s = 0.0;
-    for (int b = threadIdx.x; b < (int)gridDim.x; b += 256) s += a.block_part[b];
+    for (int b = threadIdx.x; b < nb; b += 256) s += a.block_part[b];
     s = block_sum(s, sh);
-    if (threadIdx.x == 0) {
-        a.state->inertia = s;
-        a.state->rowdist_ctr = 0u;
-    }
+    if (threadIdx.x == 0) a.state->inertia = s;
 }
 
 int rowdist_grid(long n) { return (int)max(1L, min((long)kRowDistBlocks, (n + 255) / 256)); }
 
+// LDS of k_rowdist for rows of stride ld: the tiles, and the centres when
+// they fit beside them (*cl).
+static size_t rowdist_lds(int ld, int k, bool* cl)
+{
+    constexpr size_t kBudget = 150 * 1024;
+    const size_t S = (size_t)ctg_stride(ld), tiles = 4 * 64 * S * sizeof(float);
+    const size_t cen = (size_t)k * S * sizeof(float);
+    *cl = tiles + cen <= kBudget;
+    return *cl ? tiles + cen : tiles;
+}
+
+template <int LDM>
+static hipError_t launch_rowdist_ctg(const RowDistArgs& a, hipStream_t s, int* nb)
+{
+    bool cl = false;
+    const size_t lds = rowdist_lds(a.ld, a.k, &cl);
+    auto f = cl ? k_rowdist<LDM, true> : k_rowdist<LDM, false>;
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(f),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    // one block per CU (the LDS allows no more), at most one per 256 rows
+    *nb = (int)max(1L, min((long)min(kRowDistBlocks, 256), (a.n + 255) / 256));
+    hipLaunchKernelGGL(f, dim3(*nb), dim3(256), lds, s, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_rowdist(const RowDistArgs& a, hipStream_t s)
 {
-    const int nblk = rowdist_grid(a.n);
+    int nb = rowdist_grid(a.n);
+    hipError_t e = hipSuccess;
     switch (row_path(a.ld)) {
-    case 32: hipLaunchKernelGGL(k_rowdist<32>, dim3(nblk), dim3(256), 0, s, a); break;
-    case 64: hipLaunchKernelGGL(k_rowdist<64>, dim3(nblk), dim3(256), 0, s, a); break;
-    case 104: hipLaunchKernelGGL(k_rowdist<104>, dim3(nblk), dim3(256), 0, s, a); break;
-    case 128: hipLaunchKernelGGL(k_rowdist<128>, dim3(nblk), dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL(k_rowdist<0>, dim3(nblk), dim3(256), 0, s, a); break;
+    case 32: e = launch_rowdist_ctg<32>(a, s, &nb); break;
+    case 64: e = launch_rowdist_ctg<64>(a, s, &nb); break;
+    case 104: e = launch_rowdist_ctg<104>(a, s, &nb); break;
+    case 128: e = launch_rowdist_ctg<128>(a, s, &nb); break;
+    default:
+        hipLaunchKernelGGL(k_rowdist_slab, dim3(nb), dim3(256), 0, s, a);
+        e = hipGetLastError();
     }
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_rowdist_total, dim3(1), dim3(256), 0, s, a, nb);
     return hipGetLastError();
 }
 
@@ -1392,7 +1489,7 @@ __device__ int block_excl_scan(int v, int* sh, int* total)
 template <int LDM>
 __device__ __forceinline__ void reloc_body(const InRelocArgs& a, int E)
 {
-    constexpr int TF = row_tile_floats<LDM>();
+    constexpr int TF = reloc_tile_floats<LDM>();
     __shared__ float tiles[4 * TF];
     __shared__ float sd[4];
     __shared__ long si[4];
@@ -1404,7 +1501,7 @@ __device__ __forceinline__ void reloc_body(const InRelocArgs& a, int E)
     // (A) distances of rows [r0, r1), then this block's E farthest, in order
     const long rpb = (a.n + gridDim.x - 1) / gridDim.x;
     const long r0 = min(a.n, (long)blockIdx.x * rpb), r1 = min(a.n, r0 + rpb);
-    (void)rows_dist_any<LDM>(a.X, a.ld, a.d, a.C_old, a.labels, a.k, r0, r1, a.dist, tiles + w * TF);
+    (void)reloc_rows_dist<LDM>(a.X, a.ld, a.d, a.C_old, a.labels, a.k, r0, r1, a.dist, tiles + w * TF);
     __threadfence_block();
     __syncthreads();
     {
@@ -1622,18 +1719,24 @@ __global__ __launch_bounds__(256) void k_reloc(InRelocArgs a)
     reloc_body<LDM>(a, E);
 }
 
-// The fused step's finalize and relocation in one launch: blocks b < k nch
-// take finalize chunk (b % k, b / k); then, when some cluster received no
-// row (the fused kernel's presence bits, so every block knows at once),
-// every block joins the relocation.  The last block to finish its rows
-// finds every finalize chunk written.
+// The fused step's finalize and relocation in one launch.  The F = k nch
+// finalize chunks (cluster j, column chunk cc) are numbered j nch + cc, the
+// order of their columns in memory; blocks are dealt to the 8 XCDs in turn
+// (block b on XCD b % 8), and the blocks of XCD x take chunks
+// [x per, (x + 1) per), per = ceil(F / 8), so that a cache line two
+// neighbouring chunks share is fetched into one XCD's L2 (the partials'
+// rows of d floats need not start on a line).  Then, when some cluster
+// received no row (the fused kernel's presence bits, so every block knows
+// at once), every block joins the relocation.  The last block to finish its
+// rows finds every finalize chunk written.
 template <int LDM>
 __global__ __launch_bounds__(256) void k_finalize_reloc(FinalizeArgs f, InRelocArgs a, int nch)
 {
     const int b = blockIdx.x;
-    if (b < f.k * nch) finalize_cols_block(f, b % f.k, b / f.k, nch);
     LoopState* st = f.state;
     const unsigned long long pres = st->present[f.iter & 1];
+    const int per = (f.k * nch + 7) / 8, item = (b & 7) * per + (b >> 3);
+    if ((b >> 3) < per && item < f.k * nch) finalize_cols_block(f, item / nch, item % nch, nch);
     if (b == 0 && threadIdx.x == 0) st->present[(f.iter + 1) & 1] = 0ull;  // for the next fused kernel
     if (st->done != 0) return;
     const unsigned long long all = f.k >= 64 ? ~0ull : (1ull << f.k) - 1ull;
@@ -1645,7 +1748,7 @@ __global__ __launch_bounds__(256) void k_finalize_reloc(FinalizeArgs f, InRelocA
 hipError_t launch_finalize_reloc(const FinalizeArgs& f, const InRelocArgs& a, hipStream_t s)
 {
     const int nch = finalize_col_chunks(f.d, f.R);
-    if (f.k > 64 || f.k * nch > kRelocInlineBlocks || f.rec_off != nullptr) return hipErrorInvalidValue;
+    if (f.k > 64 || 8 * ((f.k * nch + 7) / 8) > kRelocInlineBlocks || f.rec_off != nullptr) return hipErrorInvalidValue;
     const dim3 g(kRelocInlineBlocks);
     switch (row_path(a.ld)) {
     case 32: hipLaunchKernelGGL(k_finalize_reloc<32>, g, dim3(256), 0, s, f, a, nch); break;

@@ -685,7 +685,7 @@ struct Lloyd {
         const FinalizeArgs f = finalize_args(iter, tol, flags);
         const InRelocArgs r{X, n, ld, d, k, labels, cen[cur], cen[cur ^ 1], sums, counts, part,
                             finalize_col_chunks(d, f.R), rowout, r_cand_d, r_cand_i, r_amax, st, iter};
-        if (reloc_inline && fblocks > 0 && k <= 64 && k * r.nch <= kRelocInlineBlocks) {
+        if (reloc_inline && fblocks > 0 && k <= 64 && 8 * ((k * r.nch + 7) / 8) <= kRelocInlineBlocks) {
             // the fused kernel's presence bits name the empty clusters: one launch
             HIP_TRY(launch_finalize_reloc(f, r, s), "finalize launch");
         } else {
