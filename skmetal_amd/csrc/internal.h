@@ -238,7 +238,8 @@ struct InRelocArgs {
     int* amax;             // [1]
     LoopState* state; int iter;
 };
-constexpr int kRelocInlineBlocks = 512;  // grid of k_reloc (two blocks per CU)
+constexpr int kRelocInlineBlocks = 256;  // grid of k_reloc / k_finalize_reloc (one block per CU: their LDS)
+constexpr int kRelocLdsRows = 4096;      // a block's row distances kept in LDS (more rows: InRelocArgs::dist)
 constexpr int kRelocCandBlocks = kRelocInlineBlocks > kRelocBlocks ? kRelocInlineBlocks : kRelocBlocks;  // candidate list rows
 hipError_t launch_reloc_inline(const InRelocArgs& a, hipStream_t s);
 // The fused step's k_finalize_cols and k_reloc in one launch (k <= 64, at

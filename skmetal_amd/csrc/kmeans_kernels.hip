@@ -1008,14 +1008,16 @@ struct NoPrologue {
     __device__ void operator()() const {}
 };
 
-// ld: the row stride, a multiple of 4 (<= LDM); tile: the wave's
-// ROWS ctg_stride(ld) floats; pro: block-wide set-up run by every wave
-// once its first chunk's loads are in flight.  As rows_dist otherwise.
+// ld: the row stride, a multiple of 4 (<= LDM); row r's distance goes to
+// dist[r - dbase] (nullable); tile: the wave's ROWS ctg_stride(ld) floats;
+// pro: block-wide set-up run by every wave once its first chunk's loads are
+// in flight.  As rows_dist otherwise.
 template <int LDM, int ROWS, bool CL, typename Pro = NoPrologue>
 __device__ __forceinline__ double rows_dist_ctg(const float* __restrict__ X, int ld, int d,
                                                 const float* __restrict__ Cs, int cs,
                                                 const int* __restrict__ labels, int k, long r0, long r1,
-                                                long wstep, float* __restrict__ dist, float* tile, Pro pro = Pro())
+                                                long wstep, float* __restrict__ dist, long dbase, float* tile,
+                                                Pro pro = Pro())
 {
 #pragma clang fp contract(off)
     using G = CtgGeom<LDM, ROWS>;
@@ -1112,7 +1114,7 @@ __device__ __forceinline__ double rows_dist_ctg(const float* __restrict__ X, int
         }
         __builtin_amdgcn_wave_barrier();  // every lane is done with the tile
         if (lane < nrows) {
-            if (dist != nullptr) dist[c0 + lane] = ok ? res : 0.f;
+            if (dist != nullptr) dist[c0 + lane - dbase] = ok ? res : 0.f;
             total += ok ? (double)res : 0.0;
         }
         c0 = nc0;
@@ -1124,27 +1126,27 @@ __device__ __forceinline__ double rows_dist_ctg(const float* __restrict__ X, int
 // them, else the column slabs.
 int row_path(int ld) { return ld <= 32 ? 32 : ld <= 64 ? 64 : ld <= 104 ? 104 : ld <= 128 ? 128 : 0; }
 
-// The relocation's row distances (32-row chunks, centres from C): the
-// wave's tile, and the distances of rows [r0, r1) for the waves of a
-// 256-thread block.
-template <int LDM>
-constexpr int reloc_tile_floats()
-{
-    if constexpr (LDM == 0)
-        return kRowTileFloats;
-    else
-        return CtgGeom<LDM, 32>::TILE;
-}
+// The relocation's row distances, rows [r0, r1) of a 256-thread block:
+// 64-row chunks (kRelocTileFloats per wave tile), the centres from sC (CL:
+// the block's LDS copy, which pro writes) or from C.
+template <int LDM, bool CL>
+struct RelocGeom {
+    static constexpr int TF = LDM == 0 ? kRowTileFloats : CtgGeom<LDM == 0 ? 32 : LDM, 64>::TILE;  // wave tile
+    static constexpr int CF = CL ? 64 * CtgGeom<LDM == 0 ? 32 : LDM, 64>::SMAX : 1;                   // centres, k <= 64
+};
 
-template <int LDM>
-__device__ __forceinline__ double reloc_rows_dist(const float* __restrict__ X, int ld, int d,
-                                                  const float* __restrict__ C, const int* __restrict__ labels, int k,
-                                                  long r0, long r1, float* __restrict__ dist, float* tile)
+template <int LDM, bool CL, typename Pro>
+__device__ __forceinline__ void reloc_rows_dist(const float* __restrict__ X, int ld, int d, const float* __restrict__ C,
+                                                const float* sC, const int* __restrict__ labels, int k, long r0,
+                                                long r1, float* dist, long dbase, float* tile, Pro pro)
 {
-    if constexpr (LDM == 0)
-        return rows_dist(X, ld, d, C, labels, k, r0, r1, dist, tile);
-    else
-        return rows_dist_ctg<LDM, 32, false>(X, ld, d, C, ld, labels, k, r0, r1, 128, dist, tile);
+    if constexpr (LDM == 0) {
+        pro();
+        (void)rows_dist(X, ld, d, C, labels, k, r0, r1, dist, tile);
+    } else {
+        (void)rows_dist_ctg<LDM, 64, CL>(X, ld, d, CL ? sC : C, CL ? ctg_stride(ld) : ld, labels, k, r0, r1, 256,
+                                         dist, dbase, tile, pro);
+    }
 }
 
 // k_rowdist, 64-row chunks dealt round-robin to the grid's waves (wave w of
@@ -1172,7 +1174,7 @@ __global__ __launch_bounds__(256) void k_rowdist(RowDistArgs a)
         }
     };
     const double v = rows_dist_ctg<LDM, 64, CL>(a.X, a.ld, a.d, CL ? sC : a.C, CL ? S : a.ld, a.labels, a.k,
-                                                (long)blockIdx.x * 256, a.n, (long)gridDim.x * 256, a.out_rows,
+                                                (long)blockIdx.x * 256, a.n, (long)gridDim.x * 256, a.out_rows, 0,
                                                 rd_lds + (threadIdx.x >> 6) * 64 * S, copy_centres);
     const double t = block_sum(v, sh);
     if (threadIdx.x == 0) a.block_part[blockIdx.x] = t;
@@ -1486,11 +1488,13 @@ __device__ int block_excl_scan(int v, int* sh, int* total)
 
 // The relocation of E (1..kMaxReloc) empty clusters by every block of the
 // grid (gridDim.x <= kRelocCandBlocks): phases A, B and C above.
-template <int LDM>
+template <int LDM, bool CL>
 __device__ __forceinline__ void reloc_body(const InRelocArgs& a, int E)
 {
-    constexpr int TF = reloc_tile_floats<LDM>();
-    __shared__ float tiles[4 * TF];
+    using RG = RelocGeom<LDM, CL>;
+    __shared__ __attribute__((aligned(16))) float tiles[4 * RG::TF];
+    __shared__ __attribute__((aligned(16))) float sC[RG::CF];
+    __shared__ float sdist[kRelocLdsRows];
     __shared__ float sd[4];
     __shared__ long si[4];
     __shared__ int shi[4];
@@ -1498,10 +1502,28 @@ __device__ __forceinline__ void reloc_body(const InRelocArgs& a, int E)
     LoopState* st = a.state;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
 
-    // (A) distances of rows [r0, r1), then this block's E farthest, in order
+    // (A) distances of rows [r0, r1), into LDS when they fit (a.dist
+    // otherwise), then this block's E farthest, in order.  Distances left
+    // in the L2 would make the device-scope fence below write back 2 MB at
+    // 500000 rows: 29 of the step's 95 us.
     const long rpb = (a.n + gridDim.x - 1) / gridDim.x;
     const long r0 = min(a.n, (long)blockIdx.x * rpb), r1 = min(a.n, r0 + rpb);
-    (void)reloc_rows_dist<LDM>(a.X, a.ld, a.d, a.C_old, a.labels, a.k, r0, r1, a.dist, tiles + w * TF);
+    const bool in_lds = LDM != 0 && r1 - r0 <= kRelocLdsRows;
+    float* dist = in_lds ? sdist : a.dist;
+    const long dbase = in_lds ? r0 : 0;
+    auto copy_centres = [&]() {
+        if constexpr (CL) {
+            const int S = ctg_stride(a.ld), e4 = a.k * a.ld / 4;
+            const f4v* c4 = reinterpret_cast<const f4v*>(a.C_old);
+            for (int q = tid; q < e4; q += 256) {
+                const int p = 4 * q, r = p / a.ld;
+                *reinterpret_cast<f4v*>(sC + r * S + (p - r * a.ld)) = c4[q];
+            }
+            __syncthreads();
+        }
+    };
+    reloc_rows_dist<LDM, CL>(a.X, a.ld, a.d, a.C_old, sC, a.labels, a.k, r0, r1, dist, dbase, tiles + w * RG::TF,
+                             copy_centres);
     __threadfence_block();
     __syncthreads();
     {
@@ -1510,7 +1532,7 @@ __device__ __forceinline__ void reloc_body(const InRelocArgs& a, int E)
         for (int e = 0; e < E; ++e) {
             float bd = 0.f;
             long bi = -1;
-            for (long r = r0 + tid; r < r1; r += 256) far_pick(bd, bi, a.dist[r], r, dl, il);
+            for (long r = r0 + tid; r < r1; r += 256) far_pick(bd, bi, dist[r - dbase], r, dl, il);
             far_block_reduce(bd, bi, sd, si);
             if (tid == 0) {
                 a.cand_d[(long)blockIdx.x * kMaxReloc + e] = bd;
@@ -1554,7 +1576,7 @@ __device__ __forceinline__ void reloc_body(const InRelocArgs& a, int E)
     // the E farthest rows overall: a merge of the blocks' ordered lists,
     // thread t holding the heads of blocks t + 256 j
     {
-        constexpr int HPT = (kRelocInlineBlocks + 255) / 256;
+        constexpr int HPT = (kRelocInlineBlocks + 255) / 256;  // list heads per thread
         const int nb = (int)gridDim.x;  // <= 256 HPT
         int h[HPT];
         float hd[HPT];
@@ -1716,7 +1738,7 @@ __global__ __launch_bounds__(256) void k_reloc(InRelocArgs a)
     if (a.state->done != 0) return;
     const int E = a.state->empty_cnt[a.iter & 1];
     if (E == 0 || E > kMaxReloc) return;
-    reloc_body<LDM>(a, E);
+    reloc_body<LDM, false>(a, E);
 }
 
 // The fused step's finalize and relocation in one launch.  The F = k nch
@@ -1742,7 +1764,8 @@ __global__ __launch_bounds__(256) void k_finalize_reloc(FinalizeArgs f, InRelocA
     const unsigned long long all = f.k >= 64 ? ~0ull : (1ull << f.k) - 1ull;
     const int E = __popcll(all & ~pres);
     if (E == 0 || E > kMaxReloc) return;
-    reloc_body<LDM>(a, E);
+    // k <= 64: the centres fit in LDS beside the tiles up to 104 floats a row
+    reloc_body<LDM, LDM != 0 && LDM <= 104>(a, E);
 }
 
 hipError_t launch_finalize_reloc(const FinalizeArgs& f, const InRelocArgs& a, hipStream_t s)
