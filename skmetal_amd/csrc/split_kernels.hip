@@ -763,7 +763,9 @@ struct Assign3Geom {
     static constexpr int CSTR = SEG + 8;                            // bf16 per centre row: an odd number of 16-byte units
     static constexpr int CPART = CPC * CSTR;                        // bf16 from one part to the next
     static constexpr int PBYTES = 3 * CPART * 2;                    // the three parts
-    static constexpr int STAGE = (PBYTES + CPC * 4 + 1023) / 1024 * 1024;  // + ||c||^2, whole KB
+    // + ||c||^2 of the stage's pass and of the pass before it (cyclically),
+    // whole KB
+    static constexpr int STAGE = (PBYTES + 2 * CPC * 4 + 1023) / 1024 * 1024;
     static constexpr size_t LDS = size_t(2) * STAGE;
 };
 
@@ -787,10 +789,14 @@ __global__ __launch_bounds__(256) void k_centre_image(const float* __restrict__ 
         *reinterpret_cast<v4s*>(dst + G::CPART) = pt.m;
         *reinterpret_cast<v4s*>(dst + 2 * G::CPART) = pt.l;
     }
+    // ||c||^2 of pass p, then of pass p - 1 (the last pass for p = 0): the
+    // assign kernel reads the norms of the pass it has just finished from the
+    // stage that follows it
+    const int npass = (k + G::CPC - 1) / G::CPC, pp = (p + npass - 1) % npass;
     float* const sn = reinterpret_cast<float*>(out + G::PBYTES);
     for (int c = threadIdx.x; c < G::STAGE / 4 - G::PBYTES / 4; c += 256) {
-        const int j = p * G::CPC + c;
-        sn[c] = c < G::CPC ? (j < k ? cnorm[j] : INFINITY) : 0.f;  // padding centres never win
+        const int j = (c < G::CPC ? p : pp) * G::CPC + c % G::CPC;
+        sn[c] = c < 2 * G::CPC ? (j < k ? cnorm[j] : INFINITY) : 0.f;  // padding centres never win
     }
 }
 
@@ -924,36 +930,34 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
                         }
                     }
                 }
-                if (sg == nseg - 1) {
-                    // ||c||^2 - 2 x.c, first minimum wins
-                    // (_k_means_lloyd.pyx:196-212); the lane's centres come in
-                    // ascending order, passes too.  ||c||^2 rides in every
-                    // stage of the pass and is read here, from the stage in
-                    // use, before the barrier below: after it another wave may
-                    // already be copying the stage after next into this one.
-                    const float* sN = reinterpret_cast<const float*>(smem + cur * G::STAGE + G::PBYTES);
-#pragma unroll
-                    for (int g = 0; g < 2; ++g) {
-#pragma unroll
-                        for (int cb = 0; cb < CB; ++cb) {
-                            const float4 c4 = *reinterpret_cast<const float4*>(&sN[16 * cb + 4 * h]);
-                            const float cn[4] = {c4.x, c4.y, c4.z, c4.w};
-#pragma unroll
-                            for (int i = 0; i < 4; ++i) {
-                                const float dd = fmaf(-2.0f, acc[g][cb][i], cn[i]);  // NaN compares false
-                                const bool take = dd < bd[g];
-                                bd[g] = take ? dd : bd[g];
-                                bi[g] = take ? p * CPC + 16 * cb + 4 * h + i : bi[g];
-                            }
-                        }
-                    }
-                }
                 if (nst > 1) {
                     // the next stage is in (every wave's copies) and this one
                     // is read: swap
                     __builtin_amdgcn_s_waitcnt(0);
                     __syncthreads();
                     cur ^= 1;
+                }
+            }
+            // ||c||^2 - 2 x.c, first minimum wins (_k_means_lloyd.pyx:196-212);
+            // the lane's centres come in ascending order, passes too.  With
+            // one stage, the pass's ||c||^2 are in it; else they are read as
+            // the previous pass's norms of the stage now current, which the
+            // stage copies rewrite only after the next barrier (a wave past
+            // that barrier has every wave's reads of this behind it).
+            const float* sN = reinterpret_cast<const float*>(smem + cur * G::STAGE + G::PBYTES) + (nst > 1 ? CPC : 0);
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                const float4 c4 = *reinterpret_cast<const float4*>(&sN[16 * cb + 4 * h]);
+                const float cn[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+                for (int g = 0; g < 2; ++g) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float dd = fmaf(-2.0f, acc[g][cb][i], cn[i]);  // NaN compares false
+                        const bool take = dd < bd[g];
+                        bd[g] = take ? dd : bd[g];
+                        bi[g] = take ? p * CPC + 16 * cb + 4 * h + i : bi[g];
+                    }
                 }
             }
         }
