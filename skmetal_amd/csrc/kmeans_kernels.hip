@@ -906,6 +906,74 @@ __global__ __launch_bounds__(256) void k_finalize_cols(FinalizeArgs a)
     finalize_cols_block(a, blockIdx.x, blockIdx.y, gridDim.y);
 }
 
+// Record mode (the sorted update: a cluster has a few records, one per
+// chunk of sorted rows it touches): one wave per (cluster j, column chunk
+// cc), item 4 blockIdx.x + wave of k nch.  Lane (rs, q) = (lane / 8, lane %
+// 8) adds the float4 of columns 32 cc + 4q of records rs, rs + 8, .. in
+// fp64, and the eight rs lanes are combined by an xor butterfly: with at
+// most 8 records the same sums, in the same order, as finalize_cols_block
+// (whose other waves then add zeros).  A block per item made 98,304 blocks
+// at 4096 clusters of 768 floats, each waiting on one round trip.
+__global__ __launch_bounds__(256) void k_finalize_recs(FinalizeArgs a, int nch)
+{
+    const int lane = threadIdx.x & 63;
+    const long item = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= (long)a.k * nch) return;
+    const int j = (int)(item / nch), cc = (int)(item - (long)j * nch);
+    if (a.state->done != 0) return;
+    const int q = lane & 7, rs = lane >> 3;
+    const int c4 = cc * 32 + 4 * q;
+    const int ccol = cc * 32 + lane;  // lanes 0..31: one column each
+    const float c_old = lane < 32 && ccol < a.d ? a.C_old[(long)j * a.ld + ccol] : 0.f;
+    const int R = a.rec_cnt[j];
+    const int count = a.cnt_in[j];
+    const float* src = a.psum + (long)a.rec_off[j] * a.ld + c4;
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+    if (c4 < a.ld) {  // ld is a multiple of 4: the float4 is in or out
+        for (int r = rs; r < R; r += 8) {
+            const float4 v = *reinterpret_cast<const float4*>(src + (long)r * a.ld);
+            s0 += (double)v.x;
+            s1 += (double)v.y;
+            s2 += (double)v.z;
+            s3 += (double)v.w;
+        }
+    }
+    for (int off = 8; off < 64; off <<= 1) {
+        s0 += __shfl_xor(s0, off, 64);
+        s1 += __shfl_xor(s1, off, 64);
+        s2 += __shfl_xor(s2, off, 64);
+        s3 += __shfl_xor(s3, off, 64);
+    }
+    // lane c < 32 takes column 32 cc + c: component c % 4 of lane c / 4
+    const int e = lane & 3, src_lane = (lane >> 2) & 7;
+    const double t0 = __shfl(s0, src_lane, 64), t1 = __shfl(s1, src_lane, 64);
+    const double t2 = __shfl(s2, src_lane, 64), t3 = __shfl(s3, src_lane, 64);
+    const double tot = e == 0 ? t0 : e == 1 ? t1 : e == 2 ? t2 : t3;
+    double sq = 0.0, nrm = 0.0;
+    if (lane < 32 && ccol < a.d) {
+        a.sums[(long)j * a.ld + ccol] = tot;
+        if (count > 0) {
+            const float cn = (float)(tot / (double)count);
+            a.C_new[(long)j * a.ld + ccol] = cn;
+            const double df = (double)cn - (double)c_old;
+            sq = df * df;
+            nrm = (double)cn * (double)cn;
+        }
+    }
+    sq = wave_sum(sq);
+    nrm = wave_sum(nrm);
+    if (lane == 0) {
+        a.part[((long)j * nch + cc) * 2 + 0] = sq;
+        a.part[((long)j * nch + cc) * 2 + 1] = nrm;
+        if (cc == 0) a.counts[j] = count;
+        if (cc == 0 && count == 0) atomicAdd(&a.state->empty_cnt[a.iter & 1], 1);  // for k_reloc
+        if (j == 0 && cc == 0) {
+            if (a.chg_next != nullptr) *a.chg_next = 0;
+            a.state->empty_cnt[(a.iter + 1) & 1] = 0;  // read by k_reloc of iteration iter - 1, which has run
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void k_finalize_loop(FinalizeArgs a, int nch)
 {
     LoopState* st = a.state;
@@ -954,7 +1022,10 @@ __global__ __launch_bounds__(256) void k_finalize_loop(FinalizeArgs a, int nch)
 hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t s, bool with_loop)
 {
     const int nch = finalize_col_chunks(a.d, a.R);
-    hipLaunchKernelGGL(k_finalize_cols, dim3(a.k, nch), dim3(256), 0, s, a);
+    if (a.rec_off != nullptr)
+        hipLaunchKernelGGL(k_finalize_recs, dim3((unsigned)(((long)a.k * nch + 3) / 4)), dim3(256), 0, s, a, nch);
+    else
+        hipLaunchKernelGGL(k_finalize_cols, dim3(a.k, nch), dim3(256), 0, s, a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || !with_loop) return e;
     return launch_finalize_loop(a, s);
