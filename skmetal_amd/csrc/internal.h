@@ -62,6 +62,13 @@ struct AssignArgs {
     LoopState* state;      // nullable: no early exit
     int* changed;          // nullable: compare with previous labels, add the changes here
     char* img;             // k_assign3 only: [assign3_image_bytes(k, ld)] the centres' staged image
+    // k_assign3 only, nullable: the inertia of the new labels, fp64 block
+    // totals ([num_cu] at most; their number to *inert_blocks) of the rows'
+    // squared distances to their centres (direct form, as k_rowdist); d is
+    // the row length these use
+    double* inert = nullptr;
+    int* inert_blocks = nullptr;
+    int d = 0;
 };
 hipError_t launch_assign(const AssignArgs& a, int num_cu, hipStream_t s);
 // The same E-step on bf16 MFMAs over the exact three-part bf16 split of x
@@ -197,6 +204,9 @@ int rowdist_grid(long n);            // block totals to allocate for n rows
 // Row distances and their fixed-order total (k_rowdist or k_rowdist_slab,
 // then k_rowdist_total adds the block totals in block order).
 hipError_t launch_rowdist(const RowDistArgs& a, hipStream_t s);
+// The fixed-order total of nb fp64 block totals into state->inertia
+// (k_rowdist_total).
+hipError_t launch_inertia_total(const double* parts, int nb, LoopState* state, hipStream_t s);
 
 // Device relocation of up to kMaxReloc empty clusters at once (see
 // kmeans_kernels.hip); more go through the host.

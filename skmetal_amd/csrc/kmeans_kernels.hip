@@ -1396,6 +1396,15 @@ __global__ __launch_bounds__(256) void k_rowdist_total(RowDistArgs a, int nb)
     if (threadIdx.x == 0) a.state->inertia = s;
 }
 
+hipError_t launch_inertia_total(const double* parts, int nb, LoopState* state, hipStream_t s)
+{
+    RowDistArgs a{};
+    a.block_part = const_cast<double*>(parts);
+    a.state = state;
+    hipLaunchKernelGGL(k_rowdist_total, dim3(1), dim3(256), 0, s, a, nb);
+    return hipGetLastError();
+}
+
 int rowdist_grid(long n) { return (int)max(1L, min((long)kRowDistBlocks, (n + 255) / 256)); }
 
 // LDS of k_rowdist for rows of stride ld: the tiles, and the centres when

@@ -628,6 +628,31 @@ struct Lloyd {
         return 0;
     }
 
+    // The final E-step with the inertia of its labels: on the split path one
+    // pass over X (k_assign3 adds each row's distance to its new centre into
+    // per-block totals, k_rowdist_total adds those), else the E-step and then
+    // the row-distance pass.
+    int assign_inertia(const float* cents, double* out)
+    {
+        const long blocks = std::min<long>(C->num_cu, (n + 255) / 256);
+        if (split_on && a3cap && blocks <= rowdist_grid(n)) {
+            if (a3img == nullptr) TRY(grab((void**)&a3img, assign3_image_bytes(k, ld)));
+            AssignArgs a{X, n, ld, cents, cnorm, k, labels, nullptr, nullptr, a3img};
+            int nb = 0;
+            a.inert = rowpart;
+            a.inert_blocks = &nb;
+            a.d = d;
+            HIP_TRY(launch_assign3(a, C->num_cu, s), "assign launch");
+            HIP_TRY(launch_inertia_total(rowpart, nb, st, s), "inertia launch");
+            LoopState hs{};
+            TRY(read_state(&hs));
+            *out = hs.inertia;
+            return 0;
+        }
+        TRY(assign(cents, nullptr, nullptr));
+        return inertia(out);
+    }
+
     int update()
     {
         if (sg.on) {
@@ -1120,9 +1145,11 @@ struct Lloyd {
     {
         int n_iter = 0, done = 0;
         TRY(run_loop(max_iter, tol, flags, false, &n_iter, &done));
-        if (done != 1) TRY(assign(cen[cur], nullptr, nullptr));  // final E-step (_kmeans.py:736-748)
         double in = 0.0;
-        TRY(inertia(&in));
+        if (done != 1)
+            TRY(assign_inertia(cen[cur], &in));  // final E-step (_kmeans.py:736-748) and inertia (:749)
+        else
+            TRY(inertia(&in));
         if (n_iter_out) *n_iter_out = n_iter;
         if (inertia_out) *inertia_out = in;
         return 0;

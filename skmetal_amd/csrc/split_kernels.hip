@@ -803,7 +803,8 @@ __global__ __launch_bounds__(256) void k_centre_image(const float* __restrict__ 
 template <int CB>
 __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X, long n, int ld,
                                                    const char* __restrict__ img, int k, int* __restrict__ labels,
-                                                   LoopState* st, int* changed)
+                                                   LoopState* st, int* changed, const float* __restrict__ C, int d,
+                                                   double* __restrict__ inert)
 {
     if (st != nullptr && st->done != 0) return;
     using G = Assign3Geom<CB>;
@@ -816,6 +817,7 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
     const int h = lane >> 4, r16 = lane & 15;
     if (tid == 0) sChg = 0;  // (published by the first barrier)
     int nchg = 0;            // lane 0: labels this wave changed
+    double itot = 0.0;       // lanes 0..31: the inertia of their rows
     const int npass = (k + CPC - 1) / CPC;
     const int nseg = (ld + SEG - 1) / SEG;
     const int nst = npass * nseg;
@@ -984,6 +986,41 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
             labels[row] = mylab;
         }
         if (changed != nullptr) nchg += (int)__popcll(__ballot(moved));
+        // the inertia term of the row: ||x - c_label||^2 in fp32, in the
+        // association order of sklearn's _euclidean_dense_dense
+        // (_k_means_common.pyx:16-43; the same sums as k_rowdist), from the
+        // row just read (in the L2) and the fp32 centre; lane l < 32 takes
+        // row l.  (The centre's exact parts from the LDS image instead of C
+        // took 121 us instead of 87 at 500000 x 100, k = 50: bank conflicts
+        // of 32 random centre rows; each row split over lanes l and l + 32,
+        // 118 us.)
+        if (inert != nullptr && valid) {
+#pragma clang fp contract(off)
+            const float4* x4 = reinterpret_cast<const float4*>(X + row * ld);
+            const float4* c4 = reinterpret_cast<const float4*>(C + (long)mylab * ld);
+            float res = 0.f;
+            const int nfull = d >> 2;
+#pragma unroll 5
+            for (int g = 0; g < nfull; ++g) {
+                const float4 xv = x4[g], cv = c4[g];
+                const float t0 = xv.x - cv.x, t1 = xv.y - cv.y, t2 = xv.z - cv.z, t3 = xv.w - cv.w;
+                res += ((t0 * t0 + t1 * t1) + t2 * t2) + t3 * t3;
+            }
+            if (d & 3) {  // the row's last features, one by one
+                const float4 xv = x4[nfull], cv = c4[nfull];
+                float tt = xv.x - cv.x;
+                res += tt * tt;
+                if ((d & 3) > 1) {
+                    tt = xv.y - cv.y;
+                    res += tt * tt;
+                }
+                if ((d & 3) > 2) {
+                    tt = xv.z - cv.z;
+                    res += tt * tt;
+                }
+            }
+            itot += (double)res;
+        }
     }
     // one global atomic per block: a wave-level atomic per 32 rows on one
     // address serialises thousands of them while labels move
@@ -992,9 +1029,22 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
         __syncthreads();
         if (tid == 0 && sChg != 0) atomicAdd(changed, sChg);
     }
+    // the block's inertia total: lanes (butterfly), then waves in order
+    if (inert != nullptr) {
+        __shared__ double sI[8];
+        itot = wave_sum(itot);
+        if (lane == 0) sI[wave] = itot;
+        __syncthreads();
+        if (tid == 0) {
+            double t = 0.0;
+            for (int w = 0; w < 8; ++w) t += sI[w];
+            inert[blockIdx.x] = t;
+        }
+    }
 }
 
-typedef void (*assign3_fn)(const float*, long, int, const char*, int, int*, LoopState*, int*);
+typedef void (*assign3_fn)(const float*, long, int, const char*, int, int*, LoopState*, int*, const float*, int,
+                           double*);
 typedef void (*image_fn)(const float*, const float*, int, int, int, char*);
 
 static int assign3_cb(int k) { return k <= 64 ? 4 : k <= 128 ? 8 : 16; }
@@ -1064,7 +1114,8 @@ hipError_t launch_assign3(const AssignArgs& a, int num_cu, hipStream_t s)
     long blocks = (a.n + 255) / 256;
     if (blocks > num_cu) blocks = num_cu;
     hipLaunchKernelGGL(assign3_kernel(a.k), dim3((unsigned)blocks), dim3(512), assign3_lds(a.k), s, a.X, a.n, a.ld,
-                       a.img, a.k, a.labels, a.state, a.changed);
+                       a.img, a.k, a.labels, a.state, a.changed, a.C, a.d, a.inert);
+    if (a.inert_blocks != nullptr) *a.inert_blocks = (int)blocks;
     return hipGetLastError();
 }
 typedef void (*fused_fn)(FusedArgs);

@@ -119,6 +119,26 @@ def test_mindists_and_inertia_vs_oracle(bridge, d):
     parity.check_inertia(v, oracle.inertia(X, C, lab), what="kmeans_inertia")
 
 
+@pytest.mark.parametrize("n,d,k", [(20000, 100, 50), (9000, 33, 7), (12000, 128, 200), (6000, 200, 33)])
+def test_fit_inertia_from_final_estep(bridge, n, d, k):
+    """The fit's inertia comes from its final E-step (k_assign3 adds each
+    row's direct-form distance to its new centre); it equals the separate
+    row-distance pass over the same labels and centres up to the fp64
+    summation order, and the oracle's inertia of those labels and centres."""
+    rng = np.random.default_rng(11 + d)
+    X = (rng.standard_normal((n, d)) * 2 + rng.integers(-3, 4, (n, 1))).astype(np.float32)
+    C0 = X[rng.choice(n, k, replace=False)].copy()
+    with bridge.LloydHandle(n, d, k) as h:
+        h.load(X, center=False)
+        h.set_centers(C0)
+        n_iter, inertia = h.run(4, 0.0, strict=True)
+        ref = h.inertia()
+        C, lab = h.centers(), h.labels()
+    _say(f"fit inertia n={n} d={d} k={k}: {inertia!r} row-distance pass {ref!r}")
+    assert inertia == pytest.approx(ref, rel=1e-12)
+    parity.check_inertia(inertia, oracle.inertia(X, C, lab), what="fit inertia")
+
+
 def _lockstep_gpu(bridge, X, C0, steps, what, center=True, elem_rtol=None):
     """Run `steps` single GPU steps from C0, checking each against the oracle
     (in the coordinates the device runs in: X centred on its fp32 column mean,
