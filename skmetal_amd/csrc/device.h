@@ -7,6 +7,16 @@ namespace skm {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+// Native 4-float vector for staging registers: arrays of it stay in
+// registers (an array of HIP's float4 struct copied whole went to scratch
+// memory).
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// LDS row stride for rows of ld floats (ld a multiple of 4): an odd number of
+// 16-byte units, so that row-per-lane float4 reads fall in distinct bank
+// groups.
+__host__ __device__ constexpr int ctg_stride(int ld) { return 4 * ((ld / 4) | 1); }
+
 // Loads NQ float4s of this lane's row (row0 + lane) starting at feature f0,
 // with no branches: the buffer descriptor covers exactly the valid rows, so a
 // lane past the last row, and any float4 at or past `nq`, reads 0 without a

@@ -1186,13 +1186,6 @@ struct CtgGeom {
     static constexpr int TILE = ROWS * SMAX;          // floats per wave tile
 };
 
-// Tile row stride for rows of ld floats: an odd number of float4s.
-__host__ __device__ constexpr int ctg_stride(int ld) { return 4 * ((ld / 4) | 1); }
-
-// Native 4-float vector: arrays of it stay in registers (an array of the
-// float4 struct copied whole went to scratch memory).
-typedef float f4v __attribute__((ext_vector_type(4)));
-
 struct NoPrologue {
     __device__ void operator()() const {}
 };
