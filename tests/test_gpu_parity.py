@@ -139,6 +139,25 @@ def test_fit_inertia_from_final_estep(bridge, n, d, k):
     parity.check_inertia(inertia, oracle.inertia(X, C, lab), what="fit inertia")
 
 
+def test_fit_inertia_full_size_headline_workload(bridge):
+    """The 500,000 x 100, k = 50 workload: a 10-step sklearn-rule fit from the
+    seeded init ends on a step that changed labels, so its inertia comes from
+    the final E-step; it matches the row-distance pass over the same labels
+    and centres (the profile of the fit's end runs this test)."""
+    from skmetal_amd import _synth
+
+    X, C0 = _synth.generate("c2", seed=0)
+    with bridge.LloydHandle(*X.shape, C0.shape[0]) as h:
+        h.load(X, center=True)
+        for rep in range(2):
+            h.set_centers(C0)
+            n_iter, inertia = h.run(10, 0.0, strict=True)
+            ref = h.inertia()
+            _say(f"c2 fit {rep}: n_iter={n_iter} inertia={inertia!r} row-distance pass {ref!r}")
+            assert n_iter == 10
+            assert inertia == pytest.approx(ref, rel=1e-12)
+
+
 def _lockstep_gpu(bridge, X, C0, steps, what, center=True, elem_rtol=None):
     """Run `steps` single GPU steps from C0, checking each against the oracle
     (in the coordinates the device runs in: X centred on its fp32 column mean,
