@@ -264,7 +264,7 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
     // round parity
     __shared__ unsigned sMask[2][8][64];
     __shared__ __attribute__((aligned(16))) v8bf sOneHot[256];  // byte b -> its 8 bits as bf16 0 / 1
-    __shared__ int sCnt[4][64];                                 // rows per cluster, per SIMD
+    __shared__ int sCnt[4][64];                                 // rows per cluster, per SIMD (its first sums wave)
     __shared__ __attribute__((aligned(16))) float sN[CPC];
     __shared__ int sReady[8];  // half tiles E-step wave e has labelled
     __shared__ int sProg[8];   // feature blocks sums wave w has read: tile * (its blocks) + blocks
@@ -474,7 +474,6 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
             // lanes 0..15: row = lane
             __builtin_amdgcn_raw_buffer_store_b32(bi, rl, lane * 4, 0, 0);
             changed += (int)__popcll(__ballot(valid && old != bi));
-            if (valid) atomicAdd(&sCnt[m][bi], 1);  // the counts (integer adds)
             // this half tile's rows per cluster: the words of round r - 2, read
             // by both sums waves before they read any block of round r - 1
             // (waited on above), are cleared, then the bits set (an OR: any
@@ -653,6 +652,14 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
 #pragma unroll
                 for (int j = 0; j < NF; ++j) S[cb][j] = v4f{0.f, 0.f, 0.f, 0.f};
             }
+            // the first sums wave of the SIMD also counts the rows per
+            // cluster: lane (r16, h) adds the bits of the mask byte it reads
+            // (cluster 16 cb + r16, rows 8h .. 8h + 7); integer adds, so the
+            // counts are exact and order-free.  (An LDS atomic per row by the
+            // E-step waves cost up to 5 us per launch: same-address adds.)
+            int cnt[CB];
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) cnt[cb] = 0;
             for (int r = 0; r < rounds; ++r) {
                 wait_flag(&sReady[m], r + 1);
                 wait_flag(&sReady[m + 4], r + 1);
@@ -668,6 +675,10 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
                     for (int cb = 0; cb < CB; ++cb) mv[cb] = mw[16 * cb + r16];
 #pragma unroll
                     for (int cb = 0; cb < CB; ++cb) A[cb] = sOneHot[(mv[cb] >> sft) & 0xffu];
+                    if constexpr (FB0 == 0) {
+#pragma unroll
+                        for (int cb = 0; cb < CB; ++cb) cnt[cb] += __builtin_popcount((mv[cb] >> sft) & 0xffu);
+                    }
                 }
                 // the B operands of block j + 1 are read before block j's MFMAs
                 auto read_block = [&](int j, v8bf (&b)[3]) {
@@ -702,6 +713,16 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
                     }
 #pragma unroll
                     for (int p = 0; p < 3; ++p) bc[p] = bn[p];
+                }
+            }
+            if constexpr (FB0 == 0) {
+                // the SIMD's counts: the four row groups of each cluster
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    int c = cnt[cb];
+                    c += __shfl_xor(c, 16, 64);
+                    c += __shfl_xor(c, 32, 64);
+                    if (h == 0) sCnt[m][16 * cb + r16] = c;
                 }
             }
             __syncthreads();  // every wave is done with its tile
