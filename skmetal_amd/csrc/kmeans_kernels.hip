@@ -803,7 +803,10 @@ __device__ __forceinline__ float block_max(float v, float* sh)
 
 constexpr int kFinUnroll = 8;  // partials in flight per thread
 
-// One (cluster j, column chunk cc of nch) of the finalize; a whole block.
+// One (cluster j, column chunk cc of nch) of the finalize over R per-block
+// partials (partial r of cluster j at r k + j); a whole block.  Lane (rs,
+// q) = (thread / 8, thread % 8) adds the float4 of columns 32 cc + 4q of
+// partials rs, rs + 32, .. in fp64.
 __device__ __forceinline__ void finalize_cols_block(const FinalizeArgs& a, int j, int cc, int nch)
 {
     const int tid = threadIdx.x;
@@ -811,37 +814,46 @@ __device__ __forceinline__ void finalize_cols_block(const FinalizeArgs& a, int j
     const int rs = tid >> 3;        // partial lane, 0..31
     const int c4 = cc * 32 + 4 * q; // first column of this thread
     __shared__ double red[4][8][4];
+    __shared__ int rcnt[4];
 
-    // block partials: the halt flag, the old centres, the counts and the
-    // partials are all requested before any of them is used (one memory
-    // round trip); records exist only for a step whose update ran, so that
-    // mode tests the flag first
-    const bool recs = a.rec_off != nullptr;
+    // the halt flag, the old centres, each lane's first kFinUnroll partials
+    // and the counts are all requested before any of them is used: one
+    // memory round trip (a count loop that waited before the partials were
+    // requested made it four)
     const int done = a.state->done;
-    if (recs && done != 0) return;
     const int ccol = cc * 32 + tid;  // threads 0..31: one column each for the centre update
     const float c_old = tid < 32 && ccol < a.d ? a.C_old[(long)j * a.ld + ccol] : 0.f;
-    // partials of cluster j: R of them at r*k + j, or its records
-    const int R = recs ? a.rec_cnt[j] : a.R;
-    const float* src = a.psum + (recs ? (long)a.rec_off[j] * a.ld : (long)j * a.ld) + c4;
-    const long step = recs ? (long)a.ld : (long)a.k * a.ld;
-    // the count is summed by wave 0 alone, which also forms the centres
-    int cnt = 0;
-    if (tid < 64) {
-        if (recs) {
-            cnt = tid == 0 ? a.cnt_in[j] : 0;
-        } else {
-            for (int r = tid; r < a.R; r += 64) cnt += a.pcnt[(long)r * a.k + j];
+    const int R = a.R;
+    const float* src = a.psum + (long)j * a.ld + c4;
+    const long step = (long)a.k * a.ld;
+    const bool live = c4 < a.ld && R > 0;  // ld is a multiple of 4: the float4 is in or out
+    float4 v[kFinUnroll];
+    if (live) {
+#pragma unroll
+        for (int u = 0; u < kFinUnroll; ++u) {
+            const int r = rs + u * 32;
+            v[u] = *reinterpret_cast<const float4*>(src + (long)(r < R ? r : R - 1) * step);
         }
     }
+    int cnt = 0;
+    for (int r = tid; r < R; r += 256) cnt += a.pcnt[(long)r * a.k + j];
     double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
-    if (c4 < a.ld && R > 0) {  // ld is a multiple of 4: the float4 is in or out
-        for (int r0 = rs; r0 < R; r0 += kFinUnroll * 32) {
-            float4 v[kFinUnroll];
+    if (live) {
+#pragma unroll
+        for (int u = 0; u < kFinUnroll; ++u) {
+            if (rs + u * 32 < R) {
+                s0 += (double)v[u].x;
+                s1 += (double)v[u].y;
+                s2 += (double)v[u].z;
+                s3 += (double)v[u].w;
+            }
+        }
+        // R > 256 partials: further rounds in the same order
+        for (int r0 = rs + kFinUnroll * 32; r0 < R; r0 += kFinUnroll * 32) {
 #pragma unroll
             for (int u = 0; u < kFinUnroll; ++u) {
                 const int r = r0 + u * 32;
-                v[u] = *reinterpret_cast<const float4*>(src + (long)(r < R ? r : R - 1) * step);  // all in flight
+                v[u] = *reinterpret_cast<const float4*>(src + (long)(r < R ? r : R - 1) * step);
             }
 #pragma unroll
             for (int u = 0; u < kFinUnroll; ++u) {
@@ -862,18 +874,20 @@ __device__ __forceinline__ void finalize_cols_block(const FinalizeArgs& a, int j
         s2 += __shfl_xor(s2, off, 64);
         s3 += __shfl_xor(s3, off, 64);
     }
+    cnt = wave_sum(cnt);
     if ((tid & 63) < 8) {
         red[tid >> 6][q][0] = s0;
         red[tid >> 6][q][1] = s1;
         red[tid >> 6][q][2] = s2;
         red[tid >> 6][q][3] = s3;
     }
-    __syncthreads();  // red[] from every wave
+    if ((tid & 63) == 0) rcnt[tid >> 6] = cnt;
+    __syncthreads();  // red[] and rcnt[] from every wave
     if (tid >= 64) return;
     // wave 0: the count, then the new centres of the chunk's columns and
     // their shift^2 and ||c||^2 partials (fp64 sums over lanes 0..31 in a
     // fixed butterfly order; lanes 32..63 add zeros)
-    const int count = wave_sum(cnt);
+    const int count = (rcnt[0] + rcnt[1]) + (rcnt[2] + rcnt[3]);
     double sq = 0.0, nrm = 0.0;
     if (tid < 32 && ccol < a.d) {
         const int qq = tid >> 2, e = tid & 3;
@@ -910,10 +924,9 @@ __global__ __launch_bounds__(256) void k_finalize_cols(FinalizeArgs a)
 // chunk of sorted rows it touches): one wave per (cluster j, column chunk
 // cc), item 4 blockIdx.x + wave of k nch.  Lane (rs, q) = (lane / 8, lane %
 // 8) adds the float4 of columns 32 cc + 4q of records rs, rs + 8, .. in
-// fp64, and the eight rs lanes are combined by an xor butterfly: with at
-// most 8 records the same sums, in the same order, as finalize_cols_block
-// (whose other waves then add zeros).  A block per item made 98,304 blocks
-// at 4096 clusters of 768 floats, each waiting on one round trip.
+// fp64, and the eight rs lanes are combined by an xor butterfly.  A block
+// per item made 98,304 blocks at 4096 clusters of 768 floats, each waiting
+// on one round trip.
 __global__ __launch_bounds__(256) void k_finalize_recs(FinalizeArgs a, int nch)
 {
     const int lane = threadIdx.x & 63;
