@@ -377,15 +377,40 @@ hipError_t launch_update(const UpdateArgs& a, const UpdateGeom& g, hipStream_t s
 //                   offsets, and per-segment bases.
 // 4. k_label_offs   range offsets: start_j + rows of cluster j in earlier
 //                   ranges.
-// 5. k_label_scatter one wave per range: row ids and labels to their sorted
-//                   positions (ranges in order; inside a wave instruction the
-//                   LDS atomic hands out the positions).
+// 5. k_label_scatter_lds  a block of four waves per range (k_label_scatter,
+//                   one wave, when its LDS does not fit): row ids and labels
+//                   to their sorted positions (ranges in order, rows in order
+//                   inside a cluster; inside a wave instruction the LDS
+//                   atomic hands out the positions).
 // 6. k_segsum       a group of G threads sums one chunk of B sorted rows,
 //                   segment by segment (the rows of one cluster are
 //                   consecutive), gathering each X row once; a segment's sum
 //                   is the record (cluster, chunk).
 // The finalize then folds cluster j's records in chunk order.  X is read
 // once; labels a few times (4 bytes per row).
+
+// Exclusive prefix sum over a 256-thread block; *total gets the block's sum.
+// sh: 4 ints.  Ends with a barrier.
+__device__ int block_excl_scan(int v, int* sh, int* total)
+{
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    if (lane == 63) sh[w] = x;
+    __syncthreads();
+    int base = 0, tot = 0;
+    for (int i = 0; i < 4; ++i) {
+        base += i < w ? sh[i] : 0;
+        tot += sh[i];
+    }
+    __syncthreads();
+    *total = tot;
+    return base + x - v;
+}
 
 __global__ __launch_bounds__(64) void k_label_hist(SortArgs a, int wr)
 {
@@ -551,89 +576,137 @@ __global__ __launch_bounds__(64) void k_label_scatter(SortArgs a, int wr, int nw
 }
 
 // As k_label_scatter, with the range's output staged in LDS: the rows are
-// first placed in the range's own cluster order (an LDS counter per cluster
-// from the range's exclusive prefix of its cluster counts), then written
-// out in that order, so that each cluster's run of the range goes out in one
-// pass of consecutive stores instead of a few entries at a time over the
-// whole kernel (lines written in pieces and evicted in between: 7x the bytes
-// at 4M rows and 1024 clusters).  Dynamic LDS: off, lst, ctr (k ints each),
-// the staged row ids and labels (wr ints each).
-__global__ __launch_bounds__(64) void k_label_scatter_lds(SortArgs a, int wr, int nw)
+// first placed in the range's own cluster order, then written out in that
+// order, so that each cluster's run of the range goes out in one pass of
+// consecutive stores instead of a few entries at a time over the whole
+// kernel (lines written in pieces and evicted in between: 7x the bytes at
+// 4M rows and 1024 clusters).  A block of four waves per range, wave s
+// taking the s-th quarter of its rows: (1) each wave counts its quarter's
+// rows per cluster, (2) the range's staged layout -- cluster j's run starts
+// at lst[j], the exclusive prefix over j of its rows, and quarter s's rows
+// of j follow quarters 0 .. s-1's -- (3) each wave places its rows with an
+// LDS counter per (quarter, cluster): inside a wave instruction the LDS
+// atomic hands out positions in lane order, so every cluster's rows stay in
+// row order, the order a single wave over the range gives; (4) the staged
+// entries go to their sorted positions.  (One wave per range left a SIMD
+// with one wave at 4M rows: 41 us.)  Dynamic LDS: cnt (4 k ints, the counts
+// and then the counters), off and lst (k each), the staged row ids and
+// labels (wr each).
+__global__ __launch_bounds__(256) void k_label_scatter_lds(SortArgs a, int wr, int nw)
 {
     if (a.state->done != 0) return;
     const int w = scatter_range(nw);
     if (w < 0) return;
     extern __shared__ int sl[];
-    int* off = sl;           // [k] first sorted position of the range's rows of cluster j
-    int* lst = sl + a.k;     // [k] first staged position of those rows
-    int* ctr = sl + 2 * a.k; // [k] next staged position
-    int* sperm = sl + 3 * a.k;
-    int* slab = sperm + wr;
-    const int lane = threadIdx.x;
-    const int* o = a.hist + (long)w * a.k;
-    const int* on = a.hist + (long)(w + 1) * a.k;
-    // rows of cluster j in the range: the next range's offset minus this
-    // one's (the last range: the cluster's end); exclusive prefix over j, 64
-    // clusters at a time (lane order, then the running total)
-    int run = 0;
-    for (int j0 = 0; j0 < a.k; j0 += 64) {
-        const int j = j0 + lane;
-        int c = 0;
-        if (j < a.k) {
-            const int oj = o[j];
-            const int nj = w + 1 < nw ? on[j] : a.start[j] + a.counts[j];
-            off[j] = oj;
-            c = nj - oj;
-        }
-        int x = c;
-#pragma unroll
-        for (int s = 1; s < 64; s <<= 1) {
-            const int y = __shfl_up(x, s, 64);
-            if (lane >= s) x += y;
-        }
-        if (j < a.k) {
-            lst[j] = run + x - c;
-            ctr[j] = run + x - c;
-        }
-        run += __shfl(x, 63, 64);
-    }
-    __syncthreads();
+    const int k = a.k;
+    int* cnt = sl;            // [4][k] rows of cluster j in quarter s, then quarter s's next staged position
+    int* off = sl + 4 * k;    // [k] first sorted position of the range's rows of cluster j
+    int* lst = off + k;       // [k] first staged position of those rows
+    int* sperm = lst + k;     // [wr]
+    int* slab = sperm + wr;   // [wr]
+    __shared__ int shi[4];
+    const int tid = threadIdx.x, lane = tid & 63, s = tid >> 6;
     const long r0 = (long)w * wr;
     const int nr = (int)(min(a.n, r0 + wr) - r0);
-    // the labels 16 rows a lane at a time, all in flight before the first
-    // is used
+    const int qs = (nr + 3) / 4;  // rows per quarter
+    const int q0 = min(nr, s * qs), q1 = min(nr, q0 + qs);
+    for (int i = tid; i < 4 * k; i += 256) cnt[i] = 0;
+    // this thread's contiguous clusters for (2); the range's offsets are
+    // requested now
+    const int per = (k + 255) / 256;
+    const int j0 = min(k, tid * per), j1 = min(k, j0 + per);
+    const int* o = a.hist + (long)w * k;
+    for (int jb = 0; jb < k; jb += 1024) {
+        int v[4];
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+            const int j = jb + 256 * f + tid;
+            v[f] = j < k ? o[j] : 0;
+        }
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+            const int j = jb + 256 * f + tid;
+            if (j < k) off[j] = v[f];
+        }
+    }
+    __syncthreads();
+    // (1) the labels 16 rows a lane at a time, all in flight before the
+    // first is counted
     constexpr int U = 16;
-    for (int q0 = 0; q0 < nr; q0 += 64 * U) {
+    for (int qb = q0; qb < q1; qb += 64 * U) {
         int lv[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int q = q0 + 64 * u + lane;
-            lv[u] = q < nr ? a.labels[r0 + q] : 0;
+            const int q = qb + 64 * u + lane;
+            lv[u] = q < q1 ? a.labels[r0 + q] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (lv[u] >= 0) atomicAdd(&cnt[s * k + lv[u]], 1);
+    }
+    __syncthreads();
+    // (2) the staged layout
+    int mine = 0;
+    for (int j = j0; j < j1; ++j) mine += (cnt[j] + cnt[k + j]) + (cnt[2 * k + j] + cnt[3 * k + j]);
+    int tot;
+    int run = block_excl_scan(mine, shi, &tot);
+    for (int j = j0; j < j1; ++j) {
+        lst[j] = run;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int c = cnt[t * k + j];
+            cnt[t * k + j] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    // (3) the rows placed, quarter by quarter (labels read again: the L2)
+    for (int qb = q0; qb < q1; qb += 64 * U) {
+        int lv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int q = qb + 64 * u + lane;
+            lv[u] = q < q1 ? a.labels[r0 + q] : 0;
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int q = q0 + 64 * u + lane;
-            if (q < nr) {
-                const int p = atomicAdd(&ctr[lv[u]], 1);
+            const int q = qb + 64 * u + lane;
+            if (q < q1) {
+                const int p = atomicAdd(&cnt[s * k + lv[u]], 1);
                 sperm[p] = (int)(r0 + q);
                 slab[p] = lv[u];
             }
         }
     }
     __syncthreads();
-    for (int q = lane; q < nr; q += 64) {
-        const int l = slab[q];
-        const int p = off[l] + (q - lst[l]);
-        a.perm[p] = sperm[q];
-        a.slab[p] = l;
+    // (4) four entries a thread at a time: their LDS reads overlap
+    constexpr int F = 4;
+    for (int qb = 0; qb < nr; qb += 256 * F) {
+        int l[F], pr[F];
+#pragma unroll
+        for (int f = 0; f < F; ++f) {
+            const int q = min(qb + 256 * f + tid, nr - 1);
+            l[f] = slab[q];
+            pr[f] = sperm[q];
+        }
+#pragma unroll
+        for (int f = 0; f < F; ++f) {
+            const int q = qb + 256 * f + tid;
+            if (q < nr) {
+                const int p = off[l[f]] + (q - lst[l[f]]);
+                a.perm[p] = pr[f];
+                a.slab[p] = l[f];
+            }
+        }
     }
 }
 
 // LDS of k_label_scatter_lds (0: it does not fit; k_label_scatter then).
+constexpr size_t kScatterLdsMax = 150 * 1024;
 static size_t scatter_lds_bytes(int k, int wr)
 {
-    const size_t b = ((size_t)3 * k + (size_t)2 * wr) * sizeof(int);
-    return b <= 64 * 1024 ? b : 0;
+    const size_t b = ((size_t)6 * k + (size_t)2 * wr) * sizeof(int);
+    return b <= kScatterLdsMax ? b : 0;
 }
 
 // Columns per thread: CPT * G >= the tile's columns (<= 1024 per grid row).
@@ -721,7 +794,12 @@ SortGeom sort_geometry(long n, int d, int ld, int k)
     g.nseg = (g.nw + kSortSeg - 1) / kSortSeg;
     const int dcols = ld < 1024 ? ld : 1024;
     g.G = dcols <= 64 ? 64 : dcols <= 128 ? 128 : 256;
-    long B = (n + 2047) / 2048;
+    // chunks of B sorted rows (a multiple of 64), a group of G threads each:
+    // about 8192 waves in all, 32 per CU, so that enough row gathers are in
+    // flight (4M rows of 64 floats: 2,017 single-wave chunks summed at 4.9
+    // TB/s, 7,813 at 5.3)
+    const long wpc = g.G / 64;  // waves per chunk
+    long B = (n * wpc + 8191) / 8192;
     B = ((B + 63) / 64) * 64;
     if (B < 64) B = 64;
     g.B = (int)B;
@@ -741,10 +819,15 @@ hipError_t launch_sorted_update(const SortArgs& a, const SortGeom& g, hipStream_
     hipLaunchKernelGGL(k_label_scan, dim3(1), dim3(1024), 0, s, a, g.nseg, g.B);
     hipLaunchKernelGGL(k_label_offs, dim3(kb, g.nseg), dim3(256), 0, s, a, g.nw);
     const size_t slds = scatter_lds_bytes(a.k, g.wr);
-    if (slds > 0)
-        hipLaunchKernelGGL(k_label_scatter_lds, dim3(8 * ((g.nw + 7) / 8)), dim3(64), slds, s, a, g.wr, g.nw);
-    else
+    if (slds > 0) {
+        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(k_label_scatter_lds),
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                           (int)kScatterLdsMax);
+        if (attr != hipSuccess) return attr;
+        hipLaunchKernelGGL(k_label_scatter_lds, dim3(8 * ((g.nw + 7) / 8)), dim3(256), slds, s, a, g.wr, g.nw);
+    } else {
         hipLaunchKernelGGL(k_label_scatter, dim3(8 * ((g.nw + 7) / 8)), dim3(64), hlds, s, a, g.wr, g.nw);
+    }
     const int groups = 256 / g.G;
     const int dcols = a.d < 1024 ? a.d : 1024;
     const int cpt = (dcols + g.G - 1) / g.G;
@@ -1666,29 +1749,6 @@ hipError_t launch_relocate(const RelocArgs& a, int E, hipStream_t s)
 // cluster keeps what k_finalize_cols wrote.  state->reloc_iter = iter then
 // tells the loop decision that this step's empty clusters were handled.  No
 // block waits for another.
-
-// Exclusive prefix sum over a 256-thread block; *total gets the block's sum.
-// sh: 4 ints.  Ends with a barrier.
-__device__ int block_excl_scan(int v, int* sh, int* total)
-{
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    int x = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(x, off, 64);
-        if (lane >= off) x += y;
-    }
-    if (lane == 63) sh[w] = x;
-    __syncthreads();
-    int base = 0, tot = 0;
-    for (int i = 0; i < 4; ++i) {
-        base += i < w ? sh[i] : 0;
-        tot += sh[i];
-    }
-    __syncthreads();
-    *total = tot;
-    return base + x - v;
-}
 
 // The relocation of E (1..kMaxReloc) empty clusters by every block of the
 // grid (gridDim.x <= kRelocCandBlocks): phases A, B and C above.
