@@ -369,7 +369,7 @@ hipError_t launch_update(const UpdateArgs& a, const UpdateGeom& g, hipStream_t s
 // sorted update (generic path): counting sort by label + segmented sums
 // ---------------------------------------------------------------------------
 //
-// 1. k_label_hist   one wave per range of wr rows: LDS histogram of labels.
+// 1. k_label_hist   a block per range of wr rows: LDS histogram of labels.
 // 2. k_label_segs   column sums of the range histograms per segment of
 //                   kSortSeg ranges.
 // 3. k_label_scan   one block: per-cluster counts, exclusive scan over
@@ -412,36 +412,45 @@ __device__ int block_excl_scan(int v, int* sh, int* total)
     return base + x - v;
 }
 
-__global__ __launch_bounds__(64) void k_label_hist(SortArgs a, int wr)
+// The sort kernels read the halt flag beside their first loads and test it
+// once those are in flight (a test first put a memory round trip before
+// every kernel's work).
+__global__ __launch_bounds__(256) void k_label_hist(SortArgs a, int wr)
 {
-    if (a.state->done != 0) return;
+    const int done = a.state->done;
     extern __shared__ int h[];
-    for (int j = threadIdx.x; j < a.k; j += 64) h[j] = 0;
-    __syncthreads();
+    const int tid = threadIdx.x;
+    for (int j = tid; j < a.k; j += 256) h[j] = 0;
     const long r0 = (long)blockIdx.x * wr;
     const int nr = (int)(min(a.n, r0 + wr) - r0);
-    // the labels 16 rows a lane at a time, all in flight before the first
-    // is counted
+    // the labels 16 rows a thread at a time, all in flight before the
+    // first is counted (integer adds: any order gives the same counts)
     constexpr int U = 16;
-    for (int q0 = 0; q0 < nr; q0 += 64 * U) {
-        int lv[U];
+    int lv[U];
+    auto load = [&](int q0) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int q = q0 + 64 * u + (int)threadIdx.x;
+            const int q = q0 + 256 * u + tid;
             lv[u] = q < nr ? a.labels[r0 + q] : -1;
         }
+    };
+    load(0);
+    if (done != 0) return;
+    __syncthreads();  // h cleared
+    for (int q0 = 0; q0 < nr; q0 += 256 * U) {
+        if (q0 > 0) load(q0);
 #pragma unroll
         for (int u = 0; u < U; ++u)
             if (lv[u] >= 0) atomicAdd(&h[lv[u]], 1);
     }
     __syncthreads();
     int* out = a.hist + (long)blockIdx.x * a.k;
-    for (int j = threadIdx.x; j < a.k; j += 64) out[j] = h[j];
+    for (int j = tid; j < a.k; j += 256) out[j] = h[j];
 }
 
 __global__ __launch_bounds__(256) void k_label_segs(SortArgs a, int nw)
 {
-    if (a.state->done != 0) return;
+    const int done = a.state->done;
     const int j = blockIdx.x * 256 + threadIdx.x;
     if (j >= a.k) return;
     const int w0 = blockIdx.y * kSortSeg;
@@ -449,6 +458,7 @@ __global__ __launch_bounds__(256) void k_label_segs(SortArgs a, int nw)
     int v[kSortSeg];
 #pragma unroll
     for (int i = 0; i < kSortSeg; ++i) v[i] = a.hist[(long)min(w0 + i, w1 - 1) * a.k + j];  // all in flight
+    if (done != 0) return;
     int s = 0;
 #pragma unroll
     for (int i = 0; i < kSortSeg; ++i) s += w0 + i < w1 ? v[i] : 0;
@@ -485,18 +495,25 @@ __device__ int block_exclusive_scan(int v, int* sh)
 
 __global__ __launch_bounds__(1024) void k_label_scan(SortArgs a, int nseg, int B)
 {
-    if (a.state->done != 0) return;
+    const int done = a.state->done;
     __shared__ int sh[32];
+    __shared__ int sc[16384];  // cluster j's count, then its span of chunks (k <= 16384)
     const int tid = threadIdx.x;
     const int per = (a.k + 1023) / 1024;  // clusters per thread, contiguous
     const int j0 = tid * per;
     const int j1 = min(a.k, j0 + per);
-    // counts, and per-segment bases relative to the cluster's start
-    int tot = 0;
-    for (int j = j0; j < j1; ++j) {
-        int v[kSortSeg];
+    // counts, and per-segment bases relative to the cluster's start; the
+    // first cluster's loads go out before the halt flag is tested
+    int v[kSortSeg];
+    auto load = [&](int j) {
 #pragma unroll
         for (int s = 0; s < kSortSeg; ++s) v[s] = a.segsum[(long)min(s, nseg - 1) * a.k + j];  // all in flight
+    };
+    if (j0 < j1) load(j0);
+    if (done != 0) return;
+    int tot = 0;
+    for (int j = j0; j < j1; ++j) {
+        if (j > j0) load(j);
         int run = 0;
 #pragma unroll
         for (int s = 0; s < kSortSeg; ++s) {
@@ -506,28 +523,30 @@ __global__ __launch_bounds__(1024) void k_label_scan(SortArgs a, int nseg, int B
             }
         }
         a.counts[j] = run;
+        sc[j] = run;
         tot += run;
     }
     int pos = block_exclusive_scan(tot, sh);
     int spans = 0;
     for (int j = j0; j < j1; ++j) {
         a.start[j] = pos;
-        const int c = a.counts[j];
+        const int c = sc[j];
         const int span = c > 0 ? (pos + c - 1) / B - pos / B + 1 : 0;
         a.rec_cnt[j] = span;
+        sc[j] = span;
         spans += span;
         pos += c;
     }
     int rec = block_exclusive_scan(spans, sh);
     for (int j = j0; j < j1; ++j) {
         a.rec_off[j] = rec;
-        rec += a.rec_cnt[j];
+        rec += sc[j];
     }
 }
 
 __global__ __launch_bounds__(256) void k_label_offs(SortArgs a, int nw)
 {
-    if (a.state->done != 0) return;
+    const int done = a.state->done;
     const int j = blockIdx.x * 256 + threadIdx.x;
     if (j >= a.k) return;
     const int w0 = blockIdx.y * kSortSeg;
@@ -535,7 +554,9 @@ __global__ __launch_bounds__(256) void k_label_offs(SortArgs a, int nw)
     int v[kSortSeg];
 #pragma unroll
     for (int i = 0; i < kSortSeg; ++i) v[i] = a.hist[(long)min(w0 + i, w1 - 1) * a.k + j];  // all in flight
-    int run = a.start[j] + a.segsum[(long)blockIdx.y * a.k + j];
+    const int st = a.start[j], sb = a.segsum[(long)blockIdx.y * a.k + j];
+    if (done != 0) return;
+    int run = st + sb;
 #pragma unroll
     for (int i = 0; i < kSortSeg; ++i) {
         if (w0 + i < w1) a.hist[(long)(w0 + i) * a.k + j] = run;
@@ -594,7 +615,7 @@ __global__ __launch_bounds__(64) void k_label_scatter(SortArgs a, int wr, int nw
 // labels (wr each).
 __global__ __launch_bounds__(256) void k_label_scatter_lds(SortArgs a, int wr, int nw)
 {
-    if (a.state->done != 0) return;
+    const int done = a.state->done;
     const int w = scatter_range(nw);
     if (w < 0) return;
     extern __shared__ int sl[];
@@ -629,6 +650,7 @@ __global__ __launch_bounds__(256) void k_label_scatter_lds(SortArgs a, int wr, i
             if (j < k) off[j] = v[f];
         }
     }
+    if (done != 0) return;
     __syncthreads();
     // (1) the labels 16 rows a lane at a time, all in flight before the
     // first is counted
@@ -713,7 +735,7 @@ static size_t scatter_lds_bytes(int k, int wr)
 template <int CPT>
 __global__ __launch_bounds__(256) void k_segsum(SortArgs a, int B, int G)
 {
-    if (a.state->done != 0) return;
+    const int done = a.state->done;
     constexpr int U = 64 / CPT;  // sorted rows per batch: 64 loads in flight per thread
     const int groups = 256 / G;  // G >= 64: a wave lies in one group
     const int grp = threadIdx.x / G;
@@ -754,6 +776,7 @@ __global__ __launch_bounds__(256) void k_segsum(SortArgs a, int B, int G)
         ridv = a.perm[q];
     };
     load_ids(p0);
+    if (done != 0) return;
     for (long p = p0; p < p1; p += U) {
         float v[U][CPT];
 #pragma unroll
@@ -814,7 +837,7 @@ hipError_t launch_sorted_update(const SortArgs& a, const SortGeom& g, hipStream_
     if (!g.on) return hipErrorInvalidValue;
     const size_t hlds = (size_t)a.k * sizeof(int);
     const unsigned kb = (unsigned)((a.k + 255) / 256);
-    hipLaunchKernelGGL(k_label_hist, dim3(g.nw), dim3(64), hlds, s, a, g.wr);
+    hipLaunchKernelGGL(k_label_hist, dim3(g.nw), dim3(256), hlds, s, a, g.wr);
     hipLaunchKernelGGL(k_label_segs, dim3(kb, g.nseg), dim3(256), 0, s, a, g.nw);
     hipLaunchKernelGGL(k_label_scan, dim3(1), dim3(1024), 0, s, a, g.nseg, g.B);
     hipLaunchKernelGGL(k_label_offs, dim3(kb, g.nseg), dim3(256), 0, s, a, g.nw);
@@ -1016,7 +1039,7 @@ __global__ __launch_bounds__(256) void k_finalize_recs(FinalizeArgs a, int nch)
     const long item = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (item >= (long)a.k * nch) return;
     const int j = (int)(item / nch), cc = (int)(item - (long)j * nch);
-    if (a.state->done != 0) return;
+    const int done = a.state->done;
     const int q = lane & 7, rs = lane >> 3;
     const int c4 = cc * 32 + 4 * q;
     const int ccol = cc * 32 + lane;  // lanes 0..31: one column each
@@ -1024,6 +1047,7 @@ __global__ __launch_bounds__(256) void k_finalize_recs(FinalizeArgs a, int nch)
     const int R = a.rec_cnt[j];
     const int count = a.cnt_in[j];
     const float* src = a.psum + (long)a.rec_off[j] * a.ld + c4;
+    if (done != 0) return;  // tested once the loads above are in flight
     double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
     if (c4 < a.ld) {  // ld is a multiple of 4: the float4 is in or out
         for (int r = rs; r < R; r += 8) {
