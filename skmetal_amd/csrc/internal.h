@@ -104,6 +104,9 @@ struct FusedArgs {
     // split = 1: k_fused3 (E-step and sums on bf16 MFMAs over the exact
     // three-part split); see fused3_ready
     int split = 0;
+    // k_fused3, nullable: each row's minimum ||c||^2 - 2 x.c (the distance to
+    // its new centre less ||x||^2), for the relocation's candidate search
+    float* emin = nullptr;
 };
 // Row stride (floats) X must have for the fused kernel, or 0 when (d, k) does
 // not qualify; the pad columns are zero.
@@ -247,6 +250,12 @@ struct InRelocArgs {
     long* cand_i;          // [kRelocInlineBlocks x kMaxReloc]
     int* amax;             // [1]
     LoopState* state; int iter;
+    // nullable (both or neither): ||x||^2 per row and the E-step's row
+    // minima (FusedArgs::emin) of these labels; with them the blocks compute
+    // direct-form distances only for rows whose approximate distance
+    // xnorm + emin lies near the top (k_finalize_reloc, rows <= 104 floats)
+    const float* xnorm = nullptr;
+    const float* emin = nullptr;
 };
 constexpr int kRelocInlineBlocks = 256;  // grid of k_reloc / k_finalize_reloc (one block per CU: their LDS)
 constexpr int kRelocLdsRows = 4096;      // a block's row distances kept in LDS (more rows: InRelocArgs::dist)
@@ -339,6 +348,8 @@ hipError_t launch_colmean(const double* part, int nblk, long n, int d, float* me
 hipError_t launch_center(float* X, long n, int ld, int d, const float* mean, hipStream_t s);
 // max |x| over count floats (NaN as +inf) into *out as float bits
 hipError_t launch_absmax(const float* X, long count, unsigned* out, hipStream_t s);
+// out[r] = ||x_r||^2 (fp32) of the n rows of stride ld (d features)
+hipError_t launch_rownorm(const float* X, long n, int ld, int d, float* out, hipStream_t s);
 hipError_t launch_cnorm(const float* C, int k, int ld, float* cnorm, hipStream_t s);
 
 }  // namespace skm

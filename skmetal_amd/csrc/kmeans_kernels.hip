@@ -1774,6 +1774,56 @@ hipError_t launch_relocate(const RelocArgs& a, int E, hipStream_t s)
 // tells the loop decision that this step's empty clusters were handled.  No
 // block waits for another.
 
+// ||x - c||^2 of one row in fp32 with rows_dist_ctg's operations in its
+// order (whole float4 groups, then the last d % 4 features one by one), so
+// that a row gets the same value either way.
+template <int LDM>
+struct RowRegs {
+    f4v v[LDM / 4];
+};
+template <int LDM>
+__device__ __forceinline__ void load_row(RowRegs<LDM>& xv, const float* __restrict__ x, int d)
+{
+    const f4v* x4 = reinterpret_cast<const f4v*>(x);
+#pragma unroll
+    for (int g = 0; g < LDM / 4; ++g)
+        if (4 * g < d) xv.v[g] = x4[g];  // all in flight
+}
+template <int LDM>
+__device__ __forceinline__ float direct_dist(const RowRegs<LDM>& xr, const float* c, int d)
+{
+#pragma clang fp contract(off)
+    constexpr int NG = LDM / 4;
+    const f4v* c4 = reinterpret_cast<const f4v*>(c);
+    const f4v* xv = xr.v;
+    float res = 0.f;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        if (4 * g >= d) break;
+        const f4v cv = c4[g];
+        if (4 * g + 4 <= d) {
+            const float t0 = xv[g].x - cv.x, t1 = xv[g].y - cv.y;
+            const float t2 = xv[g].z - cv.z, t3 = xv[g].w - cv.w;
+            res += ((t0 * t0 + t1 * t1) + t2 * t2) + t3 * t3;
+        } else {
+            const int m = d - 4 * g;
+            float tt = xv[g].x - cv.x;
+            res += tt * tt;
+            if (m > 1) {
+                tt = xv[g].y - cv.y;
+                res += tt * tt;
+            }
+            if (m > 2) {
+                tt = xv[g].z - cv.z;
+                res += tt * tt;
+            }
+        }
+    }
+    return res;
+}
+
+constexpr int kRelocCand = 256;  // candidate rows per block, at most (one per thread)
+
 // The relocation of E (1..kMaxReloc) empty clusters by every block of the
 // grid (gridDim.x <= kRelocCandBlocks): phases A, B and C above.
 template <int LDM, bool CL>
@@ -1810,17 +1860,125 @@ __device__ __forceinline__ void reloc_body(const InRelocArgs& a, int E)
             __syncthreads();
         }
     };
-    reloc_rows_dist<LDM, CL>(a.X, a.ld, a.d, a.C_old, sC, a.labels, a.k, r0, r1, dist, dbase, tiles + w * RG::TF,
-                             copy_centres);
-    __threadfence_block();
-    __syncthreads();
+    // (A') With the E-step's row minima: the approximate distance xnorm[r]
+    // + emin[r] (= ||x||^2 + ||c||^2 - 2 x.c, c the row's centre) of every
+    // row, the block's E-th largest of them, T, and as candidates the rows
+    // within 2M of T, M = 2^-10 (max ||x||^2 + max ||c||^2): the
+    // approximation and the direct form each lie within 2^-13 of that sum of
+    // the true distance (fp32 norms and products, the split's dropped terms
+    // and the direct form's rounding), so every row of the block's E
+    // farthest by direct-form distance is a candidate.  Only the candidates
+    // get that distance, and the selection runs over them: the same rows as
+    // (A), for 8 bytes a row instead of the row.  More than kRelocCand
+    // candidates (wide ties at the top), or a bound that is not finite: (A).
+    bool exact = true;  // block-uniform
+    int ncand = 0;
+    long* const ccl = reinterpret_cast<long*>(tiles);  // (the tiles are free until (A))
+    float* const ccd = tiles + 2 * kRelocCand;
+    if constexpr (LDM != 0) {
+        if (a.emin != nullptr && a.xnorm != nullptr && in_lds && a.k <= 64) {
+            const int nr = (int)(r1 - r0);
+            float xm = 0.f;
+            constexpr int U = 8;
+            float xv[U], ev[U];
+            auto load = [&](int q0) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int q = q0 + 256 * u + tid;
+                    xv[u] = q < nr ? a.xnorm[r0 + q] : 0.f;
+                    ev[u] = q < nr ? a.emin[r0 + q] : 0.f;
+                }
+            };
+            auto put = [&](int q0) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int q = q0 + 256 * u + tid;
+                    if (q < nr) {
+                        sdist[q] = xv[u] + ev[u];
+                        xm = fmaxf(xm, xv[u]);
+                    }
+                }
+            };
+            // the first rows' values and the centres in one round trip
+            load(0);
+            copy_centres();
+            put(0);
+            for (int q0 = 256 * U; q0 < nr; q0 += 256 * U) {
+                load(q0);
+                put(q0);
+            }
+            // the largest ||c||^2 (k <= 64): four threads a centre, a
+            // quarter of its float4s each
+            float cm = 0.f;
+            {
+                const int j = tid >> 2, qq = tid & 3;
+                const int g4 = a.ld >> 2;  // float4s a row (its pad is zero)
+                float s2 = 0.f;
+                if (j < a.k) {
+                    const f4v* cr = reinterpret_cast<const f4v*>(CL ? sC + j * ctg_stride(a.ld) : a.C_old + (long)j * a.ld);
+                    for (int g = qq; g < g4; g += 4) {
+                        const f4v v = cr[g];
+                        s2 = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, s2))));
+                    }
+                }
+                s2 += __shfl_xor(s2, 1, 64);
+                s2 += __shfl_xor(s2, 2, 64);
+                cm = s2;
+            }
+            __syncthreads();  // sdist from every thread
+            const float M = 0x1p-10f * (block_max(xm, sd) + block_max(cm, sd));
+            float dl = INFINITY;
+            long il = -1;
+            for (int e = 0; e < E; ++e) {
+                float bd = 0.f;
+                long bi = -1;
+                for (int q = tid; q < nr; q += 256) far_pick(bd, bi, sdist[q], r0 + q, dl, il);
+                far_block_reduce(bd, bi, sd, si);
+                dl = bd;
+                il = bi;
+            }
+            const float thr = il < 0 ? -INFINITY : dl - 2.f * M;  // fewer than E rows: all
+            int mine = 0;
+            for (int q = tid; q < nr; q += 256) mine += sdist[q] >= thr;
+            int tot;
+            int pos = block_excl_scan(mine, shi, &tot);
+            if (M < INFINITY && tot <= kRelocCand) {
+                for (int q = tid; q < nr; q += 256)
+                    if (sdist[q] >= thr) ccl[pos++] = r0 + q;
+                __syncthreads();
+                if (tid < tot) {
+                    const long r = ccl[tid];
+                    RowRegs<LDM == 0 ? 4 : LDM> xr;
+                    load_row(xr, a.X + r * a.ld, a.d);  // the row and its label: one round trip
+                    const int lab = a.labels[r];
+                    const bool ok = lab >= 0 && lab < a.k;
+                    const float* cr = CL ? sC + (ok ? lab : 0) * ctg_stride(a.ld) : a.C_old + (long)(ok ? lab : 0) * a.ld;
+                    const float dd = direct_dist(xr, cr, a.d);
+                    ccd[tid] = ok ? dd : 0.f;
+                }
+                __syncthreads();
+                exact = false;
+                ncand = tot;
+            }
+        }
+    }
+    if (exact) {
+        reloc_rows_dist<LDM, CL>(a.X, a.ld, a.d, a.C_old, sC, a.labels, a.k, r0, r1, dist, dbase,
+                                 tiles + w * RG::TF, copy_centres);
+        __threadfence_block();
+        __syncthreads();
+    }
     {
         float dl = INFINITY;
         long il = -1;
         for (int e = 0; e < E; ++e) {
             float bd = 0.f;
             long bi = -1;
-            for (long r = r0 + tid; r < r1; r += 256) far_pick(bd, bi, dist[r - dbase], r, dl, il);
+            if (exact) {
+                for (long r = r0 + tid; r < r1; r += 256) far_pick(bd, bi, dist[r - dbase], r, dl, il);
+            } else if (tid < ncand) {
+                far_pick(bd, bi, ccd[tid], ccl[tid], dl, il);
+            }
             far_block_reduce(bd, bi, sd, si);
             if (tid == 0) {
                 a.cand_d[(long)blockIdx.x * kMaxReloc + e] = bd;
@@ -1830,17 +1988,26 @@ __device__ __forceinline__ void reloc_body(const InRelocArgs& a, int E)
             il = bi;
         }
     }
-    // the last block to get here takes (B) and (C).  Every thread's stores
-    // (the candidates, and in k_finalize_reloc the finalize chunk's sums,
-    // counts, centres and partials, written by several waves) are made
-    // visible to the device before the block takes its ticket.
-    __threadfence();
+    // the last block to get here takes (B) and (C).  The block's stores (the
+    // candidates, and in k_finalize_reloc the finalize chunk's sums, counts,
+    // centres and partials, written by several waves) are done once its
+    // waves pass the barrier; thread 0's ticket is an agent-scope release
+    // RMW (the L2's dirty lines written back first), and the last block's
+    // thread 0 acquires after it, before the barrier its other waves wait
+    // at.  One write-back per block and one invalidation in all: a
+    // __threadfence in every wave (write-back and L2 invalidation each) cost
+    // 14.6 us of the relocating step at 500000 rows.
     __syncthreads();
-    if (tid == 0) last_s = atomicAdd(&st->reloc_ctr, 1u) == gridDim.x - 1;
+    if (tid == 0)
+        last_s = __hip_atomic_fetch_add(&st->reloc_ctr, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) ==
+                 gridDim.x - 1;
     __syncthreads();
     if (!last_s) return;
-    if (tid == 0) st->reloc_ctr = 0u;
-    __threadfence();  // every block's candidates
+    if (tid == 0) {
+        st->reloc_ctr = 0u;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // every block's stores
+    }
+    __syncthreads();
 
     // each thread's contiguous share of the clusters
     const int per = (a.k + 255) / 256;
@@ -2230,6 +2397,34 @@ hipError_t launch_absmax(const float* X, long count, unsigned* out, hipStream_t 
     if (blocks > 1024) blocks = 1024;
     if (blocks < 1) blocks = 1;
     hipLaunchKernelGGL(k_absmax, dim3((unsigned)blocks), dim3(256), 0, s, X, count, out);
+    return hipGetLastError();
+}
+
+// ||x_r||^2 in fp32, one thread per row (the relocation's approximate
+// distances; their candidate margin covers its rounding).
+__global__ __launch_bounds__(256) void k_rownorm(const float* __restrict__ X, long n, int ld, int d,
+                                                 float* __restrict__ out)
+{
+    const long r = (long)blockIdx.x * 256 + threadIdx.x;
+    if (r >= n) return;
+    const float4* x4 = reinterpret_cast<const float4*>(X + r * ld);
+    float s = 0.f;
+    const int nfull = d >> 2;
+    for (int g = 0; g < nfull; ++g) {
+        const float4 v = x4[g];
+        s = fmaf(v.x, v.x, s);
+        s = fmaf(v.y, v.y, s);
+        s = fmaf(v.z, v.z, s);
+        s = fmaf(v.w, v.w, s);
+    }
+    for (int c = 4 * nfull; c < d; ++c) s = fmaf(X[r * ld + c], X[r * ld + c], s);
+    out[r] = s;
+}
+
+hipError_t launch_rownorm(const float* X, long n, int ld, int d, float* out, hipStream_t s)
+{
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rownorm, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, X, n, ld, d, out);
     return hipGetLastError();
 }
 

@@ -364,6 +364,10 @@ struct Lloyd {
     float* shift_sq = nullptr;
     double* rowpart = nullptr;
     float* rowout = nullptr;
+    // split fused path with in-stream relocation: ||x||^2 per row (set at
+    // load) and k_fused3's row minima, for the relocation's candidate search
+    float* xnorm = nullptr;
+    float* emin = nullptr;
     double* colpart = nullptr;
     LoopState* st = nullptr;
     UpdateGeom ug{};
@@ -504,6 +508,10 @@ struct Lloyd {
             TRY(grab((void**)&r_cand_d, size_t(kRelocCandBlocks) * kMaxReloc * sizeof(float)));
             TRY(grab((void**)&r_cand_i, size_t(kRelocCandBlocks) * kMaxReloc * sizeof(long)));
             TRY(grab((void**)&r_amax, sizeof(int)));
+            if (f3cap) {
+                TRY(grab((void**)&xnorm, size_t(n) * sizeof(float)));
+                TRY(grab((void**)&emin, size_t(n) * sizeof(float)));
+            }
         }
         if (sg.on) {
             TRY(grab((void**)&s_hist, size_t(sg.nw) * k * sizeof(int)));
@@ -565,6 +573,7 @@ struct Lloyd {
             TRY(measure_xmax());
             split_on = split_range_ok(xmax);
         }
+        if (xnorm != nullptr) HIP_TRY(launch_rownorm(X, n, ld, d, xnorm, s), "rownorm launch");
         return 0;
     }
 
@@ -674,6 +683,7 @@ struct Lloyd {
                     decide ? 1 : 0, iter, tol, flags, part, finalize_col_chunks(d, fblocks), counts,
                     &st->chg[(iter + 1) & 1], cnorm, shift_sq};
         a.split = split_on && f3cap ? 1 : 0;
+        if (a.split) a.emin = emin;
         HIP_TRY(launch_fused(a, s), "fused launch");
         return 0;
     }
@@ -708,8 +718,13 @@ struct Lloyd {
         }
         if (ev) HIP_TRY(hipEventRecord(ev[2], s), "hipEventRecord");
         const FinalizeArgs f = finalize_args(iter, tol, flags);
-        const InRelocArgs r{X, n, ld, d, k, labels, cen[cur], cen[cur ^ 1], sums, counts, part,
-                            finalize_col_chunks(d, f.R), rowout, r_cand_d, r_cand_i, r_amax, st, iter};
+        InRelocArgs r{X, n, ld, d, k, labels, cen[cur], cen[cur ^ 1], sums, counts, part,
+                      finalize_col_chunks(d, f.R), rowout, r_cand_d, r_cand_i, r_amax, st, iter};
+        if (fblocks > 0 && split_on && f3cap && emin != nullptr) {
+            // this step's E-step was k_fused3, which wrote its row minima
+            r.xnorm = xnorm;
+            r.emin = emin;
+        }
         if (reloc_inline && fblocks > 0 && k <= 64 && 8 * ((k * r.nch + 7) / 8) <= kRelocInlineBlocks) {
             // the fused kernel's presence bits name the empty clusters: one launch
             HIP_TRY(launch_finalize_reloc(f, r, s), "finalize launch");

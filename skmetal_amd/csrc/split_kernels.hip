@@ -473,6 +473,11 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
             argmin_swap<32>(bd, bi);
             // lanes 0..15: row = lane
             __builtin_amdgcn_raw_buffer_store_b32(bi, rl, lane * 4, 0, 0);
+            if (a.emin != nullptr) {
+                const __amdgpu_buffer_rsrc_t re = __builtin_amdgcn_make_buffer_rsrc(
+                    a.emin + t * 32 + 16 * hf, (short)0, (int)(nrow > 0 ? nrow * 4 : 0), 0x00020000);
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(bd), re, lane * 4, 0, 0);
+            }
             changed += (int)__popcll(__ballot(valid && old != bi));
             // this half tile's rows per cluster: the words of round r - 2, read
             // by both sums waves before they read any block of round r - 1
