@@ -328,9 +328,10 @@ def main():
         "dist_evals_per_s": round(n * k * it_s, 1),
         "wall_s_timed": round(wall, 4),
         "h2d_s": round(h2d_s, 4),
-        "step_mode": (f"fused: {kname} (E-step + per-cluster sums) + k_finalize_cols + k_reloc (in-stream "
-                      "empty-cluster relocation; returns at once when no cluster is empty)" if fused
-                      else f"{kname} + sorted update + k_finalize_cols + k_reloc"),
+        "step_mode": (f"fused: {kname} (E-step + per-cluster sums) + k_finalize_reloc (finalize and in-stream "
+                      "empty-cluster relocation in one launch; the relocation returns at once when no cluster "
+                      "is empty)" if fused
+                      else f"{kname} + sorted update + k_finalize_recs + k_reloc + k_finalize_loop"),
         "e_step": ("fp32-equivalent: exact three-part bf16 split of x and c (x = hi + mid + lo), 6 of 9 part "
                    "products on v_mfma_f32_16x16x32_bf16, fp32 accumulation; the 3 left out total <= 2^-23 |x_i c_i|"
                    if (split or (asplit and not fused)) else "fp32 MFMA (v_mfma_f32_4x4x1_16b_f32)"),
@@ -341,9 +342,9 @@ def main():
                            "ms_per_step": round(ms32 / args.steps, 5),
                            "kernel": "k_fused" if fp32_mode["fused"] else "k_assign"},
         "partials": mode["partials"],
-        "kernels_ms": ({kname: round(ms_assign, 5), "k_finalize_cols+k_reloc": round(ms_final, 5)} if fused
+        "kernels_ms": ({kname: round(ms_assign, 5), "k_finalize_reloc": round(ms_final, 5)} if fused
                        else {kname: round(ms_assign, 5), "update": round(ms_update, 5),
-                             "k_finalize_cols+k_reloc": round(ms_final, 5)}),
+                             "finalize": round(ms_final, 5)}),
         "roofline": roofline,
         "kmeans_plusplus_ms": pp_ms,
         "kmeans_parallel_init_ms": kpar_ms,
