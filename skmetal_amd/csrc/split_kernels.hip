@@ -633,7 +633,32 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
         }
         (&sMask[0][0][0])[wt] = 0u;
         (&sMask[0][0][0])[512 + wt] = 0u;
-        if (wave == 8) step_norms_apply<CPC>(a, lane, sni, sN, &sDone);
+        if (wave == 8) {
+            step_norms_apply<CPC>(a, lane, sni, sN, &sDone);
+            if constexpr (STK) {
+                // The stacked block's distances take all nine part products,
+                // the full blocks' six: an exact copy of an earlier centre
+                // would not tie with it, and could take rows that scikit-learn
+                // gives the lower index (the copy then never gets one).  A
+                // stacked centre equal to an earlier one, feature for feature,
+                // gets +inf here (its norm equal first: one compare a lane).
+                const int s0 = 16 * (CB - 1);
+                for (int s = 0; s < 4 && s0 + s < k; ++s) {
+                    const float ns = sN[s0 + s];
+                    unsigned long long m = __ballot(lane < s0 && sN[lane] == ns);
+                    while (m != 0ull) {
+                        const int j = __ffsll((long long)m) - 1;
+                        m &= m - 1ull;
+                        bool same = true;
+                        for (int f = lane; f < ld; f += 64) same = same && C[(long)j * ld + f] == C[(long)(s0 + s) * ld + f];
+                        if (__ballot(!same) == 0ull) {
+                            if (lane == 0) sN[s0 + s] = INFINITY;
+                            break;
+                        }
+                    }
+                }
+            }
+        }
         __syncthreads();
         if (sDone != 0) return;
         // sums wave 8 + w: SIMD m = w & 3, feature blocks [0, NFA) (w < 4) or

@@ -245,16 +245,18 @@ def test_split_assign_duplicate_centres_lowest_index(bridge):
     parity.check_labels(out, ref, best, second, X, what="split duplicate centres")
 
 
-@pytest.mark.parametrize("d,reps", [(100, 3), (40, 2), (64, 4)])
-def test_split_fused_duplicate_centres_lowest_index(bridge, d, reps):
-    """Every row is an exact tie between copies of its centre, so every
-    16-row group takes the E-step's second pass: the lowest index must win,
-    exactly as scikit-learn's strict '<' scan picks it."""
-    rng = np.random.default_rng(d + reps)
+@pytest.mark.parametrize("d,reps,extra", [(100, 3, 0), (40, 2, 0), (64, 4, 0), (100, 1, 2), (64, 2, 3), (40, 3, 4)])
+def test_split_fused_duplicate_centres_lowest_index(bridge, d, reps, extra):
+    """Every row is an exact tie between copies of its centre: the lowest
+    index must win, exactly as scikit-learn's strict '<' scan picks it.  With
+    extra > 0 the last 16-centre block holds at most four centres (the stacked
+    block, whose distances take all nine part products) and they are copies
+    of earlier ones."""
+    rng = np.random.default_rng(d + reps + 10 * extra)
     n = 9000
     base = rng.uniform(-5, 5, (16, d)).astype(np.float32)
     X = (base[rng.integers(0, 16, n)] + rng.standard_normal((n, d))).astype(np.float32)
-    C = np.concatenate([base] * reps)[:64]
+    C = np.concatenate([base] * reps + [base[:extra]])[:64]
     k = C.shape[0]
     mean = X.mean(axis=0)
     with bridge.LloydHandle(n, d, k) as h:
@@ -518,6 +520,39 @@ def test_relocation_wide_rows(bridge, d, monkeypatch):
         assert res["in-stream"][0] == res[where][0]
         parity.check_centers(res["in-stream"][2], res[where][2], rtol=1e-5,
                              what=f"in-stream vs {where} relocation d={d}, 3 steps")
+
+
+@pytest.mark.parametrize("n,tied,step", [(20000, 5, 1e-2), (150000, 600, 4e-3)])
+def test_relocation_candidates_near_the_top(bridge, n, tied, step):
+    """On the fused split path the relocated rows are searched among the
+    E-step's approximate distances (||x||^2 + the row's minimum of ||c||^2 -
+    2 x.c), with direct-form distances only for the rows within a margin of
+    each block's top.  A group of far rows whose distances differ by far less
+    than that margin (one coordinate stepped by `step`) must still move in the
+    oracle's order.  With 600 of them in consecutive rows, a block holds more
+    candidates than its list and falls back to every row's direct form."""
+    rng = np.random.default_rng(n)
+    d, kb, E = 64, 16, 3
+    cen = rng.uniform(-6, 6, (8, d))
+    X = (cen[rng.integers(0, 8, n)] + rng.standard_normal((n, d))).astype(np.float32)
+    rows = np.arange(1000, 1000 + tied) if tied > 256 else np.sort(rng.choice(n, tied, replace=False))
+    far = np.repeat((cen[0] + 40.0)[None, :], tied, axis=0)
+    far[:, 0] += step * rng.permutation(tied)  # distinct distances, in no row order
+    X[rows] = far.astype(np.float32)
+    others = np.setdiff1d(np.arange(n), rows)
+    base = X[np.sort(rng.choice(others, kb, replace=False))]
+    C0 = np.concatenate([base, base[:E]])  # the copies come later: E empty clusters
+    assert _split_engaged(bridge, X, C0)["split"]
+    _say(f"relocation near the top n={n} far rows={tied}")
+    out = oracle.lloyd(X, C0, 1)
+    C = C0.copy()
+    lab = np.empty(n, np.int32)
+    n_iter, _ = bridge.kmeans_fit(X, C, lab, 1, 0.0, strict=True)
+    assert n_iter == out["n_iter"]
+    parity.check_centers(C, out["centers"], what=f"relocation near the top n={n}")
+    # the relocated centres are the rows the oracle moved: the stepped
+    # coordinate tells them apart
+    np.testing.assert_allclose(C[kb:kb + E, 0], out["centers"][kb:kb + E, 0], rtol=0, atol=step / 8)
 
 
 @pytest.mark.parametrize("wl,steps", [("c1", 4), ("c2", 3)])
