@@ -279,12 +279,19 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
     char* const tiles = reinterpret_cast<char*>(lds);
     v8bf* const sFr = reinterpret_cast<v8bf*>(tiles + 4 * TILEB);
 
-    // 32-row tiles: SIMD m of block b handles t = 4b + m + r*P
-    const long ntiles = (n + 31) >> 5;
+    // 32-row tiles: SIMD slot t0 = 4b + m (of P = 4 x blocks) takes tile t0
+    // + r P in each of the Rf rounds in which every slot has a whole tile;
+    // the rem rows after them go out in 16-row halves, half h to slot h % P
+    // as its half h / P, so that the last round is at most one half tile for
+    // every slot when rem <= 16 P (500,000 rows on 1,024 slots: 530 halves
+    // instead of 265 whole tiles, and the last round costs one E-step wave
+    // instead of two)
     const long P = (long)gridDim.x * 4;
+    const long Rf = n / (32 * P);
+    const long rem = n - Rf * P * 32;
     auto rounds_of = [&](int m) {
         const long t0 = (long)blockIdx.x * 4 + m;
-        return t0 < ntiles ? (int)((ntiles - t0 + P - 1) / P) : 0;
+        return (int)Rf + (16 * t0 < rem ? 1 : 0);
     };
 
     if (wave < 8) {
@@ -297,9 +304,14 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
         const long t0 = (long)blockIdx.x * 4 + m;
         const int rounds = rounds_of(m);
         float4 xr[QG];
-        auto rsrc16 = [&](long t) {
-            const long r0 = t * 32 + 16 * hf;
-            const long rows = n - r0 < 16 ? (n - r0 > 0 ? n - r0 : 0) : 16;
+        // the first row of this wave's half in round r
+        auto rowbase = [&](int r) -> long {
+            return r < Rf ? (t0 + (long)r * P) * 32 + 16 * hf : Rf * P * 32 + 16 * (t0 + (long)hf * P);
+        };
+        auto rows_at = [&](long r0) { return n - r0 < 16 ? (n - r0 > 0 ? n - r0 : 0) : 16; };
+        auto rsrc16 = [&](int r) {
+            const long r0 = rowbase(r);
+            const long rows = r < rounds ? rows_at(r0) : 0;
             return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(X + (rows > 0 ? r0 * ld : 0)), (short)0,
                                                      (int)(rows * ld * 4), 0x00020000);
         };
@@ -321,7 +333,7 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
         {
             // in the order of the reloads in the rounds below (the waits at
             // the top of a step then count the same loads either way)
-            const __amdgpu_buffer_rsrc_t r0 = rsrc16(t0);
+            const __amdgpu_buffer_rsrc_t r0 = rsrc16(0);
 #pragma unroll
             for (int s = 0; s < NS; ++s) {
                 load_step(r0, s);
@@ -343,14 +355,17 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
         const unsigned mh0 = h == 0 ? ~0u : 0u, mh1 = h == 1 ? ~0u : 0u, mh2 = h == 2 ? ~0u : 0u;
         const unsigned mlt2 = h < 2 ? ~0u : 0u, mge2 = ~mlt2;
         int changed = 0;
-        for (int r = 0; r < rounds; ++r) {
-            const long t = t0 + (long)r * P;
-            const long nrow = n - t * 32 - 16 * hf < 16 ? n - t * 32 - 16 * hf : 16;
+        // only the last round's half can lie past the rows: this wave then
+        // skips it (below) instead of computing on zeros
+        const int rounds_e = rounds > 0 && rows_at(rowbase(rounds - 1)) <= 0 ? rounds - 1 : rounds;
+        for (int r = 0; r < rounds_e; ++r) {
+            const long rb = rowbase(r);
+            const long nrow = rows_at(rb);
             const bool valid = lane < nrow;
             const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(
-                labels + t * 32 + 16 * hf, (short)0, (int)(nrow > 0 ? nrow * 4 : 0), 0x00020000);
+                labels + rb, (short)0, (int)(nrow > 0 ? nrow * 4 : 0), 0x00020000);
             const int old = __builtin_amdgcn_raw_buffer_load_b32(rl, lane * 4, 0, 0);
-            const __amdgpu_buffer_rsrc_t rn = rsrc16(t + P);
+            const __amdgpu_buffer_rsrc_t rn = rsrc16(r + 1);
             v4f acc[CB];
 #pragma unroll
             for (int cb = 0; cb < CB; ++cb) acc[cb] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -475,7 +490,7 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
             __builtin_amdgcn_raw_buffer_store_b32(bi, rl, lane * 4, 0, 0);
             if (a.emin != nullptr) {
                 const __amdgpu_buffer_rsrc_t re = __builtin_amdgcn_make_buffer_rsrc(
-                    a.emin + t * 32 + 16 * hf, (short)0, (int)(nrow > 0 ? nrow * 4 : 0), 0x00020000);
+                    a.emin + rb, (short)0, (int)(nrow > 0 ? nrow * 4 : 0), 0x00020000);
                 __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(bd), re, lane * 4, 0, 0);
             }
             changed += (int)__popcll(__ballot(valid && old != bi));
@@ -486,6 +501,23 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
             unsigned* const mw = sMask[r & 1][e];
             mw[lane] = 0u;
             if (valid) atomicOr(&mw[bi], 1u << lane);
+            set_flag(&sReady[e], r + 1);
+        }
+        if (rounds_e < rounds) {
+            // the skipped half's round: once the sums waves are past the round
+            // before (as in the loop), its tile rows zeroed (they meet zero
+            // masks, but LDS a first round never wrote may hold NaN bit
+            // patterns) and its mask words cleared, then the half declared
+            // labelled: no row of it counts
+            const int r = rounds_e;
+            wait_blocks(r, 0, NFB - 1);
+            char* const half = tiles + m * TILEB + 16 * hf * RSB;  // the half tile, 16 RSB bytes
+#pragma unroll
+            for (int i = 0; i < (RSB + 63) / 64; ++i) {
+                const int c = lane + 64 * i;  // 16-byte units
+                if (c < RSB) *reinterpret_cast<v4u*>(half + 16 * c) = v4u{0u, 0u, 0u, 0u};
+            }
+            sMask[r & 1][e][lane] = 0u;
             set_flag(&sReady[e], r + 1);
         }
         // one global atomic per block (below): 2,048 waves adding to one
