@@ -69,6 +69,9 @@ struct AssignArgs {
     double* inert = nullptr;
     int* inert_blocks = nullptr;
     int d = 0;
+    // k_assign3 only, nullable: each row's minimum ||c||^2 - 2 x.c (as
+    // FusedArgs::emin), for the relocation's candidate search
+    float* emin = nullptr;
 };
 hipError_t launch_assign(const AssignArgs& a, int num_cu, hipStream_t s);
 // The same E-step on bf16 MFMAs over the exact three-part bf16 split of x
@@ -251,9 +254,10 @@ struct InRelocArgs {
     int* amax;             // [1]
     LoopState* state; int iter;
     // nullable (both or neither): ||x||^2 per row and the E-step's row
-    // minima (FusedArgs::emin) of these labels; with them the blocks compute
-    // direct-form distances only for rows whose approximate distance
-    // xnorm + emin lies near the top (k_finalize_reloc, rows <= 104 floats)
+    // minima (FusedArgs::emin, AssignArgs::emin) of these labels; with them
+    // the blocks compute direct-form distances only for rows whose
+    // approximate distance xnorm + emin lies near the top (rows of at most
+    // 128 floats)
     const float* xnorm = nullptr;
     const float* emin = nullptr;
 };

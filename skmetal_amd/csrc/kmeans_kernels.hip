@@ -1863,10 +1863,11 @@ __device__ __forceinline__ void reloc_body(const InRelocArgs& a, int E)
     // (A') With the E-step's row minima: the approximate distance xnorm[r]
     // + emin[r] (= ||x||^2 + ||c||^2 - 2 x.c, c the row's centre) of every
     // row, the block's E-th largest of them, T, and as candidates the rows
-    // within 2M of T, M = 2^-10 (max ||x||^2 + max ||c||^2): the
-    // approximation and the direct form each lie within 2^-13 of that sum of
-    // the true distance (fp32 norms and products, the split's dropped terms
-    // and the direct form's rounding), so every row of the block's E
+    // within 2M of T, M = 2^-10 (max ||x||^2 + max ||c||^2): for rows of
+    // at most 128 floats the approximation and the direct form each lie
+    // within 2^-13 of that sum of the true distance (fp32 norms, the split's
+    // dropped terms, the fp32 accumulation of at most 768 part products, and
+    // the direct form's rounding), so every row of the block's E
     // farthest by direct-form distance is a candidate.  Only the candidates
     // get that distance, and the selection runs over them: the same rows as
     // (A), for 8 bytes a row instead of the row.  More than kRelocCand
@@ -1876,7 +1877,7 @@ __device__ __forceinline__ void reloc_body(const InRelocArgs& a, int E)
     long* const ccl = reinterpret_cast<long*>(tiles);  // (the tiles are free until (A))
     float* const ccd = tiles + 2 * kRelocCand;
     if constexpr (LDM != 0) {
-        if (a.emin != nullptr && a.xnorm != nullptr && in_lds && a.k <= 64) {
+        if (a.emin != nullptr && a.xnorm != nullptr && in_lds) {
             const int nr = (int)(r1 - r0);
             float xm = 0.f;
             constexpr int U = 8;
@@ -1907,11 +1908,11 @@ __device__ __forceinline__ void reloc_body(const InRelocArgs& a, int E)
                 load(q0);
                 put(q0);
             }
-            // the largest ||c||^2 (k <= 64): four threads a centre, a
-            // quarter of its float4s each
+            // the largest ||c||^2: four threads a centre, a quarter of its
+            // float4s each (the four lanes of a quad run the same trips)
             float cm = 0.f;
-            {
-                const int j = tid >> 2, qq = tid & 3;
+            for (int j = tid >> 2; j < (a.k + 63) / 64 * 64; j += 64) {
+                const int qq = tid & 3;
                 const int g4 = a.ld >> 2;  // float4s a row (its pad is zero)
                 float s2 = 0.f;
                 if (j < a.k) {
@@ -1923,7 +1924,7 @@ __device__ __forceinline__ void reloc_body(const InRelocArgs& a, int E)
                 }
                 s2 += __shfl_xor(s2, 1, 64);
                 s2 += __shfl_xor(s2, 2, 64);
-                cm = s2;
+                cm = fmaxf(cm, s2);
             }
             __syncthreads();  // sdist from every thread
             const float M = 0x1p-10f * (block_max(xm, sd) + block_max(cm, sd));

@@ -364,8 +364,9 @@ struct Lloyd {
     float* shift_sq = nullptr;
     double* rowpart = nullptr;
     float* rowout = nullptr;
-    // split fused path with in-stream relocation: ||x||^2 per row (set at
-    // load) and k_fused3's row minima, for the relocation's candidate search
+    // split E-step with in-stream relocation (rows of at most 128 floats):
+    // ||x||^2 per row (set at load) and the E-step's row minima, for the
+    // relocation's candidate search
     float* xnorm = nullptr;
     float* emin = nullptr;
     double* colpart = nullptr;
@@ -508,7 +509,7 @@ struct Lloyd {
             TRY(grab((void**)&r_cand_d, size_t(kRelocCandBlocks) * kMaxReloc * sizeof(float)));
             TRY(grab((void**)&r_cand_i, size_t(kRelocCandBlocks) * kMaxReloc * sizeof(long)));
             TRY(grab((void**)&r_amax, sizeof(int)));
-            if (f3cap) {
+            if (f3cap || (fblocks == 0 && a3cap && ld <= 128)) {
                 TRY(grab((void**)&xnorm, size_t(n) * sizeof(float)));
                 TRY(grab((void**)&emin, size_t(n) * sizeof(float)));
             }
@@ -625,12 +626,13 @@ struct Lloyd {
 
     char* a3img = nullptr;  // k_assign3's centre image
 
-    int assign(const float* cents, LoopState* state, int* changed)
+    int assign(const float* cents, LoopState* state, int* changed, bool minima = false)
     {
         AssignArgs a{X, n, ld, cents, cnorm, k, labels, state, changed, nullptr};
         if (split_on && a3cap) {
             if (a3img == nullptr) TRY(grab((void**)&a3img, assign3_image_bytes(k, ld)));
             a.img = a3img;
+            if (minima) a.emin = emin;
             HIP_TRY(launch_assign3(a, C->num_cu, s), "assign launch");
         } else
             HIP_TRY(launch_assign(a, C->num_cu, s), "assign launch");
@@ -712,7 +714,7 @@ struct Lloyd {
             TRY(fused_step(iter, decide, tol, flags));
             if (ev) HIP_TRY(hipEventRecord(ev[1], s), "hipEventRecord");
         } else {
-            TRY(assign(cen[cur], st, &st->chg[iter & 1]));
+            TRY(assign(cen[cur], st, &st->chg[iter & 1], true));
             if (ev) HIP_TRY(hipEventRecord(ev[1], s), "hipEventRecord");
             TRY(update());
         }
@@ -720,8 +722,8 @@ struct Lloyd {
         const FinalizeArgs f = finalize_args(iter, tol, flags);
         InRelocArgs r{X, n, ld, d, k, labels, cen[cur], cen[cur ^ 1], sums, counts, part,
                       finalize_col_chunks(d, f.R), rowout, r_cand_d, r_cand_i, r_amax, st, iter};
-        if (fblocks > 0 && split_on && f3cap && emin != nullptr) {
-            // this step's E-step was k_fused3, which wrote its row minima
+        if (emin != nullptr && split_on && (fblocks > 0 ? f3cap : a3cap)) {
+            // this step's E-step was k_fused3 or k_assign3, which wrote its row minima
             r.xnorm = xnorm;
             r.emin = emin;
         }

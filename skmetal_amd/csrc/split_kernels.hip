@@ -887,7 +887,7 @@ template <int CB>
 __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X, long n, int ld,
                                                    const char* __restrict__ img, int k, int* __restrict__ labels,
                                                    LoopState* st, int* changed, const float* __restrict__ C, int d,
-                                                   double* __restrict__ inert)
+                                                   double* __restrict__ inert, float* __restrict__ emin)
 {
     if (st != nullptr && st->done != 0) return;
     using G = Assign3Geom<CB>;
@@ -1047,6 +1047,7 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
             }
         }
         int mylab = 0;
+        float mymin = 0.f;
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
             float d0 = bd[g];
@@ -1059,7 +1060,10 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
                 d0 = take ? od : d0;
                 i0 = take ? oi : i0;
             }
-            if (h == g) mylab = i0;  // lanes 0..31: row = lane
+            if (h == g) {  // lanes 0..31: row = lane
+                mylab = i0;
+                mymin = d0;
+            }
         }
         const bool valid = lane < nrow;
         const long row = wrow + lane;
@@ -1067,6 +1071,9 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
         if (valid) {
             if (changed != nullptr) moved = labels[row] != mylab;
             labels[row] = mylab;
+            // the row's minimum ||c||^2 - 2 x.c, for the relocation's
+            // candidate search (as k_fused3 writes it)
+            if (emin != nullptr) emin[row] = mymin;
         }
         if (changed != nullptr) nchg += (int)__popcll(__ballot(moved));
         // the inertia term of the row: ||x - c_label||^2 in fp32, in the
@@ -1127,7 +1134,7 @@ __global__ __launch_bounds__(512, 1) void k_assign3(const float* __restrict__ X,
 }
 
 typedef void (*assign3_fn)(const float*, long, int, const char*, int, int*, LoopState*, int*, const float*, int,
-                           double*);
+                           double*, float*);
 typedef void (*image_fn)(const float*, const float*, int, int, int, char*);
 
 static int assign3_cb(int k) { return k <= 64 ? 4 : k <= 128 ? 8 : 16; }
@@ -1197,7 +1204,7 @@ hipError_t launch_assign3(const AssignArgs& a, int num_cu, hipStream_t s)
     long blocks = (a.n + 255) / 256;
     if (blocks > num_cu) blocks = num_cu;
     hipLaunchKernelGGL(assign3_kernel(a.k), dim3((unsigned)blocks), dim3(512), assign3_lds(a.k), s, a.X, a.n, a.ld,
-                       a.img, a.k, a.labels, a.state, a.changed, a.C, a.d, a.inert);
+                       a.img, a.k, a.labels, a.state, a.changed, a.C, a.d, a.inert, a.emin);
     if (a.inert_blocks != nullptr) *a.inert_blocks = (int)blocks;
     return hipGetLastError();
 }

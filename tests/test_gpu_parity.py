@@ -522,17 +522,19 @@ def test_relocation_wide_rows(bridge, d, monkeypatch):
                              what=f"in-stream vs {where} relocation d={d}, 3 steps")
 
 
-@pytest.mark.parametrize("n,tied,step", [(20000, 5, 1e-2), (150000, 600, 4e-3)])
-def test_relocation_candidates_near_the_top(bridge, n, tied, step):
-    """On the fused split path the relocated rows are searched among the
+@pytest.mark.parametrize("n,tied,step,kb", [(20000, 5, 1e-2, 16), (150000, 600, 4e-3, 16), (20000, 5, 1e-2, 80),
+                                          (300000, 600, 4e-3, 80)])
+def test_relocation_candidates_near_the_top(bridge, n, tied, step, kb):
+    """On the split paths (kb = 16: the fused step; kb = 80: the separate
+    E-step and the sorted update) the relocated rows are searched among the
     E-step's approximate distances (||x||^2 + the row's minimum of ||c||^2 -
     2 x.c), with direct-form distances only for the rows within a margin of
     each block's top.  A group of far rows whose distances differ by far less
     than that margin (one coordinate stepped by `step`) must still move in the
     oracle's order.  With 600 of them in consecutive rows, a block holds more
     candidates than its list and falls back to every row's direct form."""
-    rng = np.random.default_rng(n)
-    d, kb, E = 64, 16, 3
+    rng = np.random.default_rng(n + kb)
+    d, E = 64, 3
     cen = rng.uniform(-6, 6, (8, d))
     X = (cen[rng.integers(0, 8, n)] + rng.standard_normal((n, d))).astype(np.float32)
     rows = np.arange(1000, 1000 + tied) if tied > 256 else np.sort(rng.choice(n, tied, replace=False))
@@ -542,17 +544,24 @@ def test_relocation_candidates_near_the_top(bridge, n, tied, step):
     others = np.setdiff1d(np.arange(n), rows)
     base = X[np.sort(rng.choice(others, kb, replace=False))]
     C0 = np.concatenate([base, base[:E]])  # the copies come later: E empty clusters
-    assert _split_engaged(bridge, X, C0)["split"]
-    _say(f"relocation near the top n={n} far rows={tied}")
-    out = oracle.lloyd(X, C0, 1)
-    C = C0.copy()
-    lab = np.empty(n, np.int32)
-    n_iter, _ = bridge.kmeans_fit(X, C, lab, 1, 0.0, strict=True)
-    assert n_iter == out["n_iter"]
-    parity.check_centers(C, out["centers"], what=f"relocation near the top n={n}")
-    # the relocated centres are the rows the oracle moved: the stepped
+    info = _split_engaged(bridge, X, C0)
+    assert info["split"] if kb <= 64 else (info["asplit"] and not info["fused"]), info
+    _say(f"relocation near the top n={n} far rows={tied} k={kb + E}")
+    # one step against the oracle: labels up to near-ties (80 centres on 8
+    # blobs meet some), the oracle's M-step and relocation on the device's
+    # labels against the device's centres
+    mean = X.mean(axis=0)
+    with bridge.LloydHandle(n, d, kb + E) as h:
+        h.load(X, center=True)
+        h.set_centers(C0)
+        h.iterate(1)
+        lab, Cn = h.labels(), h.centers()
+    parity.check_lockstep(X - mean, C0 - mean, Cn - mean, lab, what=f"relocation near the top n={n} k={kb + E}")
+    # the relocated centres are the rows the oracle moves: the stepped
     # coordinate tells them apart
-    np.testing.assert_allclose(C[kb:kb + E, 0], out["centers"][kb:kb + E, 0], rtol=0, atol=step / 8)
+    ref, _, n_empty = oracle.mstep(X - mean, lab, C0 - mean)
+    assert n_empty == E
+    np.testing.assert_allclose((Cn - mean)[kb:kb + E, 0], ref[kb:kb + E, 0], rtol=0, atol=step / 8)
 
 
 @pytest.mark.parametrize("wl,steps", [("c1", 4), ("c2", 3)])
