@@ -526,9 +526,8 @@ __global__ __launch_bounds__(1024, 1) void k_fused3(FusedArgs a)
         __syncthreads();  // every sums wave is done: the tile area is free
         __syncthreads();  // the sums are in LDS
     } else {
-        // the E-step waves wait on the sums waves' progress before rewriting
-        // their tile: issue priority for the sums waves
-        __builtin_amdgcn_s_setprio(2);
+        // (every wave at the same issue priority: raising the sums waves',
+        // whose progress the E-step waves wait on, was no faster)
         // sums waves 8..15: the centre fragments (centres >= k and features
         // >= ld zero), ||c||^2 and the halt test.  Every set-up load goes out
         // at once, before any is used (one memory round trip): the halt flag,
