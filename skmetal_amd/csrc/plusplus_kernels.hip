@@ -14,12 +14,13 @@
 //                   fp32 dot product), candidate_t = the first row whose
 //                   running sum of closest distances reaches r_t (searchsorted
 //                   over stable_cumsum, :247-250), clipped to n - 1;
-//   k_pp_dist(c)    one thread per row (rows staged through LDS in
-//                   coalesced 128-byte runs): the distance to each candidate in
+//   k_pp_rows(c)    (rows of at most 128 floats, at most 8 candidates; else
+//   k_pp_dist(c))   one lane per row: the distance to each candidate in
 //                   sklearn's form for fp32 data (_euclidean_distances_upcast:
 //                   fp64 -2 x.c + ||c||^2 + ||x||^2, cast to fp32, negatives
 //                   to 0), min with the row's closest distance so far, and
-//                   per-block fp64 sums of those minima.
+//                   per-block fp64 sums of those minima.  k_pp_select also
+//                   leaves the drawn candidates' values as fp64 for k_pp_rows.
 //
 // The running sum is a two-level fp64 scan (block sums, then the rows of the
 // block the draw falls in), so its rounding differs from numpy's sequential
@@ -183,6 +184,205 @@ __global__ __launch_bounds__(kPPRows) void k_pp_dist(PPArgs a, int c, int Tc)
     if (MIN && live) a.mind[row] = closest;
 }
 
+// Rows of at most LDM floats, exactly TP candidates, one pass.  The block's
+// 256-row range (the unit of the block sums) is read as four 64-row
+// sub-groups, each a contiguous span of X loaded whole by the block (a float4
+// a thread per instruction, every cache line once) and staged in LDS with
+// row stride ctg_stride(ld); the next sub-group's loads are in flight while
+// one is worked on.  Lane l of every wave takes row l of the sub-group; wave
+// w takes its float4 chunks w, w + 4, ..., so the candidates' values a wave
+// needs at a step are the same for all its lanes: they come through the
+// scalar cache straight from X.  The four waves' partial sums meet in LDS
+// and are added in wave order; wave 3 - w then finishes candidates w, w + 4,
+// ... (wave 0 has the most chunks when ld / 4 is not a multiple of 4).
+// Blocks are persistent over the 256-row ranges (b, b + gridDim.x, ...).
+//
+// TAB: the candidates' values as fp64 from a.ctab ([ld / 4][TP][4], written
+// by k_pp_select), not converted from X by every wave, and each row's ||x||^2
+// from a.xxn, which the launch without TAB (the first centre) writes.
+template <int TP, int LDM, bool TAB>
+__global__ __launch_bounds__(256) void k_pp_rows(PPArgs a, int c)
+{
+    typedef const __attribute__((address_space(4))) f4v sf4v;  // uniform loads: scalar cache
+    typedef const __attribute__((address_space(4))) double sdbl;
+    constexpr int SMAX = ctg_stride(LDM);
+    constexpr int NV = (16 * LDM + 255) / 256;  // float4s a thread loads per sub-group
+    constexpr int NU = (TP + 3) / 4;            // candidates a wave finishes
+    constexpr int NJ = (LDM / 4 + 3) / 4;       // chunks a wave works on
+    __shared__ __attribute__((aligned(16))) float tile[64 * SMAX];
+    constexpr int NR = TAB ? TP : TP + 1;        // partial sums per lane (+ ||x||^2)
+    __shared__ double red[4][NR][64];
+    __shared__ double ccs[TP];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tw = 3 - w;  // this wave finishes candidates tw, tw + 4, ...
+    const int ld = a.ld, c4 = ld / 4, S = ctg_stride(ld);
+    const long n = a.n;
+    const long nsg = (n + 63) / 64;
+    const int p = c & 1;
+    sf4v* Xs = (sf4v*)a.X;
+    sdbl* Cs = (sdbl*)a.ctab;
+    const f4v* X4 = reinterpret_cast<const f4v*>(a.X);
+    long coff[TP];  // candidate t's row, in float4s
+#pragma unroll
+    for (int t = 0; t < TP; ++t) coff[t] = a.cand[t] * c4;
+    const float* Dprev = c > 0 ? a.D[p ^ 1] + (long)a.best[c - 1] * n : nullptr;
+
+    // ||c_t||^2 in feature order, one lane a candidate
+    if (w == 0 && lane < TP) {
+        long o = 0;
+#pragma unroll
+        for (int t = 0; t < TP; ++t)
+            if (t == lane) o = coff[t];
+        double cc = 0.0;
+#pragma unroll 4
+        for (int j = 0; j < c4; ++j) {
+            const f4v v = X4[o + j];
+            cc = fma((double)v.x, (double)v.x, cc);
+            cc = fma((double)v.y, (double)v.y, cc);
+            cc = fma((double)v.z, (double)v.z, cc);
+            cc = fma((double)v.w, (double)v.w, cc);
+        }
+        ccs[lane] = cc;
+    }
+
+    // thread tid's float4s q = tid + 256 i of a full sub-group: tile offsets
+    int off[NV];
+    const float inv_c4 = 1.0f / (float)c4;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int q = tid + 256 * i;
+        const int r = (int)(((float)q + 0.5f) * inv_c4);
+        off[i] = r * S + 4 * (q - r * c4);
+    }
+    f4v P[NV];
+    float pclose = INFINITY;
+    double pxx = 0.0;
+    auto load = [&](long sg) {
+        const long r0 = 64 * sg;
+        const int e4 = (int)(min(64L, n - r0) * c4);
+        const f4v* base = X4 + r0 * c4;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int q = tid + 256 * i;
+            if (q < e4) P[i] = base[q];
+        }
+        if (tw < TP) {
+            const long rr = min(r0 + lane, n - 1);
+            if (Dprev != nullptr) pclose = Dprev[rr];
+            if constexpr (TAB) pxx = a.xxn[rr];
+        }
+    };
+
+    double lsum[NU];  // the lane's minima over the 256-row range's sub-groups
+#pragma unroll
+    for (int u = 0; u < NU; ++u) lsum[u] = 0.0;
+    long blk = blockIdx.x;
+    int s = 0;
+    if (4 * blk < nsg) load(4 * blk);
+    while (blk < a.nb) {
+        const long sg = 4 * blk + s;
+        const long r0 = 64 * sg;
+        const int e4 = (int)max(0L, min(64L, n - r0) * c4);
+        __syncthreads();  // every wave is done with the tile and red
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+            if (tid + 256 * i < e4) *reinterpret_cast<f4v*>(tile + off[i]) = P[i];
+        const float closest = pclose;
+        const double rxx = pxx;
+        const long nxt = s == 3 ? 4 * (blk + gridDim.x) : sg + 1;
+        if (nxt < nsg) load(nxt);  // in flight while this sub-group is worked on
+        __syncthreads();
+
+        double acc[TP], xx = 0.0;
+#pragma unroll
+        for (int t = 0; t < TP; ++t) acc[t] = 0.0;
+        const float* xr = tile + lane * S;
+#pragma unroll
+        for (int i = 0; i < NJ; ++i) {
+            const int j = w + 4 * i;
+            if (j < c4) {
+                const f4v xv = *reinterpret_cast<const f4v*>(xr + 4 * j);
+                const double x0 = xv.x, x1 = xv.y, x2 = xv.z, x3 = xv.w;
+                if constexpr (!TAB) {
+                    xx = fma(x0, x0, xx);
+                    xx = fma(x1, x1, xx);
+                    xx = fma(x2, x2, xx);
+                    xx = fma(x3, x3, xx);
+                }
+#pragma unroll
+                for (int t = 0; t < TP; ++t) {
+                    double c0, c1, c2, c3;
+                    if constexpr (TAB) {
+                        sdbl* cp = Cs + 4 * (j * TP + t);
+                        c0 = cp[0];
+                        c1 = cp[1];
+                        c2 = cp[2];
+                        c3 = cp[3];
+                    } else {
+                        const f4v cv = Xs[coff[t] + j];
+                        c0 = cv.x;
+                        c1 = cv.y;
+                        c2 = cv.z;
+                        c3 = cv.w;
+                    }
+                    double v = acc[t];
+                    v = fma(x0, c0, v);
+                    v = fma(x1, c1, v);
+                    v = fma(x2, c2, v);
+                    v = fma(x3, c3, v);
+                    acc[t] = v;
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TP; ++t) red[w][t][lane] = acc[t];
+        if constexpr (!TAB) red[w][NR - 1][lane] = xx;
+        __syncthreads();
+
+        // wave 3 - tw finishes candidates tw, tw + 4, ...: sums in wave
+        // order, the distance in sklearn's fp32-data form, min with the
+        // closest so far
+        const long row = r0 + lane;
+        const bool live = row < n;
+        if (tw < TP) {
+            double x2 = rxx;
+            if constexpr (!TAB) {
+                x2 = ((red[0][NR - 1][lane] + red[1][NR - 1][lane]) + red[2][NR - 1][lane]) + red[3][NR - 1][lane];
+                if (tw == 0 && live && a.xxn != nullptr) a.xxn[row] = x2;
+            }
+#pragma unroll
+            for (int u = 0; u < NU; ++u) {
+                const int t = tw + 4 * u;
+                if (t < TP) {
+                    const double dot = ((red[0][t][lane] + red[1][t][lane]) + red[2][t][lane]) + red[3][t][lane];
+                    float m = 0.f;
+                    if (live) {
+                        float d32 = (float)((-2.0 * dot + ccs[t]) + x2);
+                        if (d32 < 0.f) d32 = 0.f;
+                        m = d32 < closest ? d32 : closest;
+                        a.D[p][(long)t * n + row] = m;
+                    }
+                    lsum[u] += (double)m;
+                }
+            }
+        }
+        if (++s == 4) {  // the range's sums: each lane's four rows, then the lanes
+#pragma unroll
+            for (int u = 0; u < NU; ++u) {
+                const int t = tw + 4 * u;
+                if (t < TP) {
+                    const double v = wave_sum(lsum[u]);
+                    if (lane == 0) a.P[p][(long)t * a.nb + blk] = v;
+                }
+                lsum[u] = 0.0;
+            }
+            s = 0;
+            blk += gridDim.x;
+        }
+    }
+}
+
 // Inclusive scan over the 64 lanes of a wave (fixed order).
 __device__ __forceinline__ double wave_scan(double v, int lane)
 {
@@ -203,6 +403,7 @@ __global__ __launch_bounds__(1024) void k_pp_select(PPArgs a, int c)
     __shared__ double wpot[16][TB];
     __shared__ double rv[kPPMaxTrials];
     __shared__ int found[kPPMaxTrials];
+    __shared__ long picks[kPPMaxTrials];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int q = (c - 1) & 1;
     const int Tq = c == 1 ? 1 : a.T;
@@ -332,8 +533,58 @@ __global__ __launch_bounds__(1024) void k_pp_select(PPArgs a, int c)
                 pick = r0 + RPL * L + __shfl(jf, L, 64);
             }
         }
-        if (lane == 0) a.cand[t] = pick;
+        if (lane == 0) {
+            a.cand[t] = pick;
+            picks[t] = pick;
+        }
     }
+    // the candidates' values as fp64 for k_pp_rows: ctab[f / 4][t][f % 4]
+    if (a.ctab != nullptr) {
+        __syncthreads();
+        const int e = a.T * a.ld;
+        for (int i = tid; i < e; i += 1024) {
+            const int t = i / a.ld, f = i - t * a.ld;
+            a.ctab[((f >> 2) * a.T + t) * 4 + (f & 3)] = (double)a.X[picks[t] * a.ld + f];
+        }
+    }
+}
+
+typedef void (*pp_rows_fn)(PPArgs, int);
+
+template <int LDM, int... TPs>
+struct PPRowsTable {
+    static pp_rows_fn get(int T, bool tab)
+    {
+        pp_rows_fn f = nullptr;
+        ((T == TPs ? (f = tab ? &k_pp_rows<TPs, LDM, true> : &k_pp_rows<TPs, LDM, false>, 0) : 0), ...);
+        return f;
+    }
+};
+
+template <int LDM>
+pp_rows_fn pp_rows_for(int T, bool tab)
+{
+    return PPRowsTable<LDM, 1, 2, 3, 4, 5, 6, 7, 8>::get(T, tab);
+}
+
+// Resident blocks per CU of a k_pp_rows instance (cached).
+int pp_rows_occupancy(pp_rows_fn f)
+{
+    static pp_rows_fn keys[32];
+    static int vals[32];
+    static int used = 0;
+    for (int i = 0; i < used; ++i)
+        if (keys[i] == f) return vals[i];
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(f), 256, 0) != hipSuccess ||
+        nb < 1)
+        nb = 1;
+    if (used < 32) {
+        keys[used] = f;
+        vals[used] = nb;
+        ++used;
+    }
+    return nb;
 }
 
 }  // namespace
@@ -344,6 +595,17 @@ hipError_t launch_pp_dist(const PPArgs& a, int c, hipStream_t s)
     // one pass over X for T <= 16 (the candidate count exactly for T <= 8,
     // the usual 2 + ln k), passes of 16 beyond
     const int T = c == 0 ? 1 : a.T;
+    if (pp_rows_path(T, a.ld)) {  // whole rows through LDS, candidates through the scalar cache
+        const bool tab = c > 0 && a.ctab != nullptr;  // k_pp_select wrote centre c's table; launch 0 wrote xxn
+        const pp_rows_fn f = a.ld <= 32 ? pp_rows_for<32>(T, tab)
+                             : a.ld <= 64 ? pp_rows_for<64>(T, tab)
+                             : a.ld <= 104 ? pp_rows_for<104>(T, tab)
+                                           : pp_rows_for<128>(T, tab);
+        const long cap = (long)(a.cus > 0 ? a.cus : 256) * pp_rows_occupancy(f);
+        const unsigned g = (unsigned)(a.nb < cap ? a.nb : cap);
+        hipLaunchKernelGGL(f, dim3(g), dim3(256), 0, s, a, c);
+        return hipGetLastError();
+    }
     switch (T) {
     case 1: hipLaunchKernelGGL(k_pp_dist<1>, grid, block, 0, s, a, c, T); break;
     case 2: hipLaunchKernelGGL(k_pp_dist<2>, grid, block, 0, s, a, c, T); break;

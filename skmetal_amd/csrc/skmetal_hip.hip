@@ -990,6 +990,12 @@ struct Lloyd {
             TRY(pp_grab((void**)&pp.best, size_t(k) * sizeof(int)));
             TRY(pp_grab((void**)&pp.pot, size_t(k) * sizeof(double)));
             TRY(pp_grab((void**)&pp.U, std::max<size_t>(1, size_t(k - 1) * T) * sizeof(double)));
+            pp.ctab = nullptr;
+            pp.xxn = nullptr;
+            if (pp_rows_path(T, ld)) {
+                TRY(pp_grab((void**)&pp.ctab, size_t(T) * ld * sizeof(double)));
+                TRY(pp_grab((void**)&pp.xxn, size_t(n) * sizeof(double)));
+            }
             pp_T = T;
         }
         pp.X = X;
@@ -998,6 +1004,7 @@ struct Lloyd {
         pp.k = k;
         pp.T = T;
         pp.nb = nb;
+        pp.cus = C->num_cu;
         pp.centers = cen[cur];
         TRY(upload_bytes(*C, &first, sizeof(long), pp.cand, s));
         if (k > 1) TRY(upload_bytes(*C, U, size_t(k - 1) * T * sizeof(double), const_cast<double*>(pp.U), s));
