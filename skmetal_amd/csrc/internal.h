@@ -295,9 +295,12 @@ struct PPArgs {
     int cus;               // compute units of the device (the distance kernel's grid)
     double* ctab;          // [ld / 4][T][4] the drawn candidates' values as fp64 (pp_rows_path only; else null)
     double* xxn;           // [n] ||x||^2 in fp64, written by the first centre's distances (with ctab; else null)
+    double* ccn;           // k-means||: [m] the candidates' ||c||^2 (with ctab, [ld / 4][m][4]; else null)
 };
 // Whether k_pp_dist's rows path (and so a.ctab) serves T candidates of rows of ld floats.
 inline bool pp_rows_path(int T, int ld) { return T <= 8 && ld <= 128; }
+// Whether the k-means|| rounds' rows path (a.ctab, a.ccn) serves rows of ld floats.
+inline bool pp_rows_min_path(int ld) { return ld <= 128; }
 // Candidate distances of centre c (c = 0: the first row alone).
 hipError_t launch_pp_dist(const PPArgs& a, int c, hipStream_t s);
 // k-means||: mind[row] = min(mind[row] (or +inf with mind_reset), distance to

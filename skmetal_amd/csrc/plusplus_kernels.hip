@@ -383,6 +383,151 @@ __global__ __launch_bounds__(256) void k_pp_rows(PPArgs a, int c)
     }
 }
 
+// k-means|| rounds: the m candidate rows' values as fp64, ctab[f / 4][t][f %
+// 4], and ||c_t||^2 (fp64 fmas in feature order), ccn[t], for t < mp = m
+// rounded up to a multiple of 8: t >= m repeats candidate m - 1 (a repeated
+// candidate leaves every minimum as it is).
+constexpr int kMinGroup = 8;
+__global__ __launch_bounds__(256) void k_pp_ctab(PPArgs a, int m)
+{
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    const int ld = a.ld;
+    const int mp = (m + kMinGroup - 1) / kMinGroup * kMinGroup;
+    if (i < (long)mp * ld) {
+        const int t = (int)(i / ld), f = (int)(i - (long)t * ld);
+        a.ctab[(((long)(f >> 2) * mp + t) << 2) + (f & 3)] = (double)a.X[a.cand[min(t, m - 1)] * ld + f];
+    }
+    if (i < mp) {  // rows of at most 128 floats: the row's loads all in flight, then the fmas
+        const f4v* x = reinterpret_cast<const f4v*>(a.X + a.cand[min((int)i, m - 1)] * ld);
+        f4v v[32];
+#pragma unroll
+        for (int j = 0; j < 32; ++j)
+            if (4 * j < ld) v[j] = x[j];
+        double cc = 0.0;
+#pragma unroll
+        for (int j = 0; j < 32; ++j)
+            if (4 * j < ld) {
+                cc = fma((double)v[j].x, (double)v[j].x, cc);
+                cc = fma((double)v[j].y, (double)v[j].y, cc);
+                cc = fma((double)v[j].z, (double)v[j].z, cc);
+                cc = fma((double)v[j].w, (double)v[j].w, cc);
+            }
+        a.ccn[i] = cc;
+    }
+}
+
+// k-means||: a.mind[row] = min(a.mind[row] (+inf with a.mind_reset), the
+// distance to each of the m candidates), rows of at most LDM floats.  The
+// rows go through LDS as in k_pp_rows, but here wave w takes candidate
+// groups w, w + 4, ... (8 candidates a group) over whole rows, in feature
+// order: no partial sums cross waves, and only the four waves' minima meet
+// in LDS.  The candidates' values (fp64, k_pp_ctab's table) and norms come
+// through the scalar cache.
+template <int LDM>
+__global__ __launch_bounds__(256) void k_pp_rows_min(PPArgs a, int m)
+{
+    typedef const __attribute__((address_space(4))) double sdbl;  // uniform loads: scalar cache
+    constexpr int SMAX = ctg_stride(LDM);
+    constexpr int NV = (16 * LDM + 255) / 256;
+    constexpr int TG = 4;  // candidates a group (kMinGroup is a multiple)
+    constexpr int NJ = LDM / 4;
+    const int mp = (m + kMinGroup - 1) / kMinGroup * kMinGroup;  // the table's candidates
+    __shared__ __attribute__((aligned(16))) float tile[64 * SMAX];
+    __shared__ float wmins[4][64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ld = a.ld, c4 = ld / 4, S = ctg_stride(ld);
+    const long n = a.n;
+    const long nsg = (n + 63) / 64;
+    const f4v* X4 = reinterpret_cast<const f4v*>(a.X);
+    sdbl* Cs = (sdbl*)a.ctab;
+    sdbl* Cn = (sdbl*)a.ccn;
+    const int ngroups = mp / TG;
+
+    int off[NV];
+    const float inv_c4 = 1.0f / (float)c4;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int q = tid + 256 * i;
+        const int r = (int)(((float)q + 0.5f) * inv_c4);
+        off[i] = r * S + 4 * (q - r * c4);
+    }
+    f4v P[NV];
+    float pclose = INFINITY;
+    auto load = [&](long sg) {
+        const long r0 = 64 * sg;
+        const int e4 = (int)(min(64L, n - r0) * c4);
+        const f4v* base = X4 + r0 * c4;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int q = tid + 256 * i;
+            if (q < e4) P[i] = base[q];
+        }
+        if (w == 0 && !a.mind_reset) pclose = a.mind[min(r0 + lane, n - 1)];
+    };
+    // sub-groups b, b + gridDim.x, ... of 64 rows
+    long sg = blockIdx.x;
+    if (sg < nsg) load(sg);
+    for (; sg < nsg; sg += gridDim.x) {
+        const long r0 = 64 * sg;
+        const int e4 = (int)(min(64L, n - r0) * c4);
+        __syncthreads();  // every wave is done with the tile and wmins
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+            if (tid + 256 * i < e4) *reinterpret_cast<f4v*>(tile + off[i]) = P[i];
+        const float closest = pclose;
+        if (sg + gridDim.x < nsg) load(sg + gridDim.x);  // in flight while this one is worked on
+        __syncthreads();
+
+        const float* xr = tile + lane * S;
+        float best = INFINITY;
+        double xx = 0.0;
+        for (int g = w; g < ngroups; g += 4) {
+            const int t0 = TG * g;
+            double acc[TG];
+#pragma unroll
+            for (int t = 0; t < TG; ++t) acc[t] = 0.0;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+              if (j < c4) {
+                const f4v xv = *reinterpret_cast<const f4v*>(xr + 4 * j);
+                const double x0 = xv.x, x1 = xv.y, x2 = xv.z, x3 = xv.w;
+                if (g == w) {
+                    xx = fma(x0, x0, xx);
+                    xx = fma(x1, x1, xx);
+                    xx = fma(x2, x2, xx);
+                    xx = fma(x3, x3, xx);
+                }
+                sdbl* cp = Cs + 4 * ((long)j * mp + t0);
+#pragma unroll
+                for (int t = 0; t < TG; ++t) {
+                    double v = acc[t];
+                    v = fma(x0, cp[4 * t], v);
+                    v = fma(x1, cp[4 * t + 1], v);
+                    v = fma(x2, cp[4 * t + 2], v);
+                    v = fma(x3, cp[4 * t + 3], v);
+                    acc[t] = v;
+                }
+              }
+            }
+#pragma unroll
+            for (int t = 0; t < TG; ++t) {
+                float d32 = (float)((-2.0 * acc[t] + Cn[t0 + t]) + xx);
+                if (d32 < 0.f) d32 = 0.f;
+                best = d32 < best ? d32 : best;
+            }
+        }
+        wmins[w][lane] = best;
+        __syncthreads();
+        if (w == 0 && r0 + lane < n) {
+            float v = closest;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v = wmins[i][lane] < v ? wmins[i][lane] : v;
+            a.mind[r0 + lane] = v;
+        }
+    }
+}
+
 // Inclusive scan over the 64 lanes of a wave (fixed order).
 __device__ __forceinline__ double wave_scan(double v, int lane)
 {
@@ -624,6 +769,21 @@ hipError_t launch_pp_dist(const PPArgs& a, int c, hipStream_t s)
 
 hipError_t launch_pp_mindist(const PPArgs& a, int m, hipStream_t s)
 {
+    if (pp_rows_min_path(a.ld) && a.ctab != nullptr && a.ccn != nullptr) {
+        if (m > 0) {
+            const long e = (long)(m + kMinGroup - 1) / kMinGroup * kMinGroup * a.ld;
+            hipLaunchKernelGGL(k_pp_ctab, dim3((unsigned)((e + 255) / 256)), dim3(256), 0, s, a, m);
+        }
+        const pp_rows_fn f = a.ld <= 32 ? &k_pp_rows_min<32>
+                             : a.ld <= 64 ? &k_pp_rows_min<64>
+                             : a.ld <= 104 ? &k_pp_rows_min<104>
+                                           : &k_pp_rows_min<128>;
+        const long nsg = (a.n + 63) / 64;
+        const long cap = (long)(a.cus > 0 ? a.cus : 256) * pp_rows_occupancy(f);
+        const unsigned g = (unsigned)(nsg < cap ? nsg : cap);
+        hipLaunchKernelGGL(f, dim3(g), dim3(256), 0, s, a, m);
+        return hipGetLastError();
+    }
     const dim3 grid((unsigned)a.nb), block(kPPRows);
     if (m <= 8)
         hipLaunchKernelGGL((k_pp_dist<8, true>), grid, block, 0, s, a, 0, m);

@@ -1025,6 +1025,8 @@ struct Lloyd {
     // starts it from +inf).  Distances are sklearn's fp32 form, as k-means++'s.
     float* kp_mind = nullptr;
     long* kp_cand = nullptr;
+    double* kp_ctab = nullptr;  // [ld / 4][cap8][4] the candidates' values as fp64 (rows of <= 128 floats)
+    double* kp_ccn = nullptr;   // [cap8] their ||c||^2 (cap8: cap rounded up to a multiple of 8)
     long kp_cap = 0;
     bool kp_valid = false;
 
@@ -1039,13 +1041,19 @@ struct Lloyd {
         if (kp_mind == nullptr) TRY(grab((void**)&kp_mind, size_t(n) * sizeof(float)));
         if (m > kp_cap) {
             const long cap = std::max<long>(m, 2 * kp_cap);
-            if (kp_cand != nullptr) {
-                const auto it = std::find(owned.begin(), owned.end(), (void*)kp_cand);
-                if (it != owned.end()) owned.erase(it);
-                C->release(kp_cand);
-                kp_cand = nullptr;
-            }
+            for (void** p : {(void**)&kp_cand, (void**)&kp_ctab, (void**)&kp_ccn})
+                if (*p != nullptr) {
+                    const auto it = std::find(owned.begin(), owned.end(), *p);
+                    if (it != owned.end()) owned.erase(it);
+                    C->release(*p);
+                    *p = nullptr;
+                }
             TRY(grab((void**)&kp_cand, size_t(cap) * sizeof(long)));
+            if (pp_rows_min_path(ld)) {  // candidates rounded up to a multiple of 8
+                const size_t capp = size_t(cap + 7) / 8 * 8;
+                TRY(grab((void**)&kp_ctab, capp * ld * sizeof(double)));
+                TRY(grab((void**)&kp_ccn, capp * sizeof(double)));
+            }
             kp_cap = cap;
         }
         if (m > 0 || reset) {
@@ -1057,6 +1065,9 @@ struct Lloyd {
             a.cand = kp_cand;
             a.mind = kp_mind;
             a.mind_reset = reset ? 1 : 0;
+            a.cus = C->num_cu;
+            a.ctab = kp_ctab;
+            a.ccn = kp_ccn;
             if (m > 0) TRY(upload_bytes(*C, rows, size_t(m) * sizeof(long), kp_cand, s));
             HIP_TRY(launch_pp_mindist(a, (int)m, s), "mindist launch");
         }
