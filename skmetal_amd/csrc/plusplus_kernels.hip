@@ -383,21 +383,24 @@ __global__ __launch_bounds__(256) void k_pp_rows(PPArgs a, int c)
     }
 }
 
-// k-means|| rounds: the m candidate rows' values as fp64, ctab[f / 4][t][f %
-// 4], and ||c_t||^2 (fp64 fmas in feature order), ccn[t], for t < mp = m
-// rounded up to a multiple of 8: t >= m repeats candidate m - 1 (a repeated
-// candidate leaves every minimum as it is).
-constexpr int kMinGroup = 8;
-__global__ __launch_bounds__(256) void k_pp_ctab(PPArgs a, int m)
+// k-means|| rounds on the fp64 matrix cores: the m candidates as the B
+// operands of v_mfma_f64_16x16x4_f64 in 16-candidate groups,
+// bfrag[(g ld/4 + j) 64 + l] = candidate 16 g + l % 16, feature 4 j + l / 16
+// (fp64; candidates past m - 1 repeat it, which leaves every minimum as it
+// is), and ||c_t||^2 (fp64 fmas in feature order), ccn[t], t < 16 G.
+__global__ __launch_bounds__(256) void k_pp_bfrag(PPArgs a, int m)
 {
     const long i = (long)blockIdx.x * 256 + threadIdx.x;
-    const int ld = a.ld;
-    const int mp = (m + kMinGroup - 1) / kMinGroup * kMinGroup;
-    if (i < (long)mp * ld) {
-        const int t = (int)(i / ld), f = (int)(i - (long)t * ld);
-        a.ctab[(((long)(f >> 2) * mp + t) << 2) + (f & 3)] = (double)a.X[a.cand[min(t, m - 1)] * ld + f];
+    const int ld = a.ld, c4 = ld / 4;
+    const int G = (m + 15) / 16;
+    if (i < (long)G * c4 * 64) {
+        const int l = (int)(i & 63);
+        const long gj = i >> 6;
+        const int g = (int)(gj / c4), j = (int)(gj - (long)g * c4);
+        const int t = min(16 * g + (l & 15), m - 1);
+        a.ctab[i] = (double)a.X[a.cand[t] * ld + 4 * j + (l >> 4)];
     }
-    if (i < mp) {  // rows of at most 128 floats: the row's loads all in flight, then the fmas
+    if (i < 16L * G) {  // rows of at most 128 floats: the row's loads all in flight, then the fmas
         const f4v* x = reinterpret_cast<const f4v*>(a.X + a.cand[min((int)i, m - 1)] * ld);
         f4v v[32];
 #pragma unroll
@@ -418,39 +421,39 @@ __global__ __launch_bounds__(256) void k_pp_ctab(PPArgs a, int m)
 
 // k-means||: a.mind[row] = min(a.mind[row] (+inf with a.mind_reset), the
 // distance to each of the m candidates), rows of at most LDM floats.  The
-// rows go through LDS as in k_pp_rows, but here wave w takes candidate
-// groups w, w + 4, ... (8 candidates a group) over whole rows, in feature
-// order: no partial sums cross waves, and only the four waves' minima meet
-// in LDS.  The candidates' values (fp64, k_pp_ctab's table) and norms come
-// through the scalar cache.
+// rows go through LDS in 64-row sub-groups as in k_pp_rows; wave w takes
+// rows 16 w .. 16 w + 15 of a sub-group and, per 16-candidate group, chains
+// ld / 4 v_mfma_f64_16x16x4_f64 over the features: the fp64 matrix cores
+// add the exact products x_f c_f one at a time in feature order, the same
+// sums as a sequential fma chain.  Lane l then holds rows l / 16 + 4 r,
+// candidate l % 16.
 template <int LDM>
-__global__ __launch_bounds__(256) void k_pp_rows_min(PPArgs a, int m)
+__global__ __launch_bounds__(256, 4) void k_pp_mm_min(PPArgs a, int m)
 {
-    typedef const __attribute__((address_space(4))) double sdbl;  // uniform loads: scalar cache
+    typedef double v4d __attribute__((ext_vector_type(4)));
     constexpr int SMAX = ctg_stride(LDM);
     constexpr int NV = (16 * LDM + 255) / 256;
-    constexpr int TG = 4;  // candidates a group (kMinGroup is a multiple)
     constexpr int NJ = LDM / 4;
-    const int mp = (m + kMinGroup - 1) / kMinGroup * kMinGroup;  // the table's candidates
     __shared__ __attribute__((aligned(16))) float tile[64 * SMAX];
-    __shared__ float wmins[4][64];
+    __shared__ double sxx[64];  // ||x||^2 of the sub-group's rows
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ld = a.ld, c4 = ld / 4, S = ctg_stride(ld);
     const long n = a.n;
     const long nsg = (n + 63) / 64;
     const f4v* X4 = reinterpret_cast<const f4v*>(a.X);
-    sdbl* Cs = (sdbl*)a.ctab;
-    sdbl* Cn = (sdbl*)a.ccn;
-    const int ngroups = mp / TG;
+    const int G = (m + 15) / 16;
+    const int q = lane >> 4, cj = lane & 15;
+    // the row this lane writes (lanes with cj < 4): 16 w + q + 4 cj
+    const int orow = 16 * w + q + 4 * cj;
 
     int off[NV];
     const float inv_c4 = 1.0f / (float)c4;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-        const int q = tid + 256 * i;
-        const int r = (int)(((float)q + 0.5f) * inv_c4);
-        off[i] = r * S + 4 * (q - r * c4);
+        const int qq = tid + 256 * i;
+        const int r = (int)(((float)qq + 0.5f) * inv_c4);
+        off[i] = r * S + 4 * (qq - r * c4);
     }
     f4v P[NV];
     float pclose = INFINITY;
@@ -460,18 +463,17 @@ __global__ __launch_bounds__(256) void k_pp_rows_min(PPArgs a, int m)
         const f4v* base = X4 + r0 * c4;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const int q = tid + 256 * i;
-            if (q < e4) P[i] = base[q];
+            const int qq = tid + 256 * i;
+            if (qq < e4) P[i] = base[qq];
         }
-        if (w == 0 && !a.mind_reset) pclose = a.mind[min(r0 + lane, n - 1)];
+        if (cj < 4 && !a.mind_reset) pclose = a.mind[min(r0 + orow, n - 1)];
     };
-    // sub-groups b, b + gridDim.x, ... of 64 rows
     long sg = blockIdx.x;
     if (sg < nsg) load(sg);
     for (; sg < nsg; sg += gridDim.x) {
         const long r0 = 64 * sg;
         const int e4 = (int)(min(64L, n - r0) * c4);
-        __syncthreads();  // every wave is done with the tile and wmins
+        __syncthreads();  // every wave is done with the tile
 #pragma unroll
         for (int i = 0; i < NV; ++i)
             if (tid + 256 * i < e4) *reinterpret_cast<f4v*>(tile + off[i]) = P[i];
@@ -479,52 +481,67 @@ __global__ __launch_bounds__(256) void k_pp_rows_min(PPArgs a, int m)
         if (sg + gridDim.x < nsg) load(sg + gridDim.x);  // in flight while this one is worked on
         __syncthreads();
 
-        const float* xr = tile + lane * S;
-        float best = INFINITY;
-        double xx = 0.0;
-        for (int g = w; g < ngroups; g += 4) {
-            const int t0 = TG * g;
-            double acc[TG];
+        // ||x||^2 of the wave's 16 rows in feature order (lanes 0..15), then
+        // each lane takes its four rows' values
+        if (lane < 16) {
+            const float* xr = tile + (16 * w + lane) * S;
+            double xx = 0.0;
 #pragma unroll
-            for (int t = 0; t < TG; ++t) acc[t] = 0.0;
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-              if (j < c4) {
-                const f4v xv = *reinterpret_cast<const f4v*>(xr + 4 * j);
-                const double x0 = xv.x, x1 = xv.y, x2 = xv.z, x3 = xv.w;
-                if (g == w) {
-                    xx = fma(x0, x0, xx);
-                    xx = fma(x1, x1, xx);
-                    xx = fma(x2, x2, xx);
-                    xx = fma(x3, x3, xx);
+            for (int j = 0; j < NJ; ++j)
+                if (j < c4) {
+                    const f4v xv = *reinterpret_cast<const f4v*>(xr + 4 * j);
+                    xx = fma((double)xv.x, (double)xv.x, xx);
+                    xx = fma((double)xv.y, (double)xv.y, xx);
+                    xx = fma((double)xv.z, (double)xv.z, xx);
+                    xx = fma((double)xv.w, (double)xv.w, xx);
                 }
-                sdbl* cp = Cs + 4 * ((long)j * mp + t0);
+            sxx[16 * w + lane] = xx;
+        }
+        __builtin_amdgcn_wave_barrier();  // (a wave's LDS accesses complete in order)
+        double xxr[4];
 #pragma unroll
-                for (int t = 0; t < TG; ++t) {
-                    double v = acc[t];
-                    v = fma(x0, cp[4 * t], v);
-                    v = fma(x1, cp[4 * t + 1], v);
-                    v = fma(x2, cp[4 * t + 2], v);
-                    v = fma(x3, cp[4 * t + 3], v);
-                    acc[t] = v;
-                }
-              }
+        for (int r = 0; r < 4; ++r) xxr[r] = sxx[16 * w + q + 4 * r];
+
+        float best[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
+        const float* ar = tile + (16 * w + cj) * S + q;  // A: row cj, feature 4 j + q
+        for (int g = 0; g < G; ++g) {
+            const double* bf = a.ctab + ((long)g * c4 << 6) + lane;
+            v4d acc = {0.0, 0.0, 0.0, 0.0};
+            // eight K steps at a time: their B fragments and A values loaded together
+            for (int j0 = 0; j0 < c4; j0 += 8) {
+                double bv[8];
+                float av[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (j0 + u < c4) {
+                        bv[u] = bf[(long)(j0 + u) << 6];
+                        av[u] = ar[4 * (j0 + u)];
+                    }
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (j0 + u < c4) acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)av[u], bv[u], acc, 0, 0, 0);
             }
+            const double cn = a.ccn[16 * g + cj];
 #pragma unroll
-            for (int t = 0; t < TG; ++t) {
-                float d32 = (float)((-2.0 * acc[t] + Cn[t0 + t]) + xx);
+            for (int r = 0; r < 4; ++r) {
+                float d32 = (float)((-2.0 * acc[r] + cn) + xxr[r]);
                 if (d32 < 0.f) d32 = 0.f;
-                best = d32 < best ? d32 : best;
+                best[r] = d32 < best[r] ? d32 : best[r];
             }
         }
-        wmins[w][lane] = best;
-        __syncthreads();
-        if (w == 0 && r0 + lane < n) {
-            float v = closest;
+        // min over the 16 candidate lanes of each row (lanes 16 q .. 16 q + 15)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v = wmins[i][lane] < v ? wmins[i][lane] : v;
-            a.mind[r0 + lane] = v;
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) {
+                const float u = __shfl_xor(best[r], o, 64);
+                best[r] = u < best[r] ? u : best[r];
+            }
+        if (cj < 4 && r0 + orow < n) {
+            const float b = cj == 0 ? best[0] : cj == 1 ? best[1] : cj == 2 ? best[2] : best[3];
+            a.mind[r0 + orow] = b < closest ? b : closest;
         }
+        __builtin_amdgcn_wave_barrier();  // sxx is rewritten only after the next block barrier
     }
 }
 
@@ -771,13 +788,13 @@ hipError_t launch_pp_mindist(const PPArgs& a, int m, hipStream_t s)
 {
     if (pp_rows_min_path(a.ld) && a.ctab != nullptr && a.ccn != nullptr) {
         if (m > 0) {
-            const long e = (long)(m + kMinGroup - 1) / kMinGroup * kMinGroup * a.ld;
-            hipLaunchKernelGGL(k_pp_ctab, dim3((unsigned)((e + 255) / 256)), dim3(256), 0, s, a, m);
+            const long e = (long)(m + 15) / 16 * 16 * a.ld;  // G ld/4 64 fragments
+            hipLaunchKernelGGL(k_pp_bfrag, dim3((unsigned)((e + 255) / 256)), dim3(256), 0, s, a, m);
         }
-        const pp_rows_fn f = a.ld <= 32 ? &k_pp_rows_min<32>
-                             : a.ld <= 64 ? &k_pp_rows_min<64>
-                             : a.ld <= 104 ? &k_pp_rows_min<104>
-                                           : &k_pp_rows_min<128>;
+        const pp_rows_fn f = a.ld <= 32 ? &k_pp_mm_min<32>
+                             : a.ld <= 64 ? &k_pp_mm_min<64>
+                             : a.ld <= 104 ? &k_pp_mm_min<104>
+                                           : &k_pp_mm_min<128>;
         const long nsg = (a.n + 63) / 64;
         const long cap = (long)(a.cus > 0 ? a.cus : 256) * pp_rows_occupancy(f);
         const unsigned g = (unsigned)(nsg < cap ? nsg : cap);

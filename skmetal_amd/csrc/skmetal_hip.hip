@@ -1025,8 +1025,8 @@ struct Lloyd {
     // starts it from +inf).  Distances are sklearn's fp32 form, as k-means++'s.
     float* kp_mind = nullptr;
     long* kp_cand = nullptr;
-    double* kp_ctab = nullptr;  // [ld / 4][cap8][4] the candidates' values as fp64 (rows of <= 128 floats)
-    double* kp_ccn = nullptr;   // [cap8] their ||c||^2 (cap8: cap rounded up to a multiple of 8)
+    double* kp_ctab = nullptr;  // [cap16 ld] the candidates' values as fp64 MFMA fragments (rows of <= 128 floats)
+    double* kp_ccn = nullptr;   // [cap16] their ||c||^2 (cap16: cap rounded up to a multiple of 16)
     long kp_cap = 0;
     bool kp_valid = false;
 
@@ -1049,8 +1049,8 @@ struct Lloyd {
                     *p = nullptr;
                 }
             TRY(grab((void**)&kp_cand, size_t(cap) * sizeof(long)));
-            if (pp_rows_min_path(ld)) {  // candidates rounded up to a multiple of 8
-                const size_t capp = size_t(cap + 7) / 8 * 8;
+            if (pp_rows_min_path(ld)) {  // candidates rounded up to a multiple of 16
+                const size_t capp = size_t(cap + 15) / 16 * 16;
                 TRY(grab((void**)&kp_ctab, capp * ld * sizeof(double)));
                 TRY(grab((void**)&kp_ccn, capp * sizeof(double)));
             }
