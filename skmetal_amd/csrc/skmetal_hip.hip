@@ -328,17 +328,50 @@ int upload_bytes(Context& C, const void* src, size_t bytes, void* dst, hipStream
     return 0;
 }
 
+// dst[0, bytes) = src, split over up to 8 host threads for large copies (as
+// stage_rows: one thread's memcpy runs at a fraction of the host's memory
+// bandwidth).
+static void par_copy(char* dst, const char* src, size_t bytes)
+{
+    unsigned nt = std::thread::hardware_concurrency();
+    nt = nt < 1 ? 1 : nt > 8 ? 8 : nt;
+    if (bytes < (size_t(4) << 20) || nt == 1) {
+        std::memcpy(dst, src, bytes);
+        return;
+    }
+    const size_t per = (bytes / nt + 63) & ~size_t(63);
+    std::vector<std::thread> th;
+    for (unsigned t = 1; t < nt; ++t) {
+        const size_t o = t * per;
+        if (o < bytes) th.emplace_back([=] { std::memcpy(dst + o, src + o, std::min(per, bytes - o)); });
+    }
+    std::memcpy(dst, src, std::min(per, bytes));
+    for (auto& x : th) x.join();
+}
+
+// Device -> host copy through the two pinned staging buffers: chunk i + 1
+// goes over the bus into one buffer while the host moves chunk i out of the
+// other.
 int download_bytes(Context& C, const void* src, size_t bytes, void* dst, hipStream_t s)
 {
     const char* sp = static_cast<const char*>(src);
     char* dp = static_cast<char*>(dst);
-    for (size_t o = 0; o < bytes; o += kPinBytes) {
-        const size_t m = std::min(kPinBytes, bytes - o);
-        HIP_TRY(hipEventSynchronize(C.pin_ev[0]), "hipEventSynchronize(staging)");
-        HIP_TRY(hipEventSynchronize(C.pin_ev[1]), "hipEventSynchronize(staging)");
-        HIP_TRY(hipMemcpyAsync(C.pin[0], sp + o, m, hipMemcpyDeviceToHost, s), "hipMemcpyAsync(D2H)");
-        HIP_TRY(hipStreamSynchronize(s), "hipStreamSynchronize");
-        std::memcpy(dp + o, C.pin[0], m);
+    if (bytes == 0) return 0;
+    HIP_TRY(hipEventSynchronize(C.pin_ev[0]), "hipEventSynchronize(staging)");
+    HIP_TRY(hipEventSynchronize(C.pin_ev[1]), "hipEventSynchronize(staging)");
+    const size_t nch = (bytes + kPinBytes - 1) / kPinBytes;
+    auto issue = [&](size_t i) -> int {
+        const size_t o = i * kPinBytes, m = std::min(kPinBytes, bytes - o);
+        HIP_TRY(hipMemcpyAsync(C.pin[i & 1], sp + o, m, hipMemcpyDeviceToHost, s), "hipMemcpyAsync(D2H)");
+        HIP_TRY(hipEventRecord(C.pin_ev[i & 1], s), "hipEventRecord");
+        return 0;
+    };
+    TRY(issue(0));
+    for (size_t i = 0; i < nch; ++i) {
+        if (i + 1 < nch) TRY(issue(i + 1));  // its buffer's previous chunk (i - 1) is already out
+        HIP_TRY(hipEventSynchronize(C.pin_ev[i & 1]), "hipEventSynchronize(staging)");
+        const size_t o = i * kPinBytes;
+        par_copy(dp + o, static_cast<const char*>(C.pin[i & 1]), std::min(kPinBytes, bytes - o));
     }
     return 0;
 }
