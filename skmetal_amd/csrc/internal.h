@@ -351,7 +351,11 @@ struct TransformArgs {
     const float* C; int k;             // centres [k x ld]
     double* cc;                        // [k] fp64 ||c||^2 (written first)
     float* out;                        // [n x k]
+    double* cfrag = nullptr;           // transform_mm_path: [ceil(k / 16) 16 ld] the centres as fp64 MFMA fragments
+    int cus = 0;                       // compute units of the device
 };
+// Whether KMeans.transform takes the fp64 matrix-core kernel (rows of <= 128 floats).
+inline bool transform_mm_path(int ld) { return ld <= 128; }
 hipError_t launch_transform(const TransformArgs& a, hipStream_t s);
 
 hipError_t launch_colsum(const float* X, long n, int ld, int d, double* part, int nblk, hipStream_t s);

@@ -1740,11 +1740,13 @@ int skmetal_hip_kmeans_transform(const float* X, const float* centroids, float* 
     TRY(b.get((void**)&dC, k * size_t(ld) * sizeof(float)));
     TRY(b.get((void**)&dcc, k * sizeof(double)));
     TRY(b.get((void**)&dO, size_t(rows) * k * sizeof(float)));
+    double* dfrag = nullptr;
+    if (transform_mm_path(ld)) TRY(b.get((void**)&dfrag, (k + 15) / 16 * 16 * size_t(ld) * sizeof(double)));
     TRY(upload_rows(c, centroids, (long)k, (int)d, ld, dC, c.stream));
     for (long r = 0; r < (long)n; r += rows) {
         const long m = std::min<long>(rows, (long)n - r);
         TRY(upload_rows(c, X + size_t(r) * d, m, (int)d, ld, dX, c.stream));
-        TransformArgs a{dX, m, ld, dC, (int)k, dcc, dO};
+        TransformArgs a{dX, m, ld, dC, (int)k, dcc, dO, dfrag, c.num_cu};
         HIP_TRY(launch_transform(a, c.stream), "transform launch");
         TRY(download_bytes(c, dO, size_t(m) * k * sizeof(float), out + size_t(r) * k, c.stream));
     }
