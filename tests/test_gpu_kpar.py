@@ -56,7 +56,8 @@ def _check(got, ref, X, rows, what):
     assert exact >= 0.99, f"{what}: only {exact:.5f} bit-exact"
 
 
-@pytest.mark.parametrize("n,d,m", [(1000, 5, 1), (4097, 33, 20), (3001, 100, 70), (777, 1, 9)])
+@pytest.mark.parametrize("n,d,m", [(1000, 5, 1), (4097, 33, 20), (3001, 100, 70), (777, 1, 9),
+                                   (150001, 120, 37)])  # more 64-row spans than resident blocks; rows of 120
 def test_mindists_match_oracle(bridge, n, d, m):
     _say(f"k-means|| mindists n={n} d={d} m={m}")
     X = _blobs(n, d, 6, n + m)
