@@ -85,6 +85,8 @@ SHAPES = [
     (300, 3, 300, None),     # k = n: every row once
     (70000, 16, 16, 3),      # 274 row blocks in the running sum
     (20000, 100, 50, None),
+    (5000, 50, 20, None),    # rows of 52 floats (the 64-float instance), 4 candidates
+    (4000, 120, 12, 8),      # rows of 120 floats (the 128-float instance), 8 candidates
 ]
 
 
