@@ -504,29 +504,41 @@ __global__ __launch_bounds__(256, 4) void k_pp_mm_min(PPArgs a, int m)
 
         float best[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
         const float* ar = tile + (16 * w + cj) * S + q;  // A: row cj, feature 4 j + q
-        for (int g = 0; g < G; ++g) {
+        // two groups at a time: two independent chains share the A values
+        for (int g = 0; g < G; g += 2) {
+            const bool two = g + 1 < G;  // wave-uniform
             const double* bf = a.ctab + ((long)g * c4 << 6) + lane;
-            v4d acc = {0.0, 0.0, 0.0, 0.0};
-            // eight K steps at a time: their B fragments and A values loaded together
-            for (int j0 = 0; j0 < c4; j0 += 8) {
-                double bv[8];
-                float av[8];
+            const double* bf2 = two ? bf + ((long)c4 << 6) : bf;  // (in bounds either way)
+            v4d acc = {0.0, 0.0, 0.0, 0.0}, acc2 = {0.0, 0.0, 0.0, 0.0};
+            // four K steps at a time: their B fragments and A values loaded together
+            for (int j0 = 0; j0 < c4; j0 += 4) {
+                double bv[4], bv2[4];
+                float av[4];
 #pragma unroll
-                for (int u = 0; u < 8; ++u)
+                for (int u = 0; u < 4; ++u)
                     if (j0 + u < c4) {
                         bv[u] = bf[(long)(j0 + u) << 6];
+                        bv2[u] = bf2[(long)(j0 + u) << 6];
                         av[u] = ar[4 * (j0 + u)];
                     }
 #pragma unroll
-                for (int u = 0; u < 8; ++u)
-                    if (j0 + u < c4) acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)av[u], bv[u], acc, 0, 0, 0);
+                for (int u = 0; u < 4; ++u)
+                    if (j0 + u < c4) {
+                        const double x = (double)av[u];
+                        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(x, bv[u], acc, 0, 0, 0);
+                        if (two) acc2 = __builtin_amdgcn_mfma_f64_16x16x4f64(x, bv2[u], acc2, 0, 0, 0);
+                    }
             }
-            const double cn = a.ccn[16 * g + cj];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float d32 = (float)((-2.0 * acc[r] + cn) + xxr[r]);
-                if (d32 < 0.f) d32 = 0.f;
-                best[r] = d32 < best[r] ? d32 : best[r];
+            for (int p = 0; p < 2; ++p) {
+                if (p == 1 && !two) break;
+                const double cn = a.ccn[16 * (g + p) + cj];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float d32 = (float)((-2.0 * (p == 0 ? acc[r] : acc2[r]) + cn) + xxr[r]);
+                    if (d32 < 0.f) d32 = 0.f;
+                    best[r] = d32 < best[r] ? d32 : best[r];
+                }
             }
         }
         // min over the 16 candidate lanes of each row (lanes 16 q .. 16 q + 15)

@@ -216,32 +216,43 @@ __global__ __launch_bounds__(256, 4) void k_transform_mm(TransformArgs a)
         for (int r = 0; r < 4; ++r) xxr[r] = sxx[16 * w + q + 4 * r];
 
         const float* ar = tile + (16 * w + cj) * S + q;  // A: row cj, feature 4 j + q
-        for (int g = 0; g < G; ++g) {
+        // two groups at a time: two independent chains share the A values
+        for (int g = 0; g < G; g += 2) {
+            const bool two = g + 1 < G;  // wave-uniform
             const double* bf = a.cfrag + ((long)g * c4 << 6) + lane;
-            v4d acc = {0.0, 0.0, 0.0, 0.0};
-            for (int j0 = 0; j0 < c4; j0 += 8) {  // eight K steps' operands loaded together
-                double bv[8];
-                float av[8];
+            const double* bf2 = two ? bf + ((long)c4 << 6) : bf;  // (in bounds either way)
+            v4d acc = {0.0, 0.0, 0.0, 0.0}, acc2 = {0.0, 0.0, 0.0, 0.0};
+            for (int j0 = 0; j0 < c4; j0 += 4) {  // four K steps' operands loaded together
+                double bv[4], bv2[4];
+                float av[4];
 #pragma unroll
-                for (int u = 0; u < 8; ++u)
+                for (int u = 0; u < 4; ++u)
                     if (j0 + u < c4) {
                         bv[u] = bf[(long)(j0 + u) << 6];
+                        bv2[u] = bf2[(long)(j0 + u) << 6];
                         av[u] = ar[4 * (j0 + u)];
                     }
 #pragma unroll
-                for (int u = 0; u < 8; ++u)
-                    if (j0 + u < c4) acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)av[u], bv[u], acc, 0, 0, 0);
+                for (int u = 0; u < 4; ++u)
+                    if (j0 + u < c4) {
+                        const double x = (double)av[u];
+                        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(x, bv[u], acc, 0, 0, 0);
+                        if (two) acc2 = __builtin_amdgcn_mfma_f64_16x16x4f64(x, bv2[u], acc2, 0, 0, 0);
+                    }
             }
-            const int col = 16 * g + cj;
-            if (col < k) {
-                const double cn = a.cc[col];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const long row = r0 + 16 * w + q + 4 * r;
-                    if (row < n) {
-                        float d32 = (float)((-2.0 * acc[r] + xxr[r]) + cn);
-                        if (d32 < 0.f) d32 = 0.f;
-                        a.out[row * k + col] = (float)sqrt((double)d32);
+            for (int p = 0; p < 2; ++p) {
+                const int col = 16 * (g + p) + cj;
+                if (col < k && (p == 0 || two)) {
+                    const double cn = a.cc[col];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const long row = r0 + 16 * w + q + 4 * r;
+                        if (row < n) {
+                            float d32 = (float)((-2.0 * (p == 0 ? acc[r] : acc2[r]) + xxr[r]) + cn);
+                            if (d32 < 0.f) d32 = 0.f;
+                            a.out[row * k + col] = (float)sqrt((double)d32);
+                        }
                     }
                 }
             }
