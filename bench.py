@@ -140,8 +140,8 @@ def main():
                     help="also run one device-to-device copy of MIB MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the multi-GPU sharding design is described in DESIGN.md).", file=sys.stderr)
+        print(f"bench.py: one GPU per run; --gpus {args.gpus} is not supported "
+              "(the library shards nothing across GPUs).", file=sys.stderr)
         sys.exit(2)
 
     from skmetal_amd import _bridge, _synth

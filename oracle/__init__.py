@@ -1,7 +1,7 @@
 """Oracle for the KMeans Lloyd path -- TEST INFRASTRUCTURE ONLY.
 
 CPU restatement of scikit-learn 1.7.2's dense Lloyd k-means (the CPU path
-skmetal dispatches ``KMeans`` to), used exclusively as the checker by
+skmetal dispatches ``KMeans`` to), used only to check results, by
 ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py``.  Nothing in the product package imports this module.
 
