@@ -238,34 +238,59 @@ static void stage_rows(float* p, const float* src, long m, int cols, int ld)
 // row order, and both divisions by the count run in fp64 (an intp count) and
 // round to fp32.  Host threads take contiguous column ranges and run those
 // chains: two passes over X, no temporary arrays, numpy's bits.
+// Columns [c0, c0 + W) of X: numpy's fp32 chains in row order (sum, then the
+// squared deviations from the fp32 mean), the W running values in registers.
+template <int W>
+static void column_variance_block(const float* X, long n, int d, int c0, float* out)
+{
+#pragma clang fp contract(off)
+    float s[W], s2[W], mean[W];
+    for (int c = 0; c < W; ++c) s[c] = 0.f;
+    for (long r = 0; r < n; ++r) {
+        const float* row = X + r * d + c0;
+        for (int c = 0; c < W; ++c) s[c] = s[c] + row[c];
+    }
+    for (int c = 0; c < W; ++c) {
+        mean[c] = (float)((double)s[c] / (double)n);
+        s2[c] = 0.f;
+    }
+    for (long r = 0; r < n; ++r) {
+        const float* row = X + r * d + c0;
+        for (int c = 0; c < W; ++c) {
+            const float t = row[c] - mean[c];
+            const float t2 = t * t;
+            s2[c] = s2[c] + t2;
+        }
+    }
+    for (int c = 0; c < W; ++c) out[c0 + c] = (float)((double)s2[c] / (double)n);
+}
+
 static void column_variance_f32(const float* X, long n, int d, float* out)
 {
+    // a thread's columns in blocks of 16, 8, 4, 2 and 1
     auto work = [X, n, d, out](int c0, int c1) {
-#pragma clang fp contract(off)
-        const int w = c1 - c0;
-        std::vector<float> s(static_cast<size_t>(w), 0.f), s2(static_cast<size_t>(w), 0.f),
-            mean(static_cast<size_t>(w));
-        for (long r = 0; r < n; ++r) {
-            const float* row = X + r * d + c0;
-            for (int c = 0; c < w; ++c) s[size_t(c)] = s[size_t(c)] + row[c];
+        int c = c0;
+        for (; c + 16 <= c1; c += 16) column_variance_block<16>(X, n, d, c, out);
+        if (c + 8 <= c1) {
+            column_variance_block<8>(X, n, d, c, out);
+            c += 8;
         }
-        for (int c = 0; c < w; ++c) mean[size_t(c)] = (float)((double)s[size_t(c)] / (double)n);
-        for (long r = 0; r < n; ++r) {
-            const float* row = X + r * d + c0;
-            for (int c = 0; c < w; ++c) {
-                const float t = row[c] - mean[size_t(c)];
-                const float t2 = t * t;
-                s2[size_t(c)] = s2[size_t(c)] + t2;
-            }
+        if (c + 4 <= c1) {
+            column_variance_block<4>(X, n, d, c, out);
+            c += 4;
         }
-        for (int c = 0; c < w; ++c) out[c0 + c] = (float)((double)s2[size_t(c)] / (double)n);
+        if (c + 2 <= c1) {
+            column_variance_block<2>(X, n, d, c, out);
+            c += 2;
+        }
+        if (c < c1) column_variance_block<1>(X, n, d, c, out);
     };
     unsigned nt = std::thread::hardware_concurrency();
     const unsigned by_cols = unsigned((d + 7) / 8);  // at least 8 columns (32 bytes of a row) per thread
     nt = std::max(1u, std::min({nt, 16u, by_cols}));
     if (size_t(n) * size_t(d) < (size_t(1) << 20)) nt = 1;
     std::vector<std::thread> th;
-    const int per = (d + int(nt) - 1) / int(nt);
+    const int per = ((d + int(nt) - 1) / int(nt) + 7) / 8 * 8;
     for (unsigned t = 1; t < nt; ++t) {
         const int c0 = int(t) * per, c1 = std::min(d, c0 + per);
         if (c0 < c1) th.emplace_back(work, c0, c1);
