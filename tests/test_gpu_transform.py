@@ -73,7 +73,7 @@ def test_transform_golden(bridge, case):
 
 
 @pytest.mark.parametrize("n,d,k", [(1, 1, 1), (63, 5, 65), (1000, 1, 3), (777, 300, 10), (4097, 33, 130),
-                                   (5000, 100, 50), (100003, 120, 21)])
+                                   (5000, 100, 50), (100003, 120, 21), (70001, 64, 37)])
 def test_transform_vs_oracle(bridge, n, d, k):
     _say(f"transform vs oracle n={n} d={d} k={k}")
     rng = np.random.default_rng(n * 7 + d + k)
