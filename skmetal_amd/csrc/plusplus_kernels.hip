@@ -584,16 +584,37 @@ __global__ __launch_bounds__(1024) void k_pp_select(PPArgs a, int c)
 
     // centre c - 1: the candidate of least potential (first one on ties).
     // Each potential is a fixed-order sum of the block partials: thread i adds
-    // blocks i, i + 1024, ... (the loads of TB candidates in flight together),
-    // then a butterfly per wave, then the 16 waves in order.
+    // its blocks (the loads of TB candidates in flight together), then a
+    // butterfly per wave, then the 16 waves in order.  With at most TB
+    // candidates and 2048 blocks, thread i owns blocks [m i, m i + m), the
+    // same blocks as in the running sum below, which then takes the chosen
+    // candidate's values from these registers instead of loading them again;
+    // otherwise thread i adds blocks i, i + 1024, ...
+    const int m = (a.nb + 1023) / 1024;
+    const int b0 = m * tid, b1 = min(a.nb, b0 + m);
+    const bool regs = Tq <= TB && m <= 2;  // block-uniform
+    double pv[TB][2];
     for (int t0 = 0; t0 < Tq; t0 += TB) {
         double v[TB];
 #pragma unroll
         for (int t = 0; t < TB; ++t) v[t] = 0.0;
-        for (int b = tid; b < a.nb; b += 1024) {
+        if (regs) {
 #pragma unroll
             for (int t = 0; t < TB; ++t)
-                if (t0 + t < Tq) v[t] += a.P[q][(long)(t0 + t) * a.nb + b];
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    pv[t][i] = t < Tq && b0 + i < b1 ? a.P[q][(long)t * a.nb + b0 + i] : 0.0;
+#pragma unroll
+            for (int t = 0; t < TB; ++t)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    if (b0 + i < b1) v[t] += pv[t][i];
+        } else {
+            for (int b = tid; b < a.nb; b += 1024) {
+#pragma unroll
+                for (int t = 0; t < TB; ++t)
+                    if (t0 + t < Tq) v[t] += a.P[q][(long)(t0 + t) * a.nb + b];
+            }
         }
 #pragma unroll
         for (int t = 0; t < TB; ++t) {
@@ -636,10 +657,18 @@ __global__ __launch_bounds__(1024) void k_pp_select(PPArgs a, int c)
     // [m i, m i + m); its start is the scan of the thread totals before it.
     // found[t] = the first block whose running sum reaches r_t.
     const double* S = a.P[q] + (long)best * a.nb;
-    const int m = (a.nb + 1023) / 1024;
-    const int b0 = m * tid, b1 = min(a.nb, b0 + m);
+    double sv0 = 0.0, sv1 = 0.0;  // the register path's values of S[b0], S[b0 + 1]
+    if (regs) {
+#pragma unroll
+        for (int t = 0; t < TB; ++t)
+            if (t == best) {
+                sv0 = pv[t][0];
+                sv1 = pv[t][1];
+            }
+    }
+    auto sval = [&](int b) { return regs ? (b == b0 ? sv0 : sv1) : S[b]; };
     double own = 0.0;
-    for (int b = b0; b < b1; ++b) own += S[b];
+    for (int b = b0; b < b1; ++b) own += sval(b);
     const double incl = wave_scan(own, lane);
     if (lane == 63) wsum[wv] = incl;
     double excl = __shfl_up(incl, 1, 64);
@@ -650,7 +679,7 @@ __global__ __launch_bounds__(1024) void k_pp_select(PPArgs a, int c)
     run0 += excl;
     double run = run0;
     for (int b = b0; b < b1; ++b) {
-        run += S[b];
+        run += sval(b);
         a.pfx[b] = run;
     }
     // a thread's running sum only grows, so the first lane of a wave whose last
@@ -662,7 +691,7 @@ __global__ __launch_bounds__(1024) void k_pp_select(PPArgs a, int c)
             double r = run0;
             int bf = b1 - 1;
             for (int b = b0; b < b1; ++b) {
-                r += S[b];
+                r += sval(b);
                 if (r >= rv[t]) {
                     bf = b;
                     break;
