@@ -827,7 +827,10 @@ hipError_t launch_pp_dist(const PPArgs& a, int c, hipStream_t s)
 
 hipError_t launch_pp_mindist(const PPArgs& a, int m, hipStream_t s)
 {
-    if (pp_rows_min_path(a.ld) && a.ctab != nullptr && a.ccn != nullptr) {
+    // a round of at most 4 candidates (the first, against the first row) on
+    // the VALU kernel: the matrix cores would pad it to 16 (62 against 77 us at
+    // 500000 x 100); the sums are the same fma chains in feature order
+    if (m > 4 && pp_rows_min_path(a.ld) && a.ctab != nullptr && a.ccn != nullptr) {
         if (m > 0) {
             const long e = (long)(m + 15) / 16 * 16 * a.ld;  // G ld/4 64 fragments
             hipLaunchKernelGGL(k_pp_bfrag, dim3((unsigned)((e + 255) / 256)), dim3(256), 0, s, a, m);
