@@ -132,15 +132,18 @@ class HipKMeans(BaseGPUEstimator):
 
         best = None
         plusplus = isinstance(init, str) and init == "k-means++"
-        # The first seeding's random draws run while X is uploaded and centred, and
-        # the tolerance's column variances (host threads, no device) once the upload
-        # is done, while the device seeds: both the upload's staging and the
-        # variances are bound by the host's memory bandwidth.  Nothing else draws
-        # from random_state in between, so the draws are those of the serial order.
+        # The first seeding's random draws run while X is uploaded and centred.  The
+        # tolerance's column variances (host threads, no device) run once the
+        # upload is done, while the device seeds with k-means++ (both the upload's
+        # staging and the variances are bound by the host's memory bandwidth), and
+        # beside the upload for the other inits.  Nothing else draws from
+        # random_state in between, so the draws are those of the serial order.
         with ThreadPoolExecutor(max_workers=2) as pool, _bridge.LloydHandle(n, d, k) as h:
             draws_f = pool.submit(_bridge.plusplus_draws, random_state, n, k) if plusplus else None
+            tol_f = None if plusplus else pool.submit(_tolerance, X, est.tol)
             h.load(X, center=True)
-            tol_f = pool.submit(_tolerance, X, est.tol)
+            if tol_f is None:
+                tol_f = pool.submit(_tolerance, X, est.tol)
             if not np.isfinite(h.max_abs()):
                 # NaN or infinity in X (or a centring that overflowed): scikit-learn's
                 # check raises its own error for the first two and passes the last
